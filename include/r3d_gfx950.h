@@ -1,0 +1,59 @@
+/* r3d_gfx950.h -- the C ABI exported by libr3d_gfx950.so.
+ *
+ * Every entry point replaces the reference libr3d export of the same name; the engine
+ * (radiance, ABI 26) dlopens the library, reads the row table through the rad_* calls
+ * and reaches the gemm_nt_q entries through RadKernelInfo::launch.  Plain C types and
+ * device pointers only.
+ */
+#ifndef R3D_GFX950_H
+#define R3D_GFX950_H
+
+#include <stdint.h>
+#include "rad_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Plugin identity.  Replaces src/r3d_rows.cpp:16 (returns RAD_ABI_VERSION, 26) and
+ * src/r3d_rows.cpp:18-27 (name, version, description, targets "gfx950"). */
+uint32_t rad_plugin_abi_version(void);
+const RadPluginInfo* rad_plugin_info(void);
+
+/* Op schemas this plugin declares: gemm_nt_q, parameters and operands exactly as
+ * src/r3d_rows.cpp:186-210.  Replaces src/r3d_rows.cpp:2238-2247. */
+int rad_kernel_schema_count(void);
+const RadOpSchema* rad_kernel_schema_at(int i);
+
+/* The row table after the registration-time kill switches (R3D_NO_MXFP4,
+ * R3D_NO_FP4_DEC, R3D_NO_FP8A8, R3D_NO_FP8_DEC).  Replaces src/r3d_rows.cpp:2266-2278
+ * with the gate of src/r3d_rows.cpp:2216-2236. */
+int rad_kernel_count(void);
+const RadKernelInfo* rad_kernel_at(int i);
+
+/* gemm_nt_q at mxfp4a8, prefill row (any M).  Replaces src/r3d_gemm_mxfp4.hip:1587-1691.
+ * Operands (a, a_scale, b, b_scale, y, a_sum?, b_ref?); params N, K, dtype "mxfp4a8";
+ * M = numel(y)/N.  Returns RAD_OK, or RAD_E_UNSUPPORTED / RAD_E_SHAPE / RAD_E_STRIDE for a
+ * refused format and RAD_E_DEVICE for a failed launch.  Asynchronous on `s`. */
+int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s);
+
+/* gemm_nt_q at mxfp4a8, decode band M <= 16.  Replaces src/r3d_gemm_mxfp4.hip:1712-2170
+ * (r3d_rad_gemm_nt_q_mxfp4_decode and its q8x sibling share this one row here). */
+int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s);
+
+/* gemm_nt_q at fp8a8, prefill row.  Replaces src/r3d_gemm_fp8a8.hip:1054-1099. */
+int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s);
+
+/* gemm_nt_q at fp8a8, decode band M <= 16.  Replaces src/r3d_gemm_fp8a8.hip:1101-1130. */
+int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
+
+/* Host-only diagnostic with no counterpart in the reference: runs `row`'s preamble and
+ * plan on `a` and writes the chosen arm and launch geometry (or the refusal) into buf.
+ * Launches nothing, touches no device memory.  Returns the plan's status code. */
+int r3d_gfx950_describe(const char* row, const RadArgs* a, char* buf, int len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* R3D_GFX950_H */

@@ -1,0 +1,45 @@
+/* rad_plugin.h -- host-side argument helpers a radiance kernel row uses, reconstructed
+ * from their call sites in the reference (rad_arg_in: src/r3d_gemm_mxfp4.hip:1594-1600;
+ * rad_args_geti / rad_args_gets: :1523-1529; rad_tensor_numel: :1536).  Semantics:
+ *   rad_arg_in(a, i)      the i-th operand, or null when absent (index past n_t or null
+ *                         data pointer);
+ *   rad_args_geti/gets    look a parameter up by key, 1 when found with that kind;
+ *   rad_tensor_numel      product of the shape (0 for a null tensor).
+ */
+#ifndef RAD_PLUGIN_H
+#define RAD_PLUGIN_H
+
+#include <string.h>
+#include "rad_abi.h"
+
+static inline const RadTensor* rad_arg_in(const RadArgs* a, int i) {
+    if (!a || i < 0 || i >= a->n_t || !a->t) return 0;
+    return a->t[i].data ? &a->t[i] : 0;
+}
+
+static inline int rad_args_geti(const RadArgs* a, const char* key, long long* out) {
+    if (!a || !a->p) return 0;
+    for (int i = 0; i < a->n_p; ++i)
+        if (a->p[i].key && strcmp(a->p[i].key, key) == 0 && a->p[i].kind == RAD_P_INT) {
+            *out = a->p[i].ival;
+            return 1;
+        }
+    return 0;
+}
+
+static inline const char* rad_args_gets(const RadArgs* a, const char* key) {
+    if (!a || !a->p) return 0;
+    for (int i = 0; i < a->n_p; ++i)
+        if (a->p[i].key && strcmp(a->p[i].key, key) == 0 && a->p[i].kind == RAD_P_STR)
+            return a->p[i].sval;
+    return 0;
+}
+
+static inline long long rad_tensor_numel(const RadTensor* t) {
+    if (!t) return 0;
+    long long n = 1;
+    for (uint32_t i = 0; i < t->rank && i < RAD_MAX_RANK; ++i) n *= t->shape[i];
+    return n;
+}
+
+#endif /* RAD_PLUGIN_H */

@@ -1,0 +1,308 @@
+"""libr3d_amd -- Python host mirror of the gfx950 gemm_nt_q rows (libr3d_gfx950.so).
+
+The shared library is the product: a radiance kernel plugin (ABI 26) whose rows are
+reached through ``rad_kernel_at(i)->launch(const RadArgs*, RadStream)``.  This module
+binds that C ABI with ctypes -- the structures below mirror ``include/rad_abi.h`` field
+for field -- and adds what an engine would do around it: build ``RadArgs`` from device
+tensors and resolve a row per op and band (constraints + priority, the resolver the
+reference describes at src/r3d_rows.cpp:1105-1110,1165-1177).
+
+PyTorch is used only for device memory and streams.  Every compute call goes through the
+HIP library; if the library is missing this module raises instead of computing anything
+another way.
+"""
+import ctypes
+import os
+
+__all__ = [
+    "RAD_OK", "RAD_E_UNSUPPORTED", "RAD_E_SHAPE", "RAD_E_STRIDE", "RAD_E_DTYPE",
+    "RAD_E_INVAL", "RAD_E_DEVICE", "DT", "RadTensor", "RadParam", "RadArgs",
+    "RadKernelInfo", "RadOpSchema", "lib", "lib_path", "rows", "schemas", "resolve",
+    "launch_row", "gemm_nt_q", "describe", "GemmOperands",
+]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+lib_path = os.path.join(_HERE, "libr3d_gfx950.so")
+
+RAD_MAX_RANK = 8
+RAD_OK, RAD_E_UNSUPPORTED, RAD_E_SHAPE, RAD_E_STRIDE, RAD_E_DTYPE, RAD_E_INVAL, RAD_E_DEVICE = range(7)
+
+# enum RadDtype (include/rad_abi.h)
+DT = {name: i for i, name in enumerate(
+    ["F32", "BF16", "F16", "F8E4M3", "F8E5M2", "FP4E2M1", "E8M0", "U8", "I8", "I16", "I32",
+     "U32", "I64", "BOOL"])}
+RAD_P_INT, RAD_P_STR, RAD_P_F64 = 0, 1, 2
+RAD_C_EQ, RAD_C_LE, RAD_C_GE, RAD_C_DIV, RAD_C_IN = range(5)
+
+
+class RadTensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_uint32), ("rank", ctypes.c_uint32),
+                ("shape", ctypes.c_int64 * RAD_MAX_RANK), ("stride", ctypes.c_int64 * RAD_MAX_RANK)]
+
+
+class RadParam(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("key", ctypes.c_char_p), ("ival", ctypes.c_longlong),
+                ("ihi", ctypes.c_longlong), ("sval", ctypes.c_char_p), ("dval", ctypes.c_double)]
+
+
+class RadTunableValue(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("value", ctypes.c_longlong)]
+
+
+class RadArgs(ctypes.Structure):
+    _fields_ = [("t", ctypes.POINTER(RadTensor)), ("n_t", ctypes.c_int),
+                ("p", ctypes.POINTER(RadParam)), ("n_p", ctypes.c_int),
+                ("tv", ctypes.POINTER(RadTunableValue)), ("n_tv", ctypes.c_int),
+                ("scratch", ctypes.c_void_p), ("scratch_bytes", ctypes.c_int64),
+                ("flags", ctypes.c_uint32)]
+
+
+class RadConstraint(ctypes.Structure):
+    _fields_ = [("key", ctypes.c_char_p), ("op", ctypes.c_int), ("ival", ctypes.c_longlong),
+                ("sval", ctypes.c_char_p)]
+
+
+LaunchFn = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.POINTER(RadArgs), ctypes.c_void_p)
+
+
+class RadKernelInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("op", ctypes.c_char_p), ("family", ctypes.c_char_p),
+                ("summary", ctypes.c_char_p), ("limits", ctypes.c_char_p),
+                ("formats", ctypes.c_char_p), ("domain", ctypes.c_int),
+                ("priority", ctypes.c_int), ("constraints", ctypes.POINTER(RadConstraint)),
+                ("n_constraints", ctypes.c_int), ("tunables", ctypes.c_void_p),
+                ("n_tunables", ctypes.c_int), ("replaces", ctypes.c_char_p),
+                ("init", ctypes.c_void_p), ("fini", ctypes.c_void_p), ("launch", ctypes.c_void_p),
+                ("scratch", ctypes.c_void_p), ("layout", ctypes.c_void_p),
+                ("relayout", ctypes.c_void_p), ("opd_shape", ctypes.c_void_p),
+                ("unrelayout", ctypes.c_void_p)]
+
+
+class RadParamSpec(ctypes.Structure):
+    _fields_ = [("key", ctypes.c_char_p), ("kind", ctypes.c_int), ("req", ctypes.c_int),
+                ("role", ctypes.c_int)]
+
+
+class RadOperandSpec(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("role", ctypes.c_int), ("optional", ctypes.c_int)]
+
+
+class RadOpSchema(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_char_p), ("params", ctypes.POINTER(RadParamSpec)),
+                ("n_params", ctypes.c_int), ("operands", ctypes.POINTER(RadOperandSpec)),
+                ("n_operands", ctypes.c_int), ("prose", ctypes.c_char_p)]
+
+
+class RadPluginInfo(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("name", ctypes.c_char_p), ("version", ctypes.c_char_p),
+                ("description", ctypes.c_char_p), ("targets", ctypes.c_char_p)]
+
+
+_LIB = None
+
+
+def lib():
+    """The loaded libr3d_gfx950.so (raises if it has not been built)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(lib_path):
+            raise RuntimeError("libr3d_gfx950.so is not built (run __graft_entry__.build() or "
+                               "python -m libr3d_amd.build): %s" % lib_path)
+        L = ctypes.CDLL(lib_path)
+        L.rad_plugin_abi_version.restype = ctypes.c_uint32
+        L.rad_plugin_info.restype = ctypes.POINTER(RadPluginInfo)
+        L.rad_kernel_schema_count.restype = ctypes.c_int
+        L.rad_kernel_schema_at.restype = ctypes.POINTER(RadOpSchema)
+        L.rad_kernel_schema_at.argtypes = [ctypes.c_int]
+        L.rad_kernel_count.restype = ctypes.c_int
+        L.rad_kernel_at.restype = ctypes.POINTER(RadKernelInfo)
+        L.rad_kernel_at.argtypes = [ctypes.c_int]
+        for name in ("r3d_rad_gemm_nt_q", "r3d_rad_gemm_nt_q_mxfp4_decode",
+                     "r3d_rad_gemm_nt_q_fp8", "r3d_rad_gemm_nt_q_fp8_decode"):
+            fn = getattr(L, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.POINTER(RadArgs), ctypes.c_void_p]
+        L.r3d_gfx950_describe.restype = ctypes.c_int
+        L.r3d_gfx950_describe.argtypes = [ctypes.c_char_p, ctypes.POINTER(RadArgs),
+                                          ctypes.c_char_p, ctypes.c_int]
+        _LIB = L
+    return _LIB
+
+
+def _s(b):
+    return b.decode() if isinstance(b, bytes) else b
+
+
+def rows():
+    """The registered rows as dicts (after the registration-time kill switches)."""
+    L = lib()
+    out = []
+    for i in range(L.rad_kernel_count()):
+        k = L.rad_kernel_at(i).contents
+        cons = [(_s(k.constraints[c].key), k.constraints[c].op, k.constraints[c].ival,
+                 _s(k.constraints[c].sval)) for c in range(k.n_constraints)]
+        out.append({"name": _s(k.name), "op": _s(k.op), "priority": k.priority,
+                    "domain": k.domain, "constraints": cons, "launch": k.launch})
+    return out
+
+
+def schemas():
+    L = lib()
+    out = []
+    for i in range(L.rad_kernel_schema_count()):
+        s = L.rad_kernel_schema_at(i).contents
+        out.append({
+            "op": _s(s.op),
+            "params": [(_s(s.params[j].key), s.params[j].kind, s.params[j].req)
+                       for j in range(s.n_params)],
+            "operands": [(_s(s.operands[j].name), s.operands[j].role, s.operands[j].optional)
+                         for j in range(s.n_operands)],
+        })
+    return out
+
+
+def _holds(c, query):
+    key, op, ival, sval = c
+    if key not in query:
+        return False                     # a constraint on an absent key never holds
+    v = query[key]
+    if op == RAD_C_IN:
+        return isinstance(v, str) and v in (sval or "").split()
+    if isinstance(v, str):
+        return False
+    if op == RAD_C_EQ:
+        return v == ival
+    if op == RAD_C_LE:
+        return v <= ival
+    if op == RAD_C_GE:
+        return v >= ival
+    if op == RAD_C_DIV:
+        return ival != 0 and v % ival == 0
+    return False
+
+
+def resolve(op, query):
+    """Highest-priority registered row of `op` whose constraints all hold, or None."""
+    best = None
+    for r in rows():
+        if r["op"] != op:
+            continue
+        if all(_holds(c, query) for c in r["constraints"]):
+            if best is None or r["priority"] > best["priority"]:
+                best = r
+    return best
+
+
+class GemmOperands:
+    """Owns the ctypes RadArgs for one gemm_nt_q call over device tensors.
+
+    a      uint8 [M, K]           e4m3 codes
+    a_scale float32 [M, K/128]
+    b      uint8 [N, K/2] (mxfp4a8: packed e2m1, low nibble = even k) or [N, K] (fp8a8)
+    b_scale uint8 [N, K/32] E8M0 (mxfp4a8) or bf16/int16 [N or N/128, K/128] (fp8a8)
+    y      bf16/int16 [M, N]
+    """
+
+    def __init__(self, a, a_scale, b, b_scale, y, *, dtype, N, K, group=None, M=None,
+                 a_sum=None, b_ref=None, extra_params=None, y_shape=None, tunables=None):
+        mx = dtype == "mxfp4a8"
+        self.dtype = dtype
+        group = group if group is not None else (32 if mx else 128)
+        t = (RadTensor * 7)()
+
+        def fill(i, x, dt, shape=None, stride=None):
+            if x is None:
+                t[i].data = None
+                t[i].rank = 0
+                return
+            t[i].data = x.data_ptr()
+            t[i].dtype = DT[dt]
+            shp = list(shape if shape is not None else x.shape)
+            std = list(stride if stride is not None else x.stride())
+            t[i].rank = len(shp)
+            for r, (s_, st) in enumerate(zip(shp, std)):
+                t[i].shape[r] = int(s_)
+                t[i].stride[r] = int(st)
+
+        fill(0, a, "F8E4M3")
+        fill(1, a_scale, "F32")
+        if mx:
+            # FP4 counts nibbles: [N, K] with strides {K, 1}
+            fill(2, b, "FP4E2M1", [b.shape[0], b.shape[1] * 2], [b.stride(0) * 2, 1])
+            fill(3, b_scale, "E8M0")
+        else:
+            fill(2, b, "F8E4M3")
+            fill(3, b_scale, "BF16")
+        fill(4, y, "BF16", y_shape)
+        fill(5, a_sum, "F32")
+        fill(6, b_ref, "BF16")
+        self._t = t
+        params = [("dtype", dtype), ("N", int(N)), ("K", int(K)), ("group", int(group))]
+        if M is not None:
+            params.append(("M", int(M)))
+        params += list(extra_params or [])
+        p = (RadParam * len(params))()
+        self._keep = []
+        for i, (k, v) in enumerate(params):
+            kb = k.encode()
+            self._keep.append(kb)
+            p[i].key = kb
+            if isinstance(v, str):
+                vb = v.encode()
+                self._keep.append(vb)
+                p[i].kind = RAD_P_STR
+                p[i].sval = vb
+            elif isinstance(v, float):
+                p[i].kind = RAD_P_F64
+                p[i].dval = v
+            else:
+                p[i].kind = RAD_P_INT
+                p[i].ival = v
+        self._p = p
+        tunables = list(tunables or [])
+        tv = (RadTunableValue * max(1, len(tunables)))()
+        for i, (k, v) in enumerate(tunables):
+            kb = k.encode()
+            self._keep.append(kb)
+            tv[i].name = kb
+            tv[i].value = int(v)
+        self._tv = tv
+        self.args = RadArgs(ctypes.cast(t, ctypes.POINTER(RadTensor)), 7,
+                            ctypes.cast(p, ctypes.POINTER(RadParam)), len(params),
+                            ctypes.cast(tv, ctypes.POINTER(RadTunableValue)), len(tunables),
+                            None, 0, 0)
+
+    def set_y(self, y):
+        self._t[4].data = y.data_ptr()
+
+
+def launch_row(row_name, ops, stream=0):
+    """Call the named row's launch pointer (as the engine does) and return its status."""
+    for r in rows():
+        if r["name"] == row_name:
+            fn = LaunchFn(r["launch"])
+            return fn(ctypes.byref(ops.args), ctypes.c_void_p(stream))
+    raise KeyError("row %s is not registered" % row_name)
+
+
+def describe(row_name, ops):
+    buf = ctypes.create_string_buffer(512)
+    rc = lib().r3d_gfx950_describe(row_name.encode(), ctypes.byref(ops.args), buf, 512)
+    return rc, buf.value.decode()
+
+
+def gemm_nt_q(a, a_scale, b, b_scale, y, *, dtype, N, K, group=None, stream=None, row=None):
+    """Resolve and launch gemm_nt_q on `stream` (a raw hipStream_t int, default the
+    current torch stream).  Returns (status, row name)."""
+    import torch
+    ops = GemmOperands(a, a_scale, b, b_scale, y, dtype=dtype, N=N, K=K, group=group)
+    M = y.numel() // N
+    if row is None:
+        r = resolve("gemm_nt_q", {"dtype": dtype, "M": M, "N": N, "K": K,
+                                  "group": group if group is not None else (32 if dtype == "mxfp4a8" else 128)})
+        if r is None:
+            return RAD_E_UNSUPPORTED, None
+        row = r["name"]
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    return launch_row(row, ops, stream), row

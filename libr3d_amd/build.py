@@ -1,0 +1,63 @@
+"""Build libr3d_gfx950.so (gfx950 only) and the CPU oracle library in-tree.
+
+    python -m libr3d_amd.build            # or: python libr3d_amd/build.py
+
+hipcc compiles the HIP kernels for --offload-arch=gfx950 with packed-fp32 code
+generation switched off; the host C++ (row table, plans) goes into the same shared
+object.  The oracle (oracle/Makefile) is test infrastructure and is built beside it.
+"""
+import os
+import shutil
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "libr3d_amd")
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "libr3d_gfx950.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+SOURCES = ["r3d_gemm.hip", "r3d_plan.cpp", "r3d_rows.cpp"]
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+    "-I" + os.path.join(ROOT, "include"), "-I" + CSRC,
+]
+
+
+def _run(cmd, cwd=None):
+    r = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if r.returncode != 0:
+        sys.stderr.write(out + "\n")
+        raise RuntimeError("command failed (%d): %s" % (r.returncode, " ".join(cmd)))
+    return out
+
+
+def build_library():
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC] + FLAGS + [os.path.join(CSRC, s) for s in SOURCES] + ["-o", tmp]
+    out = _run(cmd)
+    if out.strip():
+        sys.stderr.write(out + "\n")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle():
+    make = shutil.which("make")
+    if make is None:
+        raise RuntimeError("make not found")
+    _run([make, "-s", "-C", os.path.join(ROOT, "oracle")])
+    return os.path.join(ROOT, "oracle", "libr3d_oracle.so")
+
+
+def build_all():
+    build_oracle()
+    return build_library()
+
+
+if __name__ == "__main__":
+    print(build_all())

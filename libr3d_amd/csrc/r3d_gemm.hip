@@ -1,0 +1,134 @@
+/* r3d_gemm.hip -- the gfx950 gemm_nt_q row entries (mxfp4a8 and fp8a8, decode band and
+ * prefill tile) behind radiance's kernel-row launch signature
+ *     int launch(const RadArgs* a, RadStream s)
+ * (src/r3d_gemm_mxfp4.hip:1587-1588,1717-1718; src/r3d_gemm_fp8a8.hip:1054-1056,1108-1110).
+ *
+ * Each entry: kill-switch backstop (the registration gate in r3d_rows.cpp is where the
+ * engine re-resolves), the shared preamble (operands, M = numel(Y)/N), the format plan,
+ * the gfx950 chip gate, then one launch on the caller's stream.  No allocation, no
+ * synchronisation, no host<->device traffic in any entry.
+ */
+#include <hip/hip_runtime.h>
+
+#include <stdio.h>
+#include <string.h>
+
+#include "r3d_gemm_kernels.h"
+#include "r3d_plan.h"
+#include "rad_plugin.h"
+
+namespace r3d {
+
+/* Chip gate, per device, answered once: the rows are gfx950 code objects only. */
+static bool chip_ok() {
+    static int cache[64];                       /* 0 unknown, 1 yes, 2 no */
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    if (cache[dev] == 0) {
+        hipDeviceProp_t p;
+        memset(&p, 0, sizeof p);
+        const bool ok = hipGetDeviceProperties(&p, dev) == hipSuccess &&
+                        strncmp(p.gcnArchName, "gfx950", 6) == 0;
+        cache[dev] = ok ? 1 : 2;
+    }
+    return cache[dev] == 1;
+}
+
+static void debug_once(const char* what, int key) {
+    if (!env_debug()) return;
+    static unsigned long long seen[4] = {0, 0, 0, 0};
+    const int w = (key >> 6) & 3, b = key & 63;
+    if (seen[w] & (1ull << b)) return;
+    seen[w] |= 1ull << b;
+    fprintf(stderr, "libr3d_gfx950: %s launched\n", what);
+}
+
+static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) {
+    DecodeGeom g{};
+    decode_geom(P.M, P.N, P.K, splitk, &g);
+    const dim3 grid((unsigned)g.blocks), block((unsigned)(64 * g.waves));
+#define R3D_GEMV(ENC_, MT_)                                                             \
+    hipLaunchKernelGGL((gemv_kernel<ENC_, MT_, 4>), grid, block, 0, stream, P.A, P.AS, P.B, \
+                       P.BS, P.Y, (int)P.M, (int)P.N, g.steps, g.chunks, P.rblk,         \
+                       P.a_pitch, P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch)
+    if (P.enc == ENC_MXFP4A8) {
+        if (g.mt == 1) R3D_GEMV(ENC_MXFP4A8, 1);
+        else if (g.mt == 4) R3D_GEMV(ENC_MXFP4A8, 4);
+        else R3D_GEMV(ENC_MXFP4A8, 16);
+    } else {
+        if (g.mt == 1) R3D_GEMV(ENC_FP8A8, 1);
+        else if (g.mt == 4) R3D_GEMV(ENC_FP8A8, 4);
+        else R3D_GEMV(ENC_FP8A8, 16);
+    }
+#undef R3D_GEMV
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "libr3d_gfx950: decode GEMV launch FAILED (%s)\n", hipGetErrorName(e));
+        return RAD_E_DEVICE;
+    }
+    debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 decode GEMV" : "fp8a8 decode GEMV",
+               (P.enc << 4) | (g.mt << 1));
+    return RAD_OK;
+}
+
+static int launch_tile(const GemmPlan& P, hipStream_t stream) {
+    TileGeom g{};
+    tile_geom(P.M, P.N, &g);
+    if (g.grid_m > 65535) return RAD_E_SHAPE;
+    const dim3 grid((unsigned)g.grid_n, (unsigned)g.grid_m), block(256);
+    const int steps = (int)(P.K / 128);
+    if (P.enc == ENC_MXFP4A8)
+        hipLaunchKernelGGL((tile_kernel<ENC_MXFP4A8>), grid, block, 0, stream, P.A, P.AS, P.B,
+                           P.BS, P.Y, (int)P.M, (int)P.N, steps, P.rblk, P.a_pitch, P.as_pitch,
+                           P.b_pitch, P.bs_pitch, P.y_pitch);
+    else
+        hipLaunchKernelGGL((tile_kernel<ENC_FP8A8>), grid, block, 0, stream, P.A, P.AS, P.B,
+                           P.BS, P.Y, (int)P.M, (int)P.N, steps, P.rblk, P.a_pitch, P.as_pitch,
+                           P.b_pitch, P.bs_pitch, P.y_pitch);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "libr3d_gfx950: prefill tile launch FAILED (%s)\n", hipGetErrorName(e));
+        return RAD_E_DEVICE;
+    }
+    debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 prefill tile" : "fp8a8 prefill tile",
+               64 + P.enc);
+    return RAD_OK;
+}
+
+static int entry(const RadArgs* a, RadStream s, int enc, bool decode) {
+    if (enc == ENC_MXFP4A8 && (env_no_mxfp4() || (decode && env_no_fp4_dec())))
+        return RAD_E_UNSUPPORTED;               /* backstop: registration already hid it */
+    if (enc == ENC_FP8A8 && (env_no_fp8a8() || (decode && env_no_fp8_dec())))
+        return RAD_E_UNSUPPORTED;
+    int64_t M = 0, N = 0;
+    int rc = entry_preamble(a, enc, decode ? 16 : 0, &M, &N);
+    if (rc) return rc;
+    GemmPlan P{};
+    rc = enc == ENC_MXFP4A8 ? plan_mxfp4a8(a, M, N, &P) : plan_fp8a8(a, M, &P);
+    if (rc) return rc;
+    if (!chip_ok()) return RAD_E_UNSUPPORTED;
+    hipStream_t stream = (hipStream_t)s;
+    return decode ? launch_decode(P, decode_splitk(a), stream) : launch_tile(P, stream);
+}
+
+}  // namespace r3d
+
+extern "C" {
+
+int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s) {
+    return r3d::entry(a, s, r3d::ENC_MXFP4A8, false);
+}
+int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s) {
+    return r3d::entry(a, s, r3d::ENC_MXFP4A8, true);
+}
+int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s) {
+    return r3d::entry(a, s, r3d::ENC_FP8A8, false);
+}
+int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s) {
+    return r3d::entry(a, s, r3d::ENC_FP8A8, true);
+}
+int r3d_gfx950_describe(const char* row, const RadArgs* a, char* buf, int len) {
+    return r3d::describe(row, a, buf, len);
+}
+
+}  /* extern "C" */

@@ -1,0 +1,273 @@
+/* r3d_plan.cpp -- host plans for the gfx950 gemm_nt_q rows (see r3d_plan.h). */
+#include "r3d_plan.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "rad_plugin.h"
+
+namespace r3d {
+
+/* libref grid_block as the reference restates it (src/r3d_gemm_mxfp4.hip:71-84): the
+ * block a scale grid of `blocks` columns implies over `ext`. */
+int64_t grid_block(int64_t ext, int64_t blocks) {
+    if (ext <= 0) return 1;
+    if (blocks <= 1) return ext;
+    const int64_t lo = (ext + blocks - 1) / blocks;
+    int64_t p = 1;
+    while (p < lo) p <<= 1;
+    return ((ext + p - 1) / p == blocks) ? p : lo;
+}
+
+/* libref row_stride (src/r3d_gemm_mxfp4.hip:86-95): fold trailing axes until they span
+ * `cols`; the next axis out is the row. */
+int64_t row_stride(const RadTensor* t, int64_t cols) {
+    if (!t || t->rank < 2) return cols;
+    int64_t span = 1;
+    for (int i = (int)t->rank - 1; i >= 0; --i) {
+        span *= t->shape[i];
+        if (span == cols) return i > 0 ? t->stride[i - 1] : cols;
+        if (span > cols) break;
+    }
+    return t->stride[t->rank - 2];
+}
+
+static bool inner_contig(const RadTensor* t) {
+    return t->rank < 2 || t->stride[t->rank - 1] == 1;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static const int64_t kDimMax = 0x7FFFFFFLL;
+
+int entry_preamble(const RadArgs* a, int enc, int64_t m_max, int64_t* M, int64_t* N) {
+    const RadTensor* A    = rad_arg_in(a, 0);
+    const RadTensor* AS   = rad_arg_in(a, 1);
+    const RadTensor* B    = rad_arg_in(a, 2);
+    const RadTensor* BS   = rad_arg_in(a, 3);
+    const RadTensor* Y    = rad_arg_in(a, 4);
+    const RadTensor* ASUM = rad_arg_in(a, 5);
+    const RadTensor* BREF = rad_arg_in(a, 6);
+    if (!A || !AS || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
+    if (ASUM) return RAD_E_UNSUPPORTED;                 /* no zero point at either encoding */
+    if (enc == ENC_FP8A8 && BREF) return RAD_E_UNSUPPORTED;   /* b_ref: e2m1 weights only */
+    if (Y->dtype != RAD_BF16) return RAD_E_UNSUPPORTED;
+    long long n = 0;
+    if (!rad_args_geti(a, "N", &n) || n <= 0) return RAD_E_SHAPE;
+    const long long yn = rad_tensor_numel(Y);
+    if (yn <= 0 || yn % n) return RAD_E_SHAPE;
+    if (m_max > 0 && yn / n > m_max) return RAD_E_UNSUPPORTED;   /* the band's own bound */
+    if (!inner_contig(Y)) return RAD_E_STRIDE;
+    *M = yn / n;
+    *N = n;
+    return RAD_OK;
+}
+
+int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
+    const char* dtype = rad_args_gets(a, "dtype");
+    if (!dtype || strcmp(dtype, "mxfp4a8") != 0) return RAD_E_UNSUPPORTED;
+    long long pb = 0;
+    if (rad_args_geti(a, "pb1", &pb) && pb > 0) return RAD_E_UNSUPPORTED;   /* no parts */
+    if (rad_args_geti(a, "pb2", &pb) && pb > 0) return RAD_E_UNSUPPORTED;
+
+    const RadTensor* A  = rad_arg_in(a, 0);
+    const RadTensor* AS = rad_arg_in(a, 1);
+    const RadTensor* B  = rad_arg_in(a, 2);
+    const RadTensor* BS = rad_arg_in(a, 3);
+    const RadTensor* Y  = rad_arg_in(a, 4);
+    if (!A || !AS || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
+    if (A->dtype != RAD_F8E4M3 || B->dtype != RAD_FP4E2M1 || Y->dtype != RAD_BF16 ||
+        AS->dtype != RAD_F32 || (BS->dtype != RAD_E8M0 && BS->dtype != RAD_U8))
+        return RAD_E_UNSUPPORTED;
+
+    long long K = 0;
+    if (!rad_args_geti(a, "K", &K)) return RAD_E_SHAPE;
+    if (N <= 0 || K <= 0 || M <= 0) return RAD_E_SHAPE;
+    if (M > kDimMax || N > kDimMax || K > kDimMax) return RAD_E_SHAPE;
+    if (rad_tensor_numel(A) < M * K || rad_tensor_numel(B) < N * K) return RAD_E_SHAPE;
+
+    /* Scale grids derived from the operands, then pinned to b 32 / a 128. */
+    if (BS->rank != 2 || BS->stride[1] != 1 || BS->shape[0] < N) return RAD_E_UNSUPPORTED;
+    if (AS->rank != 2 || AS->stride[1] != 1 || AS->shape[0] < M) return RAD_E_UNSUPPORTED;
+    const int64_t bs_cols = BS->shape[1], as_cols = AS->shape[1];
+    if (grid_block(K, bs_cols) != 32 || grid_block(K, as_cols) != 128) return RAD_E_UNSUPPORTED;
+    if (bs_cols != (K + 31) / 32 || as_cols != (K + 127) / 128) return RAD_E_UNSUPPORTED;
+    if (rad_tensor_numel(AS) < M * as_cols) return RAD_E_SHAPE;
+
+    if (!inner_contig(A) || !inner_contig(B) || !inner_contig(Y)) return RAD_E_STRIDE;
+    if ((K & 1) || row_stride(B, K) != K) return RAD_E_STRIDE;   /* nibble rows packed */
+
+    /* gfx950 gates: whole 128-wide MFMA steps, 16-byte operand walks. */
+    if (K % 128) return RAD_E_UNSUPPORTED;
+    const int64_t a_pitch = row_stride(A, K);
+    if (!aligned16(A->data) || !aligned16(B->data) || (a_pitch & 15)) return RAD_E_UNSUPPORTED;
+
+    P->enc = ENC_MXFP4A8;
+    P->A = (const uint8_t*)A->data;
+    P->AS = (const float*)AS->data;
+    P->B = (const uint8_t*)B->data;
+    P->BS = BS->data;
+    P->Y = (uint16_t*)Y->data;
+    P->M = M; P->N = N; P->K = K;
+    P->a_pitch = a_pitch;
+    P->b_pitch = K / 2;
+    P->y_pitch = row_stride(Y, N);
+    P->as_pitch = row_stride(AS, as_cols);
+    P->bs_pitch = row_stride(BS, bs_cols);
+    P->as_cols = (int)as_cols;
+    P->bs_cols = (int)bs_cols;
+    P->rblk = 1;
+    return RAD_OK;
+}
+
+int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
+    const char* dtype = rad_args_gets(a, "dtype");
+    if (!dtype || strcmp(dtype, "fp8a8") != 0) return RAD_E_UNSUPPORTED;
+    long long pb = 0;
+    if (rad_args_geti(a, "pb1", &pb) && pb > 0) return RAD_E_UNSUPPORTED;   /* e2m1-only parts */
+    if (rad_args_geti(a, "pb2", &pb) && pb > 0) return RAD_E_UNSUPPORTED;
+
+    const RadTensor* A  = rad_arg_in(a, 0);
+    const RadTensor* AS = rad_arg_in(a, 1);
+    const RadTensor* B  = rad_arg_in(a, 2);
+    const RadTensor* BS = rad_arg_in(a, 3);
+    const RadTensor* Y  = rad_arg_in(a, 4);
+    if (!A || !AS || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
+    if (A->dtype != RAD_F8E4M3 || B->dtype != RAD_F8E4M3 || AS->dtype != RAD_F32 ||
+        BS->dtype != RAD_BF16 || Y->dtype != RAD_BF16)
+        return RAD_E_UNSUPPORTED;
+
+    long long N = 0, K = 0;
+    if (!rad_args_geti(a, "N", &N) || !rad_args_geti(a, "K", &K)) return RAD_E_SHAPE;
+    if (N <= 0 || K <= 0) return RAD_E_SHAPE;
+    if (K % 128) return RAD_E_UNSUPPORTED;        /* the scale grid closes on whole blocks */
+    if (M <= 0) return RAD_E_SHAPE;
+    if (M > kDimMax || N > kDimMax || K > kDimMax) return RAD_E_SHAPE;
+    if (rad_tensor_numel(A) < M * K || rad_tensor_numel(B) < N * K) return RAD_E_SHAPE;
+
+    if (BS->rank != 2 || BS->stride[1] != 1) return RAD_E_UNSUPPORTED;
+    if (AS->rank != 2 || AS->stride[1] != 1 || AS->shape[0] < M) return RAD_E_UNSUPPORTED;
+    const int64_t bs_cols = BS->shape[1], as_cols = AS->shape[1];
+    if (grid_block(K, bs_cols) != 128 || grid_block(K, as_cols) != 128) return RAD_E_UNSUPPORTED;
+    if (bs_cols != (K + 127) / 128 || as_cols != (K + 127) / 128) return RAD_E_SHAPE;
+    if (rad_tensor_numel(AS) < M * as_cols) return RAD_E_SHAPE;
+    int rblk;
+    if (BS->shape[0] >= N) {
+        if (BS->shape[0] != N) return RAD_E_SHAPE;
+        rblk = 1;                                  /* per-row grid */
+    } else {
+        if (grid_block(N, BS->shape[0]) != 128 || BS->shape[0] != (N + 127) / 128)
+            return RAD_E_UNSUPPORTED;
+        rblk = 128;                                /* 128 x 128 checkpoint block grid */
+    }
+    if (rad_tensor_numel(BS) < (rblk > 1 ? (N + 127) / 128 : N) * bs_cols) return RAD_E_SHAPE;
+
+    long long gp = 0;   /* the group parameter must not contradict the bytes */
+    if (rad_args_geti(a, "group", &gp) && gp > 0 && gp != 128) return RAD_E_SHAPE;
+
+    if (!inner_contig(A) || !inner_contig(B) || !inner_contig(Y)) return RAD_E_STRIDE;
+
+    const int64_t a_pitch = row_stride(A, K), b_pitch = row_stride(B, K);
+    if (!aligned16(A->data) || !aligned16(B->data) || (a_pitch & 15) || (b_pitch & 15))
+        return RAD_E_UNSUPPORTED;
+
+    P->enc = ENC_FP8A8;
+    P->A = (const uint8_t*)A->data;
+    P->AS = (const float*)AS->data;
+    P->B = (const uint8_t*)B->data;
+    P->BS = BS->data;
+    P->Y = (uint16_t*)Y->data;
+    P->M = M; P->N = N; P->K = K;
+    P->a_pitch = a_pitch;
+    P->b_pitch = b_pitch;
+    P->y_pitch = row_stride(Y, N);
+    P->as_pitch = row_stride(AS, as_cols);
+    P->bs_pitch = row_stride(BS, bs_cols);
+    P->as_cols = (int)as_cols;
+    P->bs_cols = (int)bs_cols;
+    P->rblk = rblk;
+    return RAD_OK;
+}
+
+/* Split-K policy: enough waves in flight to cover HBM latency (a 16-row tile is one wave
+ * per chunk), without cutting a chunk below 8 steps (1024 of K) when avoidable. */
+void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGeom* g) {
+    g->mt = M <= 1 ? 1 : M <= 4 ? 4 : 16;          /* rounds UP: every row is written */
+    g->steps = (int)(K / 128);
+    g->tiles = (N + 15) / 16;
+    int c = 1;
+    if (force_chunks > 0) {
+        c = force_chunks >= 8 ? 8 : force_chunks >= 4 ? 4 : force_chunks >= 2 ? 2 : 1;
+    } else {
+        const int64_t target_waves = 2048;
+        while (c < 8 && g->tiles * c < target_waves && g->steps / (2 * c) >= 4) c *= 2;
+    }
+    if (c > g->steps) c = 1;
+    while (c > 1 && c > g->steps) c >>= 1;
+    g->chunks = c;
+    g->waves = c > 4 ? c : 4;
+    g->tiles_per_block = g->waves / c;
+    g->blocks = (g->tiles + g->tiles_per_block - 1) / g->tiles_per_block;
+}
+
+void tile_geom(int64_t M, int64_t N, TileGeom* g) {
+    g->bm = 128;
+    g->bn = 128;
+    g->grid_m = (M + g->bm - 1) / g->bm;
+    g->grid_n = (N + g->bn - 1) / g->bn;
+}
+
+bool env_no_mxfp4()   { static const bool v = getenv("R3D_NO_MXFP4") != nullptr;   return v; }
+bool env_no_fp4_dec() { static const bool v = getenv("R3D_NO_FP4_DEC") != nullptr; return v; }
+bool env_no_fp8a8()   { static const bool v = getenv("R3D_NO_FP8A8") != nullptr;   return v; }
+bool env_no_fp8_dec() { static const bool v = getenv("R3D_NO_FP8_DEC") != nullptr; return v; }
+bool env_debug()      { static const bool v = getenv("R3D_DEBUG_GEMM") != nullptr; return v; }
+int64_t env_splitk() {
+    static const int64_t v = [] {
+        const char* e = getenv("R3D_GFX950_SPLITK");
+        return e ? (int64_t)atoll(e) : (int64_t)0;
+    }();
+    return v;
+}
+
+int64_t decode_splitk(const RadArgs* a) {
+    if (a && a->tv)
+        for (int i = 0; i < a->n_tv; ++i)
+            if (a->tv[i].name && strcmp(a->tv[i].name, "splitk") == 0 && a->tv[i].value > 0)
+                return a->tv[i].value;
+    return env_splitk();
+}
+
+int describe(const char* row, const RadArgs* a, char* buf, int len) {
+    if (!row || !buf || len <= 0) return RAD_E_INVAL;
+    const bool mx = strstr(row, "mxfp4") != nullptr;
+    const bool dec = strstr(row, "decode") != nullptr;
+    const int enc = mx ? ENC_MXFP4A8 : ENC_FP8A8;
+    int64_t M = 0, N = 0;
+    int rc = entry_preamble(a, enc, dec ? 16 : 0, &M, &N);
+    if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (preamble)", rc); return rc; }
+    GemmPlan P{};
+    rc = mx ? plan_mxfp4a8(a, M, N, &P) : plan_fp8a8(a, M, &P);
+    if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
+    if (dec) {
+        DecodeGeom g{};
+        decode_geom(P.M, P.N, P.K, decode_splitk(a), &g);
+        snprintf(buf, (size_t)len,
+                 "arm=decode enc=%s M=%lld N=%lld K=%lld mt=%d chunks=%d waves=%d tiles=%lld "
+                 "blocks=%lld steps=%d rblk=%d",
+                 mx ? "mxfp4a8" : "fp8a8", (long long)P.M, (long long)P.N, (long long)P.K,
+                 g.mt, g.chunks, g.waves, (long long)g.tiles, (long long)g.blocks, g.steps,
+                 P.rblk);
+    } else {
+        TileGeom g{};
+        tile_geom(P.M, P.N, &g);
+        snprintf(buf, (size_t)len,
+                 "arm=tile enc=%s M=%lld N=%lld K=%lld bm=%d bn=%d grid=%lldx%lld rblk=%d",
+                 mx ? "mxfp4a8" : "fp8a8", (long long)P.M, (long long)P.N, (long long)P.K,
+                 g.bm, g.bn, (long long)g.grid_n, (long long)g.grid_m, P.rblk);
+    }
+    return RAD_OK;
+}
+
+}  // namespace r3d

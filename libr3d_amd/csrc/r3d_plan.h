@@ -1,0 +1,85 @@
+/* r3d_plan.h -- host-side plans for the gfx950 gemm_nt_q rows: the format / shape /
+ * stride gates every entry runs before it launches, and the launch geometry it picks.
+ * Pure host C++ (no HIP), so every refusal and every geometry choice is testable on a
+ * machine without a GPU.
+ */
+#ifndef R3D_PLAN_H
+#define R3D_PLAN_H
+
+#include <stdint.h>
+#include "rad_abi.h"
+
+namespace r3d {
+
+enum Encoding { ENC_MXFP4A8 = 0, ENC_FP8A8 = 1 };
+
+struct GemmPlan {
+    int enc;
+    const uint8_t* A;        /* e4m3 [M, K] */
+    const float*   AS;       /* f32 [M, K/128] */
+    const uint8_t* B;        /* mxfp4: [N, K/2] packed e2m1; fp8a8: [N, K] e4m3 */
+    const void*    BS;       /* mxfp4: E8M0 [N, K/32]; fp8a8: bf16 [N or N/128, K/128] */
+    uint16_t*      Y;        /* bf16 [M, N] */
+    int64_t M, N, K;
+    int64_t a_pitch, as_pitch, b_pitch, bs_pitch, y_pitch;   /* bytes for A/B, elements else */
+    int as_cols, bs_cols;
+    int rblk;                /* fp8a8 weight-scale rows per scale row: 1 or 128 */
+};
+
+/* Which kernel family an entry launches. */
+enum Arm { ARM_DECODE = 0, ARM_TILE = 1 };
+
+/* Launch geometry of the decode GEMV: a 16-row weight tile per wave, the K steps (128
+ * wide) of a tile split over `chunks` waves of the same workgroup, reduced through LDS
+ * in chunk order. */
+struct DecodeGeom {
+    int mt;                  /* activation rows the kernel instantiation covers: 1, 4, 16 */
+    int chunks;              /* waves per tile (split-K), 1/2/4/8 */
+    int waves;               /* waves per workgroup */
+    int tiles_per_block;
+    int64_t tiles;           /* ceil(N / 16) */
+    int64_t blocks;
+    int steps;               /* K / 128 */
+};
+
+/* Launch geometry of the prefill tile. */
+struct TileGeom {
+    int bm, bn;              /* output tile of one workgroup */
+    int64_t grid_m, grid_n;
+};
+
+int64_t grid_block(int64_t ext, int64_t blocks);
+int64_t row_stride(const RadTensor* t, int64_t cols);
+
+/* Format gates (src/r3d_gemm_mxfp4.hip:1521-1582 and src/r3d_gemm_fp8a8.hip:852-924)
+ * plus this build's gfx950 gates: K % 128 == 0 and 16-byte aligned A/B bases and
+ * pitches.  M must already be numel(Y)/N.  Returns RAD_OK or the refusal code. */
+int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P);
+int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P);
+
+/* The shared entry preamble: operands present, a_sum (and for fp8a8 b_ref) refused,
+ * Y bf16 and inner-contiguous, N from the schema parameter, M = numel(Y)/N (never the
+ * M parameter), and the band's own M bound when `m_max` > 0. */
+int entry_preamble(const RadArgs* a, int enc, int64_t m_max, int64_t* M, int64_t* N);
+
+void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGeom* g);
+void tile_geom(int64_t M, int64_t N, TileGeom* g);
+
+/* Environment levers, read once per process (function-local statics). */
+bool env_no_mxfp4();        /* R3D_NO_MXFP4: all mxfp4a8 rows */
+bool env_no_fp4_dec();      /* R3D_NO_FP4_DEC: the mxfp4a8 decode row */
+bool env_no_fp8a8();        /* R3D_NO_FP8A8: all fp8a8 rows */
+bool env_no_fp8_dec();      /* R3D_NO_FP8_DEC: the fp8a8 decode row */
+bool env_debug();           /* R3D_DEBUG_GEMM: one stderr line per distinct launch arm */
+int64_t env_splitk();       /* R3D_GFX950_SPLITK: force the decode chunk count (0 = policy) */
+
+/* The decode rows' "splitk" tunable (RadArgs::tv): chunks per tile, 0 = the policy.  An
+ * engine-chosen value wins over R3D_GFX950_SPLITK. */
+int64_t decode_splitk(const RadArgs* a);
+
+/* Human-readable plan + geometry for `row` without launching anything. */
+int describe(const char* row, const RadArgs* a, char* buf, int len);
+
+}  // namespace r3d
+
+#endif /* R3D_PLAN_H */

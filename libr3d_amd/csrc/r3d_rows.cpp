@@ -1,0 +1,192 @@
+/* r3d_rows.cpp -- plugin identity, the gemm_nt_q op schema and the gfx950 row table of
+ * libr3d_gfx950, behind radiance's kernel-plugin ABI 26 (src/r3d_rows.cpp:14-27,
+ * 2238-2278 of the reference).  Pure host C++.
+ *
+ * Rows (resolver: per op and band, the highest-priority row whose constraints hold;
+ * src/r3d_rows.cpp:1165-1177):
+ *   gemm_nt_q_mxfp4          prio 1000  dtype IN mxfp4a8, K DIV 128      prefill tile
+ *   gemm_nt_q_mxfp4_decode   prio 1100  + M LE 16                         decode GEMV
+ *   gemm_nt_q_fp8a8          prio 1000  dtype IN fp8a8, K DIV 128, group EQ 128
+ *   gemm_nt_q_fp8a8_decode   prio 1100  + M LE 16
+ * Deviations from the reference rows (src/r3d_rows.cpp:1601-1675): the decode bands
+ * widen M <= 8 to M <= 16 (one MFMA covers 16 activation rows at the cost of one), and
+ * the mxfp4 tile row adds K DIV 128 (the MFMA walks whole 128-wide steps; ragged K
+ * resolves past the row, to the host reference, as the reference's fp8 row already does).
+ *
+ * Kill switches act HERE, at registration (src/r3d_rows.cpp:2197-2236): an issue-time
+ * refusal is an engine abort, so a lever hides rows and the band re-resolves.
+ *   R3D_NO_MXFP4   hides both mxfp4a8 rows;  R3D_NO_FP4_DEC  the mxfp4a8 decode row;
+ *   R3D_NO_FP8A8   hides both fp8a8 rows;    R3D_NO_FP8_DEC  the fp8a8 decode row.
+ * Presence-tested (getenv != null), read once.  R3D_MXFP4_Q8X is accepted and inert:
+ * this library has no repacked-plane arm for it to withdraw.
+ */
+#include <stdint.h>
+#include <string.h>
+
+#include "rad_abi.h"
+#include "r3d_plan.h"
+
+extern "C" {
+int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s);
+int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s);
+int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s);
+int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
+}
+
+namespace {
+
+/* gemm_nt_q's schema: parameter and operand lists exactly as the reference declares
+ * them (src/r3d_rows.cpp:186-210), so a loader's schema comparison passes when this
+ * library co-loads with another declarer of the op. */
+const RadParamSpec kGemmNtQParams[] = {
+    {"M", RAD_P_INT, RAD_REQUIRED, 0},
+    {"N", RAD_P_INT, RAD_REQUIRED, 0},
+    {"K", RAD_P_INT, RAD_REQUIRED, 0},
+    {"group", RAD_P_INT, RAD_REQUIRED, 0},
+    {"dtype", RAD_P_STR, RAD_REQUIRED, 0},
+    {"pb1", RAD_P_INT, RAD_OPTIONAL, 0},
+    {"pb2", RAD_P_INT, RAD_OPTIONAL, 0},
+    {"split_n", RAD_P_INT, RAD_OPTIONAL, 0},
+};
+const RadOperandSpec kGemmNtQOperands[] = {
+    {"a", RAD_OPD_IN, 0},
+    {"a_scale", RAD_OPD_IN, 1},
+    {"b", RAD_OPD_WEIGHT, 0},
+    {"b_scale", RAD_OPD_WEIGHT, 0},
+    {"y", RAD_OPD_OUT, 0},
+    {"a_sum", RAD_OPD_IN, 1},
+    {"b_ref", RAD_OPD_WEIGHT, 1},
+};
+
+const RadOpSchema kSchemas[] = {
+    {"gemm_nt_q", kGemmNtQParams, 8, kGemmNtQOperands, 7,
+     "Y[M,N] = A[M,K] . dequant(B)[N,K]^T with block-scaled operands; `dtype` names the "
+     "operand combination (mxfp4a8: e4m3 A + f32 a_scale per 128 of K, e2m1 B + E8M0 per "
+     "32; fp8a8: e4m3 A + f32 a_scale, e4m3 B + bf16 scale per 128 x 128 tile or per row)."},
+};
+
+const RadConstraint cMxfp4Tile[] = {
+    {"dtype", RAD_C_IN, 0, "mxfp4a8"},
+    {"K", RAD_C_DIV, 128, nullptr},
+};
+const RadConstraint cMxfp4Decode[] = {
+    {"dtype", RAD_C_IN, 0, "mxfp4a8"},
+    {"M", RAD_C_LE, 16, nullptr},
+    {"K", RAD_C_DIV, 128, nullptr},
+};
+const RadConstraint cFp8Tile[] = {
+    {"dtype", RAD_C_IN, 0, "fp8a8"},
+    {"K", RAD_C_DIV, 128, nullptr},
+    {"group", RAD_C_EQ, 128, nullptr},
+};
+const RadConstraint cFp8Decode[] = {
+    {"dtype", RAD_C_IN, 0, "fp8a8"},
+    {"M", RAD_C_LE, 16, nullptr},
+    {"K", RAD_C_DIV, 128, nullptr},
+    {"group", RAD_C_EQ, 128, nullptr},
+};
+
+enum { kPrioTile = 1000, kPrioDecode = 1100 };
+
+/* The decode rows' split-K lever: waves per 16-row weight tile (0 = the library's policy,
+ * which targets ~2048 waves in flight). */
+const long long kSplitKValues[] = {0, 1, 2, 4, 8};
+const RadTunable tSplitK[] = {
+    {"splitk", kSplitKValues, 5, 0,
+     "K chunks per 16-row weight tile, folded through LDS in chunk order; 0 = fill the CUs"},
+};
+
+const RadKernelInfo kRows[] = {
+    {"gemm_nt_q_mxfp4", "gemm_nt_q", "gemm",
+     "mxfp4a8 prefill tile on gfx950 block-scaled MFMA: 128x128 output tile per workgroup, "
+     "e2m1 weights with their E8M0 scales fed to v_mfma_scale_f32_16x16x128_f8f6f4 as is, "
+     "e4m3 activations, one MFMA per 128-of-K activation group scaled by a_scale in f32",
+     "K a multiple of 128; 16-byte aligned A/B bases and A pitch; ragged M/N tiles stage "
+     "zeros and are never stored; M derives from numel(y)/N",
+     "fp8_e4m3 a with f32 a_scale per (row, 128 K), e2m1 b with E8M0 b_scale per (row, 32 K), "
+     "bf16 y; b_ref accepted and ignored; a_sum refused",
+     RAD_DOMAIN_DEVICE, kPrioTile, cMxfp4Tile, 2, nullptr, 0, nullptr,
+     nullptr, nullptr, r3d_rad_gemm_nt_q, nullptr, nullptr, nullptr, nullptr, nullptr},
+
+    {"gemm_nt_q_mxfp4_decode", "gemm_nt_q", "gemm",
+     "mxfp4a8 decode-band GEMV on gfx950: one wave per 16-row weight tile and K chunk, "
+     "16-byte non-temporal loads of the nibble plane straight into the MFMA's fp4 operand "
+     "with the E8M0 bytes as its scale operand, split-K folded through LDS in chunk order",
+     "M <= 16 (decode and speculative verify; widened from the reference's 8); K a multiple "
+     "of 128; N any (dead rows clamp their loads and never store); M derives from numel(y)/N",
+     "fp8_e4m3 a with f32 a_scale per (row, 128 K), e2m1 b with E8M0 b_scale per (row, 32 K), "
+     "bf16 y; b_ref accepted and ignored; a_sum refused",
+     RAD_DOMAIN_DEVICE, kPrioDecode, cMxfp4Decode, 3, tSplitK, 1, nullptr,
+     nullptr, nullptr, r3d_rad_gemm_nt_q_mxfp4_decode, nullptr, nullptr, nullptr, nullptr,
+     nullptr},
+
+    {"gemm_nt_q_fp8a8", "gemm_nt_q", "gemm",
+     "fp8a8 prefill tile on gfx950 MFMA: 128x128 output tile, e4m3 on both operands, one MFMA "
+     "per 128-of-K scale group flushed as (sub * a_scale) * b_scale in the oracle's order",
+     "K a multiple of 128; 16-byte aligned A/B bases and pitches; b_scale either the 128x128 "
+     "block grid or a per-row grid; M derives from numel(y)/N",
+     "fp8_e4m3 a with f32 a_scale per (row, 128 K), fp8_e4m3 b with bf16 scale per 128x128 "
+     "tile (or per row), bf16 y; a_sum and b_ref refused",
+     RAD_DOMAIN_DEVICE, kPrioTile, cFp8Tile, 3, nullptr, 0, nullptr,
+     nullptr, nullptr, r3d_rad_gemm_nt_q_fp8, nullptr, nullptr, nullptr, nullptr, nullptr},
+
+    {"gemm_nt_q_fp8a8_decode", "gemm_nt_q", "gemm",
+     "fp8a8 decode-band GEMV on gfx950: one wave per 16-row weight tile and K chunk, two "
+     "16-byte non-temporal loads per lane per 128-of-K group into the MFMA's fp8 operand, "
+     "(sub * a_scale) * b_scale per group, split-K folded through LDS in chunk order",
+     "M <= 16; K a multiple of 128; N any; b_scale either the 128x128 block grid or a per-row "
+     "grid",
+     "fp8_e4m3 a with f32 a_scale per (row, 128 K), fp8_e4m3 b with bf16 scale per 128x128 "
+     "tile (or per row), bf16 y; a_sum and b_ref refused",
+     RAD_DOMAIN_DEVICE, kPrioDecode, cFp8Decode, 4, tSplitK, 1, nullptr,
+     nullptr, nullptr, r3d_rad_gemm_nt_q_fp8_decode, nullptr, nullptr, nullptr, nullptr,
+     nullptr},
+};
+
+bool row_hidden(const RadKernelInfo& k) {
+    const bool no_mx = r3d::env_no_mxfp4(), no_mxd = r3d::env_no_fp4_dec();
+    const bool no_f8 = r3d::env_no_fp8a8(), no_f8d = r3d::env_no_fp8_dec();
+    if (!strcmp(k.name, "gemm_nt_q_mxfp4")) return no_mx;
+    if (!strcmp(k.name, "gemm_nt_q_mxfp4_decode")) return no_mx || no_mxd;
+    if (!strcmp(k.name, "gemm_nt_q_fp8a8")) return no_f8;
+    if (!strcmp(k.name, "gemm_nt_q_fp8a8_decode")) return no_f8 || no_f8d;
+    return false;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t rad_plugin_abi_version(void) { return RAD_ABI_VERSION; }
+
+const RadPluginInfo* rad_plugin_info(void) {
+    static const RadPluginInfo info = {
+        RAD_PLUGIN_KERNEL, "libr3d_gfx950", "0.1.0",
+        "radiance gemm_nt_q rows (mxfp4a8, fp8a8) for AMD Instinct MI355X (CDNA4)",
+        "gfx950",
+    };
+    return &info;
+}
+
+int rad_kernel_schema_count(void) { return (int)(sizeof kSchemas / sizeof kSchemas[0]); }
+
+const RadOpSchema* rad_kernel_schema_at(int i) {
+    if (i < 0 || i >= rad_kernel_schema_count()) return nullptr;
+    return &kSchemas[i];
+}
+
+int rad_kernel_count(void) {
+    int n = 0;
+    for (const RadKernelInfo& k : kRows)
+        if (!row_hidden(k)) ++n;
+    return n;
+}
+
+const RadKernelInfo* rad_kernel_at(int i) {
+    if (i < 0) return nullptr;
+    for (const RadKernelInfo& k : kRows)
+        if (!row_hidden(k) && i-- == 0) return &k;
+    return nullptr;
+}
+
+}  /* extern "C" */

@@ -1,0 +1,197 @@
+"""GPU parity of the gfx950 gemm_nt_q rows against the CPU oracle, through the C ABI.
+
+Every launch goes through the registered row's launch pointer on guarded operands
+(red zones on both sides of every operand, Y poisoned with a sentinel).  A case passes
+when: the status is RAD_OK; no red zone was touched; every Y element was written; NaN
+classes match; and per element
+    |y - y_oracle| <= ulp_bf16 + 2*K*2^-24*S + 2^-10*S8
+(S the oracle's magnitude sum; S8 the sum over 8-wide k groups of the largest scaled
+product -- the block-scaled MFMA sums each 8 products at a width that truncates bits
+below 2^-13 of the group's largest, measured on MI355X; see oracle/r3d_oracle.h).
+Whole-tensor rel_l2 must stay inside the reference's own kbench tolerances (3e-2
+mxfp4a8, 5e-3 fp8a8; docs/COVERAGE.md:868,1296).  On the BASELINE configs' data
+(tests/test_gpu_configs.py) the per-row rel_l2 is held to 2^-8 (one bf16 ulp) as well.
+The operand law of most cases here is the reference probe's (full-range NaN-free e4m3
+codes, tools/probe_m4_entry.cpp:36-40): it maximises cancellation, so it tests the bound,
+not the typical error.
+"""
+import numpy as np
+import pytest
+
+import libr3d_amd as R
+from libr3d_amd import synth
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+MX_DEC, MX_TILE = "gemm_nt_q_mxfp4_decode", "gemm_nt_q_mxfp4"
+F8_DEC, F8_TILE = "gemm_nt_q_fp8a8_decode", "gemm_nt_q_fp8a8"
+
+
+def _gu():
+    from tests import gpu_util
+    return gpu_util
+
+
+def _mx_case(M, N, K, seed, bs_lo=115, bs_hi=139):
+    """The reference probe's operand law (tools/probe_m4_entry.cpp:36-40): NaN-free e4m3
+    codes, random nibble bytes, E8M0 in 115..139, a_scale in [0.001, 0.011]."""
+    rng = np.random.default_rng(seed)
+    A = synth.random_e4m3_codes((M, K), rng)
+    AS = (0.001 + 0.01 * rng.random((M, K // 128))).astype(np.float32)
+    B = rng.integers(0, 256, size=(N, K // 2), dtype=np.uint8)
+    BS = rng.integers(bs_lo, bs_hi + 1, size=(N, K // 32)).astype(np.uint8)
+    return A, AS, B, BS
+
+
+def _f8_case(M, N, K, seed, rblk):
+    rng = np.random.default_rng(seed)
+    A = synth.random_e4m3_codes((M, K), rng)
+    AS = (0.001 + 0.01 * rng.random((M, K // 128))).astype(np.float32)
+    B = synth.random_e4m3_codes((N, K), rng)
+    rows = N if rblk == 1 else (N + 127) // 128
+    BS = synth.bf16_bits((0.001 + 0.01 * rng.random((rows, K // 128))).astype(np.float32))
+    return A, AS, B, BS
+
+
+KBENCH_TOL = {"mxfp4a8": 3e-2, "fp8a8": 5e-3}
+
+
+def _check(row, dtype, A, AS, B, BS, M, N, K, gpu, rblk=1, row_rel_max=None, tunables=None):
+    gu = _gu()
+    rc, Y, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, gpu, tunables=tunables)
+    assert rc == R.RAD_OK, "row %s refused rc=%d" % (row, rc)
+    assert guards, "red zone written"
+    if dtype == "mxfp4a8":
+        Yr, Yf, S = O.quant_dot_mxfp4a8(A, AS, B, BS, nthreads=16)
+    else:
+        Yr, Yf, S = O.quant_dot_fp8a8(A, AS, B, BS, rblk, nthreads=16)
+    S8 = O.group8_mag(dtype, A, AS, B, BS, rblk, nthreads=16)
+    c = gu.compare(Y, Yr, Yf, S, K, S8)
+    assert c["sentinel_left"] == 0, c
+    assert c["nan_mismatch"] == 0 and c["inf_mismatch"] == 0, c
+    assert c["max_viol"] <= 1.0, c
+    assert c["rel_l2"] <= KBENCH_TOL[dtype], c
+    if row_rel_max is not None:
+        assert c["row_rel_l2_max"] <= row_rel_max, c
+    return c, Y
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 7, 8, 9, 15, 16])
+def test_mxfp4_decode_small(gpu, M):
+    A, AS, B, BS = _mx_case(M, 200, 640, 100 + M)
+    _check(MX_DEC, "mxfp4a8", A, AS, B, BS, M, 200, 640, gpu)
+
+
+@pytest.mark.parametrize("N,K", [(16, 128), (17, 256), (1000, 4096), (4096, 1152)])
+def test_mxfp4_decode_shapes(gpu, N, K):
+    for M in (1, 4):
+        A, AS, B, BS = _mx_case(M, N, K, N + K + M)
+        _check(MX_DEC, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 7, 8, 9, 15, 16])
+@pytest.mark.parametrize("rblk", [1, 128])
+def test_fp8_decode_small(gpu, M, rblk):
+    A, AS, B, BS = _f8_case(M, 200, 640, 300 + M, rblk)
+    _check(F8_DEC, "fp8a8", A, AS, B, BS, M, 200, 640, gpu, rblk=rblk)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (17, 200, 256), (64, 256, 512),
+                                   (130, 300, 384), (256, 512, 1024)])
+def test_mxfp4_tile(gpu, M, N, K):
+    A, AS, B, BS = _mx_case(M, N, K, 7 * M + N)
+    _check(MX_TILE, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (17, 200, 256), (130, 300, 384)])
+@pytest.mark.parametrize("rblk", [1, 128])
+def test_fp8_tile(gpu, M, N, K, rblk):
+    A, AS, B, BS = _f8_case(M, N, K, 11 * M + N, rblk)
+    _check(F8_TILE, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk)
+
+
+@pytest.mark.parametrize("row", [MX_DEC, MX_TILE])
+def test_mxfp4_dequant_bit_exact(gpu, row):
+    """Every (e2m1 code, E8M0 byte) pair through the product path: activation row m is
+    one-hot 1.0 at k = m with a_scale 1, weight row n carries the 16 codes at k = 0..15
+    and E8M0 byte n on group 0, so Y[m, n] = bf16(e2m1(m) * 2^(n-127)) -- exactly the
+    dequantised weight (<= 2 mantissa bits fit bf16).  Compared bit for bit against the
+    oracle's dequantisation; byte 0xFF must give NaN."""
+    gu = _gu()
+    M, N, K = 16, 256, 128
+    A = np.zeros((M, K), np.uint8)
+    for m in range(M):
+        A[m, m] = 0x38                                   # e4m3 1.0
+    AS = np.ones((M, 1), np.float32)
+    codes = np.arange(16, dtype=np.uint8)
+    B = np.zeros((N, K // 2), np.uint8)
+    B[:, :8] = (codes[0::2] | (codes[1::2] << 4))[None, :]
+    BS = np.full((N, K // 32), 127, np.uint8)
+    BS[:, 0] = np.arange(256, dtype=np.uint8)
+    rc, Y, guards = gu.run_row(row, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+    assert rc == R.RAD_OK and guards
+    deq = O.mxfp4_dequant(B, BS)[:, :16].T               # [m = code, n]
+    got = O.bf16_to_f32(Y)
+    got_nan = np.isnan(got)
+    ref_nan = np.isnan(deq)
+    assert np.array_equal(got_nan, ref_nan)
+    assert ref_nan[:, 255].all()
+    fin = ~ref_nan
+    # value-exact against the dequantised weights (e2m1 * 2^(x-127) is exact in bf16); a
+    # sum that starts at +0 returns +0 for code 8 (-0), so zeros compare by value ...
+    bad = np.argwhere((got != deq) & fin)
+    assert bad.size == 0, "dequant mismatch at %s: got %s want %s" % (
+        bad[:5].tolist(), [got[tuple(b)] for b in bad[:5]], [deq[tuple(b)] for b in bad[:5]])
+    # ... and bit-exact against the oracle's quant_dot on the same operands
+    Yr, _, _ = O.quant_dot_mxfp4a8(A, AS, B, BS)
+    assert np.array_equal(Y[fin], Yr[fin])
+
+
+@pytest.mark.parametrize("row", [MX_DEC, MX_TILE])
+def test_mxfp4_nan_scale_poisons(gpu, row):
+    """A 0xFF scale byte poisons its whole output element even when every code in its
+    group is zero (oracle: (sub * sa) * NaN with sub = 0)."""
+    M, N, K = 4, 64, 256
+    A, AS, B, BS = _mx_case(M, N, K, 5)
+    B[3, :16] = 0                                        # group 0 of row 3: all zero codes
+    BS[3, 0] = 0xFF
+    BS[10, 5] = 0xFF
+    c, Y = _check(row, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+    y = O.bf16_to_f32(Y)
+    assert np.isnan(y[:, 3]).all() and np.isnan(y[:, 10]).all()
+    assert np.isfinite(np.delete(y, [3, 10], axis=1)).all()
+
+
+def test_decode_m_from_numel_y(gpu):
+    """M is numel(y)/N, never the M parameter: an M=99 param with a 3-row y computes 3 rows."""
+    gu = _gu()
+    M, N, K = 3, 64, 256
+    A, AS, B, BS = _mx_case(M, N, K, 9)
+    rc, Y, guards = gu.run_row(MX_DEC, "mxfp4a8", A, AS, B, BS, M, N, K, gpu,
+                               extra=[("M", 99)])
+    assert rc == R.RAD_OK and guards
+    Yr, Yf, S = O.quant_dot_mxfp4a8(A, AS, B, BS)
+    S8 = O.group8_mag("mxfp4a8", A, AS, B, BS)
+    c = gu.compare(Y, Yr, Yf, S, K, S8)
+    assert c["max_viol"] <= 1.0 and c["sentinel_left"] == 0
+
+
+@pytest.mark.parametrize("splitk", [1, 2, 4, 8])
+@pytest.mark.parametrize("dtype", ["mxfp4a8", "fp8a8"])
+def test_decode_splitk_deterministic(gpu, splitk, dtype):
+    """Every chunk count (the decode rows' "splitk" tunable) stays in bound, and repeated
+    calls are bit-identical (the LDS fold runs in chunk order)."""
+    gu = _gu()
+    M, N, K = 4, 512, 2048
+    if dtype == "mxfp4a8":
+        A, AS, B, BS = _mx_case(M, N, K, 77)
+        row = MX_DEC
+    else:
+        A, AS, B, BS = _f8_case(M, N, K, 77, 1)
+        row = F8_DEC
+    tv = [("splitk", splitk)]
+    _, y1 = _check(row, dtype, A, AS, B, BS, M, N, K, gpu, tunables=tv)
+    rc, y2, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, gpu, tunables=tv)
+    assert rc == R.RAD_OK and guards
+    assert np.array_equal(y1, y2)
