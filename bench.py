@@ -1,0 +1,339 @@
+"""Benchmark of the gfx950 gemm_nt_q rows on one MI355X (BASELINE.json's metric).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-extra] [--no-cpu]
+
+A "step" is one gemm_nt_q launch over one batch.  The headline workload is BASELINE's
+config 1 -- the fp8a8 W8A8 decode GEMV at M=1, K=5376, N=21504 -- read cold from HBM:
+the weight planes rotate over enough copies to exceed 1 GiB, well past the 256 MB
+Infinity Cache.  `value` is algorithmic bytes per step (weights + scales + activations +
+output, counted once) times steps over the wall time between two synchronised points.
+`roofline.achieved` divides the same bytes by the kernel's average duration measured with
+HIP events on the launch stream.  The other configs (C0, C2, C3, C4) are reported under
+`extra`.  The CPU baseline is the C restatement of libref (oracle/) on the host's cores,
+timed on a bounded sample.  One GPU only: --gpus above 1 exits with a message.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP8_PEAK_TFLOPS = 5000.0       # dense MFMA fp8 (the rate of an fp8 x fp4 scaled MFMA)
+FP4_PEAK_TFLOPS = 10100.0      # dense MFMA fp4 x fp4
+ROTATE_BYTES = 1.1 * 2 ** 30
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def mx_bytes(M, N, K):
+    """mxfp4a8 algorithmic bytes: nibbles + E8M0 + e4m3 A + f32 a_scale + bf16 Y."""
+    return N * K // 2 + N * K // 32 + M * K + M * ((K + 127) // 128) * 4 + M * N * 2
+
+
+def f8_bytes(M, N, K, rblk=1):
+    srows = N if rblk == 1 else (N + 127) // 128
+    return N * K + srows * (K // 128) * 2 + M * K + M * ((K + 127) // 128) * 4 + M * N * 2
+
+
+class Case:
+    """Device operands for one gemm_nt_q call, with `copies` rotated weight planes."""
+
+    def __init__(self, dtype, A, AS, B, BS, M, N, K, copies, dev):
+        import torch
+        import libr3d_amd as R
+        self.M, self.N, self.K, self.dtype = M, N, K, dtype
+        self.a = torch.from_numpy(A).to(dev)
+        self.as_ = torch.from_numpy(AS).to(dev)
+        b0 = torch.from_numpy(B).to(dev)
+        bs0 = torch.from_numpy(BS.view(np.int16) if BS.dtype == np.uint16 else BS).to(dev)
+        self.b = [b0] + [b0.clone() for _ in range(copies - 1)]
+        self.bs = [bs0] + [bs0.clone() for _ in range(copies - 1)]
+        self.y = torch.empty((M, N), dtype=torch.int16, device=dev)
+        self.ops = [R.GemmOperands(self.a, self.as_, b, bs, self.y, dtype=dtype, N=N, K=K)
+                    for b, bs in zip(self.b, self.bs)]
+
+
+def copies_for(nbytes):
+    return max(1, int(np.ceil(ROTATE_BYTES / nbytes)))
+
+
+def time_case(case, row, steps, warmup, stream):
+    """-> (wall seconds for `steps` launches, mean kernel seconds from per-launch events)."""
+    import torch
+    import libr3d_amd as R
+    launch = R.row_launcher(row)
+    n = len(case.ops)
+    for i in range(warmup):
+        rc = launch(case.ops[i % n], stream)
+        assert rc == 0, "row %s refused: %d" % (row, rc)
+    torch.cuda.synchronize()
+    # wall-clock timed region: back-to-back launches
+    t0 = time.perf_counter()
+    for i in range(steps):
+        launch(case.ops[i % n], stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # kernel durations: one event pair per launch on the launch stream
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record()
+        launch(case.ops[i % n], stream)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    kern = float(np.mean([a.elapsed_time(b) for a, b in ev])) * 1e-3
+    return wall, kern
+
+
+def cpu_baseline(seconds=10.0):
+    """The oracle (libref restatement, OpenMP over output rows) on config 1, repeated for
+    about `seconds` of wall time."""
+    import oracle as O
+    from libr3d_amd import synth
+    M, K, N = 1, 5376, 21504
+    A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 10)
+    B, BS = synth.fp8_weights(N, K, 0x5EED + 11)
+    nth = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    O.quant_dot_fp8a8(A, AS, B, BS, 1, nthreads=nth)         # warm
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        O.quant_dot_fp8a8(A, AS, B, BS, 1, nthreads=nth)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    gbs = f8_bytes(M, N, K) * calls / el / 1e9
+    cpu = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": nth, "kind": "port",
+            "sample": "config 1 (fp8a8 GEMV M=1 K=5376 N=21504), full problem x %d calls, "
+                      "%.1f s wall, oracle/ C restatement of libref quant_dot, OpenMP %d "
+                      "threads on %s" % (calls, el, nth, cpu or "host CPU")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the gemm_nt_q path is built and measured on a single "
+              "MI355X (multi-GPU sharding is design only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import libr3d_amd as R
+    from libr3d_amd import synth
+    R.lib()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    # ---- headline: config 1, fp8a8 decode GEMV, cold
+    M, K, N = 1, 5376, 21504
+    log("[bench] config 1: fp8a8 decode GEMV M=%d K=%d N=%d" % (M, K, N))
+    A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 10)
+    B, BS = synth.fp8_weights(N, K, 0x5EED + 11)
+    nbytes = f8_bytes(M, N, K)
+    c1 = Case("fp8a8", A, AS, B, BS, M, N, K, copies_for(B.nbytes), dev)
+    torch.cuda.synchronize()
+    wall, kern = time_case(c1, "gemm_nt_q_fp8a8_decode", args.steps, args.warmup, stream)
+    value = nbytes * args.steps / wall / 1e9
+    achieved = nbytes / kern / 1e9
+    log("[bench] config 1: wall %.2f GB/s, kernel %.2f us -> %.1f GB/s (%.1f%% of HBM peak)"
+        % (value, kern * 1e6, achieved, 100 * achieved / HBM_PEAK_GBS))
+    del c1
+
+    out = {
+        "metric": "fp8 decode GEMV HBM GB/s @M=1 (BASELINE config 1)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3 x fp8e4m3 -> f32 accumulate, bf16 out",
+        "data": "synthetic (seeded; BASELINE config 1 distributions)",
+        "config": {"workload": "config 1: gemm_nt_q fp8a8 decode GEMV, M=1 K=5376 N=21504, "
+                               "per-row bf16 weight scales, per-token a_scale, cold HBM "
+                               "(weights rotated over >1 GiB)",
+                   "row": "gemm_nt_q_fp8a8_decode", "bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "r3d::gemv_kernel<1,1,4> (fp8a8, MT=1)",
+                     "kernel_us": round(kern * 1e6, 3)},
+    }
+
+    extra = {}
+    if not args.quick and not args.no_extra:
+        ksteps = max(20, args.steps // 4)
+        # C0: cache-fit parity config
+        M, K, N = 1, 4096, 4096
+        _, A, AS = synth.activations(M, K, 0x5EED)
+        B, BS = synth.mxfp4_weights(N, K, 0x5EED + 1)
+        c = Case("mxfp4a8", A, AS, B, BS, M, N, K, 1, dev)
+        wall, kern = time_case(c, "gemm_nt_q_mxfp4_decode", ksteps, 10, stream)
+        nb = mx_bytes(M, N, K)
+        extra["c0_mxfp4_gemv_cachefit"] = {"M": M, "K": K, "N": N, "kernel_us": round(kern * 1e6, 3),
+                                           "GBps_kernel": round(nb / kern / 1e9, 1)}
+        del c
+        # C2: mxfp4 decode, three shapes x M in {1, 4, 16}, cold
+        for name, (K, N) in (("gate_up", (5376, 21504)), ("down", (21504, 5376)),
+                             ("qkv", (5376, 8192))):
+            B, BS = synth.mxfp4_weights(N, K, 0x5EED + 21 + K)
+            for M in (1, 4, 16):
+                _, A, AS = synth.activations(M, K, 0x5EED + 20 + M)
+                c = Case("mxfp4a8", A, AS, B, BS, M, N, K, copies_for(B.nbytes + BS.nbytes), dev)
+                wall, kern = time_case(c, "gemm_nt_q_mxfp4_decode", ksteps, 10, stream)
+                nb = mx_bytes(M, N, K)
+                gbs = nb / kern / 1e9
+                extra["c2_mxfp4_%s_M%d" % (name, M)] = {
+                    "K": K, "N": N, "kernel_us": round(kern * 1e6, 3),
+                    "GBps_kernel": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                    "GBps_wall": round(nb * ksteps / wall / 1e9, 1)}
+                log("[bench] C2 %s M=%d: %.2f us, %.1f GB/s (%.1f%%)" % (
+                    name, M, kern * 1e6, gbs, 100 * gbs / HBM_PEAK_GBS))
+                del c
+        # C3: mxfp4a8 prefill tile, M=2048
+        M, K, N = 2048, 5376, 21504
+        _, A, AS = synth.activations(M, K, 0x5EED + 30)
+        B, BS = synth.mxfp4_weights(N, K, 0x5EED + 31)
+        c = Case("mxfp4a8", A, AS, B, BS, M, N, K, 1, dev)
+        wall, kern = time_case(c, "gemm_nt_q_mxfp4", 10, 3, stream)
+        tf = 2.0 * M * N * K / kern / 1e12
+        extra["c3_mxfp4a8_prefill"] = {"M": M, "K": K, "N": N, "kernel_us": round(kern * 1e6, 1),
+                                       "TFLOPs": round(tf, 1),
+                                       "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
+                                       "frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4)}
+        log("[bench] C3 prefill: %.1f us, %.1f TFLOP/s" % (kern * 1e6, tf))
+        del c
+        torch.cuda.empty_cache()
+        extra.update(bench_c4(dev, stream, steps=5))
+    if extra:
+        out["extra"] = extra
+
+    if not args.no_cpu:
+        log("[bench] CPU baseline (oracle, bounded sample) ...")
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+def bench_c4(dev, stream, steps=5):
+    """Config 4: one decode step of a 27B-class model at M=4 -- 62 layers of q/k/v/o and
+    gate/up/down in mxfp4a8 plus an fp8a8 lm_head (K=5376, N=262144).  Weights are random
+    codes generated on the device (bandwidth does not depend on values; NaN-free); the
+    435 launches run eagerly and as one captured HIP graph."""
+    import torch
+    import libr3d_amd as R
+    M, H, I, L, V = 4, 5376, 21504, 62, 262144
+    shapes = [("q", H, 4096), ("k", H, 2048), ("v", H, 2048), ("o", 4096, H),
+              ("gate", H, I), ("up", H, I), ("down", I, H)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x5EED + 4)
+
+    def codes(n, fp8):
+        t = torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev, generator=g)
+        if fp8:
+            t = torch.where((t & 0x7F) == 0x7F, t & 0xFE, t)
+        return t
+
+    acts = {}
+    for K in (H, 4096, I):
+        a = codes(M * K, True).view(M, K)
+        s = torch.full((M, K // 128), 0.01, dtype=torch.float32, device=dev)
+        acts[K] = (a, s)
+    y_bufs = {}
+    launches = []
+    mx_dec = R.row_launcher("gemm_nt_q_mxfp4_decode")
+    f8_dec = R.row_launcher("gemm_nt_q_fp8a8_decode")
+    keep = []
+    total = 0
+    for layer in range(L):
+        for name, K, N in shapes:
+            b = codes(N * K // 2, False).view(N, K // 2)
+            bs = (127 - torch.randint(0, 9, (N, K // 32), dtype=torch.int32, device=dev,
+                                      generator=g)).to(torch.uint8)
+            y = y_bufs.setdefault(N, torch.empty((M, N), dtype=torch.int16, device=dev))
+            a, s = acts[K]
+            ops = R.GemmOperands(a, s, b, bs, y, dtype="mxfp4a8", N=N, K=K)
+            keep.append((b, bs, ops))
+            launches.append((mx_dec, ops))
+            total += mx_bytes(M, N, K)
+    b = codes(V * H, True).view(V, H)
+    bs = torch.full((V, H // 128), 0x3C00, dtype=torch.int16, device=dev)   # bf16 0.0078125
+    y = torch.empty((M, V), dtype=torch.int16, device=dev)
+    a, s = acts[H]
+    ops = R.GemmOperands(a, s, b, bs, y, dtype="fp8a8", N=V, K=H)
+    keep.append((b, bs, ops))
+    launches.append((f8_dec, ops))
+    total += f8_bytes(M, V, H)
+    torch.cuda.synchronize()
+
+    def step(st):
+        for fn, o in launches:
+            fn(o, st)
+
+    step(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(stream)
+    torch.cuda.synchronize()
+    eager = (time.perf_counter() - t0) / steps
+
+    res = {"c4_decode_step_eager": {"bytes": total, "ms": round(eager * 1e3, 3),
+                                    "GBps": round(total / eager / 1e9, 1),
+                                    "frac_hbm": round(total / eager / 1e9 / HBM_PEAK_GBS, 4),
+                                    "launches": len(launches)}}
+    try:
+        s2 = torch.cuda.Stream()
+        with torch.cuda.stream(s2):
+            step(s2.cuda_stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s2):
+            step(s2.cuda_stream)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        gt = (time.perf_counter() - t0) / steps
+        res["c4_decode_step_graph"] = {"bytes": total, "ms": round(gt * 1e3, 3),
+                                       "GBps": round(total / gt / 1e9, 1),
+                                       "frac_hbm": round(total / gt / 1e9 / HBM_PEAK_GBS, 4)}
+        log("[bench] C4 decode step: eager %.3f ms (%.1f GB/s), graph %.3f ms (%.1f GB/s)" % (
+            eager * 1e3, total / eager / 1e9, gt * 1e3, total / gt / 1e9))
+    except Exception as e:          # graph capture unavailable: report eager only
+        res["c4_decode_step_graph"] = {"error": repr(e)[:200]}
+        log("[bench] C4 graph capture failed: %r" % (e,))
+    del keep, launches
+    return res
+
+
+if __name__ == "__main__":
+    main()

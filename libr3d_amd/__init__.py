@@ -276,13 +276,21 @@ class GemmOperands:
         self._t[4].data = y.data_ptr()
 
 
-def launch_row(row_name, ops, stream=0):
-    """Call the named row's launch pointer (as the engine does) and return its status."""
+def row_launcher(row_name):
+    """The named row's launch pointer as a callable f(ops, stream) -> status."""
     for r in rows():
         if r["name"] == row_name:
             fn = LaunchFn(r["launch"])
-            return fn(ctypes.byref(ops.args), ctypes.c_void_p(stream))
+
+            def call(ops, stream=0):
+                return fn(ctypes.byref(ops.args), ctypes.c_void_p(stream))
+            return call
     raise KeyError("row %s is not registered" % row_name)
+
+
+def launch_row(row_name, ops, stream=0):
+    """Call the named row's launch pointer (as the engine does) and return its status."""
+    return row_launcher(row_name)(ops, stream)
 
 
 def describe(row_name, ops):
