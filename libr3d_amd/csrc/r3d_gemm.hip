@@ -45,11 +45,12 @@ static void debug_once(const char* what, int key) {
 
 static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) {
     DecodeGeom g{};
-    decode_geom(P.M, P.N, P.K, splitk, &g);
+    decode_geom(P.M, P.N, P.K, splitk, &g, gemv_wave_lds(P.enc, P.M <= 1 ? 1 : P.M <= 4 ? 4 : 16));
     const dim3 grid((unsigned)g.blocks), block((unsigned)(64 * g.waves));
-#define R3D_GEMV(ENC_, MT_)                                                             \
-    hipLaunchKernelGGL((gemv_kernel<ENC_, MT_, 4>), grid, block, 0, stream, P.A, P.AS, P.B, \
-                       P.BS, P.Y, (int)P.M, (int)P.N, g.steps, g.chunks, P.rblk,         \
+    const size_t lds = (size_t)g.waves * gemv_wave_lds(P.enc, g.mt);
+#define R3D_GEMV(ENC_, MT_)                                                               \
+    hipLaunchKernelGGL((gemv_kernel<ENC_, MT_>), grid, block, lds, stream, P.A, P.AS, P.B,  \
+                       P.BS, P.Y, (int)P.M, (int)P.N, g.steps, g.chunks, P.rblk,          \
                        P.a_pitch, P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch)
     if (P.enc == ENC_MXFP4A8) {
         if (g.mt == 1) R3D_GEMV(ENC_MXFP4A8, 1);

@@ -19,26 +19,54 @@
 
 #include "r3d_device.h"
 #include "r3d_plan.h"
+#include "r3d_gemv_layout.h"
 
 namespace r3d {
 
 /* ---------------------------------------------------------------- decode GEMV ------
  * One wave owns a 16-row weight tile and one contiguous chunk of its K steps; the
  * `chunks` waves of a tile sit in the same workgroup and fold their f32 partials through
- * LDS in chunk order (deterministic).  Weight bytes are read once, with non-temporal
- * 16-byte loads, PF steps ahead of use; activation rows m >= M load nothing (zeros),
- * weight rows n >= N clamp their loads to row N-1 and never store. */
-template <int ENC, int MT, int PF>
+ * LDS in chunk order (deterministic).
+ *
+ * The chunk is walked in runs of kRunBytes bytes per weight row.  Everything a run needs
+ * -- the 16 weight rows, the activation rows, the weight scales and the activation
+ * scales -- arrives by direct global->LDS loads (global_load_lds, 16 bytes per lane for
+ * the planes, 2 or 4 for the scales), issued one run ahead into the other half of a
+ * double buffer.  Each weight instruction reads 512 contiguous bytes of two rows: HBM
+ * streams contiguous bursts, where the MFMA operand's native 16-rows-per-instruction walk
+ * measured well under two thirds of that on MI355X.  The only wait in the steady state is
+ * vmcnt(<loads of the next run>), so the next run is always in flight while this one is
+ * consumed from LDS.  Odd rows store their 16-byte chunks pairwise swapped so the MFMA
+ * operand reads (16 rows at one offset) spread over the LDS banks.
+ *
+ * Every load is unconditional and in bounds: weight rows n >= N clamp to row N-1,
+ * activation rows m >= M duplicate row M-1, a short last run clamps its lanes inside the
+ * chunk, and nothing clamped is ever used or stored. */
+__device__ __forceinline__ void r3d_lds_load(const void* g, void* l, int bytes) {
+    if (bytes == 16)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                         (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+    else if (bytes == 4)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                         (__attribute__((address_space(3))) void*)l, 4, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                         (__attribute__((address_space(3))) void*)l, 2, 0, 0);
+}
+
+template <int ENC, int MT>
 __global__ __launch_bounds__(512) void gemv_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ AS,
     const uint8_t* __restrict__ B, const void* __restrict__ BSv,
     uint16_t* __restrict__ Y,
     int M, int N, int steps, int chunks, int rblk,
     int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch) {
-    __shared__ r3d_f32x4 red[8][64];
+    using L = GemvLayout<ENC, MT>;
+    constexpr int SB = L::SB, RS = L::RS;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int waves = blockDim.x >> 6;
     const int tpb = waves / chunks;
     const int64_t tile = (int64_t)blockIdx.x * tpb + wave / chunks;
@@ -49,90 +77,134 @@ __global__ __launch_bounds__(512) void gemv_kernel(
     const int q = lane >> 4;           /* K sub-block of this lane inside a step */
     const int li = lane & 15;          /* weight row (src A) / activation row (src B) */
     const int64_t n0 = tile * 16;
-    int64_t nl = n0 + li;
-    if (nl > N - 1) nl = N - 1;        /* dead rows and whole dead tiles clamp their loads */
+    uint8_t* wbase = smem + wave * L::WAVE;
 
-    const bool a_live = li < M && li < MT;
-    const uint8_t* wrow;
-    const uint8_t* srow = nullptr;
-    if (ENC == ENC_MXFP4A8) {
-        wrow = B + nl * b_pitch + 16 * q;
-        srow = reinterpret_cast<const uint8_t*>(BSv) + nl * bs_pitch + q;
-    } else {
-        wrow = B + nl * b_pitch;
-    }
-    const uint8_t* arow = A + (int64_t)(a_live ? li : 0) * a_pitch;
-    const float* asrow = AS + (int64_t)(a_live ? li : 0) * as_pitch;
+    /* ---- issue side: lane roles for the direct loads (all wave-uniform LDS bases) */
+    const int pr = lane >> 5;                         /* row within a weight pair */
+    const int pc = (lane & 31) ^ pr;                  /* chunk this lane fetches (odd rows swap) */
+    const uint16_t* BS16 = reinterpret_cast<const uint16_t*>(BSv);
+    const uint8_t* BS8 = reinterpret_cast<const uint8_t*>(BSv);
 
-    /* fp8a8 weight scales: four weight rows per lane (rows 4q .. 4q+3 of the tile). */
-    const uint16_t* sbrow[4] = {nullptr, nullptr, nullptr, nullptr};
-    if (ENC == ENC_FP8A8) {
-        const uint16_t* BS16 = reinterpret_cast<const uint16_t*>(BSv);
-        for (int i = 0; i < 4; ++i) {
-            int64_t nr = n0 + 4 * q + i;
+    auto issue = [&](int rs, int ns, uint8_t* buf) {
+        /* weights: pair p = rows 2p, 2p+1; lane -> row 2p+pr, chunk pc (clamped in run) */
+        const int rl = ns * SB;
+        const int wo = (16 * pc < rl - 16) ? 16 * pc : rl - 16;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            int64_t nr = n0 + 2 * p + pr;
             if (nr > N - 1) nr = N - 1;
-            sbrow[i] = BS16 + (nr / rblk) * bs_pitch;
+            r3d_lds_load(B + nr * b_pitch + (int64_t)rs * SB + wo, buf + L::W + p * kPairPitch, 16);
         }
-    }
-
-    r3d_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    /* prefetch ring */
-    r3d_i32x4 wq[PF];
-    r3d_i32x8 w8[PF];
-    int sc[PF];
-    r3d_i32x8 av[PF];
-    float sa[PF];
-    float sb[PF][4];
-
-    auto issue = [&](int u, int s) {
+        /* activations: token t's run bytes [128 rs, +1024) (fp8 runs use the first 512) */
+        {
+            const int ab = ns * 128;
+            const int ao = (16 * lane < ab - 16) ? 16 * lane : ab - 16;
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const int tm = t < M ? t : M - 1;
+                r3d_lds_load(A + (int64_t)tm * a_pitch + (int64_t)rs * 128 + ao, buf + L::AC + t * 1040, 16);
+            }
+        }
+        /* weight scales */
         if (ENC == ENC_MXFP4A8) {
-            wq[u] = r3d_ld16_stream(wrow + 64 * (int64_t)s);
-            sc[u] = srow[4 * (int64_t)s];
+            /* [16 rows][RS dwords]: lane -> row (lane / RS) + 8h, dword lane % RS (clamped) */
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int row = (lane / RS) + 8 * h;
+                int64_t nr = n0 + row;
+                if (nr > N - 1) nr = N - 1;
+                const int d = (lane % RS) < ns ? (lane % RS) : ns - 1;
+                r3d_lds_load(BS8 + nr * bs_pitch + 4 * ((int64_t)rs + d), buf + L::SC + h * 256, 4);
+            }
         } else {
-            w8[u] = r3d_ld_fp8_operand_stream(wrow + 128 * (int64_t)s, q);
-            for (int i = 0; i < 4; ++i) sb[u][i] = r3d_bf16_to_f32(sbrow[i][s]);
+            /* [16 rows][RS] slots of 4 bytes (bf16 in the low half): lane -> row lane / RS,
+             * step lane % RS (clamped) */
+            const int row = lane / RS;
+            int64_t nr = n0 + row;
+            if (nr > N - 1) nr = N - 1;
+            const int d = (lane % RS) < ns ? (lane % RS) : ns - 1;
+            r3d_lds_load(BS16 + (nr / rblk) * bs_pitch + rs + d, buf + L::SC, 2);
         }
-        if (a_live) {
-            av[u] = r3d_ld_fp8_operand(arow + 128 * (int64_t)s, q);
-            sa[u] = asrow[s];
-        } else {
-            const r3d_i32x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-            av[u] = z;
-            sa[u] = 0.0f;
+        /* activation scales: [MT][RS] f32, 64 per instruction */
+#pragma unroll
+        for (int h = 0; h < L::N_AS; ++h) {
+            const int e = lane + 64 * h;
+            int t = e / RS;
+            if (t > MT - 1) t = MT - 1;
+            const int tm = t < M ? t : M - 1;
+            const int d = (e % RS) < ns ? (e % RS) : ns - 1;
+            r3d_lds_load(AS + (int64_t)tm * as_pitch + rs + d, buf + L::AS + h * 256, 4);
         }
     };
 
-#pragma unroll
-    for (int u = 0; u < PF; ++u)
-        if (s0 + u < s1) issue(u, s0 + u);
+    /* ---- consume side */
+    const int wrow_off = L::W + (li >> 1) * kPairPitch + (li & 1) * kRunBytes;
+    const int wsw = li & 1;
+    const int tok = MT == 1 ? 0 : li;
+    r3d_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int s = s0; s < s1; s += PF) {
-#pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            const int ss = s + u;
-            if (ss < s1) {
-                r3d_f32x4 d;
-                if (ENC == ENC_MXFP4A8) {
-                    d = r3d_mfma_fp4_fp8(wq[u], sc[u], av[u], R3D_E8M0_ONE);
-                    const float a_s = sa[u];
-                    for (int i = 0; i < 4; ++i) acc[i] = acc[i] + d[i] * a_s;
-                } else {
-                    d = r3d_mfma_fp8_fp8(w8[u], av[u]);
-                    const float a_s = sa[u];
-                    for (int i = 0; i < 4; ++i) acc[i] = acc[i] + (d[i] * a_s) * sb[u][i];
-                }
-                if (ss + PF < s1) issue(u, ss + PF);
+    auto consume = [&](const uint8_t* buf, int j) {
+        const uint8_t* ap = buf + L::AC + tok * 1040 + 128 * j + 16 * q;
+        const r3d_i32x4 alo = *reinterpret_cast<const r3d_i32x4*>(ap);
+        const r3d_i32x4 ahi = *reinterpret_cast<const r3d_i32x4*>(ap + 64);
+        const r3d_i32x8 av = {alo[0], alo[1], alo[2], alo[3], ahi[0], ahi[1], ahi[2], ahi[3]};
+        const float a_s = *reinterpret_cast<const float*>(buf + L::AS + 4 * (tok * RS + j));
+        if (ENC == ENC_MXFP4A8) {
+            const int ch = (4 * j + q) ^ wsw;
+            const r3d_i32x4 w = *reinterpret_cast<const r3d_i32x4*>(buf + wrow_off + 16 * ch);
+            const int sc = buf[L::SC + li * 4 * RS + 4 * j + q];
+            const r3d_f32x4 d = r3d_mfma_fp4_fp8(w, sc, av, R3D_E8M0_ONE);
+            for (int i = 0; i < 4; ++i) acc[i] = acc[i] + d[i] * a_s;
+        } else {
+            const int c0 = (8 * j + q) ^ wsw, c1 = (8 * j + 4 + q) ^ wsw;
+            const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(buf + wrow_off + 16 * c0);
+            const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(buf + wrow_off + 16 * c1);
+            const r3d_i32x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const r3d_f32x4 d = r3d_mfma_fp8_fp8(w, av);
+            /* a 2-byte direct load still fills one 4-byte LDS slot per lane */
+            const uint32_t* sbp = reinterpret_cast<const uint32_t*>(buf + L::SC);
+            for (int i = 0; i < 4; ++i) {
+                const float sbv = __uint_as_float(sbp[(4 * q + i) * RS + j] << 16);
+                acc[i] = acc[i] + (d[i] * a_s) * sbv;
             }
         }
+    };
+
+    /* ---- walk: with two buffers, run r+1 is in flight while run r is consumed */
+    const int nrun = (s1 - s0 + RS - 1) / RS;
+    if (L::DB == 2 && nrun > 0) issue(s0, (s1 - s0) < RS ? (s1 - s0) : RS, wbase);
+    for (int r = 0; r < nrun; ++r) {
+        uint8_t* cur = wbase + (L::DB == 2 ? (r & 1) * L::BUF : 0);
+        const int rs = s0 + r * RS;
+        const int ns = (s1 - rs) < RS ? (s1 - rs) : RS;
+        if (L::DB == 1) {
+            issue(rs, ns, cur);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else if (r + 1 < nrun) {
+            const int rn = rs + RS;
+            issue(rn, (s1 - rn) < RS ? (s1 - rn) : RS, wbase + ((r + 1) & 1) * L::BUF);
+            asm volatile("s_waitcnt vmcnt(%0)" :: "n"(L::LOADS) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        if (ns == RS) {
+#pragma unroll
+            for (int j = 0; j < RS; ++j) consume(cur, j);
+        } else {
+            for (int j = 0; j < ns; ++j) consume(cur, j);
+        }
+        /* this buffer is refilled by a later issue: its reads are done */
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 
     if (chunks > 1) {
-        if (c != 0) red[wave][lane] = acc;
+        __syncthreads();                                  /* every wave is done with LDS */
+        r3d_f32x4* red = reinterpret_cast<r3d_f32x4*>(smem);
+        if (c != 0) red[wave * 64 + lane] = acc;
         __syncthreads();
         if (c == 0)
             for (int cc = 1; cc < chunks; ++cc) {
-                const r3d_f32x4 p = red[wave + cc][lane];
+                const r3d_f32x4 p = red[(wave + cc) * 64 + lane];
                 for (int i = 0; i < 4; ++i) acc[i] = acc[i] + p[i];
             }
     }

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include "rad_plugin.h"
+#include "r3d_gemv_layout.h"
 
 namespace r3d {
 
@@ -102,6 +103,7 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     if (K % 128) return RAD_E_UNSUPPORTED;
     const int64_t a_pitch = row_stride(A, K);
     if (!aligned16(A->data) || !aligned16(B->data) || (a_pitch & 15)) return RAD_E_UNSUPPORTED;
+    if ((uintptr_t)BS->data & 3) return RAD_E_UNSUPPORTED;      /* dword scale walk */
 
     P->enc = ENC_MXFP4A8;
     P->A = (const uint8_t*)A->data;
@@ -190,23 +192,35 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
     return RAD_OK;
 }
 
-/* Split-K policy: enough waves in flight to cover HBM latency (a 16-row tile is one wave
- * per chunk), without cutting a chunk below 8 steps (1024 of K) when avoidable. */
-void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGeom* g) {
+/* Decode geometry: a 16-row weight tile is one wave per K chunk; the chunks of a tile share
+ * a workgroup (LDS fold in chunk order).  Waves per workgroup come from the LDS budget of
+ * one wave's run buffers (160 KB per CU). */
+void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGeom* g,
+                 int wave_lds) {
     g->mt = M <= 1 ? 1 : M <= 4 ? 4 : 16;          /* rounds UP: every row is written */
     g->steps = (int)(K / 128);
     g->tiles = (N + 15) / 16;
+    /* waves one workgroup can hold in 160 KB of LDS, as a power of two <= 8 */
+    int maxw = 8;
+    if (wave_lds > 0) {
+        const int fit = (160 * 1024) / wave_lds;
+        maxw = fit >= 8 ? 8 : fit >= 4 ? 4 : fit >= 2 ? 2 : 1;
+    }
     int c = 1;
     if (force_chunks > 0) {
         c = force_chunks >= 8 ? 8 : force_chunks >= 4 ? 4 : force_chunks >= 2 ? 2 : 1;
     } else {
-        const int64_t target_waves = 2048;
-        while (c < 8 && g->tiles * c < target_waves && g->steps / (2 * c) >= 4) c *= 2;
+        /* measured on MI355X at the 27B-class shapes: two chunks per tile wins wherever a
+         * chunk keeps >= 8 steps (more resident waves, each still many runs long); more
+         * only when the tile count is small */
+        if (g->steps >= 16) c = 2;
+        while (c < 8 && g->tiles * c < 512 && g->steps / (2 * c) >= 8) c *= 2;
     }
-    if (c > g->steps) c = 1;
+    if (c > maxw) c = maxw;
     while (c > 1 && c > g->steps) c >>= 1;
     g->chunks = c;
-    g->waves = c > 4 ? c : 4;
+    const int w0 = maxw < 4 ? maxw : 4;
+    g->waves = c > w0 ? c : w0;
     g->tiles_per_block = g->waves / c;
     g->blocks = (g->tiles + g->tiles_per_block - 1) / g->tiles_per_block;
 }
@@ -227,6 +241,14 @@ int64_t env_splitk() {
     static const int64_t v = [] {
         const char* e = getenv("R3D_GFX950_SPLITK");
         return e ? (int64_t)atoll(e) : (int64_t)0;
+    }();
+    return v;
+}
+int env_prefetch() {
+    static const int v = [] {
+        const char* e = getenv("R3D_GFX950_PF");
+        const int p = e ? atoi(e) : 4;
+        return p >= 8 ? 8 : p <= 2 ? 2 : 4;
     }();
     return v;
 }
@@ -252,7 +274,8 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
     if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
     if (dec) {
         DecodeGeom g{};
-        decode_geom(P.M, P.N, P.K, decode_splitk(a), &g);
+        decode_geom(P.M, P.N, P.K, decode_splitk(a), &g,
+                    gemv_wave_lds(P.enc, P.M <= 1 ? 1 : P.M <= 4 ? 4 : 16));
         snprintf(buf, (size_t)len,
                  "arm=decode enc=%s M=%lld N=%lld K=%lld mt=%d chunks=%d waves=%d tiles=%lld "
                  "blocks=%lld steps=%d rblk=%d",

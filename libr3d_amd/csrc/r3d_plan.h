@@ -62,7 +62,9 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P);
  * M parameter), and the band's own M bound when `m_max` > 0. */
 int entry_preamble(const RadArgs* a, int enc, int64_t m_max, int64_t* M, int64_t* N);
 
-void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGeom* g);
+/* wave_lds: LDS bytes one wave needs (0 = unknown: assume it fits 8 waves per workgroup). */
+void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGeom* g,
+                 int wave_lds = 0);
 void tile_geom(int64_t M, int64_t N, TileGeom* g);
 
 /* Environment levers, read once per process (function-local statics). */
@@ -72,6 +74,7 @@ bool env_no_fp8a8();        /* R3D_NO_FP8A8: all fp8a8 rows */
 bool env_no_fp8_dec();      /* R3D_NO_FP8_DEC: the fp8a8 decode row */
 bool env_debug();           /* R3D_DEBUG_GEMM: one stderr line per distinct launch arm */
 int64_t env_splitk();       /* R3D_GFX950_SPLITK: force the decode chunk count (0 = policy) */
+int env_prefetch();         /* R3D_GFX950_PF: decode prefetch depth in K steps, 2/4/8 (default 4) */
 
 /* The decode rows' "splitk" tunable (RadArgs::tv): chunks per tile, 0 = the policy.  An
  * engine-chosen value wins over R3D_GFX950_SPLITK. */
