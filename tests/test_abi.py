@@ -1,0 +1,256 @@
+"""The C-ABI boundary on the CPU: exports, plugin identity, the gemm_nt_q schema, the row
+table and its resolver behaviour, the registration-time kill switches, and every plan
+refusal and geometry choice (through r3d_gfx950_describe, which launches nothing and
+touches no device memory)."""
+import ctypes
+import json
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import libr3d_amd as R
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_every_declared_symbol_is_exported():
+    L = R.lib()
+    names = []
+    for h in ("r3d_gfx950.h",):
+        txt = open(os.path.join(ROOT, "include", h)).read()
+        names += re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(\w+)\s*\([^;]*\);", txt, re.M)
+    assert len(names) >= 10, names
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_plugin_identity_and_schema():
+    L = R.lib()
+    assert L.rad_plugin_abi_version() == 26
+    info = L.rad_plugin_info().contents
+    assert info.targets == b"gfx950" and info.kind == 1
+    sch = R.schemas()
+    assert [s["op"] for s in sch] == ["gemm_nt_q"]
+    s = sch[0]
+    assert [p[0] for p in s["params"]] == ["M", "N", "K", "group", "dtype", "pb1", "pb2", "split_n"]
+    assert [p[2] for p in s["params"]] == [0, 0, 0, 0, 0, 1, 1, 1]          # required / optional
+    assert [(o[0], o[2]) for o in s["operands"]] == [
+        ("a", 0), ("a_scale", 1), ("b", 0), ("b_scale", 0), ("y", 0), ("a_sum", 1), ("b_ref", 1)]
+    assert [o[1] for o in s["operands"]] == [0, 0, 3, 3, 1, 0, 3]            # IN/WEIGHT/OUT
+
+
+def test_rows_and_resolver():
+    rows = {r["name"]: r for r in R.rows()}
+    assert set(rows) == {"gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", "gemm_nt_q_fp8a8",
+                         "gemm_nt_q_fp8a8_decode"}
+    assert rows["gemm_nt_q_mxfp4_decode"]["priority"] == 1100
+    assert rows["gemm_nt_q_mxfp4"]["priority"] == 1000
+    q = lambda **kw: R.resolve("gemm_nt_q", kw)["name"] if R.resolve("gemm_nt_q", kw) else None
+    assert q(dtype="mxfp4a8", M=1, K=4096, N=4096, group=32) == "gemm_nt_q_mxfp4_decode"
+    assert q(dtype="mxfp4a8", M=16, K=4096, N=4096, group=32) == "gemm_nt_q_mxfp4_decode"
+    assert q(dtype="mxfp4a8", M=17, K=4096, N=4096, group=32) == "gemm_nt_q_mxfp4"
+    assert q(dtype="mxfp4a8", M=1, K=4160, N=4096, group=32) is None        # ragged K -> host
+    assert q(dtype="fp8a8", M=4, K=5376, N=21504, group=128) == "gemm_nt_q_fp8a8_decode"
+    assert q(dtype="fp8a8", M=2048, K=5376, N=21504, group=128) == "gemm_nt_q_fp8a8"
+    assert q(dtype="fp8a8", M=4, K=5376, N=21504, group=64) is None
+    assert q(dtype="w2a8", M=1, K=5376, N=16, group=128) is None
+    # a constraint on an absent key never holds: without M only the decode row drops out
+    assert q(dtype="mxfp4a8", K=4096, N=4096, group=32) == "gemm_nt_q_mxfp4"
+    assert q(dtype="fp8a8", M=4, K=5376, N=21504) is None                   # no group key
+
+
+_ROWS_SCRIPT = r"""
+import json, sys
+sys.path.insert(0, %r)
+import libr3d_amd as R
+print(json.dumps(sorted(r["name"] for r in R.rows())))
+"""
+
+
+@pytest.mark.parametrize("env,expect", [
+    ({}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode"]),
+    ({"R3D_NO_MXFP4": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode"]),
+    ({"R3D_NO_FP4_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4"]),
+    ({"R3D_NO_FP8A8": "1"}, ["gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode"]),
+    ({"R3D_NO_FP8_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode"]),
+    ({"R3D_NO_FP8_DEC": "", "R3D_NO_FP4_DEC": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4"]),
+    ({"R3D_MXFP4_Q8X": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4",
+                              "gemm_nt_q_mxfp4_decode"]),
+    ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, []),
+])
+def test_kill_switch_matrix(env, expect):
+    """Presence-tested levers hide rows at registration (the value does not matter: an
+    empty or "0" value still counts as set); R3D_MXFP4_Q8X is inert here."""
+    e = {k: v for k, v in os.environ.items() if not k.startswith("R3D_")}
+    e.update(env)
+    out = subprocess.run([sys.executable, "-c", _ROWS_SCRIPT % ROOT], env=e, capture_output=True,
+                         text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert json.loads(out.stdout.strip().splitlines()[-1]) == expect
+
+
+# ------------------------------------------------------------------ plans (host only)
+class FakeT:
+    """Host numpy buffer standing in for a device tensor: describe() never dereferences."""
+
+    def __init__(self, arr, offset=0):
+        self.arr = arr
+        self.offset = offset
+        self.shape = arr.shape
+        self.dtype = arr.dtype
+
+    def data_ptr(self):
+        return self.arr.ctypes.data + self.offset
+
+    def stride(self, dim=None):
+        st = tuple(s // self.arr.itemsize for s in self.arr.strides)
+        return st if dim is None else st[dim]
+
+    def numel(self):
+        return self.arr.size
+
+
+def _aligned(shape, dtype):
+    n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+    raw = np.zeros(n + 256, np.uint8)
+    off = (-raw.ctypes.data) % 256
+    return raw[off:off + n].view(dtype).reshape(shape)
+
+
+def _mx_ops(M=1, N=64, K=256, **kw):
+    a = FakeT(_aligned((M, K), np.uint8))
+    s = FakeT(_aligned((M, K // 128), np.float32))
+    b = FakeT(_aligned((N, K // 2), np.uint8))
+    bs = FakeT(_aligned((N, K // 32), np.uint8))
+    y = FakeT(_aligned((M, N), np.uint16))
+    kw.setdefault("dtype", "mxfp4a8")
+    return R.GemmOperands(a, s, b, bs, y, N=N, K=K, **kw), (a, s, b, bs, y)
+
+
+def _f8_ops(M=1, N=256, K=256, rblk=1, **kw):
+    a = FakeT(_aligned((M, K), np.uint8))
+    s = FakeT(_aligned((M, K // 128), np.float32))
+    b = FakeT(_aligned((N, K), np.uint8))
+    rows = N if rblk == 1 else (N + 127) // 128
+    bs = FakeT(_aligned((rows, K // 128), np.uint16))
+    y = FakeT(_aligned((M, N), np.uint16))
+    kw.setdefault("dtype", "fp8a8")
+    return R.GemmOperands(a, s, b, bs, y, N=N, K=K, **kw), (a, s, b, bs, y)
+
+
+def _geom(desc):
+    return dict(kv.split("=") for kv in desc.split() if "=" in kv)
+
+
+def test_plan_accepts_and_derives_m_from_y():
+    ops, _ = _mx_ops(M=3, extra_params=[("M", 99)])
+    rc, d = R.describe("gemm_nt_q_mxfp4_decode", ops)
+    assert rc == R.RAD_OK, d
+    g = _geom(d)
+    assert g["M"] == "3" and g["mt"] == "4"              # M = numel(y)/N; MT rounds up
+
+
+@pytest.mark.parametrize("M,mt", [(1, "1"), (2, "4"), (4, "4"), (5, "16"), (9, "16"), (16, "16")])
+def test_mt_ladder_rounds_up(M, mt):
+    ops, _ = _mx_ops(M=M)
+    rc, d = R.describe("gemm_nt_q_mxfp4_decode", ops)
+    assert rc == R.RAD_OK and _geom(d)["mt"] == mt
+
+
+def test_decode_band_bound_and_tile_any_m():
+    ops, _ = _mx_ops(M=17)
+    assert R.describe("gemm_nt_q_mxfp4_decode", ops)[0] == R.RAD_E_UNSUPPORTED
+    rc, d = R.describe("gemm_nt_q_mxfp4", ops)
+    assert rc == R.RAD_OK and _geom(d)["arm"] == "tile"
+
+
+def test_decode_geometry_policy():
+    for (M, N, K, chunks) in [(1, 21504, 5376, "2"), (1, 5376, 21504, "2"), (1, 4096, 4096, "2"),
+                              (1, 1000, 4096, "4"), (1, 64, 256, "1")]:
+        ops, _ = _mx_ops(M=M, N=N, K=K)
+        rc, d = R.describe("gemm_nt_q_mxfp4_decode", ops)
+        assert rc == R.RAD_OK, d
+        assert _geom(d)["chunks"] == chunks, (M, N, K, d)
+    ops, _ = _mx_ops(M=1, N=21504, K=5376, tunables=[("splitk", 8)])
+    assert _geom(R.describe("gemm_nt_q_mxfp4_decode", ops)[1])["chunks"] == "8"
+
+
+@pytest.mark.parametrize("case,rc", [
+    ("dtype", R.RAD_E_UNSUPPORTED), ("a_sum", R.RAD_E_UNSUPPORTED), ("pb1", R.RAD_E_UNSUPPORTED),
+    ("k_ragged", R.RAD_E_UNSUPPORTED), ("a_misaligned", R.RAD_E_UNSUPPORTED),
+    ("no_n", R.RAD_E_SHAPE), ("y_ragged", R.RAD_E_SHAPE), ("bs_grid", R.RAD_E_UNSUPPORTED),
+    ("y_dtype", R.RAD_E_UNSUPPORTED), ("b_ref_ok", R.RAD_OK), ("a_small", R.RAD_E_SHAPE),
+])
+def test_mxfp4_plan_refusals(case, rc):
+    M, N, K = 2, 64, 256
+    kw = {}
+    if case == "dtype":
+        kw["dtype"] = "fp8a8"
+    if case == "pb1":
+        kw["extra_params"] = [("pb1", 2)]
+    a = FakeT(_aligned((M, K), np.uint8))
+    s = FakeT(_aligned((M, K // 128), np.float32))
+    b = FakeT(_aligned((N, K // 2), np.uint8))
+    bs = FakeT(_aligned((N, K // 32), np.uint8))
+    y = FakeT(_aligned((M, N), np.uint16))
+    extra = {}
+    if case == "a_sum":
+        extra["a_sum"] = FakeT(_aligned((M, 2), np.float32))
+    if case == "b_ref_ok":
+        extra["b_ref"] = FakeT(_aligned((N, 2), np.uint16))
+    if case == "a_misaligned":
+        a = FakeT(_aligned((M, K + 16), np.uint8), offset=4)
+    if case == "bs_grid":
+        bs = FakeT(_aligned((N, K // 64), np.uint8))
+    if case == "a_small":
+        a = FakeT(_aligned((1, K), np.uint8))
+    Kp = K + 64 if case == "k_ragged" else K
+    if case == "k_ragged":
+        a = FakeT(_aligned((M, Kp), np.uint8))
+        b = FakeT(_aligned((N, Kp // 2), np.uint8))
+        bs = FakeT(_aligned((N, (Kp + 31) // 32), np.uint8))
+        s = FakeT(_aligned((M, (Kp + 127) // 128), np.float32))
+    ops = R.GemmOperands(a, s, b, bs, y, dtype=kw.get("dtype", "mxfp4a8"), N=N, K=Kp,
+                         extra_params=kw.get("extra_params"), **extra)
+    if case == "no_n":
+        ops._p[1].key = b"Nx"
+    if case == "y_ragged":
+        ops._t[4].shape[1] = N - 1
+    if case == "y_dtype":
+        ops._t[4].dtype = R.DT["F32"]
+    got, d = R.describe("gemm_nt_q_mxfp4_decode", ops)
+    assert got == rc, (case, d)
+
+
+@pytest.mark.parametrize("case,rc", [
+    ("ok_row", R.RAD_OK), ("ok_block", R.RAD_OK), ("b_ref", R.RAD_E_UNSUPPORTED),
+    ("group64", R.RAD_E_SHAPE), ("bs_dtype", R.RAD_E_UNSUPPORTED), ("inner_stride", R.RAD_E_STRIDE),
+])
+def test_fp8_plan_refusals(case, rc):
+    rblk = 128 if case == "ok_block" else 1
+    extra = {}
+    if case == "b_ref":
+        extra["b_ref"] = FakeT(_aligned((256, 2), np.uint16))
+    ops, (a, s, b, bs, y) = _f8_ops(rblk=rblk, group=64 if case == "group64" else None, **extra)
+    if case == "bs_dtype":
+        ops._t[3].dtype = R.DT["F32"]
+    if case == "inner_stride":
+        ops._t[2].stride[1] = 2
+    got, d = R.describe("gemm_nt_q_fp8a8_decode", ops)
+    assert got == rc, (case, d)
+    if rc == R.RAD_OK:
+        assert _geom(d)["rblk"] == str(rblk)
+
+
+def test_entries_refuse_without_gfx950():
+    """On a host without a gfx950 device a valid plan stops at the chip gate: the entry
+    returns RAD_E_UNSUPPORTED and launches nothing."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    ops, _ = _mx_ops(M=1)
+    assert R.launch_row("gemm_nt_q_mxfp4_decode", ops, 0) == R.RAD_E_UNSUPPORTED
