@@ -27,6 +27,11 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP8_PEAK_TFLOPS = 5000.0       # dense MFMA fp8 (the rate of an fp8 x fp4 scaled MFMA)
 FP4_PEAK_TFLOPS = 10100.0      # dense MFMA fp4 x fp4
 ROTATE_BYTES = 1.1 * 2 ** 30
+# HBM bytes per launch of the headline kernel from two rocprofv3 --pmc passes over this
+# script (--quick), FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 -- the factors a plain 256 MiB
+# device copy reads on the same counters (bench.py --copy-calib).  Re-measured whenever
+# the decode kernel changes; profiles/gemv_fp8a8_c1_pmc_traffic.md has the numbers.
+HEADLINE_TRAFFIC_BYTES = 117812643
 
 
 def log(*a):
@@ -66,7 +71,10 @@ def copies_for(nbytes):
 
 
 def time_case(case, row, steps, warmup, stream):
-    """-> (wall seconds for `steps` launches, mean kernel seconds from per-launch events)."""
+    """-> (wall seconds for `steps` back-to-back launches between two synchronised points,
+    average launch duration in seconds from HIP events recorded on the launch stream
+    around the same launches -- the GPU-side span divided by the launch count, which is
+    what rocprofv3's per-kernel average measures plus the back-to-back dispatch gaps)."""
     import torch
     import libr3d_amd as R
     launch = R.row_launcher(row)
@@ -74,22 +82,17 @@ def time_case(case, row, steps, warmup, stream):
     for i in range(warmup):
         rc = launch(case.ops[i % n], stream)
         assert rc == 0, "row %s refused: %d" % (row, rc)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    # wall-clock timed region: back-to-back launches
     t0 = time.perf_counter()
+    e0.record()
     for i in range(steps):
         launch(case.ops[i % n], stream)
+    e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # kernel durations: one event pair per launch on the launch stream
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
-    for i in range(steps):
-        ev[i][0].record()
-        launch(case.ops[i % n], stream)
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    kern = float(np.mean([a.elapsed_time(b) for a, b in ev])) * 1e-3
+    kern = e0.elapsed_time(e1) * 1e-3 / steps
     return wall, kern
 
 
@@ -135,7 +138,18 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run a plain 256 MiB device copy (counter calibration for PMC runs)")
     args = ap.parse_args()
+    if args.copy_calib:
+        import torch
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel(), "launches": 5}), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the gemm_nt_q path is built and measured on a single "
               "MI355X (multi-GPU sharding is design only); run with --gpus 1", file=sys.stderr)
@@ -181,8 +195,9 @@ def main():
                                "(weights rotated over >1 GiB)",
                    "row": "gemm_nt_q_fp8a8_decode", "bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "r3d::gemv_kernel<1,1,4> (fp8a8, MT=1)",
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": HEADLINE_TRAFFIC_BYTES,
+                     "kernel": "r3d::gemv_kernel<1, 1> (fp8a8, MT=1)",
                      "kernel_us": round(kern * 1e6, 3)},
     }
 
