@@ -47,6 +47,20 @@ int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s);
 /* gemm_nt_q at fp8a8, decode band M <= 16.  Replaces src/r3d_gemm_fp8a8.hip:1101-1130. */
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
 
+/* gemm_nt_q at dtype "mxfp4a16", prefill row (any M).  No counterpart in the reference:
+ * the bf16-activation variant of the mxfp4 prefill (a bf16 [M, K], a_scale absent,
+ * weights as mxfp4a8), for engines that feed unquantised activations.  The launch
+ * quantises a to mxfp8 (e4m3 + E8M0 per 32 of K) into RadArgs::scratch, then runs the
+ * block-scaled MFMA GEMM; both kernels run on `s`.  The launch-signature convention is
+ * src/r3d_gemm_mxfp4.hip:1587-1588; the scratch refusal follows
+ * src/r3d_gemm_fp8a8.hip:1214-1218 (RAD_E_UNSUPPORTED when scratch is missing or short). */
+int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s);
+
+/* The mxfp4a16 row's scratch hook (RadKernelInfo::scratch): bytes of launch scratch for
+ * the M and K parameters, 0 when either is missing.  Same role as the reference's
+ * src/r3d_gemm_fp8a8.hip:1249-1253. */
+int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a);
+
 /* Host-only diagnostic with no counterpart in the reference: runs `row`'s preamble and
  * plan on `a` and writes the chosen arm and launch geometry (or the refusal) into buf.
  * Launches nothing, touches no device memory.  Returns the plan's status code. */

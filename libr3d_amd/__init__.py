@@ -63,6 +63,7 @@ class RadConstraint(ctypes.Structure):
 
 
 LaunchFn = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.POINTER(RadArgs), ctypes.c_void_p)
+ScratchFn = ctypes.CFUNCTYPE(ctypes.c_int64, ctypes.POINTER(RadArgs))
 
 
 class RadKernelInfo(ctypes.Structure):
@@ -142,7 +143,8 @@ def rows():
         cons = [(_s(k.constraints[c].key), k.constraints[c].op, k.constraints[c].ival,
                  _s(k.constraints[c].sval)) for c in range(k.n_constraints)]
         out.append({"name": _s(k.name), "op": _s(k.op), "priority": k.priority,
-                    "domain": k.domain, "constraints": cons, "launch": k.launch})
+                    "domain": k.domain, "constraints": cons, "launch": k.launch,
+                    "scratch": k.scratch})
     return out
 
 
@@ -196,16 +198,18 @@ def resolve(op, query):
 class GemmOperands:
     """Owns the ctypes RadArgs for one gemm_nt_q call over device tensors.
 
-    a      uint8 [M, K]           e4m3 codes
-    a_scale float32 [M, K/128]
-    b      uint8 [N, K/2] (mxfp4a8: packed e2m1, low nibble = even k) or [N, K] (fp8a8)
-    b_scale uint8 [N, K/32] E8M0 (mxfp4a8) or bf16/int16 [N or N/128, K/128] (fp8a8)
+    a      uint8 [M, K]           e4m3 codes (mxfp4a16: bf16/int16 [M, K])
+    a_scale float32 [M, K/128]    (mxfp4a16: None)
+    b      uint8 [N, K/2] (mxfp4a8/a16: packed e2m1, low nibble = even k) or [N, K] (fp8a8)
+    b_scale uint8 [N, K/32] E8M0 (mxfp4) or bf16/int16 [N or N/128, K/128] (fp8a8)
     y      bf16/int16 [M, N]
+    scratch optional device tensor handed over as RadArgs::scratch (mxfp4a16)
     """
 
     def __init__(self, a, a_scale, b, b_scale, y, *, dtype, N, K, group=None, M=None,
-                 a_sum=None, b_ref=None, extra_params=None, y_shape=None, tunables=None):
-        mx = dtype == "mxfp4a8"
+                 a_sum=None, b_ref=None, extra_params=None, y_shape=None, tunables=None,
+                 scratch=None):
+        mx = dtype in ("mxfp4a8", "mxfp4a16")
         self.dtype = dtype
         group = group if group is not None else (32 if mx else 128)
         t = (RadTensor * 7)()
@@ -224,7 +228,7 @@ class GemmOperands:
                 t[i].shape[r] = int(s_)
                 t[i].stride[r] = int(st)
 
-        fill(0, a, "F8E4M3")
+        fill(0, a, "BF16" if dtype == "mxfp4a16" else "F8E4M3")
         fill(1, a_scale, "F32")
         if mx:
             # FP4 counts nibbles: [N, K] with strides {K, 1}
@@ -271,6 +275,14 @@ class GemmOperands:
                             ctypes.cast(p, ctypes.POINTER(RadParam)), len(params),
                             ctypes.cast(tv, ctypes.POINTER(RadTunableValue)), len(tunables),
                             None, 0, 0)
+        if scratch is not None:
+            self.set_scratch(scratch)
+
+    def set_scratch(self, scratch, nbytes=None):
+        """Hand `scratch` (a device tensor) to the launch as RadArgs::scratch."""
+        self.args.scratch = scratch.data_ptr()
+        self.args.scratch_bytes = int(nbytes if nbytes is not None
+                                      else scratch.numel() * scratch.element_size())
 
     def set_y(self, y):
         self._t[4].data = y.data_ptr()
@@ -285,6 +297,16 @@ def row_launcher(row_name):
             def call(ops, stream=0):
                 return fn(ctypes.byref(ops.args), ctypes.c_void_p(stream))
             return call
+    raise KeyError("row %s is not registered" % row_name)
+
+
+def row_scratch_bytes(row_name, ops):
+    """The named row's scratch hook on `ops` (bytes; 0 when the row has no hook)."""
+    for r in rows():
+        if r["name"] == row_name:
+            if not r.get("scratch"):
+                return 0
+            return int(ScratchFn(r["scratch"])(ctypes.byref(ops.args)))
     raise KeyError("row %s is not registered" % row_name)
 
 

@@ -36,6 +36,28 @@ __device__ __forceinline__ r3d_f32x4 r3d_mfma_fp4_fp8(r3d_i32x4 a, int scale_a, 
                                                             0, scale_a, 0, scale_b);
 }
 
+/* C += A(16 x 128, fp4, scale per lane) . B(16 x 128, fp8, scale per lane)^T. */
+__device__ __forceinline__ r3d_f32x4 r3d_mfma_fp4_fp8_acc(r3d_i32x4 a, int scale_a, r3d_i32x8 b,
+                                                          int scale_b, r3d_f32x4 c) {
+    const r3d_i32x8 a8 = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, b, c, R3D_MFMA_FP4, R3D_MFMA_FP8,
+                                                            0, scale_a, 0, scale_b);
+}
+
+/* Direct global -> LDS load of `bytes` (16, 4 or 2) per lane: lane l's data lands at
+ * lds + l * max(bytes, 4); the LDS base must be wave-uniform. */
+__device__ __forceinline__ void r3d_lds_load(const void* g, void* l, int bytes) {
+    if (bytes == 16)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                         (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+    else if (bytes == 4)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                         (__attribute__((address_space(3))) void*)l, 4, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                         (__attribute__((address_space(3))) void*)l, 2, 0, 0);
+}
+
 /* D = A(16 x 128, fp8) . B(16 x 128, fp8)^T, unit scales, fresh accumulator. */
 __device__ __forceinline__ r3d_f32x4 r3d_mfma_fp8_fp8(r3d_i32x8 a, r3d_i32x8 b) {
     const r3d_f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};

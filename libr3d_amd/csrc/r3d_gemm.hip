@@ -1,5 +1,6 @@
 /* r3d_gemm.hip -- the gfx950 gemm_nt_q row entries (mxfp4a8 and fp8a8, decode band and
- * prefill tile) behind radiance's kernel-row launch signature
+ * prefill tile; the bf16-in mxfp4a16 prefill row) behind radiance's kernel-row launch
+ * signature
  *     int launch(const RadArgs* a, RadStream s)
  * (src/r3d_gemm_mxfp4.hip:1587-1588,1717-1718; src/r3d_gemm_fp8a8.hip:1054-1056,1108-1110).
  *
@@ -15,6 +16,7 @@
 
 #include "r3d_gemm_kernels.h"
 #include "r3d_plan.h"
+#include "r3d_prefill.h"
 #include "rad_plugin.h"
 
 namespace r3d {
@@ -32,6 +34,21 @@ static bool chip_ok() {
         cache[dev] = ok ? 1 : 2;
     }
     return cache[dev] == 1;
+}
+
+/* Compute units of the current device, answered once per device. */
+static int cu_count() {
+    static int cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
 }
 
 static void debug_once(const char* what, int key) {
@@ -72,31 +89,92 @@ static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) 
     return RAD_OK;
 }
 
+/* The fp8a8 prefill tile. */
 static int launch_tile(const GemmPlan& P, hipStream_t stream) {
     TileGeom g{};
     tile_geom(P.M, P.N, &g);
     if (g.grid_m > 65535) return RAD_E_SHAPE;
     const dim3 grid((unsigned)g.grid_n, (unsigned)g.grid_m), block(256);
     const int steps = (int)(P.K / 128);
-    if (P.enc == ENC_MXFP4A8)
-        hipLaunchKernelGGL((tile_kernel<ENC_MXFP4A8>), grid, block, 0, stream, P.A, P.AS, P.B,
-                           P.BS, P.Y, (int)P.M, (int)P.N, steps, P.rblk, P.a_pitch, P.as_pitch,
-                           P.b_pitch, P.bs_pitch, P.y_pitch);
-    else
-        hipLaunchKernelGGL((tile_kernel<ENC_FP8A8>), grid, block, 0, stream, P.A, P.AS, P.B,
-                           P.BS, P.Y, (int)P.M, (int)P.N, steps, P.rblk, P.a_pitch, P.as_pitch,
-                           P.b_pitch, P.bs_pitch, P.y_pitch);
+    hipLaunchKernelGGL((tile_kernel<ENC_FP8A8>), grid, block, 0, stream, P.A, P.AS, P.B,
+                       P.BS, P.Y, (int)P.M, (int)P.N, steps, P.rblk, P.a_pitch, P.as_pitch,
+                       P.b_pitch, P.bs_pitch, P.y_pitch);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         fprintf(stderr, "libr3d_gfx950: prefill tile launch FAILED (%s)\n", hipGetErrorName(e));
         return RAD_E_DEVICE;
     }
-    debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 prefill tile" : "fp8a8 prefill tile",
-               64 + P.enc);
+    debug_once("fp8a8 prefill tile", 64 + P.enc);
+    return RAD_OK;
+}
+
+/* The mxfp4 prefill GEMM: mode PF_A8 reads A/AS as given (e4m3 + f32 per 128), mode
+ * PF_MX8 reads the mxfp8 planes the quantiser left in P.scratch. */
+static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
+    const int mode = P.enc == ENC_MXFP4A16 ? PF_MX8 : PF_A8;
+    PrefillGeom g{};
+    prefill_geom(P.M, P.N, P.K, mode, cu_count(), &g);
+    if (g.tiles > 0x7FFFFFFF || g.grid_m > 0x7FFFFFFF) return RAD_E_SHAPE;
+    const uint8_t* A = P.A;
+    const void* AS = P.AS;
+    int64_t a_pitch = P.a_pitch, as_pitch = P.as_pitch;
+    if (mode == PF_MX8) {
+        const int64_t qbytes = ((P.M * P.K + 255) / 256) * 256;
+        uint8_t* Q = P.scratch;
+        uint8_t* SX = P.scratch + qbytes;
+        const int64_t threads = P.M * (P.K / 8);
+        const int64_t qblocks = (threads + 255) / 256;
+        if (qblocks > 0x7FFFFFFF) return RAD_E_SHAPE;
+        hipLaunchKernelGGL(quant_mx8_kernel, dim3((unsigned)qblocks), dim3(256), 0, stream,
+                           reinterpret_cast<const uint16_t*>(P.A), P.a_pitch, Q, P.K, SX,
+                           P.K / 32, P.M, (int)P.K);
+        A = Q;
+        AS = SX;
+        a_pitch = P.K;
+        as_pitch = P.K / 32;
+    }
+    /* the kernel addresses 256 rows of any operand with 32-bit lane offsets */
+    const int64_t lim = (int64_t)1 << 31;
+    if (256 * a_pitch >= lim || 256 * P.b_pitch >= lim || 256 * P.bs_pitch >= lim ||
+        256 * (mode == PF_MX8 ? as_pitch : 4 * as_pitch) >= lim)
+        return RAD_E_UNSUPPORTED;
+    const dim3 grid((unsigned)g.tiles), block(256);
+#define R3D_PF(MODE_, WNF_, WMF_)                                                          \
+    static_assert(PrefillLayout<WNF_, WMF_, 3>::LDS == 3 * prefill_stage_bytes(WNF_, WMF_), \
+                  "host and kernel ring sizes differ");                                    \
+    hipLaunchKernelGGL((prefill_kernel<MODE_, WNF_, WMF_>), grid, block,                    \
+                       (size_t)(PrefillLayout<WNF_, WMF_, 3>::LDS), stream, A, AS, P.B,     \
+                       (const uint8_t*)P.BS, P.Y, (int)P.M, (int)P.N, g.steps,             \
+                       (int)g.grid_m, (int)g.tiles, a_pitch, as_pitch, P.b_pitch,          \
+                       P.bs_pitch, P.y_pitch)
+    if (mode == PF_MX8) {
+        switch (g.wnf) {
+            case 8: R3D_PF(PF_MX8, 8, 8); break;
+            case 7: R3D_PF(PF_MX8, 7, 8); break;
+            case 6: R3D_PF(PF_MX8, 6, 8); break;
+            default: R3D_PF(PF_MX8, 4, 8); break;
+        }
+    } else {
+        switch (g.wnf) {
+            case 8: R3D_PF(PF_A8, 8, 4); break;
+            case 7: R3D_PF(PF_A8, 7, 4); break;
+            case 6: R3D_PF(PF_A8, 6, 4); break;
+            default: R3D_PF(PF_A8, 4, 4); break;
+        }
+    }
+#undef R3D_PF
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "libr3d_gfx950: prefill launch FAILED (%s)\n", hipGetErrorName(e));
+        return RAD_E_DEVICE;
+    }
+    debug_once(mode == PF_MX8 ? "mxfp4a16 prefill (mxfp8 quantiser + MFMA)" : "mxfp4a8 prefill",
+               128 + 8 * mode + g.wnf);
     return RAD_OK;
 }
 
 static int entry(const RadArgs* a, RadStream s, int enc, bool decode) {
+    if (enc == ENC_MXFP4A16 && env_no_mxfp4()) return RAD_E_UNSUPPORTED;
     if (enc == ENC_MXFP4A8 && (env_no_mxfp4() || (decode && env_no_fp4_dec())))
         return RAD_E_UNSUPPORTED;               /* backstop: registration already hid it */
     if (enc == ENC_FP8A8 && (env_no_fp8a8() || (decode && env_no_fp8_dec())))
@@ -105,11 +183,13 @@ static int entry(const RadArgs* a, RadStream s, int enc, bool decode) {
     int rc = entry_preamble(a, enc, decode ? 16 : 0, &M, &N);
     if (rc) return rc;
     GemmPlan P{};
-    rc = enc == ENC_MXFP4A8 ? plan_mxfp4a8(a, M, N, &P) : plan_fp8a8(a, M, &P);
+    rc = enc == ENC_MXFP4A8 ? plan_mxfp4a8(a, M, N, &P)
+       : enc == ENC_MXFP4A16 ? plan_mxfp4a16(a, M, N, &P) : plan_fp8a8(a, M, &P);
     if (rc) return rc;
     if (!chip_ok()) return RAD_E_UNSUPPORTED;
     hipStream_t stream = (hipStream_t)s;
-    return decode ? launch_decode(P, decode_splitk(a), stream) : launch_tile(P, stream);
+    if (decode) return launch_decode(P, decode_splitk(a), stream);
+    return enc == ENC_FP8A8 ? launch_tile(P, stream) : launch_prefill(P, stream);
 }
 
 }  // namespace r3d
@@ -121,6 +201,15 @@ int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s) {
 }
 int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s) {
     return r3d::entry(a, s, r3d::ENC_MXFP4A8, true);
+}
+int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s) {
+    return r3d::entry(a, s, r3d::ENC_MXFP4A16, false);
+}
+int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a) {
+    long long M = 0, K = 0;
+    if (!rad_args_geti(a, "M", &M) || !rad_args_geti(a, "K", &K)) return 0;   /* 0 = none */
+    if (M <= 0 || K <= 0 || M > (1LL << 27) || K > (1LL << 27)) return 0;
+    return r3d::mxfp4a16_scratch_bytes(M, K);
 }
 int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s) {
     return r3d::entry(a, s, r3d::ENC_FP8A8, false);

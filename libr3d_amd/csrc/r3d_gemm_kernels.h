@@ -42,18 +42,6 @@ namespace r3d {
  * Every load is unconditional and in bounds: weight rows n >= N clamp to row N-1,
  * activation rows m >= M duplicate row M-1, a short last run clamps its lanes inside the
  * chunk, and nothing clamped is ever used or stored. */
-__device__ __forceinline__ void r3d_lds_load(const void* g, void* l, int bytes) {
-    if (bytes == 16)
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                         (__attribute__((address_space(3))) void*)l, 16, 0, 0);
-    else if (bytes == 4)
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                         (__attribute__((address_space(3))) void*)l, 4, 0, 0);
-    else
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                         (__attribute__((address_space(3))) void*)l, 2, 0, 0);
-}
-
 template <int ENC, int MT>
 __global__ __launch_bounds__(512) void gemv_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ AS,

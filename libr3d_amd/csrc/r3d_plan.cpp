@@ -7,6 +7,7 @@
 
 #include "rad_plugin.h"
 #include "r3d_gemv_layout.h"
+#include "r3d_prefill_layout.h"
 
 namespace r3d {
 
@@ -50,8 +51,9 @@ int entry_preamble(const RadArgs* a, int enc, int64_t m_max, int64_t* M, int64_t
     const RadTensor* Y    = rad_arg_in(a, 4);
     const RadTensor* ASUM = rad_arg_in(a, 5);
     const RadTensor* BREF = rad_arg_in(a, 6);
-    if (!A || !AS || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
-    if (ASUM) return RAD_E_UNSUPPORTED;                 /* no zero point at either encoding */
+    if (!A || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
+    if (enc == ENC_MXFP4A16 ? AS != nullptr : AS == nullptr) return RAD_E_UNSUPPORTED;
+    if (ASUM) return RAD_E_UNSUPPORTED;                 /* no zero point at any encoding */
     if (enc == ENC_FP8A8 && BREF) return RAD_E_UNSUPPORTED;   /* b_ref: e2m1 weights only */
     if (Y->dtype != RAD_BF16) return RAD_E_UNSUPPORTED;
     long long n = 0;
@@ -120,6 +122,72 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     P->as_cols = (int)as_cols;
     P->bs_cols = (int)bs_cols;
     P->rblk = 1;
+    return RAD_OK;
+}
+
+int64_t mxfp4a16_scratch_bytes(int64_t M, int64_t K) {
+    if (M <= 0 || K <= 0) return 0;
+    return ((M * K + 255) / 256) * 256 + M * ((K + 31) / 32);
+}
+
+/* The bf16-in mxfp4 row.  Weights exactly as plan_mxfp4a8; A is bf16 [M, K] with no
+ * a_scale: the launch quantises it to mxfp8 (e4m3 + E8M0 per 32 of K) in the caller's
+ * scratch, so the row refuses (never overruns) a launch whose scratch is short. */
+int plan_mxfp4a16(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
+    const char* dtype = rad_args_gets(a, "dtype");
+    if (!dtype || strcmp(dtype, "mxfp4a16") != 0) return RAD_E_UNSUPPORTED;
+    long long pb = 0;
+    if (rad_args_geti(a, "pb1", &pb) && pb > 0) return RAD_E_UNSUPPORTED;
+    if (rad_args_geti(a, "pb2", &pb) && pb > 0) return RAD_E_UNSUPPORTED;
+
+    const RadTensor* A  = rad_arg_in(a, 0);
+    const RadTensor* B  = rad_arg_in(a, 2);
+    const RadTensor* BS = rad_arg_in(a, 3);
+    const RadTensor* Y  = rad_arg_in(a, 4);
+    if (!A || !B || !BS || !Y || rad_arg_in(a, 1)) return RAD_E_UNSUPPORTED;
+    if (A->dtype != RAD_BF16 || B->dtype != RAD_FP4E2M1 || Y->dtype != RAD_BF16 ||
+        (BS->dtype != RAD_E8M0 && BS->dtype != RAD_U8))
+        return RAD_E_UNSUPPORTED;
+
+    long long K = 0;
+    if (!rad_args_geti(a, "K", &K)) return RAD_E_SHAPE;
+    if (N <= 0 || K <= 0 || M <= 0) return RAD_E_SHAPE;
+    if (M > kDimMax || N > kDimMax || K > kDimMax) return RAD_E_SHAPE;
+    if (rad_tensor_numel(A) < M * K || rad_tensor_numel(B) < N * K) return RAD_E_SHAPE;
+
+    if (BS->rank != 2 || BS->stride[1] != 1 || BS->shape[0] < N) return RAD_E_UNSUPPORTED;
+    const int64_t bs_cols = BS->shape[1];
+    if (grid_block(K, bs_cols) != 32 || bs_cols != (K + 31) / 32) return RAD_E_UNSUPPORTED;
+    long long gp = 0;   /* the group parameter must not contradict the bytes */
+    if (rad_args_geti(a, "group", &gp) && gp > 0 && gp != 32) return RAD_E_SHAPE;
+
+    if (!inner_contig(A) || !inner_contig(B) || !inner_contig(Y)) return RAD_E_STRIDE;
+    if ((K & 1) || row_stride(B, K) != K) return RAD_E_STRIDE;
+
+    if (K % 128) return RAD_E_UNSUPPORTED;
+    const int64_t a_pitch = row_stride(A, K);                 /* bf16 elements */
+    if (!aligned16(A->data) || !aligned16(B->data) || (a_pitch & 7)) return RAD_E_UNSUPPORTED;
+    if ((uintptr_t)BS->data & 3) return RAD_E_UNSUPPORTED;
+    if (!a->scratch || !aligned16(a->scratch) ||
+        a->scratch_bytes < mxfp4a16_scratch_bytes(M, K))
+        return RAD_E_UNSUPPORTED;
+
+    P->enc = ENC_MXFP4A16;
+    P->A = (const uint8_t*)A->data;
+    P->AS = nullptr;
+    P->B = (const uint8_t*)B->data;
+    P->BS = BS->data;
+    P->Y = (uint16_t*)Y->data;
+    P->M = M; P->N = N; P->K = K;
+    P->a_pitch = a_pitch;
+    P->b_pitch = K / 2;
+    P->y_pitch = row_stride(Y, N);
+    P->as_pitch = K / 32;                                     /* of the scratch E8M0 plane */
+    P->bs_pitch = row_stride(BS, bs_cols);
+    P->as_cols = (int)(K / 32);
+    P->bs_cols = (int)bs_cols;
+    P->rblk = 1;
+    P->scratch = (uint8_t*)a->scratch;
     return RAD_OK;
 }
 
@@ -232,6 +300,34 @@ void tile_geom(int64_t M, int64_t N, TileGeom* g) {
     g->grid_n = (N + g->bn - 1) / g->bn;
 }
 
+/* Prefill tile choice: 32 wmf tokens (8 fragments in mxfp8 mode, where the MFMA
+ * accumulates in place; 4 in the f32-a_scale mode, whose per-step flush needs a second
+ * register set) by 32 wnf weight rows.  Workgroups run one per CU, so the launch takes
+ * ceil(tiles / ncu) rounds; a round costs about wnf + 1/2 fragment-steps (the fixed
+ * activation reads of a step).  The cheapest total wins, ties to the larger tile. */
+void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeom* g) {
+    static const int kWnf[] = {8, 7, 6, 4};
+    const int wmf = mode == PF_MX8 ? 8 : 4;
+    if (ncu <= 0) ncu = 256;
+    int best = 8;
+    double best_cost = 0.0;
+    for (int w : kWnf) {
+        const int64_t tiles = ((N + 32 * w - 1) / (32 * w)) * ((M + 32 * wmf - 1) / (32 * wmf));
+        const double cost = (double)((tiles + ncu - 1) / ncu) * (w + 0.5);
+        if (w == 8 || cost < best_cost) { best = w; best_cost = cost; }
+    }
+    g->wnf = best;
+    g->wmf = wmf;
+    g->nst = 3;
+    g->bn = 32 * best;
+    g->bm = 32 * wmf;
+    g->grid_m = (M + g->bm - 1) / g->bm;
+    g->grid_n = (N + g->bn - 1) / g->bn;
+    g->tiles = g->grid_m * g->grid_n;
+    g->steps = (int)(K / 128);
+    g->lds = g->nst * prefill_stage_bytes(g->wnf, g->wmf);
+}
+
 bool env_no_mxfp4()   { static const bool v = getenv("R3D_NO_MXFP4") != nullptr;   return v; }
 bool env_no_fp4_dec() { static const bool v = getenv("R3D_NO_FP4_DEC") != nullptr; return v; }
 bool env_no_fp8a8()   { static const bool v = getenv("R3D_NO_FP8A8") != nullptr;   return v; }
@@ -263,14 +359,16 @@ int64_t decode_splitk(const RadArgs* a) {
 
 int describe(const char* row, const RadArgs* a, char* buf, int len) {
     if (!row || !buf || len <= 0) return RAD_E_INVAL;
+    const bool a16 = strstr(row, "mxfp4a16") != nullptr;
     const bool mx = strstr(row, "mxfp4") != nullptr;
     const bool dec = strstr(row, "decode") != nullptr;
-    const int enc = mx ? ENC_MXFP4A8 : ENC_FP8A8;
+    const int enc = a16 ? ENC_MXFP4A16 : mx ? ENC_MXFP4A8 : ENC_FP8A8;
+    const char* ename = a16 ? "mxfp4a16" : mx ? "mxfp4a8" : "fp8a8";
     int64_t M = 0, N = 0;
     int rc = entry_preamble(a, enc, dec ? 16 : 0, &M, &N);
     if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (preamble)", rc); return rc; }
     GemmPlan P{};
-    rc = mx ? plan_mxfp4a8(a, M, N, &P) : plan_fp8a8(a, M, &P);
+    rc = a16 ? plan_mxfp4a16(a, M, N, &P) : mx ? plan_mxfp4a8(a, M, N, &P) : plan_fp8a8(a, M, &P);
     if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
     if (dec) {
         DecodeGeom g{};
@@ -279,15 +377,24 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
         snprintf(buf, (size_t)len,
                  "arm=decode enc=%s M=%lld N=%lld K=%lld mt=%d chunks=%d waves=%d tiles=%lld "
                  "blocks=%lld steps=%d rblk=%d",
-                 mx ? "mxfp4a8" : "fp8a8", (long long)P.M, (long long)P.N, (long long)P.K,
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K,
                  g.mt, g.chunks, g.waves, (long long)g.tiles, (long long)g.blocks, g.steps,
                  P.rblk);
+    } else if (mx) {
+        PrefillGeom g{};
+        prefill_geom(P.M, P.N, P.K, a16 ? PF_MX8 : PF_A8, 256, &g);
+        snprintf(buf, (size_t)len,
+                 "arm=prefill enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d grid=%lldx%lld "
+                 "tiles=%lld nst=%d lds=%d steps=%d",
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K, g.bn, g.bm,
+                 (long long)g.grid_n, (long long)g.grid_m, (long long)g.tiles, g.nst, g.lds,
+                 g.steps);
     } else {
         TileGeom g{};
         tile_geom(P.M, P.N, &g);
         snprintf(buf, (size_t)len,
                  "arm=tile enc=%s M=%lld N=%lld K=%lld bm=%d bn=%d grid=%lldx%lld rblk=%d",
-                 mx ? "mxfp4a8" : "fp8a8", (long long)P.M, (long long)P.N, (long long)P.K,
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K,
                  g.bm, g.bn, (long long)g.grid_n, (long long)g.grid_m, P.rblk);
     }
     return RAD_OK;

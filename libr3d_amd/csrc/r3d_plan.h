@@ -11,20 +11,28 @@
 
 namespace r3d {
 
-enum Encoding { ENC_MXFP4A8 = 0, ENC_FP8A8 = 1 };
+/* ENC_MXFP4A16: e2m1 weights as mxfp4a8, bf16 activations quantised by the library to
+ * mxfp8 (e4m3 + E8M0 per 32 of K) in launch scratch before the prefill GEMM. */
+enum Encoding { ENC_MXFP4A8 = 0, ENC_FP8A8 = 1, ENC_MXFP4A16 = 2 };
 
 struct GemmPlan {
     int enc;
-    const uint8_t* A;        /* e4m3 [M, K] */
-    const float*   AS;       /* f32 [M, K/128] */
+    const uint8_t* A;        /* e4m3 [M, K] (mxfp4a16: bf16 [M, K]) */
+    const float*   AS;       /* f32 [M, K/128] (mxfp4a16: none) */
     const uint8_t* B;        /* mxfp4: [N, K/2] packed e2m1; fp8a8: [N, K] e4m3 */
     const void*    BS;       /* mxfp4: E8M0 [N, K/32]; fp8a8: bf16 [N or N/128, K/128] */
     uint16_t*      Y;        /* bf16 [M, N] */
     int64_t M, N, K;
-    int64_t a_pitch, as_pitch, b_pitch, bs_pitch, y_pitch;   /* bytes for A/B, elements else */
+    int64_t a_pitch, as_pitch, b_pitch, bs_pitch, y_pitch;   /* bytes for A/B, elements else
+                                                                (mxfp4a16 A: elements) */
     int as_cols, bs_cols;
     int rblk;                /* fp8a8 weight-scale rows per scale row: 1 or 128 */
+    uint8_t* scratch;        /* mxfp4a16: e4m3 codes [M, K] then E8M0 [M, K/32] */
 };
+
+/* Launch scratch the mxfp4a16 row needs at M rows: the e4m3 plane (rounded up to 256
+ * bytes) followed by the E8M0 plane. */
+int64_t mxfp4a16_scratch_bytes(int64_t M, int64_t K);
 
 /* Which kernel family an entry launches. */
 enum Arm { ARM_DECODE = 0, ARM_TILE = 1 };
@@ -42,7 +50,17 @@ struct DecodeGeom {
     int steps;               /* K / 128 */
 };
 
-/* Launch geometry of the prefill tile. */
+/* Launch geometry of the mxfp4 prefill GEMM (block-scaled MFMA, direct-to-LDS ring):
+ * a workgroup of 4 waves owns bn = 32 wnf weight rows x bm = 32 wmf tokens. */
+struct PrefillGeom {
+    int wnf, wmf, nst;       /* 16-row fragments per wave along N / M; ring depth */
+    int bn, bm;
+    int64_t grid_m, grid_n, tiles;
+    int steps;               /* K / 128 */
+    int lds;                 /* dynamic LDS bytes per workgroup */
+};
+
+/* Launch geometry of the fp8a8 prefill tile. */
 struct TileGeom {
     int bm, bn;              /* output tile of one workgroup */
     int64_t grid_m, grid_n;
@@ -56,16 +74,23 @@ int64_t row_stride(const RadTensor* t, int64_t cols);
  * pitches.  M must already be numel(Y)/N.  Returns RAD_OK or the refusal code. */
 int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P);
 int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P);
+/* The bf16-in mxfp4 row: A bf16 [M, K], a_scale absent, weights as mxfp4a8, and launch
+ * scratch of at least mxfp4a16_scratch_bytes(M, K), 16-byte aligned. */
+int plan_mxfp4a16(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P);
 
-/* The shared entry preamble: operands present, a_sum (and for fp8a8 b_ref) refused,
- * Y bf16 and inner-contiguous, N from the schema parameter, M = numel(Y)/N (never the
- * M parameter), and the band's own M bound when `m_max` > 0. */
+/* The shared entry preamble: operands present (a_scale except at mxfp4a16), a_sum (and
+ * for fp8a8 b_ref) refused, Y bf16 and inner-contiguous, N from the schema parameter,
+ * M = numel(Y)/N (never the M parameter), and the band's own M bound when `m_max` > 0. */
 int entry_preamble(const RadArgs* a, int enc, int64_t m_max, int64_t* M, int64_t* N);
 
 /* wave_lds: LDS bytes one wave needs (0 = unknown: assume it fits 8 waves per workgroup). */
 void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGeom* g,
                  int wave_lds = 0);
 void tile_geom(int64_t M, int64_t N, TileGeom* g);
+/* mode: 0 = e4m3 activations with f32 scale per 128 (mxfp4a8), 1 = mxfp8 (mxfp4a16);
+ * ncu: compute units the launch can fill (tiles are sized so the last round of
+ * workgroups is as full as possible). */
+void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeom* g);
 
 /* Environment levers, read once per process (function-local statics). */
 bool env_no_mxfp4();        /* R3D_NO_MXFP4: all mxfp4a8 rows */

@@ -8,6 +8,10 @@
  *   gemm_nt_q_mxfp4_decode   prio 1100  + M LE 16                         decode GEMV
  *   gemm_nt_q_fp8a8          prio 1000  dtype IN fp8a8, K DIV 128, group EQ 128
  *   gemm_nt_q_fp8a8_decode   prio 1100  + M LE 16
+ *   gemm_nt_q_mxfp4a16       prio 1000  dtype IN mxfp4a16, K DIV 128     bf16-in prefill
+ * gemm_nt_q_mxfp4a16 has no counterpart in the reference: it takes bf16 activations (no
+ * a_scale), quantises them to mxfp8 (e4m3 + E8M0 per 32 of K) in the launch scratch its
+ * hook sizes, and runs the prefill GEMM with both block scales inside the MFMA.
  * Deviations from the reference rows (src/r3d_rows.cpp:1601-1675): the decode bands
  * widen M <= 8 to M <= 16 (one MFMA covers 16 activation rows at the cost of one), and
  * the mxfp4 tile row adds K DIV 128 (the MFMA walks whole 128-wide steps; ragged K
@@ -15,7 +19,7 @@
  *
  * Kill switches act HERE, at registration (src/r3d_rows.cpp:2197-2236): an issue-time
  * refusal is an engine abort, so a lever hides rows and the band re-resolves.
- *   R3D_NO_MXFP4   hides both mxfp4a8 rows;  R3D_NO_FP4_DEC  the mxfp4a8 decode row;
+ *   R3D_NO_MXFP4   hides every mxfp4 row;    R3D_NO_FP4_DEC  the mxfp4a8 decode row;
  *   R3D_NO_FP8A8   hides both fp8a8 rows;    R3D_NO_FP8_DEC  the fp8a8 decode row.
  * Presence-tested (getenv != null), read once.  R3D_MXFP4_Q8X is accepted and inert:
  * this library has no repacked-plane arm for it to withdraw.
@@ -31,6 +35,8 @@ int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
+int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s);
+int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a);
 }
 
 namespace {
@@ -74,6 +80,10 @@ const RadConstraint cMxfp4Decode[] = {
     {"M", RAD_C_LE, 16, nullptr},
     {"K", RAD_C_DIV, 128, nullptr},
 };
+const RadConstraint cMxfp4A16[] = {
+    {"dtype", RAD_C_IN, 0, "mxfp4a16"},
+    {"K", RAD_C_DIV, 128, nullptr},
+};
 const RadConstraint cFp8Tile[] = {
     {"dtype", RAD_C_IN, 0, "fp8a8"},
     {"K", RAD_C_DIV, 128, nullptr},
@@ -98,11 +108,12 @@ const RadTunable tSplitK[] = {
 
 const RadKernelInfo kRows[] = {
     {"gemm_nt_q_mxfp4", "gemm_nt_q", "gemm",
-     "mxfp4a8 prefill tile on gfx950 block-scaled MFMA: 128x128 output tile per workgroup, "
-     "e2m1 weights with their E8M0 scales fed to v_mfma_scale_f32_16x16x128_f8f6f4 as is, "
-     "e4m3 activations, one MFMA per 128-of-K activation group scaled by a_scale in f32",
-     "K a multiple of 128; 16-byte aligned A/B bases and A pitch; ragged M/N tiles stage "
-     "zeros and are never stored; M derives from numel(y)/N",
+     "mxfp4a8 prefill GEMM on gfx950 block-scaled MFMA: up to 256 weight rows x 128 tokens "
+     "per workgroup, a three-deep direct-to-LDS ring, e2m1 weights with their E8M0 scales "
+     "fed to v_mfma_scale_f32_16x16x128_f8f6f4 as is, e4m3 activations, one MFMA per "
+     "128-of-K activation group scaled by a_scale in f32",
+     "K a multiple of 128; 16-byte aligned A/B bases and A pitch; ragged M/N tiles clamp "
+     "their loads and are never stored; M derives from numel(y)/N",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), e2m1 b with E8M0 b_scale per (row, 32 K), "
      "bf16 y; b_ref accepted and ignored; a_sum refused",
      RAD_DOMAIN_DEVICE, kPrioTile, cMxfp4Tile, 2, nullptr, 0, nullptr,
@@ -141,12 +152,27 @@ const RadKernelInfo kRows[] = {
      RAD_DOMAIN_DEVICE, kPrioDecode, cFp8Decode, 4, tSplitK, 1, nullptr,
      nullptr, nullptr, r3d_rad_gemm_nt_q_fp8_decode, nullptr, nullptr, nullptr, nullptr,
      nullptr},
+
+    {"gemm_nt_q_mxfp4a16", "gemm_nt_q", "gemm",
+     "mxfp4 prefill GEMM with bf16 activations on gfx950: the activations are quantised to "
+     "mxfp8 (e4m3 + E8M0 per 32 of K) into launch scratch, then both E8M0 planes ride in "
+     "v_mfma_scale_f32_16x16x128_f8f6f4, which accumulates in place; up to 256 x 256 "
+     "output tile per workgroup over a three-deep direct-to-LDS ring",
+     "K a multiple of 128; a_scale absent; launch scratch >= M*K (rounded to 256) + M*K/32 "
+     "bytes, 16-byte aligned (the row's scratch hook sizes it from M and K); A rows 16-byte "
+     "aligned; M derives from numel(y)/N",
+     "bf16 a, e2m1 b with E8M0 b_scale per (row, 32 K), bf16 y; b_ref accepted and ignored; "
+     "a_scale and a_sum refused",
+     RAD_DOMAIN_DEVICE, kPrioTile, cMxfp4A16, 2, nullptr, 0, nullptr,
+     nullptr, nullptr, r3d_rad_gemm_nt_q_mxfp4a16, r3d_rad_gemm_nt_q_mxfp4a16_scratch,
+     nullptr, nullptr, nullptr, nullptr},
 };
 
 bool row_hidden(const RadKernelInfo& k) {
     const bool no_mx = r3d::env_no_mxfp4(), no_mxd = r3d::env_no_fp4_dec();
     const bool no_f8 = r3d::env_no_fp8a8(), no_f8d = r3d::env_no_fp8_dec();
     if (!strcmp(k.name, "gemm_nt_q_mxfp4")) return no_mx;
+    if (!strcmp(k.name, "gemm_nt_q_mxfp4a16")) return no_mx;
     if (!strcmp(k.name, "gemm_nt_q_mxfp4_decode")) return no_mx || no_mxd;
     if (!strcmp(k.name, "gemm_nt_q_fp8a8")) return no_f8;
     if (!strcmp(k.name, "gemm_nt_q_fp8a8_decode")) return no_f8 || no_f8d;
@@ -162,7 +188,7 @@ uint32_t rad_plugin_abi_version(void) { return RAD_ABI_VERSION; }
 const RadPluginInfo* rad_plugin_info(void) {
     static const RadPluginInfo info = {
         RAD_PLUGIN_KERNEL, "libr3d_gfx950", "0.1.0",
-        "radiance gemm_nt_q rows (mxfp4a8, fp8a8) for AMD Instinct MI355X (CDNA4)",
+        "radiance gemm_nt_q rows (mxfp4a8, fp8a8, mxfp4a16) for AMD Instinct MI355X (CDNA4)",
         "gfx950",
     };
     return &info;

@@ -344,7 +344,7 @@ void r3d_ref_group8_mag(int enc, const uint8_t* A, int64_t a_pitch, const float*
                 double mx = 0.0;
                 for (int64_t k = k0; k < k0 + 8 && k < K; ++k) {
                     double w, sb;
-                    if (enc == 0) {
+                    if (enc != 1) {
                         const uint8_t byte = B[n * b_pitch + (k >> 1)];
                         const uint8_t nib = (k & 1) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 0xF);
                         w = r3d_ref_e2m1_to_f32(nib);
@@ -354,7 +354,7 @@ void r3d_ref_group8_mag(int enc, const uint8_t* A, int64_t a_pitch, const float*
                         sb = r3d_ref_bf16_to_f32(((const uint16_t*)BS)[(n / rblk) * bs_pitch + k / 128]);
                     }
                     const double t = fabs(r3d_ref_e4m3_to_f32(arow[k]) * w * sb *
-                                          AS[m * as_pitch + k / 128]);
+                                          AS[m * as_pitch + (enc == 2 ? k / 32 : k / 128)]);
                     if (t > mx) mx = t;           /* NaN never wins: the class check covers it */
                 }
                 tot += mx;

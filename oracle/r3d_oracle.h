@@ -95,7 +95,8 @@ void r3d_ref_dot_mx8_mxfp4(const uint8_t* A, int64_t a_pitch, const uint8_t* SX,
  * group's largest product and truncates bits below 2^-13 of it (measured on MI355X), so
  * a kernel built on it can differ from the exact product by up to 7 * 2^-13 of each
  * group's largest |a*b| * |sa| * |sb|.  S8[m, n] = sum over 8-groups of that maximum.
- * enc 0 = mxfp4a8 operands (BS E8M0), 1 = fp8a8 operands (BS bf16, rblk). */
+ * enc 0 = mxfp4a8 operands (BS E8M0), 1 = fp8a8 operands (BS bf16, rblk), 2 = mxfp4
+ * weights with activation scales per 32 of K (AS holds the decoded E8M0 values). */
 void r3d_ref_group8_mag(int enc, const uint8_t* A, int64_t a_pitch, const float* AS,
                         int64_t as_pitch, const uint8_t* B, int64_t b_pitch, const void* BS,
                         int64_t bs_pitch, int rblk, int64_t M, int64_t N, int64_t K,

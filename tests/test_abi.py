@@ -46,7 +46,7 @@ def test_plugin_identity_and_schema():
 def test_rows_and_resolver():
     rows = {r["name"]: r for r in R.rows()}
     assert set(rows) == {"gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", "gemm_nt_q_fp8a8",
-                         "gemm_nt_q_fp8a8_decode"}
+                         "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4a16"}
     assert rows["gemm_nt_q_mxfp4_decode"]["priority"] == 1100
     assert rows["gemm_nt_q_mxfp4"]["priority"] == 1000
     q = lambda **kw: R.resolve("gemm_nt_q", kw)["name"] if R.resolve("gemm_nt_q", kw) else None
@@ -71,15 +71,18 @@ print(json.dumps(sorted(r["name"] for r in R.rows())))
 """
 
 
+A16 = "gemm_nt_q_mxfp4a16"
+
+
 @pytest.mark.parametrize("env,expect", [
-    ({}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode"]),
+    ({}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16]),
     ({"R3D_NO_MXFP4": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode"]),
-    ({"R3D_NO_FP4_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4"]),
-    ({"R3D_NO_FP8A8": "1"}, ["gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode"]),
-    ({"R3D_NO_FP8_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode"]),
-    ({"R3D_NO_FP8_DEC": "", "R3D_NO_FP4_DEC": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4"]),
+    ({"R3D_NO_FP4_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", A16]),
+    ({"R3D_NO_FP8A8": "1"}, ["gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16]),
+    ({"R3D_NO_FP8_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16]),
+    ({"R3D_NO_FP8_DEC": "", "R3D_NO_FP4_DEC": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", A16]),
     ({"R3D_MXFP4_Q8X": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4",
-                              "gemm_nt_q_mxfp4_decode"]),
+                              "gemm_nt_q_mxfp4_decode", A16]),
     ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, []),
 ])
 def test_kill_switch_matrix(env, expect):
@@ -165,7 +168,7 @@ def test_decode_band_bound_and_tile_any_m():
     ops, _ = _mx_ops(M=17)
     assert R.describe("gemm_nt_q_mxfp4_decode", ops)[0] == R.RAD_E_UNSUPPORTED
     rc, d = R.describe("gemm_nt_q_mxfp4", ops)
-    assert rc == R.RAD_OK and _geom(d)["arm"] == "tile"
+    assert rc == R.RAD_OK and _geom(d)["arm"] == "prefill"
 
 
 def test_decode_geometry_policy():
@@ -254,3 +257,66 @@ def test_entries_refuse_without_gfx950():
         pytest.skip("a GPU is present")
     ops, _ = _mx_ops(M=1)
     assert R.launch_row("gemm_nt_q_mxfp4_decode", ops, 0) == R.RAD_E_UNSUPPORTED
+
+
+# ------------------------------------------------------------------ prefill plans
+def _a16_ops(M=64, N=256, K=256, scratch=True, with_as=False, **kw):
+    a = FakeT(_aligned((M, K), np.uint16))
+    s = FakeT(_aligned((M, K // 128), np.float32)) if with_as else None
+    b = FakeT(_aligned((N, K // 2), np.uint8))
+    bs = FakeT(_aligned((N, K // 32), np.uint8))
+    y = FakeT(_aligned((M, N), np.uint16))
+    kw.setdefault("extra_params", [("M", M)])
+    ops = R.GemmOperands(a, s, b, bs, y, dtype="mxfp4a16", N=N, K=K, group=32, **kw)
+    need = ((M * K + 255) // 256) * 256 + M * (K // 32)
+    sc = FakeT(_aligned((need + 64,), np.uint8))
+    if scratch:
+        ops.set_scratch(sc, need if scratch is True else scratch)
+    return ops, (a, s, b, bs, y, sc), need
+
+
+def test_prefill_tile_choice_fills_the_last_round():
+    # config 3: 96 x 8 = 768 tiles of 224 x 256 -- exactly three rounds of 256 CUs
+    ops, keep, need = _a16_ops(M=2048, N=21504, K=5376)
+    rc, d = R.describe("gemm_nt_q_mxfp4a16", ops)
+    assert rc == R.RAD_OK, d
+    g = _geom(d)
+    assert (g["arm"], g["bn"], g["bm"], g["tiles"], g["steps"]) == ("prefill", "224", "256", "768", "42")
+    assert int(g["lds"]) <= 160 * 1024
+    # the f32-a_scale mode keeps 128-token tiles
+    ops, _ = _mx_ops(M=2048, N=21504, K=5376)
+    g = _geom(R.describe("gemm_nt_q_mxfp4", ops)[1])
+    assert (g["bn"], g["bm"]) == ("224", "128")
+    # few tiles: the narrowest tile spreads the work over more CUs
+    ops, _ = _mx_ops(M=256, N=4096, K=1024)
+    g = _geom(R.describe("gemm_nt_q_mxfp4", ops)[1])
+    assert g["bn"] == "128", g
+
+
+def test_a16_scratch_hook_and_refusals():
+    ops, keep, need = _a16_ops()
+    assert R.row_scratch_bytes("gemm_nt_q_mxfp4a16", ops) == need
+    assert R.describe("gemm_nt_q_mxfp4a16", ops)[0] == R.RAD_OK
+    ops, keep, need = _a16_ops(scratch=False)
+    assert R.describe("gemm_nt_q_mxfp4a16", ops)[0] == R.RAD_E_UNSUPPORTED
+    ops, keep, need = _a16_ops(scratch=need - 1)
+    assert R.describe("gemm_nt_q_mxfp4a16", ops)[0] == R.RAD_E_UNSUPPORTED
+    ops, keep, need = _a16_ops(with_as=True)               # a_scale has no meaning here
+    assert R.describe("gemm_nt_q_mxfp4a16", ops)[0] == R.RAD_E_UNSUPPORTED
+    ops, keep, need = _a16_ops(K=320)                      # whole 128-wide steps only
+    assert R.describe("gemm_nt_q_mxfp4a16", ops)[0] != R.RAD_OK
+    # the a8 row refuses bf16 activations and the a16 row refuses e4m3 ones
+    ops, keep, need = _a16_ops()
+    ops.dtype = "mxfp4a8"
+    ops2, _ = _mx_ops(M=64, N=256, K=256)
+    ops2.set_scratch(keep[5], need)
+    assert R.describe("gemm_nt_q_mxfp4a16", ops2)[0] == R.RAD_E_UNSUPPORTED
+    # no M parameter: the hook has nothing to size
+    ops, keep, need = _a16_ops(extra_params=[])
+    assert R.row_scratch_bytes("gemm_nt_q_mxfp4a16", ops) == 0
+
+
+def test_resolver_routes_a16_to_its_row():
+    r = R.resolve("gemm_nt_q", {"dtype": "mxfp4a16", "M": 2048, "N": 21504, "K": 5376, "group": 32})
+    assert r["name"] == "gemm_nt_q_mxfp4a16"
+    assert R.resolve("gemm_nt_q", {"dtype": "mxfp4a16", "M": 4, "N": 64, "K": 320, "group": 32}) is None
