@@ -14,14 +14,29 @@
  *   PF_MX8 : e4m3 + one E8M0 per (token, 32 K) -- the mxfp8 activations of the bf16-in
  *            row.  Both scales ride in the MFMA, which accumulates in place.
  *
- * Staging: every byte a step needs arrives by direct global->LDS loads (16 bytes per lane
- * for the planes, 4 for the scales) into a three-deep ring, with one barrier per step.
- * Each 1 KB plane load fills exactly the LDS image of one MFMA operand fragment (lane l at
- * +16 l: 16 rows x 64 bytes of one step), so every fragment read is one contiguous
- * ds_read_b128 per lane, free of bank conflicts.  Weight rows past N and tokens past M
- * clamp to the last valid one; clamped lanes feed only outputs that are never stored.
- * Every load is unconditional (a step past the end reloads the last step into a ring slot
- * nobody reads), so the vmcnt bookkeeping is the same on every iteration.
+ * Staging: every byte a step needs arrives by buffer loads straight into LDS (16 bytes
+ * per lane for the planes, 4 for the scales) into a three-deep ring, with one barrier per
+ * step.  Each 1 KB plane load fills exactly the LDS image of one MFMA operand fragment
+ * (16 rows x 64 bytes of one step, four lanes per row, XOR-swizzled), so every fragment
+ * read is one ds_read_b128 per lane, free of bank conflicts.  Weight rows past N and
+ * tokens past M clamp to the last valid one; clamped lanes feed only outputs that are
+ * never stored.  Every load is unconditional (a step past the end reloads the last step
+ * into a ring slot nobody reads), so the vmcnt bookkeeping is the same on every step.
+ *
+ * Register pipeline: the activation fragments are read two groups ahead into a ring of
+ * four, and the weight fragments of step s + 1 are read -- right after step s's barrier,
+ * while its last two fragment groups issue -- into the second of three weight register
+ * sets.  The K loop is unrolled by three so every LDS ring slot and register set is named
+ * statically (immediate LDS offsets, no address arithmetic in the loop).
+ *
+ * The mxfp8 MFMAs are issued through inline assembly with the accumulator tied to its
+ * AGPRs ("+a"): it accumulates in place, and the register allocator cannot split the
+ * accumulators' live ranges into copy chains.  Because the compiler then does not see
+ * these MFMAs, each one carries its own s_nop 2 ahead of it (a VALU write of an operand
+ * VGPR needs two wait states before an MFMA reads it), and the accumulators are read
+ * after the loop only past 24 further wait states (an 8-pass MFMA result needs 11 before
+ * a VALU or v_accvgpr_read may read it).  Nothing else writes an accumulator, and each
+ * accumulator is rewritten only once per K step, dozens of MFMAs apart.
  */
 #ifndef R3D_PREFILL_H
 #define R3D_PREFILL_H
@@ -30,6 +45,34 @@
 #include "r3d_prefill_layout.h"
 
 namespace r3d {
+
+/* acc += A(16 x 128 fp4, E8M0 scale per lane) . B(16 x 128 fp8, E8M0 scale per lane)^T,
+ * in place in the accumulator's AGPRs (see the header comment for the hazard rules). */
+__device__ __forceinline__ void r3d_mfma_mx_inplace(r3d_f32x4& acc, r3d_i32x4 a, int sa,
+                                                    r3d_i32x8 b, int sb) {
+    asm("s_nop 2\n\tv_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4 blgp:0"
+        : "+a"(acc)
+        : "v"(a), "v"(b), "v"(sa), "v"(sb));
+}
+
+/* Buffer resource over [base, base + bytes) (raw, stride 0): loads past `bytes` read 0. */
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t r3d_rsrc(const void* base, int64_t bytes) {
+    const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+/* Buffer load of `bytes` (16 or 4) per lane straight into LDS at lds + lane * bytes. */
+template <int BYTES>
+__device__ __forceinline__ void r3d_buf_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff,
+                                            uint32_t soff) {
+    static_assert(BYTES == 16 || BYTES == 4, "dwordx4 or dword loads");
+    if constexpr (BYTES == 16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                                 voff, soff, 0, 0);
+    else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
+                                                 voff, soff, 0, 0);
+}
 
 template <int MODE, int WNF, int WMF>
 __global__ __launch_bounds__(256) void prefill_kernel(
@@ -55,23 +98,30 @@ __global__ __launch_bounds__(256) void prefill_kernel(
     const int tm = t % grid_m, tn = t / grid_m;
     const int64_t n0 = (int64_t)tn * L::BN, m0 = (int64_t)tm * L::BM;
 
-    /* ---- issue side.  Every source address is a wave-uniform tile base (advanced by one
-     * K step per stage) plus a per-lane 32-bit offset fixed over K, so each direct load
-     * is one VGPR offset on an SGPR base.  The host keeps 256 rows of any operand under
-     * 2^31 bytes. */
-    const uint8_t* const Bt = B + n0 * b_pitch;
-    const uint8_t* const BSt = BS + n0 * bs_pitch;
-    const uint8_t* const At = A + m0 * a_pitch;
+    /* ---- issue side: one buffer resource per operand, based at this tile's first row and
+     * bounded by the operand's end; per-lane 32-bit offsets fixed over K; the K step
+     * rides in the scalar offset.  The host keeps 256 rows of any operand under 2^31
+     * bytes. */
     const int64_t xs_pitch = MODE == PF_MX8 ? as_pitch : 4 * as_pitch;     /* bytes */
-    const uint8_t* const Xt = reinterpret_cast<const uint8_t*>(ASv) + m0 * xs_pitch;
+    const __amdgpu_buffer_rsrc_t rB = r3d_rsrc(B + n0 * b_pitch, (N - n0) * b_pitch);
+    const __amdgpu_buffer_rsrc_t rS = r3d_rsrc(BS + n0 * bs_pitch, (N - n0) * bs_pitch);
+    const __amdgpu_buffer_rsrc_t rA = r3d_rsrc(A + m0 * a_pitch, (M - m0) * a_pitch);
+    const __amdgpu_buffer_rsrc_t rX =
+        r3d_rsrc(reinterpret_cast<const uint8_t*>(ASv) + m0 * xs_pitch, (M - m0) * xs_pitch);
+    /* A plane load covers 16 rows x 64 bytes with four consecutive lanes on each row
+     * (lane l: row l / 4), so every row is one 64-byte run; chunk l % 4 of the run is
+     * fetched XOR-swizzled by (row / 4) % 4, which places the MFMA operand reads (row li,
+     * chunk q: position 4 li + (q ^ (li / 4) % 4)) on 16 distinct bank groups. */
+    const int lr = lane >> 2;                                /* row of this lane's load */
+    const int lc = (lane & 3) ^ ((lr >> 2) & 3);             /* chunk it fetches */
     uint32_t woff[L::WLD];
 #pragma unroll
     for (int i = 0; i < L::WLD; ++i) {
         const int f = wave + 4 * i;
         const int fr = f < L::WFR ? f : L::WFR - 1;         /* pad slots reload the last */
-        int64_t n = n0 + 16 * fr + li;
+        int64_t n = n0 + 16 * fr + lr;
         if (n > N - 1) n = N - 1;
-        woff[i] = (uint32_t)((n - n0) * b_pitch + 16 * q);
+        woff[i] = (uint32_t)((n - n0) * b_pitch + 16 * lc);
     }
     uint32_t soff;
     {
@@ -84,9 +134,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(
 #pragma unroll
     for (int i = 0; i < L::ALD; ++i) {
         const int j = wave + 4 * i;                          /* fragment j/2, half j%2 */
-        int64_t m = m0 + 16 * (j >> 1) + li;
+        int64_t m = m0 + 16 * (j >> 1) + lr;
         if (m > M - 1) m = M - 1;
-        aoff[i] = (uint32_t)((m - m0) * a_pitch + 64 * (j & 1) + 16 * q);
+        aoff[i] = (uint32_t)((m - m0) * a_pitch + 64 * (j & 1) + 16 * lc);
     }
     uint32_t xoff;
     {
@@ -100,14 +150,14 @@ __global__ __launch_bounds__(256) void prefill_kernel(
      * weight-scale dwords, activation half-fragments, the activation-scale dwords. */
     auto load = [&](int k, int s, uint8_t* st) {
         if (k < L::WLD) {
-            r3d_lds_load(Bt + 64 * (int64_t)s + woff[k], st + L::W + 1024 * (wave + 4 * k), 16);
+            r3d_buf_lds<16>(rB, st + L::W + 1024 * (wave + 4 * k), woff[k], 64 * s);
         } else if (k == L::WLD) {
-            r3d_lds_load(BSt + 4 * (int64_t)s + soff, st + L::S + 256 * wave, 4);
+            r3d_buf_lds<4>(rS, st + L::S + 256 * wave, soff, 4 * s);
         } else if (k < L::WLD + 1 + L::ALD) {
             const int i = k - L::WLD - 1;
-            r3d_lds_load(At + 128 * (int64_t)s + aoff[i], st + L::A + 1024 * (wave + 4 * i), 16);
+            r3d_buf_lds<16>(rA, st + L::A + 1024 * (wave + 4 * i), aoff[i], 128 * s);
         } else {
-            r3d_lds_load(Xt + 4 * (int64_t)s + xoff, st + L::AS + 256 * wave, 4);
+            r3d_buf_lds<4>(rX, st + L::AS + 256 * wave, xoff, 4 * s);
         }
     };
     /* the loads of one stage, spread over the first WMF - 2 fragment groups of a step */
@@ -119,9 +169,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(
             if (k < L::LOADS) load(k, s, st);
     };
 
-    /* ---- consume side: wave (wn, wm) owns WNF weight fragments x WMF token fragments.
-     * Registers: two sets of weight fragments (this step's and the next's) and a ring of
-     * four activation fragments, read two groups ahead. */
+    /* ---- consume side: wave (wn, wm) owns WNF weight fragments x WMF token fragments */
     const int wn = wave & 1, wm = wave >> 1;
     r3d_f32x4 acc[WNF][WMF];
 #pragma unroll
@@ -129,8 +177,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(
 #pragma unroll
         for (int b = 0; b < WMF; ++b) acc[a][b] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    r3d_i32x4 wA[WNF], wB[WNF];
-    int xA[WNF], xB[WNF];
+    r3d_i32x4 wS[3][WNF];
+    int xS[3][WNF];
     r3d_i32x8 ar[4];
     int ax[4];
     float af[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -142,51 +190,55 @@ __global__ __launch_bounds__(256) void prefill_kernel(
 #pragma unroll
         for (int a = 0; a < WNF; ++a) dq[b][a] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto read_w = [&](const uint8_t* st, r3d_i32x4 (&w)[WNF], int (&xs)[WNF]) {
+    /* this lane's operand chunk (row li, chunk q) inside any 1 KB fragment image */
+    const int rd = 16 * (4 * li + (q ^ ((li >> 2) & 3)));
+    auto read_w = [&](const uint8_t* st, int set) {
 #pragma unroll
         for (int ni = 0; ni < WNF; ++ni) {
             const int f = wn * WNF + ni;
-            w[ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 1024 * f + 16 * lane);
-            xs[ni] = st[L::S + 4 * (16 * f + li) + q];
+            wS[set][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 1024 * f + rd);
+            xS[set][ni] = st[L::S + 4 * (16 * f + li) + q];
         }
     };
     auto read_a = [&](const uint8_t* st, int mi) {
         const int g = wm * WMF + mi, slot = mi & 3;
-        const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(st + L::A + 2048 * g + 16 * lane);
-        const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(st + L::A + 2048 * g + 1024 + 16 * lane);
+        const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(st + L::A + 2048 * g + rd);
+        const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(st + L::A + 2048 * g + 1024 + rd);
         ar[slot] = r3d_i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         if (MODE == PF_MX8)
             ax[slot] = st[L::AS + 4 * (16 * g + li) + q];
         else
             af[slot] = *reinterpret_cast<const float*>(st + L::AS + 4 * (16 * g + li));
     };
-    auto group = [&](int mi, const r3d_i32x4 (&w)[WNF], const int (&xs)[WNF]) {
+    auto group = [&](int mi, int set) {
         const int slot = mi & 3;
         if (MODE == PF_MX8) {
 #pragma unroll
             for (int ni = 0; ni < WNF; ++ni)
-                acc[ni][mi] = r3d_mfma_fp4_fp8_acc(w[ni], xs[ni], ar[slot], ax[slot], acc[ni][mi]);
+                r3d_mfma_mx_inplace(acc[ni][mi], wS[set][ni], xS[set][ni], ar[slot], ax[slot]);
         } else {
             const int pm = mi == 0 ? WMF - 1 : mi - 1;         /* the group flushed now */
             const float sp = af[(mi + 3) & 3];
 #pragma unroll
             for (int ni = 0; ni < WNF; ++ni) {
-                dq[mi & 1][ni] = r3d_mfma_fp4_fp8(w[ni], xs[ni], ar[slot], R3D_E8M0_ONE);
+                dq[mi & 1][ni] = r3d_mfma_fp4_fp8(wS[set][ni], xS[set][ni], ar[slot], R3D_E8M0_ONE);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     acc[ni][pm][i] = acc[ni][pm][i] + dq[(mi + 1) & 1][ni][i] * sp;
             }
         }
     };
-    /* One K step: stage s from ring slot cur, stage s + 2 loaded into slot fill, and --
-     * after the step's barrier -- the first fragments of stage s + 1 read from slot nxt. */
-    auto step = [&](int s, const uint8_t* cur, uint8_t* fill, const uint8_t* nxt,
-                    const r3d_i32x4 (&wc)[WNF], const int (&xc)[WNF],
-                    r3d_i32x4 (&wnx)[WNF], int (&xnx)[WNF]) {
+    /* One K step from ring slot `sl` (stage s): stage s + 2 is loaded into slot sl + 2,
+     * and after the step's barrier the first fragments of stage s + 1 are read from slot
+     * sl + 1 into weight set sl + 1. */
+    auto step = [&](int s, int sl) {
+        uint8_t* const cur = smem + sl * L::STAGE;
+        uint8_t* const nxt = smem + (sl == 2 ? 0 : sl + 1) * L::STAGE;
+        uint8_t* const fill = smem + (sl == 0 ? 2 : sl - 1) * L::STAGE;
         const int sf = s + 2 < steps ? s + 2 : steps - 1;
 #pragma unroll
         for (int mi = 0; mi < WMF; ++mi) {
-            group(mi, wc, xc);
+            group(mi, sl);
             if (mi + 2 < WMF) {
                 read_a(cur, mi + 2);
                 issue_part(mi, sf, fill);
@@ -194,40 +246,43 @@ __global__ __launch_bounds__(256) void prefill_kernel(
                 /* every read of stage s is issued and stage s + 2 is in flight: wait for
                  * this wave's reads and for stage s + 1, then meet the other waves */
                 asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(L::LOADS) : "memory");
-                read_w(nxt, wnx, xnx);
+                read_w(nxt, sl == 2 ? 0 : sl + 1);
                 read_a(nxt, 0);
             } else {
                 read_a(nxt, 1);
             }
+            /* keep each group's reads and loads beside its own MFMAs */
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    /* ---- K walk */
-    uint8_t* const st0 = smem;
-    uint8_t* const st1 = smem + L::STAGE;
-    uint8_t* const st2 = smem + 2 * L::STAGE;
+    /* ---- K walk: stage s lives in ring slot s % 3 and weight set s % 3 */
 #pragma unroll
-    for (int k = 0; k < L::LOADS; ++k) load(k, 0, st0);
+    for (int k = 0; k < L::LOADS; ++k) load(k, 0, smem);
 #pragma unroll
-    for (int k = 0; k < L::LOADS; ++k) load(k, steps > 1 ? 1 : 0, st1);
+    for (int k = 0; k < L::LOADS; ++k) load(k, steps > 1 ? 1 : 0, smem + L::STAGE);
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(L::LOADS) : "memory");
-    read_w(st0, wA, xA);
-    read_a(st0, 0);
-    read_a(st0, 1);
-    /* ring slots rotate 0 -> 1 -> 2 (stage s lives in slot s % 3); weight registers
-     * alternate A / B, so the loop body is two steps */
-    uint8_t* cur = st0;
-    uint8_t* nxt = st1;
-    uint8_t* fill = st2;
-    for (int s = 0; s < steps; ++s) {
-        step(s, cur, fill, nxt, wA, xA, wB, xB);
-        uint8_t* t0 = cur; cur = nxt; nxt = fill; fill = t0;
-#pragma unroll
-        for (int ni = 0; ni < WNF; ++ni) { wA[ni] = wB[ni]; xA[ni] = xB[ni]; }
+    read_w(smem, 0);
+    read_a(smem, 0);
+    read_a(smem, 1);
+    int s = 0;
+    for (; s + 3 <= steps; s += 3) {
+        step(s, 0);
+        step(s + 1, 1);
+        step(s + 2, 2);
     }
+    if (s < steps) step(s, 0);
+    if (s + 1 < steps) step(s + 1, 1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* drain the tail reloads */
-    if (MODE == PF_A8) {
+    if (MODE == PF_MX8) {
+        /* 24 wait states between the last in-place MFMA and any read of an accumulator;
+         * the empty statements order every read after them */
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+        for (int a = 0; a < WNF; ++a)
+#pragma unroll
+            for (int b = 0; b < WMF; ++b) asm volatile("" : "+a"(acc[a][b]));
+    } else {
         /* the last group's results */
         const float sp = af[(WMF - 1) & 3];
 #pragma unroll
@@ -237,26 +292,39 @@ __global__ __launch_bounds__(256) void prefill_kernel(
                 acc[ni][WMF - 1][i] = acc[ni][WMF - 1][i] + dq[(WMF - 1) & 1][ni][i] * sp;
     }
 
-    /* ---- epilogue: lane holds Y[m0 + 16 g + li][n0 + 16 f + 4 q + i], i = 0..3 */
-    const bool vec = ((uintptr_t)Y & 7) == 0 && (y_pitch & 3) == 0;
+    /* ---- epilogue: lane holds Y[m0 + 16 g + li][n0 + 16 f + 4 q + i], i = 0..3.  The bf16
+     * tile is staged through the (now idle) LDS ring and leaves as whole 16-byte row chunks,
+     * so every store instruction writes full contiguous row segments. */
+    constexpr int YP = 2 * L::BN + 16;                 /* LDS row pitch, bytes (padded) */
+    constexpr int CPR = L::BN / 8;                     /* 16-byte chunks per tile row */
+    static_assert(L::BM * YP <= L::LDS, "the output tile fits the ring");
+    __syncthreads();                                   /* every wave is done with the ring */
 #pragma unroll
     for (int ni = 0; ni < WNF; ++ni)
 #pragma unroll
         for (int mi = 0; mi < WMF; ++mi) {
-            const int64_t m = m0 + 16 * (wm * WMF + mi) + li;
-            const int64_t n = n0 + 16 * (wn * WNF + ni) + 4 * q;
-            if (m >= M || n >= N) continue;
-            uint16_t* yp = Y + m * y_pitch + n;
+            const int ml = 16 * (wm * WMF + mi) + li;
+            const int nl = 16 * (wn * WNF + ni) + 4 * q;
             const r3d_f32x4 v = acc[ni][mi];
-            if (vec && n + 3 < N) {
-                const uint32_t lo = (uint32_t)r3d_bf16_rne(v[0]) | ((uint32_t)r3d_bf16_rne(v[1]) << 16);
-                const uint32_t hi = (uint32_t)r3d_bf16_rne(v[2]) | ((uint32_t)r3d_bf16_rne(v[3]) << 16);
-                *reinterpret_cast<uint2*>(yp) = make_uint2(lo, hi);
-            } else {
-                for (int i = 0; i < 4; ++i)
-                    if (n + i < N) yp[i] = r3d_bf16_rne(v[i]);
-            }
+            *reinterpret_cast<uint2*>(smem + ml * YP + 2 * nl) =
+                make_uint2(r3d_pack_bf16x2(v[0], v[1]), r3d_pack_bf16x2(v[2], v[3]));
         }
+    __syncthreads();
+    const bool vec = ((uintptr_t)Y & 15) == 0 && (y_pitch & 7) == 0;
+    for (int e = threadIdx.x; e < L::BM * CPR; e += 256) {
+        const int r = e / CPR, c = e - (e / CPR) * CPR;
+        const int64_t m = m0 + r, n = n0 + 8 * c;
+        if (m >= M || n >= N) continue;
+        const r3d_i32x4 v = *reinterpret_cast<const r3d_i32x4*>(smem + r * YP + 16 * c);
+        uint16_t* yp = Y + m * y_pitch + n;
+        if (vec && n + 8 <= N) {
+            *reinterpret_cast<r3d_i32x4*>(yp) = v;
+        } else {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+            for (int i = 0; i < 8; ++i)
+                if (n + i < N) yp[i] = h[i];
+        }
+    }
 }
 
 /* ------------------------------------------------------------ mxfp8 quantiser -------
