@@ -138,7 +138,7 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
     if (256 * a_pitch >= lim || 256 * P.b_pitch >= lim || 256 * P.bs_pitch >= lim ||
         256 * (mode == PF_MX8 ? as_pitch : 4 * as_pitch) >= lim)
         return RAD_E_UNSUPPORTED;
-    const dim3 grid((unsigned)g.tiles), block(256);
+    const dim3 grid((unsigned)g.tiles), block(512);
 #define R3D_PF(MODE_, WNF_, WMF_)                                                          \
     static_assert(PrefillLayout<WNF_, WMF_, 3>::LDS == 3 * prefill_stage_bytes(WNF_, WMF_), \
                   "host and kernel ring sizes differ");                                    \
@@ -149,17 +149,17 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
                        P.bs_pitch, P.y_pitch)
     if (mode == PF_MX8) {
         switch (g.wnf) {
-            case 8: R3D_PF(PF_MX8, 8, 8); break;
-            case 7: R3D_PF(PF_MX8, 7, 8); break;
-            case 6: R3D_PF(PF_MX8, 6, 8); break;
-            default: R3D_PF(PF_MX8, 4, 8); break;
+            case 8: R3D_PF(PF_MX8, 8, 4); break;
+            case 7: R3D_PF(PF_MX8, 7, 4); break;
+            case 6: R3D_PF(PF_MX8, 6, 4); break;
+            default: R3D_PF(PF_MX8, 4, 4); break;
         }
     } else {
         switch (g.wnf) {
-            case 8: R3D_PF(PF_A8, 8, 4); break;
-            case 7: R3D_PF(PF_A8, 7, 4); break;
-            case 6: R3D_PF(PF_A8, 6, 4); break;
-            default: R3D_PF(PF_A8, 4, 4); break;
+            case 8: R3D_PF(PF_A8, 8, 2); break;
+            case 7: R3D_PF(PF_A8, 7, 2); break;
+            case 6: R3D_PF(PF_A8, 6, 2); break;
+            default: R3D_PF(PF_A8, 4, 2); break;
         }
     }
 #undef R3D_PF

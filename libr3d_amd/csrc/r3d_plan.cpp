@@ -300,27 +300,27 @@ void tile_geom(int64_t M, int64_t N, TileGeom* g) {
     g->grid_n = (N + g->bn - 1) / g->bn;
 }
 
-/* Prefill tile choice: 32 wmf tokens (8 fragments in mxfp8 mode, where the MFMA
- * accumulates in place; 4 in the f32-a_scale mode, whose per-step flush needs a second
- * register set) by 32 wnf weight rows.  Workgroups run one per CU, so the launch takes
- * ceil(tiles / ncu) rounds; a round costs about wnf + 1/2 fragment-steps (the fixed
- * activation reads of a step).  The cheapest total wins, ties to the larger tile. */
+/* Prefill tile choice: 64 wmw tokens (4 fragments per wave in mxfp8 mode, where the
+ * MFMA accumulates in place; 2 in the f32-a_scale mode, whose per-step flush needs a
+ * second register set) by 32 wnf weight rows.  Workgroups run one per CU, so the launch
+ * takes ceil(tiles / ncu) rounds; a round costs about wnf + 1/2 fragment-steps (the
+ * fixed activation reads of a step).  The cheapest total wins, ties to the larger tile. */
 void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeom* g) {
     static const int kWnf[] = {8, 7, 6, 4};
-    const int wmf = mode == PF_MX8 ? 8 : 4;
+    const int wmw = mode == PF_MX8 ? 4 : 2;
     if (ncu <= 0) ncu = 256;
     int best = 8;
     double best_cost = 0.0;
     for (int w : kWnf) {
-        const int64_t tiles = ((N + 32 * w - 1) / (32 * w)) * ((M + 32 * wmf - 1) / (32 * wmf));
+        const int64_t tiles = ((N + 32 * w - 1) / (32 * w)) * ((M + 64 * wmw - 1) / (64 * wmw));
         const double cost = (double)((tiles + ncu - 1) / ncu) * (w + 0.5);
         if (w == 8 || cost < best_cost) { best = w; best_cost = cost; }
     }
     g->wnf = best;
-    g->wmf = wmf;
+    g->wmf = wmw;
     g->nst = 3;
     g->bn = 32 * best;
-    g->bm = 32 * wmf;
+    g->bm = 64 * wmw;
     g->grid_m = (M + g->bm - 1) / g->bm;
     g->grid_n = (N + g->bn - 1) / g->bn;
     g->tiles = g->grid_m * g->grid_n;

@@ -51,7 +51,7 @@ struct DecodeGeom {
 };
 
 /* Launch geometry of the mxfp4 prefill GEMM (block-scaled MFMA, direct-to-LDS ring):
- * a workgroup of 4 waves owns bn = 32 wnf weight rows x bm = 32 wmf tokens. */
+ * a workgroup of 8 waves (2 x 4) owns bn = 32 wnf weight rows x bm = 64 wmf tokens. */
 struct PrefillGeom {
     int wnf, wmf, nst;       /* 16-row fragments per wave along N / M; ring depth */
     int bn, bm;

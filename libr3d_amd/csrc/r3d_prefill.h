@@ -16,18 +16,17 @@
  *
  * Staging: every byte a step needs arrives by buffer loads straight into LDS (16 bytes
  * per lane for the planes, 4 for the scales) into a three-deep ring, with one barrier per
- * step.  Each 1 KB plane load fills exactly the LDS image of one MFMA operand fragment
+ * step; a stage is loaded the moment its slot frees, two steps ahead of its use.  Each 1 KB plane load fills exactly the LDS image of one MFMA operand fragment
  * (16 rows x 64 bytes of one step, four lanes per row, XOR-swizzled), so every fragment
  * read is one ds_read_b128 per lane, free of bank conflicts.  Weight rows past N and
  * tokens past M clamp to the last valid one; clamped lanes feed only outputs that are
  * never stored.  Every load is unconditional (a step past the end reloads the last step
  * into a ring slot nobody reads), so the vmcnt bookkeeping is the same on every step.
  *
- * Register pipeline: the activation fragments are read two groups ahead into a ring of
- * four, and the weight fragments of step s + 1 are read -- right after step s's barrier,
- * while its last two fragment groups issue -- into the second of three weight register
- * sets.  The K loop is unrolled by three so every LDS ring slot and register set is named
- * statically (immediate LDS offsets, no address arithmetic in the loop).
+ * Register pipeline: activation fragments are read two groups ahead into a ring of four;
+ * the weight fragments of step s + 1 are read into the second of two weight sets right
+ * after step s's barrier (two groups before its end), which also releases the ring slot
+ * just consumed for the load of stage s + 3.
  *
  * The mxfp8 MFMAs are issued through inline assembly with the accumulator tied to its
  * AGPRs ("+a"): it accumulates in place, and the register allocator cannot split the
@@ -74,19 +73,18 @@ __device__ __forceinline__ void r3d_buf_lds(__amdgpu_buffer_rsrc_t r, uint8_t* l
                                                  voff, soff, 0, 0);
 }
 
-template <int MODE, int WNF, int WMF>
-__global__ __launch_bounds__(256) void prefill_kernel(
+template <int MODE, int WNF, int WMW>
+__global__ __launch_bounds__(512) void prefill_kernel(
     const uint8_t* __restrict__ A, const void* __restrict__ ASv,
     const uint8_t* __restrict__ B, const uint8_t* __restrict__ BS,
     uint16_t* __restrict__ Y,
     int M, int N, int steps, int grid_m, int tiles,
     int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch) {
-    using L = PrefillLayout<WNF, WMF, 3>;
-    static_assert(WMF % 4 == 0, "activation fragments rotate through four register slots");
+    using L = PrefillLayout<WNF, WMW, 3>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     /* 0 .. 7 */
     const int li = lane & 15, q = lane >> 4;
 
     /* Workgroups go round-robin over the 8 XCDs; give each XCD a contiguous run of tiles,
@@ -104,84 +102,86 @@ __global__ __launch_bounds__(256) void prefill_kernel(
      * bytes. */
     const int64_t xs_pitch = MODE == PF_MX8 ? as_pitch : 4 * as_pitch;     /* bytes */
     const __amdgpu_buffer_rsrc_t rB = r3d_rsrc(B + n0 * b_pitch, (N - n0) * b_pitch);
-    const __amdgpu_buffer_rsrc_t rS = r3d_rsrc(BS + n0 * bs_pitch, (N - n0) * bs_pitch);
     const __amdgpu_buffer_rsrc_t rA = r3d_rsrc(A + m0 * a_pitch, (M - m0) * a_pitch);
-    const __amdgpu_buffer_rsrc_t rX =
-        r3d_rsrc(reinterpret_cast<const uint8_t*>(ASv) + m0 * xs_pitch, (M - m0) * xs_pitch);
+    /* scales: waves 0-3 fetch the weight rows' E8M0 dwords, waves 4-7 the tokens' */
+    const bool wsc = wave < 4;
+    const __amdgpu_buffer_rsrc_t rSX =
+        wsc ? r3d_rsrc(BS + n0 * bs_pitch, (N - n0) * bs_pitch)
+            : r3d_rsrc(reinterpret_cast<const uint8_t*>(ASv) + m0 * xs_pitch, (M - m0) * xs_pitch);
     /* A plane load covers 16 rows x 64 bytes with four consecutive lanes on each row
      * (lane l: row l / 4), so every row is one 64-byte run; chunk l % 4 of the run is
-     * fetched XOR-swizzled by (row / 4) % 4, which places the MFMA operand reads (row li,
-     * chunk q: position 4 li + (q ^ (li / 4) % 4)) on 16 distinct bank groups. */
+     * fetched XOR-swizzled by (row / 2) % 4.  An MFMA operand read (row li, chunk q) then
+     * sits at 16-byte position 4 li + (q ^ (li / 2) % 4), and any 8 consecutive lanes --
+     * one 128-byte LDS cycle of a ds_read_b128 -- hit 8 distinct bank groups. */
     const int lr = lane >> 2;                                /* row of this lane's load */
-    const int lc = (lane & 3) ^ ((lr >> 2) & 3);             /* chunk it fetches */
+    const int lc = (lane & 3) ^ ((lr >> 1) & 3);             /* chunk it fetches */
     uint32_t woff[L::WLD];
 #pragma unroll
     for (int i = 0; i < L::WLD; ++i) {
-        const int f = wave + 4 * i;
+        const int f = wave + 8 * i;
         const int fr = f < L::WFR ? f : L::WFR - 1;         /* pad slots reload the last */
         int64_t n = n0 + 16 * fr + lr;
         if (n > N - 1) n = N - 1;
         woff[i] = (uint32_t)((n - n0) * b_pitch + 16 * lc);
     }
-    uint32_t soff;
+    uint32_t sxoff;
     {
-        const int r = 64 * wave + lane < L::BN ? 64 * wave + lane : L::BN - 1;
-        int64_t n = n0 + r;
-        if (n > N - 1) n = N - 1;
-        soff = (uint32_t)((n - n0) * bs_pitch);
+        const int r0 = 64 * (wave & 3) + lane;
+        if (wsc) {
+            int64_t n = n0 + (r0 < L::BN ? r0 : L::BN - 1);
+            if (n > N - 1) n = N - 1;
+            sxoff = (uint32_t)((n - n0) * bs_pitch);
+        } else {
+            int64_t m = m0 + (r0 < L::BM ? r0 : L::BM - 1);
+            if (m > M - 1) m = M - 1;
+            sxoff = (uint32_t)((m - m0) * xs_pitch);
+        }
     }
+    const int sxdst = (wsc ? L::S : L::AS) + 256 * (wave & 3);
     uint32_t aoff[L::ALD];
 #pragma unroll
     for (int i = 0; i < L::ALD; ++i) {
-        const int j = wave + 4 * i;                          /* fragment j/2, half j%2 */
+        const int j = wave + 8 * i;                          /* fragment j/2, half j%2 */
         int64_t m = m0 + 16 * (j >> 1) + lr;
         if (m > M - 1) m = M - 1;
         aoff[i] = (uint32_t)((m - m0) * a_pitch + 64 * (j & 1) + 16 * lc);
     }
-    uint32_t xoff;
-    {
-        const int r = 64 * wave + lane < L::BM ? 64 * wave + lane : L::BM - 1;
-        int64_t m = m0 + r;
-        if (m > M - 1) m = M - 1;
-        xoff = (uint32_t)((m - m0) * xs_pitch);
-    }
-
-    /* Direct load k (0 .. LOADS-1) of stage s into ring slot st: weight fragments, the
-     * weight-scale dwords, activation half-fragments, the activation-scale dwords. */
+    /* load k (0 .. LOADS-1) of stage s into ring slot st */
     auto load = [&](int k, int s, uint8_t* st) {
-        if (k < L::WLD) {
-            r3d_buf_lds<16>(rB, st + L::W + 1024 * (wave + 4 * k), woff[k], 64 * s);
-        } else if (k == L::WLD) {
-            r3d_buf_lds<4>(rS, st + L::S + 256 * wave, soff, 4 * s);
-        } else if (k < L::WLD + 1 + L::ALD) {
-            const int i = k - L::WLD - 1;
-            r3d_buf_lds<16>(rA, st + L::A + 1024 * (wave + 4 * i), aoff[i], 128 * s);
-        } else {
-            r3d_buf_lds<4>(rX, st + L::AS + 256 * wave, xoff, 4 * s);
-        }
+        if (k < L::WLD)
+            r3d_buf_lds<16>(rB, st + L::W + 1024 * (wave + 8 * k), woff[k], 64 * s);
+        else if (k == L::WLD)
+            r3d_buf_lds<4>(rSX, st + sxdst, sxoff, 4 * s);
+        else
+            r3d_buf_lds<16>(rA, st + L::A + 1024 * (wave + 8 * (k - L::WLD - 1)),
+                            aoff[k - L::WLD - 1], 128 * s);
     };
-    /* the loads of one stage, spread over the first WMF - 2 fragment groups of a step */
-    constexpr int kParts = WMF - 2;
-    constexpr int kPer = (L::LOADS + kParts - 1) / kParts;
+    /* a stage's loads go out in WMW parts, one per fragment group, so the load issue
+     * never stalls a wave for a whole stage at once */
+    constexpr int kPer = (L::LOADS + WMW - 1) / WMW;
     auto issue_part = [&](int part, int s, uint8_t* st) {
+        const int sc = s < steps ? s : steps - 1;
 #pragma unroll
         for (int k = part * kPer; k < (part + 1) * kPer; ++k)
-            if (k < L::LOADS) load(k, s, st);
+            if (k < L::LOADS) load(k, sc, st);
     };
 
-    /* ---- consume side: wave (wn, wm) owns WNF weight fragments x WMF token fragments */
+    /* ---- consume side: wave (wn, wm) owns WNF weight fragments x WMW token fragments.
+     * Two weight sets (this step's and the next's) and a ring of four activation
+     * fragments read two groups ahead. */
     const int wn = wave & 1, wm = wave >> 1;
-    r3d_f32x4 acc[WNF][WMF];
+    r3d_f32x4 acc[WNF][WMW];
 #pragma unroll
     for (int a = 0; a < WNF; ++a)
 #pragma unroll
-        for (int b = 0; b < WMF; ++b) acc[a][b] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int b = 0; b < WMW; ++b) acc[a][b] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    r3d_i32x4 wS[3][WNF];
-    int xS[3][WNF];
+    r3d_i32x4 wS[2][WNF];
+    int xS[2][WNF];
     r3d_i32x8 ar[4];
     int ax[4];
     float af[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float sprev = 0.0f;
     /* PF_A8: the MFMA results of the previous group, scaled and added one group later so
      * the VALU never waits on a result that is still in the matrix pipe */
     r3d_f32x4 dq[2][WNF];
@@ -191,7 +191,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(
         for (int a = 0; a < WNF; ++a) dq[b][a] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     /* this lane's operand chunk (row li, chunk q) inside any 1 KB fragment image */
-    const int rd = 16 * (4 * li + (q ^ ((li >> 2) & 3)));
+    const int rd = 16 * (4 * li + (q ^ ((li >> 1) & 3)));
     auto read_w = [&](const uint8_t* st, int set) {
 #pragma unroll
         for (int ni = 0; ni < WNF; ++ni) {
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(
         }
     };
     auto read_a = [&](const uint8_t* st, int mi) {
-        const int g = wm * WMF + mi, slot = mi & 3;
+        const int g = wm * WMW + mi, slot = mi & 3;
         const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(st + L::A + 2048 * g + rd);
         const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(st + L::A + 2048 * g + 1024 + rd);
         ar[slot] = r3d_i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -217,38 +217,38 @@ __global__ __launch_bounds__(256) void prefill_kernel(
             for (int ni = 0; ni < WNF; ++ni)
                 r3d_mfma_mx_inplace(acc[ni][mi], wS[set][ni], xS[set][ni], ar[slot], ax[slot]);
         } else {
-            const int pm = mi == 0 ? WMF - 1 : mi - 1;         /* the group flushed now */
-            const float sp = af[(mi + 3) & 3];
+            const int pm = mi == 0 ? WMW - 1 : mi - 1;         /* the group flushed now */
 #pragma unroll
             for (int ni = 0; ni < WNF; ++ni) {
                 dq[mi & 1][ni] = r3d_mfma_fp4_fp8(wS[set][ni], xS[set][ni], ar[slot], R3D_E8M0_ONE);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[ni][pm][i] = acc[ni][pm][i] + dq[(mi + 1) & 1][ni][i] * sp;
+                    acc[ni][pm][i] = acc[ni][pm][i] + dq[(mi + 1) & 1][ni][i] * sprev;
             }
+            sprev = af[slot];        /* this group's scale, kept past the slot's refill */
         }
     };
-    /* One K step from ring slot `sl` (stage s): stage s + 2 is loaded into slot sl + 2,
-     * and after the step's barrier the first fragments of stage s + 1 are read from slot
-     * sl + 1 into weight set sl + 1. */
-    auto step = [&](int s, int sl) {
-        uint8_t* const cur = smem + sl * L::STAGE;
-        uint8_t* const nxt = smem + (sl == 2 ? 0 : sl + 1) * L::STAGE;
-        uint8_t* const fill = smem + (sl == 0 ? 2 : sl - 1) * L::STAGE;
-        const int sf = s + 2 < steps ? s + 2 : steps - 1;
+    /* One K step on weight set `set` from ring slot cur (stage s); nxt and prv are the
+     * slots of stages s + 1 and s - 1 (= s + 2).  At group WMW - 2 every read of stage s
+     * has been issued: once this wave's reads are done and stage s + 1 has landed, the
+     * barrier releases slot cur for stage s + 3, and the first fragments of stage s + 1
+     * are read from slot nxt into the other weight set.  Stage k's loads go out in the
+     * WMW groups between the barriers of steps k - 3 and k - 2, so at each barrier exactly
+     * one stage (LOADS loads) is younger than the one it waits for. */
+    auto step = [&](int s, int set, uint8_t* cur, const uint8_t* nxt, uint8_t* prv) {
 #pragma unroll
-        for (int mi = 0; mi < WMF; ++mi) {
-            group(mi, sl);
-            if (mi + 2 < WMF) {
+        for (int mi = 0; mi < WMW; ++mi) {
+            group(mi, set);
+            if (mi + 2 < WMW) {
                 read_a(cur, mi + 2);
-                issue_part(mi, sf, fill);
-            } else if (mi + 2 == WMF) {
-                /* every read of stage s is issued and stage s + 2 is in flight: wait for
-                 * this wave's reads and for stage s + 1, then meet the other waves */
+                issue_part(mi + 2, s + 2, prv);
+            } else if (mi + 2 == WMW) {
                 asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(L::LOADS) : "memory");
-                read_w(nxt, sl == 2 ? 0 : sl + 1);
+                issue_part(0, s + 3, cur);
+                read_w(nxt, set ^ 1);
                 read_a(nxt, 0);
             } else {
+                issue_part(1, s + 3, cur);
                 read_a(nxt, 1);
             }
             /* keep each group's reads and loads beside its own MFMAs */
@@ -256,23 +256,29 @@ __global__ __launch_bounds__(256) void prefill_kernel(
         }
     };
 
-    /* ---- K walk: stage s lives in ring slot s % 3 and weight set s % 3 */
+    /* ---- K walk: stage s lives in ring slot s % 3 and weight set s % 2 */
 #pragma unroll
-    for (int k = 0; k < L::LOADS; ++k) load(k, 0, smem);
+    for (int p = 0; p < WMW; ++p) issue_part(p, 0, smem);
 #pragma unroll
-    for (int k = 0; k < L::LOADS; ++k) load(k, steps > 1 ? 1 : 0, smem + L::STAGE);
+    for (int p = 0; p < WMW; ++p) issue_part(p, 1, smem + L::STAGE);
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(L::LOADS) : "memory");
+    issue_part(0, 2, smem + 2 * L::STAGE);
+    issue_part(1, 2, smem + 2 * L::STAGE);
     read_w(smem, 0);
     read_a(smem, 0);
     read_a(smem, 1);
+    int sl = 0;                                         /* ring slot of stage s */
     int s = 0;
-    for (; s + 3 <= steps; s += 3) {
-        step(s, 0);
-        step(s + 1, 1);
-        step(s + 2, 2);
+    for (; s + 2 <= steps; s += 2) {
+        const int s1 = sl == 2 ? 0 : sl + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+        step(s, 0, smem + sl * L::STAGE, smem + s1 * L::STAGE, smem + s2 * L::STAGE);
+        step(s + 1, 1, smem + s1 * L::STAGE, smem + s2 * L::STAGE, smem + sl * L::STAGE);
+        sl = s2;
     }
-    if (s < steps) step(s, 0);
-    if (s + 1 < steps) step(s + 1, 1);
+    if (s < steps) {
+        const int s1 = sl == 2 ? 0 : sl + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+        step(s, 0, smem + sl * L::STAGE, smem + s1 * L::STAGE, smem + s2 * L::STAGE);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* drain the tail reloads */
     if (MODE == PF_MX8) {
         /* 24 wait states between the last in-place MFMA and any read of an accumulator;
@@ -281,29 +287,30 @@ __global__ __launch_bounds__(256) void prefill_kernel(
 #pragma unroll
         for (int a = 0; a < WNF; ++a)
 #pragma unroll
-            for (int b = 0; b < WMF; ++b) asm volatile("" : "+a"(acc[a][b]));
+            for (int b = 0; b < WMW; ++b) asm volatile("" : "+a"(acc[a][b]));
     } else {
         /* the last group's results */
-        const float sp = af[(WMF - 1) & 3];
 #pragma unroll
         for (int ni = 0; ni < WNF; ++ni)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                acc[ni][WMF - 1][i] = acc[ni][WMF - 1][i] + dq[(WMF - 1) & 1][ni][i] * sp;
+                acc[ni][WMW - 1][i] = acc[ni][WMW - 1][i] + dq[(WMW - 1) & 1][ni][i] * sprev;
     }
 
     /* ---- epilogue: lane holds Y[m0 + 16 g + li][n0 + 16 f + 4 q + i], i = 0..3.  The bf16
      * tile is staged through the (now idle) LDS ring and leaves as whole 16-byte row chunks,
-     * so every store instruction writes full contiguous row segments. */
-    constexpr int YP = 2 * L::BN + 16;                 /* LDS row pitch, bytes (padded) */
+     * so every store instruction writes full contiguous row segments.  LDS row pitch: 2 BN
+     * bytes padded to 32 mod 128, so the 16 lanes of one 8-byte write cycle (4 rows x 4
+     * column chunks) cover 32 distinct banks. */
+    constexpr int YP = 2 * L::BN + (32 - (2 * L::BN) % 128 + 128) % 128;
     constexpr int CPR = L::BN / 8;                     /* 16-byte chunks per tile row */
     static_assert(L::BM * YP <= L::LDS, "the output tile fits the ring");
     __syncthreads();                                   /* every wave is done with the ring */
 #pragma unroll
     for (int ni = 0; ni < WNF; ++ni)
 #pragma unroll
-        for (int mi = 0; mi < WMF; ++mi) {
-            const int ml = 16 * (wm * WMF + mi) + li;
+        for (int mi = 0; mi < WMW; ++mi) {
+            const int ml = 16 * (wm * WMW + mi) + li;
             const int nl = 16 * (wn * WNF + ni) + 4 * q;
             const r3d_f32x4 v = acc[ni][mi];
             *reinterpret_cast<uint2*>(smem + ml * YP + 2 * nl) =
@@ -311,7 +318,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(
         }
     __syncthreads();
     const bool vec = ((uintptr_t)Y & 15) == 0 && (y_pitch & 7) == 0;
-    for (int e = threadIdx.x; e < L::BM * CPR; e += 256) {
+    for (int e = threadIdx.x; e < L::BM * CPR; e += 64 * L::WAVES) {
         const int r = e / CPR, c = e - (e / CPR) * CPR;
         const int64_t m = m0 + r, n = n0 + 8 * c;
         if (m >= M || n >= N) continue;
