@@ -122,8 +122,7 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
         const int64_t qbytes = ((P.M * P.K + 255) / 256) * 256;
         uint8_t* Q = P.scratch;
         uint8_t* SX = P.scratch + qbytes;
-        const int64_t threads = P.M * (P.K / 8);
-        const int64_t qblocks = (threads + 255) / 256;
+        const int64_t qblocks = P.M;                     /* one workgroup per row */
         if (qblocks > 0x7FFFFFFF) return RAD_E_SHAPE;
         hipLaunchKernelGGL(quant_mx8_kernel, dim3((unsigned)qblocks), dim3(256), 0, stream,
                            reinterpret_cast<const uint16_t*>(P.A), P.a_pitch, Q, P.K, SX,

@@ -338,43 +338,55 @@ __global__ __launch_bounds__(512) void prefill_kernel(
  * bf16 [M, K] -> e4m3 codes [M, K] + one E8M0 per 32 along K: the scale exponent is the
  * least e with amax * 2^-e <= 448 (clamped to [-127, 127]; 0 for an all-zero or
  * non-finite block), codes are x * 2^-e clamped to +-448 and rounded to nearest even.
- * Four lanes share a block (8 elements each, one 16-byte load); NaN elements never set
- * the block maximum and encode as 0x7F with their sign.  K % 32 == 0. */
+ * NaN elements never set the block maximum and encode as 0x7F with their sign. */
+/* f32 -> e4m3 code, round to nearest even, saturating at +-448, NaN -> 0x7F with the sign.
+ * Branch-free (selects only): on MI355X it gives the same code as the step-by-step form
+ * (exponent / mantissa split, explicit subnormal shift and tie test) for every one of the
+ * 2^32 inputs after the quantiser's +-448 clamp (checked exhaustively on the device). */
 __device__ __forceinline__ uint32_t r3d_e4m3_rne(float f) {
     const uint32_t u = __float_as_uint(f);
     const uint32_t s = (u >> 24) & 0x80u;
     const uint32_t a = u & 0x7FFFFFFFu;
-    if (a > 0x7F800000u) return s | 0x7Fu;
-    if (a >= 0x43E00000u) return s | 0x7Eu;                    /* >= 448 */
-    const int e = (int)(a >> 23) - 127;
-    uint32_t m = a & 0x7FFFFFu;
-    if (e < -10) return s;                                       /* below half the least subnormal */
-    if (e < -6) {                                                /* e4m3 subnormal: m * 2^-9 */
-        const int sh = 14 - e;
-        m |= 0x800000u;
-        const uint32_t lo = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
-        uint32_t qq = m >> sh;
-        if (lo > half || (lo == half && (qq & 1u))) ++qq;
-        return s | qq;
-    }
-    uint32_t qq = m >> 20;
+    /* normal range: exponent field, top 3 mantissa bits, nearest-even on the other 20; a
+     * carry out of the mantissa moves into the exponent through the plain add */
+    const uint32_t m = a & 0x7FFFFFu;
     const uint32_t lo = m & 0xFFFFFu;
-    if (lo > 0x80000u || (lo == 0x80000u && (qq & 1u))) ++qq;
-    int ee = e + 7;
-    if (qq == 8u) { qq = 0; ++ee; }
-    if (ee > 15 || (ee == 15 && qq >= 7u)) return s | 0x7Eu;
-    return s | ((uint32_t)ee << 3) | qq;
+    const uint32_t rnd = (lo > 0x80000u) | ((lo == 0x80000u) & (m >> 20) & 1u);
+    const uint32_t nrm = ((((a >> 23) - 120u) << 3) | (m >> 20)) + rnd;
+    /* |x| < 2^-6 (e4m3 subnormals m * 2^-9): x * 2^9 rounded to an integer, nearest even,
+     * by the 2^23 magic add; a result of 8 is the least normal, code 0x08 */
+    const uint32_t sub = __float_as_uint(__uint_as_float(a) * 512.0f + 8388608.0f) - 0x4B000000u;
+    uint32_t r = a < 0x3C800000u ? sub : nrm;
+    r = a >= 0x43E00000u ? 0x7Eu : r;
+    r = r > 0x7Eu ? 0x7Eu : r;
+    r = a > 0x7F800000u ? 0x7Fu : r;
+    return s | r;
 }
 
-__global__ __launch_bounds__(256) void quant_mx8_kernel(
-    const uint16_t* __restrict__ X, int64_t x_pitch, uint8_t* __restrict__ Q, int64_t q_pitch,
-    uint8_t* __restrict__ SX, int64_t sx_pitch, int64_t M, int K) {
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int per_row = K >> 3;
-    const int64_t m = gid / per_row;
-    const int c = (int)(gid - m * per_row);
-    if (m >= M) return;                     /* whole 4-lane groups leave together */
-    const r3d_i32x4 raw = *reinterpret_cast<const r3d_i32x4*>(X + m * x_pitch + 8 * c);
+/* Four f32 (already inside +-448) -> four e4m3 codes, a in the low byte: two
+ * v_cvt_pk_fp8_f32, then NaN inputs are set to 0x7F with their sign.  On MI355X this is
+ * the same code as r3d_e4m3_rne for every one of the 2^32 inputs after the +-448 clamp
+ * (checked exhaustively on the device; the conversion alone differs only on NaNs). */
+__device__ __forceinline__ uint32_t r3d_e4m3x4_rne(float a, float b, float c, float d) {
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+    const float x[4] = {a, b, c, d};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t nan = ((__float_as_uint(x[i]) >> 24) & 0x80u) | 0x7Fu;
+        w = x[i] != x[i] ? (w & ~(0xFFu << (8 * i))) | (nan << (8 * i)) : w;
+    }
+    return w;
+}
+
+/* Each thread converts 8 consecutive elements (one 16-byte load) and four lanes share a
+ * 32-element block; a thread handles up to kQU such chunks of its row, 256 chunks apart,
+ * with every load issued before the first conversion so each wave keeps kQU x 1 KB in
+ * flight.  K % 32 == 0 keeps every 4-lane group inside the row. */
+constexpr int kQU = 4;
+
+__device__ __forceinline__ void r3d_quant_mx8_chunk(r3d_i32x4 raw, uint8_t* q, uint8_t* sx,
+                                                    bool write_scale) {
     float v[8];
     float amax = 0.0f;
 #pragma unroll
@@ -408,18 +420,42 @@ __global__ __launch_bounds__(256) void quant_mx8_kernel(
     }
     const float inv = (127 - e) >= 1 ? __uint_as_float((uint32_t)(127 - e) << 23)
                                      : __uint_as_float(0x00400000u);      /* 2^-127 */
-    uint32_t lo = 0, hi = 0;
+    float cv[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        float cv = v[i] * inv;
-        if (cv > 448.0f) cv = 448.0f;
-        if (cv < -448.0f) cv = -448.0f;
-        const uint32_t b = r3d_e4m3_rne(cv);
-        if (i < 4) lo |= b << (8 * i);
-        else hi |= b << (8 * (i - 4));
+        float c = v[i] * inv;
+        if (c > 448.0f) c = 448.0f;
+        if (c < -448.0f) c = -448.0f;
+        cv[i] = c;
     }
-    *reinterpret_cast<uint2*>(Q + m * q_pitch + 8 * c) = make_uint2(lo, hi);
-    if ((threadIdx.x & 3) == 0) SX[m * sx_pitch + (c >> 2)] = (uint8_t)(e + 127);
+    const uint32_t lo = r3d_e4m3x4_rne(cv[0], cv[1], cv[2], cv[3]);
+    const uint32_t hi = r3d_e4m3x4_rne(cv[4], cv[5], cv[6], cv[7]);
+    *reinterpret_cast<uint2*>(q) = make_uint2(lo, hi);
+    if (write_scale) *sx = (uint8_t)(e + 127);
+}
+
+__global__ __launch_bounds__(256) void quant_mx8_kernel(
+    const uint16_t* __restrict__ X, int64_t x_pitch, uint8_t* __restrict__ Q, int64_t q_pitch,
+    uint8_t* __restrict__ SX, int64_t sx_pitch, int64_t M, int K) {
+    /* one workgroup per row; chunk c = 8 elements, 16 bytes */
+    const int64_t m = blockIdx.x;
+    const int per_row = K >> 3;
+    const uint16_t* xr = X + m * x_pitch;
+    uint8_t* qr = Q + m * q_pitch;
+    uint8_t* sr = SX + m * sx_pitch;
+    for (int c0 = threadIdx.x; c0 < per_row; c0 += 256 * kQU) {
+        r3d_i32x4 raw[kQU];
+#pragma unroll
+        for (int u = 0; u < kQU; ++u)
+            if (c0 + 256 * u < per_row)
+                raw[u] = *reinterpret_cast<const r3d_i32x4*>(xr + 8 * (c0 + 256 * u));
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) {
+            const int c = c0 + 256 * u;
+            if (c >= per_row) break;                     /* whole 4-lane groups leave together */
+            r3d_quant_mx8_chunk(raw[u], qr + 8 * c, sr + (c >> 2), (threadIdx.x & 3) == 0);
+        }
+    }
 }
 
 }  // namespace r3d
