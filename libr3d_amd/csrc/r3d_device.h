@@ -75,6 +75,13 @@ __device__ __forceinline__ r3d_i32x4 r3d_ld16_stream(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const r3d_i32x4*>(p));
 }
 
+/* Non-temporal 16-byte buffer load (buffer_load_dwordx4 ... nt) at byte `off` of the
+ * resource; an offset past the resource's num_records returns zeros without touching
+ * memory. */
+__device__ __forceinline__ r3d_i32x4 r3d_buf_ld16_stream(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(r3d_i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2));
+}
+
 /* The fp8 operand of one 128-wide K step for the row starting at p: bytes [16kb, +16)
  * and [64+16kb, +16). */
 __device__ __forceinline__ r3d_i32x8 r3d_ld_fp8_operand(const uint8_t* p, int kb) {

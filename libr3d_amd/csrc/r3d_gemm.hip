@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include "r3d_gemm_kernels.h"
+#include "r3d_gemv_quad.h"
 #include "r3d_plan.h"
 #include "r3d_prefill.h"
 #include "rad_plugin.h"
@@ -60,7 +61,45 @@ static void debug_once(const char* what, int key) {
     fprintf(stderr, "libr3d_gfx950: %s launched\n", what);
 }
 
+static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream) {
+    const dim3 grid((unsigned)g.blocks), block(256);
+#define R3D_QUAD(ENC_, MT_, D_)                                                              \
+    hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, D_>), grid, block, (size_t)g.lds, stream,  \
+                       P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K, g.chunks,      \
+                       P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, P.a_pitch, P.as_pitch,  \
+                       P.b_pitch, P.bs_pitch, P.y_pitch)
+#define R3D_QUAD_D(ENC_, MT_)                                                                \
+    do {                                                                                     \
+        switch (g.depth) {                                                                   \
+        case 8: R3D_QUAD(ENC_, MT_, 8); break;                                               \
+        case 4: R3D_QUAD(ENC_, MT_, 4); break;                                               \
+        case 2: R3D_QUAD(ENC_, MT_, 2); break;                                               \
+        default: R3D_QUAD(ENC_, MT_, 1); break;                                              \
+        }                                                                                    \
+    } while (0)
+    if (P.enc == ENC_MXFP4A8) {
+        if (g.mt == 1) R3D_QUAD_D(ENC_MXFP4A8, 1);
+        else R3D_QUAD_D(ENC_MXFP4A8, 4);
+    } else {
+        if (g.mt == 1) R3D_QUAD_D(ENC_FP8A8, 1);
+        else R3D_QUAD_D(ENC_FP8A8, 4);
+    }
+#undef R3D_QUAD_D
+#undef R3D_QUAD
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "libr3d_gfx950: quad decode GEMV launch FAILED (%s)\n", hipGetErrorName(e));
+        return RAD_E_DEVICE;
+    }
+    debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 quad decode GEMV" : "fp8a8 quad decode GEMV",
+               128 + (P.enc << 4) + g.mt);
+    return RAD_OK;
+}
+
 static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) {
+    QuadGeom qg{};
+    if (quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg))
+        return launch_quad(P, qg, stream);
     DecodeGeom g{};
     decode_geom(P.M, P.N, P.K, splitk, &g, gemv_wave_lds(P.enc, P.M <= 1 ? 1 : P.M <= 4 ? 4 : 16));
     const dim3 grid((unsigned)g.blocks), block((unsigned)(64 * g.waves));

@@ -293,6 +293,50 @@ void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGe
     g->blocks = (g->tiles + g->tiles_per_block - 1) / g->tiles_per_block;
 }
 
+bool quad_fits(const GemmPlan& P) { return 4 * P.b_pitch < ((int64_t)1 << 31); }
+
+/* Quad geometry: split K until about env_quad_waves() waves are in flight, keeping >= 16
+ * groups per chunk. */
+bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, QuadGeom* g) {
+    if (M < 1 || M > 4 || N < 1 || K < 128 || K % 128 != 0) return false;
+    if (force_chunks > 0 && force_chunks != 1 && force_chunks != 2 && force_chunks != 4)
+        return false;
+    g->mt = M <= 1 ? 1 : 4;
+    g->groups = (int)(K / 128);
+    g->quads = (N + 3) / 4;
+    const int64_t target = env_quad_waves();
+    int c = 1;
+    if (force_chunks > 0) {
+        c = (int)force_chunks;
+    } else {
+        while (c < 4 && g->quads * c < target && g->groups >= 16 * c) c *= 2;
+    }
+    while (c > 1 && c > g->groups) c >>= 1;
+    g->chunks = c;
+    g->qpb = 4 / c;
+    g->blocks = (g->quads + g->qpb - 1) / g->qpb;
+    g->gmax = (g->groups + c - 1) / c;
+    {
+        /* the deepest supported ring that no wave's step count falls below */
+        static const int kDepths[] = {8, 4, 2, 1};
+        const int ns_min = (g->groups / c + 3) / 4;
+        const int want = env_quad_depth(enc);
+        g->depth = 1;
+        for (int d : kDepths)
+            if (d <= want && d <= ns_min) { g->depth = d; break; }
+    }
+    const int64_t blob = ((int64_t)g->mt * (K + 16) + 1023) / 1024 * 1024;
+    const int64_t xs = ((int64_t)g->mt * g->groups * 4 + 255) / 256 * 256;
+    const int64_t scb = (16 * (int64_t)g->gmax + 255) / 256 * 256;
+    const int64_t lds = blob + xs + 4 * scb;
+    if (lds > kQuadMaxLds || g->blocks > 0x7FFFFFFF) return false;
+    g->xs_off = (int)blob;
+    g->sc_off = (int)(blob + xs);
+    g->sc_bytes = (int)scb;
+    g->lds = (int)lds;
+    return true;
+}
+
 void tile_geom(int64_t M, int64_t N, TileGeom* g) {
     g->bm = 128;
     g->bn = 128;
@@ -349,6 +393,24 @@ int env_prefetch() {
     return v;
 }
 
+int64_t env_quad_waves() {
+    static const int64_t v = [] {
+        const char* e = getenv("R3D_GFX950_QWAVES");
+        const int64_t w = e ? (int64_t)atoll(e) : 0;
+        return w > 0 ? w : (int64_t)4096;
+    }();
+    return v;
+}
+
+int env_quad_depth(int enc) {
+    static const int v = [] {
+        const char* e = getenv("R3D_GFX950_QD");
+        return e ? atoi(e) : 0;
+    }();
+    (void)enc;   /* 4 steps measured best for both encodings on MI355X at the 27B shapes */
+    return v > 0 ? v : 4;
+}
+
 int64_t decode_splitk(const RadArgs* a) {
     if (a && a->tv)
         for (int i = 0; i < a->n_tv; ++i)
@@ -370,12 +432,19 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
     GemmPlan P{};
     rc = a16 ? plan_mxfp4a16(a, M, N, &P) : mx ? plan_mxfp4a8(a, M, N, &P) : plan_fp8a8(a, M, &P);
     if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
-    if (dec) {
+    QuadGeom qg{};
+    if (dec && quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &qg)) {
+        snprintf(buf, (size_t)len,
+                 "arm=decode kernel=quad enc=%s M=%lld N=%lld K=%lld mt=%d chunks=%d waves=4 "
+                 "quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d",
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K, qg.mt, qg.chunks,
+                 (long long)qg.quads, (long long)qg.blocks, qg.groups, qg.depth, qg.lds, P.rblk);
+    } else if (dec) {
         DecodeGeom g{};
         decode_geom(P.M, P.N, P.K, decode_splitk(a), &g,
                     gemv_wave_lds(P.enc, P.M <= 1 ? 1 : P.M <= 4 ? 4 : 16));
         snprintf(buf, (size_t)len,
-                 "arm=decode enc=%s M=%lld N=%lld K=%lld mt=%d chunks=%d waves=%d tiles=%lld "
+                 "arm=decode kernel=tile16 enc=%s M=%lld N=%lld K=%lld mt=%d chunks=%d waves=%d tiles=%lld "
                  "blocks=%lld steps=%d rblk=%d",
                  ename, (long long)P.M, (long long)P.N, (long long)P.K,
                  g.mt, g.chunks, g.waves, (long long)g.tiles, (long long)g.blocks, g.steps,

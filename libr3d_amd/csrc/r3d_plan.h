@@ -50,6 +50,22 @@ struct DecodeGeom {
     int steps;               /* K / 128 */
 };
 
+/* Launch geometry of the quad decode GEMV (M <= 4): one wave per quad of 4 weight rows and
+ * K chunk, 4 waves per workgroup (4 / chunks quads x chunks). */
+struct QuadGeom {
+    int mt;                  /* activation rows of the instantiation: 1 or 4 */
+    int chunks;              /* waves per quad (split-K): 1, 2 or 4 */
+    int qpb;                 /* quads per workgroup: 4 / chunks */
+    int groups;              /* K / 128 */
+    int gmax;                /* most groups one chunk holds: ceil(groups / chunks) */
+    int depth;               /* ring depth in K steps (<= every wave's step count) */
+    int64_t quads, blocks;
+    int xs_off;              /* LDS: activation rows at 0 ([mt][K + 16], 1 KB rounded),
+                                a_scales ([mt][groups] f32) at xs_off */
+    int sc_off, sc_bytes;    /* LDS: per-wave weight scales */
+    int lds;                 /* dynamic LDS bytes per workgroup */
+};
+
 /* Launch geometry of the mxfp4 prefill GEMM (block-scaled MFMA, direct-to-LDS ring):
  * a workgroup of 8 waves (2 x 4) owns bn = 32 wnf weight rows x bm = 64 wmf tokens. */
 struct PrefillGeom {
@@ -86,6 +102,15 @@ int entry_preamble(const RadArgs* a, int enc, int64_t m_max, int64_t* M, int64_t
 /* wave_lds: LDS bytes one wave needs (0 = unknown: assume it fits 8 waves per workgroup). */
 void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGeom* g,
                  int wave_lds = 0);
+/* Quad GEMV geometry; false when the shape is outside what it serves (M > 4, or the
+ * workgroup's LDS -- whole-K activation rows -- over kQuadMaxLds), and the 16-row GEMV
+ * runs instead.  force_chunks: 1/2/4 pin the split, anything else above 0
+ * leaves the quad kernel. */
+constexpr int kQuadMaxLds = 48 * 1024;
+bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, QuadGeom* g);
+/* The quad kernel addresses a quad's 4 weight rows through one buffer resource: they must
+ * span less than 2^31 bytes. */
+bool quad_fits(const GemmPlan& P);
 void tile_geom(int64_t M, int64_t N, TileGeom* g);
 /* mode: 0 = e4m3 activations with f32 scale per 128 (mxfp4a8), 1 = mxfp8 (mxfp4a16);
  * ncu: compute units the launch can fill (tiles are sized so the last round of
@@ -100,6 +125,8 @@ bool env_no_fp8_dec();      /* R3D_NO_FP8_DEC: the fp8a8 decode row */
 bool env_debug();           /* R3D_DEBUG_GEMM: one stderr line per distinct launch arm */
 int64_t env_splitk();       /* R3D_GFX950_SPLITK: force the decode chunk count (0 = policy) */
 int env_prefetch();         /* R3D_GFX950_PF: decode prefetch depth in K steps, 2/4/8 (default 4) */
+int64_t env_quad_waves();   /* R3D_GFX950_QWAVES: waves the quad split aims for (default 4096) */
+int env_quad_depth(int enc);/* R3D_GFX950_QD: quad ring depth 1/2/4/8 (default 4) */
 
 /* The decode rows' "splitk" tunable (RadArgs::tv): chunks per tile, 0 = the policy.  An
  * engine-chosen value wins over R3D_GFX950_SPLITK. */

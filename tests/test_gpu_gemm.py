@@ -97,6 +97,18 @@ def test_fp8_decode_small(gpu, M, rblk):
     _check(F8_DEC, "fp8a8", A, AS, B, BS, M, 200, 640, gpu, rblk=rblk)
 
 
+@pytest.mark.parametrize("N,K", [(17, 256), (1001, 4096), (4096, 1152), (6, 21504)])
+@pytest.mark.parametrize("rblk", [1, 128])
+def test_fp8_decode_shapes(gpu, N, K, rblk):
+    """Ragged N (a partial last quad of weight rows), one to 168 groups, both scale grids
+    (a 128-row grid needs N > 128 to be told apart from a per-row one)."""
+    if rblk == 128 and N <= 128:
+        pytest.skip("one block row is a per-row grid")
+    for M in (1, 3):
+        A, AS, B, BS = _f8_case(M, N, K, N + K + M + rblk, rblk)
+        _check(F8_DEC, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk)
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 128, 128), (17, 200, 256), (64, 256, 512),
                                    (130, 300, 384), (256, 512, 1024)])
 def test_mxfp4_tile(gpu, M, N, K):
