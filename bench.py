@@ -30,8 +30,8 @@ ROTATE_BYTES = 1.1 * 2 ** 30
 # HBM bytes per launch of the headline kernel from two rocprofv3 --pmc passes over this
 # script (--quick), FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 -- the factors a plain 256 MiB
 # device copy reads on the same counters (bench.py --copy-calib).  Re-measured whenever
-# the decode kernel changes; profiles/gemv_fp8a8_c1_pmc_traffic.md has the numbers.
-HEADLINE_TRAFFIC_BYTES = 117812643
+# the decode kernel changes; profiles/gemv_quad_fp8a8_c1_pmc_traffic.md has the numbers.
+HEADLINE_TRAFFIC_BYTES = 117738496
 
 
 def log(*a):
@@ -140,6 +140,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy (counter calibration for PMC runs)")
+    ap.add_argument("--c3-only", action="store_true",
+                    help="only time config 3 (mxfp4a16 prefill) and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.copy_calib:
         import torch
@@ -161,6 +163,9 @@ def main():
     R.lib()
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream().cuda_stream
+    if args.c3_only:
+        print(json.dumps(bench_c3(dev, stream, steps=args.steps, warmup=args.warmup)), flush=True)
+        return
 
     # ---- headline: config 1, fp8a8 decode GEMV, cold
     M, K, N = 1, 5376, 21504
@@ -197,7 +202,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": HEADLINE_TRAFFIC_BYTES,
-                     "kernel": "r3d::gemv_kernel<1, 1> (fp8a8, MT=1)",
+                     "kernel": "r3d::gemv_quad_kernel<1, 1, 4> (fp8a8, MT=1, 4-step ring)",
                      "kernel_us": round(kern * 1e6, 3)},
     }
 
@@ -262,6 +267,7 @@ def bench_c3(dev, stream, steps=10, warmup=3):
     per 32) -- gemm_nt_q_mxfp4a16, quantiser and GEMM both inside the timed launches."""
     import torch
     import libr3d_amd as R
+    from libr3d_amd import synth
     M, K, N = 2048, 5376, 21504
     rng = np.random.default_rng(0x5EED + 32)
     X = synth.bf16_bits(rng.standard_normal((M, K), dtype=np.float32))

@@ -384,15 +384,6 @@ int64_t env_splitk() {
     }();
     return v;
 }
-int env_prefetch() {
-    static const int v = [] {
-        const char* e = getenv("R3D_GFX950_PF");
-        const int p = e ? atoi(e) : 4;
-        return p >= 8 ? 8 : p <= 2 ? 2 : 4;
-    }();
-    return v;
-}
-
 int64_t env_quad_waves() {
     static const int64_t v = [] {
         const char* e = getenv("R3D_GFX950_QWAVES");

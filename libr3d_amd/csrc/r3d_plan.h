@@ -124,7 +124,6 @@ bool env_no_fp8a8();        /* R3D_NO_FP8A8: all fp8a8 rows */
 bool env_no_fp8_dec();      /* R3D_NO_FP8_DEC: the fp8a8 decode row */
 bool env_debug();           /* R3D_DEBUG_GEMM: one stderr line per distinct launch arm */
 int64_t env_splitk();       /* R3D_GFX950_SPLITK: force the decode chunk count (0 = policy) */
-int env_prefetch();         /* R3D_GFX950_PF: decode prefetch depth in K steps, 2/4/8 (default 4) */
 int64_t env_quad_waves();   /* R3D_GFX950_QWAVES: waves the quad split aims for (default 4096) */
 int env_quad_depth(int enc);/* R3D_GFX950_QD: quad ring depth 1/2/4/8 (default 4) */
 

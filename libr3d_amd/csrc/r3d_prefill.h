@@ -2,7 +2,8 @@
  * MFMA, and the bf16 -> mxfp8 activation quantiser that feeds its bf16-in row.
  *
  * Y[m, n] = sum_k A[m, k] * W[n, k], W in mxfp4 (e2m1 codes + one E8M0 per 32 along K),
- * A in e4m3.  A workgroup of 4 waves (2 x 2) owns a BN x BM tile (weight rows x tokens).
+ * A in e4m3.  A workgroup of 8 waves (2 along N x 4 along M, two per SIMD) owns a BN x BM
+ * tile (weight rows x tokens).
  * Each 128-wide K step is one v_mfma_scale_f32_16x16x128_f8f6f4 per 16 x 16 sub-tile:
  * the weights are src A (fp4; lane (row r, q) holds the whole 32-wide block q, so the
  * row's E8M0 byte q is that lane's scale operand) and the activations src B (fp8).
@@ -16,7 +17,8 @@
  *
  * Staging: every byte a step needs arrives by buffer loads straight into LDS (16 bytes
  * per lane for the planes, 4 for the scales) into a three-deep ring, with one barrier per
- * step; a stage is loaded the moment its slot frees, two steps ahead of its use.  Each 1 KB plane load fills exactly the LDS image of one MFMA operand fragment
+ * step; a stage is loaded the moment its slot frees, two steps ahead of its use.  Each 1 KB
+ * plane load fills exactly the LDS image of one MFMA operand fragment
  * (16 rows x 64 bytes of one step, four lanes per row, XOR-swizzled), so every fragment
  * read is one ds_read_b128 per lane, free of bank conflicts.  Weight rows past N and
  * tokens past M clamp to the last valid one; clamped lanes feed only outputs that are
