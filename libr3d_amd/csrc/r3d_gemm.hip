@@ -63,11 +63,20 @@ static void debug_once(const char* what, int key) {
 
 static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream) {
     const dim3 grid((unsigned)g.blocks), block(256);
+    /* mxfp4 scale rows contiguous (pitch = K/32) in a 16-byte aligned plane: 1 KB staging loads */
+    const int sc16 = P.enc == ENC_MXFP4A8 && P.bs_pitch == P.K / 32 &&
+                     ((uintptr_t)P.BS & 15) == 0;
 #define R3D_QUAD(ENC_, MT_, D_)                                                              \
-    hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, D_>), grid, block, (size_t)g.lds, stream,  \
+    if (g.qpw == 2)                                                                          \
+        hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, 2, D_>), grid, block, (size_t)g.lds,   \
+                           stream, P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K,   \
+                           g.chunks, P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, sc16,    \
+                           P.a_pitch, P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch);          \
+    else                                                                                     \
+    hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, 1, D_>), grid, block, (size_t)g.lds, stream, \
                        P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K, g.chunks,      \
-                       P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, P.a_pitch, P.as_pitch,  \
-                       P.b_pitch, P.bs_pitch, P.y_pitch)
+                       P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, sc16, P.a_pitch,       \
+                       P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch)
 #define R3D_QUAD_D(ENC_, MT_)                                                                \
     do {                                                                                     \
         switch (g.depth) {                                                                   \

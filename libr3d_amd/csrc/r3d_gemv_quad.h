@@ -33,12 +33,13 @@
  *
  * Every load is in bounds: rows past N clamp to row N-1, groups past K clamp to the last
  * group, activation rows past M duplicate row M-1; none of these is ever accumulated or
- * stored.  Each wave loads exactly its chunk's steps: the launch picks a ring depth D no
- * larger than any wave's step count, and the last steps run as a static tail.
+ * stored.  The launch picks a ring depth D no larger than any wave's step count; a wave
+ * issues at most D - 1 loads past its chunk, answered as out-of-range (no memory access).
  *
  * LDS: [MT][K + 16] activation bytes (rounded up to 1 KB) at 0, [MT][groups] f32 a_scales
- * at xs_off, then per wave sc_bytes of weight scales at sc_off -- mxfp4a8: [4 rows][gmax
- * dwords] of E8M0 bytes, fp8a8: [gmax groups][4 rows] 4-byte slots, bf16 in the low half.
+ * at xs_off, then the weight scales at sc_off -- mxfp4a8: the workgroup's rows, whole K,
+ * [rows][groups dwords] of E8M0 bytes (sc_bytes in all); fp8a8: sc_bytes per wave of
+ * [gmax groups][RB rows] 4-byte slots, bf16 in the low half.
  * The fold reuses the first 1 KB after the K loop. */
 #ifndef R3D_GEMV_QUAD_H
 #define R3D_GEMV_QUAD_H
@@ -55,48 +56,24 @@ struct QuadStep {
     r3d_i32x4 w1;           /* fp8a8: the rows 2-3 load */
 };
 
-/* The weight loads of the step whose group base (for this lane) is `grp`. */
+/* The weight loads of the step whose group base (for this lane) is `grp` -- or, when `in` is
+ * false (a step past the wave's chunk), loads at offsets past the resource's range, which
+ * the hardware answers with zeros and no memory access.  Issuing a load either way keeps
+ * the code free of conditional loads (whose register merges would cost a full wait in the
+ * loop); the two skipped offsets differ so the compiler cannot merge the two loads. */
 template <int ENC>
 __device__ __forceinline__ QuadStep<ENC> r3d_quad_load(__amdgpu_buffer_rsrc_t r, uint32_t o0,
-                                                      uint32_t o1, uint32_t grp) {
+                                                      uint32_t o1, uint32_t grp, bool in) {
+    const uint32_t kSkip = 0x80000000u;
     QuadStep<ENC> v;
     if (ENC == ENC_MXFP4A8) {
-        v.w0 = r3d_buf_ld16_stream(r, o0 + 64 * grp);
+        v.w0 = r3d_buf_ld16_stream(r, in ? o0 + 64 * grp : kSkip);
         v.w1 = v.w0;
     } else {
-        v.w0 = r3d_buf_ld16_stream(r, o0 + 128 * grp);
-        v.w1 = r3d_buf_ld16_stream(r, o1 + 128 * grp);
+        v.w0 = r3d_buf_ld16_stream(r, in ? o0 + 128 * grp : kSkip);
+        v.w1 = r3d_buf_ld16_stream(r, in ? o1 + 128 * grp : kSkip + 64);
     }
     return v;
-}
-
-/* The last 2D - 1 or fewer steps of the ring walk, T of them still to load: consume the D
- * ring slots, refilling the first T, then consume those T.  T is a compile-time constant
- * so every slot index and load is static (no conditional load, hence no register merge
- * and no full wait in the compiled code).  quad_tail_at picks T at run time. */
-template <int T, int D, typename Ring, typename Consume, typename Load>
-__device__ __forceinline__ void quad_tail(Ring& ring, int s0, Consume& consume, Load& load) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        consume(ring[d], s0 + d);
-        if (d < T) ring[d] = load(s0 + d + D);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int d = 0; d < T; ++d) {
-        consume(ring[d], s0 + D + d);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-template <int T, int D, typename Ring, typename Consume, typename Load>
-__device__ __forceinline__ void quad_tail_at(int t, Ring& ring, int s0, Consume& consume,
-                                             Load& load) {
-    if (t == T) {
-        quad_tail<T, D>(ring, s0, consume, load);
-    } else if constexpr (T + 1 < D) {
-        quad_tail_at<T + 1, D>(t, ring, s0, consume, load);
-    }
 }
 
 /* Direct global -> LDS load of `BYTES` (16, 4 or 2) per lane, lane l's data landing at LDS
@@ -122,60 +99,23 @@ __device__ __forceinline__ void r3d_quad_dma(const void* g, uint32_t lds) {
 }
 #pragma clang diagnostic pop
 
-/* One step's LDS operands -- the B fragment (two 16-byte reads), the used lanes' a_scale,
- * and the weight scale(s) -- read in one asm block that also waits for them.  The compiler
- * cannot see these reads, which is the point: LDS filled by direct global->LDS loads would
- * otherwise make it wait for every outstanding global load (the whole weight ring) before
- * each step.  The fill is complete and published by the s_waitcnt + s_barrier that ends
- * the prologue. */
-struct QuadLds {
-    r3d_i32x4 lo, hi;
-    float as;
-    r3d_i32x4 sb;           /* fp8a8: 4 slots of bf16 weight scales; mxfp4a8: sb[0] = E8M0 */
-};
-
-template <int ENC>
-__device__ __forceinline__ QuadLds r3d_quad_lds(uint32_t x, uint32_t a, uint32_t sc) {
-    QuadLds r;
-    if (ENC == ENC_MXFP4A8) {
-        int e;
-        asm volatile(
-            "ds_read_b128 %0, %4\n\t"
-            "ds_read_b128 %1, %4 offset:64\n\t"
-            "ds_read_b32 %2, %5\n\t"
-            "ds_read_u8 %3, %6\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(r.lo), "=&v"(r.hi), "=&v"(r.as), "=&v"(e)
-            : "v"(x), "v"(a), "v"(sc));
-        r.sb = r3d_i32x4{e, 0, 0, 0};
-    } else {
-        asm volatile(
-            "ds_read_b128 %0, %4\n\t"
-            "ds_read_b128 %1, %4 offset:64\n\t"
-            "ds_read_b32 %2, %5\n\t"
-            "ds_read_b128 %3, %6\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(r.lo), "=&v"(r.hi), "=&v"(r.as), "=&v"(r.sb)
-            : "v"(x), "v"(a), "v"(sc));
-    }
-    return r;
-}
-
-template <int ENC, int MT, int D>
+template <int ENC, int MT, int QPW, int D>
 __global__ __launch_bounds__(256) void gemv_quad_kernel(
     const uint8_t* A, const float* AS, const uint8_t* B, const void* BSv,
     uint16_t* __restrict__ Y,
     int M, int N, int K, int chunks, int rblk, int gmax, int xs_off, int sc_off, int sc_bytes,
+    int sc16,
     int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch) {
-    constexpr int LPS = ENC == ENC_MXFP4A8 ? 1 : 2;        /* weight loads per step */
+    constexpr int LPS = QPW * (ENC == ENC_MXFP4A8 ? 1 : 2);  /* weight loads per step */
+    constexpr int RB = 4 * QPW;                               /* weight rows per wave */
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int groups = K >> 7;
-    const int qpb = 4 / chunks;                           /* quads per workgroup */
-    const int qi = wave / chunks, c = wave % chunks;
-    const int64_t n0 = ((int64_t)blockIdx.x * qpb + qi) * 4;
+    const int bpb = 4 / chunks;                           /* row blocks per workgroup */
+    const int bi = wave / chunks, c = wave % chunks;
+    const int64_t n0 = ((int64_t)blockIdx.x * bpb + bi) * RB;
     const int g0 = (int)((int64_t)groups * c / chunks);
     const int gc = (int)((int64_t)groups * (c + 1) / chunks) - g0;   /* >= 1: chunks <= groups */
     const int ns = (gc + 3) >> 2;                                     /* K steps of this wave */
@@ -185,27 +125,42 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
     const int wg = (lane >> 2) & 3;    /* group slot of this lane's A row and B column */
     const int kq = lane >> 4;          /* 32-wide K block inside the group; slot of used lanes */
     const uint32_t lds0 = (uint32_t)(uintptr_t)smem;      /* LDS byte address of the blob */
-    const uint32_t scl = lds0 + (uint32_t)(sc_off + wave * sc_bytes);   /* this wave's scales */
+    /* weight scales in LDS: mxfp4a8 -- the workgroup's rows, whole K ([rows][groups dwords],
+     * the plane's own layout); fp8a8 -- per wave, its chunk ([gmax][RB] 4-byte slots) */
+    const int rbw = RB * bpb;                             /* weight rows of the workgroup */
+    const uint32_t scl = lds0 + (uint32_t)(sc_off + (ENC == ENC_MXFP4A8 ? 0 : wave * sc_bytes));
 
-    /* ---- 1. LDS staging.  The wave's weight scales first ... */
-    {
+    /* ---- 1. LDS staging.  Weight scales first ... */
+    if (ENC == ENC_MXFP4A8) {
         const uint8_t* BS8 = reinterpret_cast<const uint8_t*>(BSv);
+        const int64_t wn0 = (int64_t)blockIdx.x * rbw;
+        if (sc16 && wn0 + rbw <= N) {
+            /* the workgroup's rows are one contiguous, 16-byte aligned run of the plane:
+             * 1 KB per load (lanes past the run reload its last 16 bytes into padding) */
+            const int blk = rbw * 4 * groups;
+            for (int i = wave; i < (sc_bytes >> 10); i += 4) {
+                const int o = 1024 * i + 16 * lane < blk - 16 ? 1024 * i + 16 * lane : blk - 16;
+                r3d_quad_dma<16>(BS8 + wn0 * bs_pitch + o, scl + 1024 * i);
+            }
+        } else {
+            const int nd = rbw * groups;                  /* dwords */
+            for (int h = wave; h < (sc_bytes >> 8); h += 4) {
+                int e = lane + 64 * h;
+                if (e > nd - 1) e = nd - 1;
+                const int r = e / groups, d = e - r * groups;
+                const int64_t nr = wn0 + r < N ? wn0 + r : N - 1;
+                r3d_quad_dma<4>(BS8 + nr * bs_pitch + 4 * (int64_t)d, scl + 256 * h);
+            }
+        }
+    } else {
         const uint16_t* BS16 = reinterpret_cast<const uint16_t*>(BSv);
         for (int h = 0; h < (sc_bytes >> 8); ++h) {
             const int e = lane + 64 * h;
-            if (ENC == ENC_MXFP4A8) {
-                int r = e / gmax, d = e - r * gmax;
-                if (r > 3) r = 3;
-                if (d > gc - 1) d = gc - 1;
-                const int64_t nr = n0 + r < N ? n0 + r : N - 1;
-                r3d_quad_dma<4>(BS8 + nr * bs_pitch + 4 * (int64_t)(g0 + d), scl + 256 * h);
-            } else {
-                int d = e >> 2;
-                if (d > gc - 1) d = gc - 1;
-                const int64_t nr = n0 + (e & 3) < N ? n0 + (e & 3) : N - 1;
-                const int64_t sr = rblk == 1 ? nr : nr >> 7;
-                r3d_quad_dma<2>(BS16 + sr * bs_pitch + g0 + d, scl + 256 * h);
-            }
+            int d = e / RB;
+            if (d > gc - 1) d = gc - 1;
+            const int64_t nr = n0 + (e % RB) < N ? n0 + (e % RB) : N - 1;
+            const int64_t sr = rblk == 1 ? nr : nr >> 7;
+            r3d_quad_dma<2>(BS16 + sr * bs_pitch + g0 + d, scl + 256 * h);
         }
     }
     /* ... then the workgroup's activation rows ([MT][K + 16] bytes, whole K) and a_scales
@@ -231,33 +186,45 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
         }
     }
 
-    /* ---- 2. the weight stream, through a buffer resource over the quad's 4 rows */
+    /* ---- 2. the weight stream, through a buffer resource over the wave's RB rows */
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(B + n0 * b_pitch), (short)0, (int)(4 * b_pitch), 0x00020000);
-    uint32_t wo0, wo1;
-    if (ENC == ENC_MXFP4A8) {
-        const int64_t nr = n0 + wr < N ? n0 + wr : N - 1;
-        wo0 = (uint32_t)((nr - n0) * b_pitch + 16 * kq);
-        wo1 = wo0;
-    } else {
-        /* load 0 covers rows 0-1, load 1 rows 2-3, each in whole 128-byte groups: a lane
-         * fetches its own low half (bytes [16kq, +16) of the group) from the pair that holds
-         * its row and the high half ([64 + 16kq, +16)) of lane l ^ 2's row from the other */
-        const int64_t r0 = n0 + (wr & 1) < N ? n0 + (wr & 1) : N - 1;
-        const int64_t r1 = n0 + 2 + (wr & 1) < N ? n0 + 2 + (wr & 1) : N - 1;
-        wo0 = (uint32_t)((r0 - n0) * b_pitch + 16 * kq + (wr >= 2 ? 64 : 0));
-        wo1 = (uint32_t)((r1 - n0) * b_pitch + 16 * kq + (wr < 2 ? 64 : 0));
+        const_cast<uint8_t*>(B + n0 * b_pitch), (short)0, (int)(RB * b_pitch), 0x00020000);
+    uint32_t wo0[QPW], wo1[QPW];
+#pragma unroll
+    for (int q = 0; q < QPW; ++q) {
+        const int64_t rq = n0 + 4 * q;
+        if (ENC == ENC_MXFP4A8) {
+            const int64_t nr = rq + wr < N ? rq + wr : N - 1;
+            wo0[q] = (uint32_t)((nr - n0) * b_pitch + 16 * kq);
+            wo1[q] = wo0[q];
+        } else {
+            /* load 0 covers rows 0-1 of the quad, load 1 rows 2-3, each in whole 128-byte
+             * groups: a lane fetches its own low half (bytes [16kq, +16) of the group) from
+             * the pair that holds its row and the high half ([64 + 16kq, +16)) of lane
+             * l ^ 2's row from the other */
+            const int64_t r0 = rq + (wr & 1) < N ? rq + (wr & 1) : N - 1;
+            const int64_t r1 = rq + 2 + (wr & 1) < N ? rq + 2 + (wr & 1) : N - 1;
+            wo0[q] = (uint32_t)((r0 - n0) * b_pitch + 16 * kq + (wr >= 2 ? 64 : 0));
+            wo1[q] = (uint32_t)((r1 - n0) * b_pitch + 16 * kq + (wr < 2 ? 64 : 0));
+        }
     }
     auto grp_of = [&](int s) -> uint32_t {
         const int g = g0 + 4 * s + wg;
         return (uint32_t)(g < groups ? g : groups - 1);
     };
 
-    auto load = [&](int s) { return r3d_quad_load<ENC>(wrs, wo0, wo1, grp_of(s)); };
+    struct Step { QuadStep<ENC> q[QPW]; };
+    auto load = [&](int s) {
+        Step v;
+#pragma unroll
+        for (int q = 0; q < QPW; ++q)
+            v.q[q] = r3d_quad_load<ENC>(wrs, wo0[q], wo1[q], grp_of(s), s < ns);
+        return v;
+    };
 
     /* Scheduling barriers keep each step's loads in step order, in the prologue as in the
      * loop, so every wait is "the oldest step's loads".  The launch picks D <= ns. */
-    QuadStep<ENC> ring[D];
+    Step ring[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         ring[d] = load(d);
@@ -267,50 +234,60 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
      * then meet the other waves */
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(D * LPS) : "memory");
 
-    /* ---- 3. consume: B operand, a_scale and weight scales from LDS (byte addresses) */
+    /* ---- 3. consume: B operand, a_scale and weight scales from LDS.  These are ordinary
+     * LDS reads: the compiler knows nothing of the LDS fill (inline asm above), so it
+     * waits only on lgkmcnt for them. */
     const int tB = MT == 1 ? 0 : wr;
-    const uint32_t xrow = lds0 + (uint32_t)(tB * (K + 16) + 16 * kq);
-    const uint32_t xs = lds0 + (uint32_t)(xs_off + 4 * tB * groups);
-    r3d_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint8_t* xrow = smem + tB * (K + 16) + 16 * kq;
+    const float* xs = reinterpret_cast<const float*>(smem + xs_off) + tB * groups;
+    const uint8_t* sc = smem + sc_off + (ENC == ENC_MXFP4A8 ? 0 : wave * sc_bytes);
+    r3d_f32x4 acc[QPW];
+#pragma unroll
+    for (int q = 0; q < QPW; ++q) acc[q] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto consume = [&](const QuadStep<ENC>& v, int s) {
+    auto consume = [&](const Step& v, int s) {
+        const uint32_t gb = grp_of(s);
+        const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(xrow + 128 * gb);
+        const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(xrow + 128 * gb + 64);
+        const r3d_i32x8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         const int su = 4 * s + kq;                        /* the used lanes' slot in the chunk */
-        const int gs = g0 + su < groups ? g0 + su : groups - 1;
-        uint32_t sca;
-        if (ENC == ENC_MXFP4A8) {
-            const int sl = 4 * s + wg < gc ? 4 * s + wg : gc - 1;
-            sca = scl + (uint32_t)(wr * 4 * gmax + 4 * sl + kq);
-        } else {
-            sca = scl + (uint32_t)(16 * (su < gc ? su : gc - 1));
-        }
-        const QuadLds l = r3d_quad_lds<ENC>(xrow + 128 * grp_of(s), xs + 4 * (uint32_t)gs, sca);
-        const r3d_i32x8 bv = {l.lo[0], l.lo[1], l.lo[2], l.lo[3], l.hi[0], l.hi[1], l.hi[2], l.hi[3]};
+        const float a_s = xs[g0 + su < groups ? g0 + su : groups - 1];
         const bool live = su < gc;
-        if (ENC == ENC_MXFP4A8) {
-            const r3d_f32x4 d = r3d_mfma_fp4_fp8(v.w0, l.sb[0], bv, R3D_E8M0_ONE);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] += live ? d[i] * l.as : 0.0f;
-        } else {
-            const bool own = wr < 2;
-            r3d_i32x4 wl, wh;
+        for (int q = 0; q < QPW; ++q) {
+            if (ENC == ENC_MXFP4A8) {
+                const int sl = 4 * s + wg < gc ? 4 * s + wg : gc - 1;
+                const int sa = sc[(bi * RB + 4 * q + wr) * 4 * groups + 4 * (g0 + sl) + kq];
+                const r3d_f32x4 d = r3d_mfma_fp4_fp8(v.q[q].w0, sa, bv, R3D_E8M0_ONE);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                wl[i] = own ? v.w0[i] : v.w1[i];
-                /* quad_perm [2,3,0,1]: lane l takes lane l ^ 2's other half */
-                wh[i] = __builtin_amdgcn_mov_dpp(own ? v.w1[i] : v.w0[i], 0x4E, 0xF, 0xF, false);
-            }
-            const r3d_i32x8 wv = {wl[0], wl[1], wl[2], wl[3], wh[0], wh[1], wh[2], wh[3]};
-            const r3d_f32x4 d = r3d_mfma_fp8_fp8(wv, bv);
+                for (int i = 0; i < 4; ++i) acc[q][i] += live ? d[i] * a_s : 0.0f;
+            } else {
+                const bool own = wr < 2;
+                r3d_i32x4 wl, wh;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float sbv = __uint_as_float((uint32_t)l.sb[i] << 16);
-                acc[i] += live ? (d[i] * l.as) * sbv : 0.0f;
+                for (int i = 0; i < 4; ++i) {
+                    wl[i] = own ? v.q[q].w0[i] : v.q[q].w1[i];
+                    /* quad_perm [2,3,0,1]: lane l takes lane l ^ 2's other half */
+                    wh[i] = __builtin_amdgcn_mov_dpp(own ? v.q[q].w1[i] : v.q[q].w0[i], 0x4E,
+                                                     0xF, 0xF, false);
+                }
+                const r3d_i32x8 wv = {wl[0], wl[1], wl[2], wl[3], wh[0], wh[1], wh[2], wh[3]};
+                const r3d_f32x4 d = r3d_mfma_fp8_fp8(wv, bv);
+                const int sl = su < gc ? su : gc - 1;
+                const r3d_i32x4 sb = *reinterpret_cast<const r3d_i32x4*>(sc + 4 * (sl * RB + 4 * q));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float sbv = __uint_as_float((uint32_t)sb[i] << 16);
+                    acc[q][i] += live ? (d[i] * a_s) * sbv : 0.0f;
+                }
             }
         }
     };
 
-    /* whole blocks of D steps while a full block of loads remains, then the static tail:
-     * exactly ns steps are loaded and consumed */
+    /* Whole blocks of D steps while a full block of real loads remains; then one block that
+     * loads the last (fewer than D) steps, skipping the rest; then the last steps, with no
+     * loads.  Every wave loads and consumes exactly its ns steps (plus at most D - 1
+     * skipped loads). */
     int s0 = 0;
     for (; s0 + 2 * D <= ns; s0 += D) {
 #pragma unroll
@@ -320,22 +297,42 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    quad_tail_at<0, D>(ns - s0 - D, ring, s0, consume, load);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        consume(ring[d], s0 + d);
+        ring[d] = load(s0 + d + D);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if (s0 + D + d < ns) consume(ring[d], s0 + D + d);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    /* The accumulators are complete here in every lane: without this the compiler may sink
+     * the last MFMAs into the used-lanes-only branch below, where a partial exec mask
+     * corrupts them (an MFMA reads its operands across the whole wave). */
+#pragma unroll
+    for (int q = 0; q < QPW; ++q) asm volatile("" : "+v"(acc[q]));
 
     /* ---- 4. fold: used lanes (kq == wg) hold slot kq's partials of activation row wr;
      * sum slots then chunks in a fixed order */
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   /* LDS reads done */
     r3d_f32x4* red = reinterpret_cast<r3d_f32x4*>(smem);
-    if (kq == wg) red[wave * 16 + 4 * kq + wr] = acc;
+    if (kq == wg)
+#pragma unroll
+        for (int q = 0; q < QPW; ++q) red[(wave * QPW + q) * 16 + 4 * kq + wr] = acc[q];
     __syncthreads();
     const int tid = threadIdx.x;
-    if (tid < qpb * 4 * MT) {
-        const int q = tid / (4 * MT), i = (tid / MT) & 3, t = tid % MT;
+    if (tid < bpb * RB * MT) {
+        const int b = tid / (RB * MT), r = (tid / MT) % RB, t = tid % MT;
+        const int q = r >> 2, i = r & 3;
         const float* rf = reinterpret_cast<const float*>(smem);
         float y = 0.0f;
         for (int cc = 0; cc < chunks; ++cc)
-            for (int g = 0; g < 4; ++g) y += rf[((q * chunks + cc) * 16 + 4 * g + t) * 4 + i];
-        const int64_t n = n0 - 4 * qi + 4 * q + i;
+            for (int g = 0; g < 4; ++g)
+                y += rf[(((b * chunks + cc) * QPW + q) * 16 + 4 * g + t) * 4 + i];
+        const int64_t n = ((int64_t)blockIdx.x * bpb + b) * RB + r;
         if (t < M && n < N) Y[(int64_t)t * y_pitch + n] = r3d_bf16_rne(y);
     }
 }

@@ -119,6 +119,7 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     P->y_pitch = row_stride(Y, N);
     P->as_pitch = row_stride(AS, as_cols);
     P->bs_pitch = row_stride(BS, bs_cols);
+    if (P->bs_pitch & 3) return RAD_E_UNSUPPORTED;               /* dword scale walk */
     P->as_cols = (int)as_cols;
     P->bs_cols = (int)bs_cols;
     P->rblk = 1;
@@ -184,6 +185,7 @@ int plan_mxfp4a16(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     P->y_pitch = row_stride(Y, N);
     P->as_pitch = K / 32;                                     /* of the scratch E8M0 plane */
     P->bs_pitch = row_stride(BS, bs_cols);
+    if (P->bs_pitch & 3) return RAD_E_UNSUPPORTED;               /* dword scale walk */
     P->as_cols = (int)(K / 32);
     P->bs_cols = (int)bs_cols;
     P->rblk = 1;
@@ -293,7 +295,7 @@ void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGe
     g->blocks = (g->tiles + g->tiles_per_block - 1) / g->tiles_per_block;
 }
 
-bool quad_fits(const GemmPlan& P) { return 4 * P.b_pitch < ((int64_t)1 << 31); }
+bool quad_fits(const GemmPlan& P) { return 8 * P.b_pitch < ((int64_t)1 << 31); }
 
 /* Quad geometry: split K until about env_quad_waves() waves are in flight, keeping >= 16
  * groups per chunk. */
@@ -302,19 +304,21 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     if (force_chunks > 0 && force_chunks != 1 && force_chunks != 2 && force_chunks != 4)
         return false;
     g->mt = M <= 1 ? 1 : 4;
+    g->qpw = env_quad_qpw();
     g->groups = (int)(K / 128);
     g->quads = (N + 3) / 4;
+    g->nblk = (N + 4 * g->qpw - 1) / (4 * g->qpw);
     const int64_t target = env_quad_waves();
     int c = 1;
     if (force_chunks > 0) {
         c = (int)force_chunks;
     } else {
-        while (c < 4 && g->quads * c < target && g->groups >= 16 * c) c *= 2;
+        while (c < 4 && g->nblk * c < target && g->groups >= 16 * c) c *= 2;
     }
     while (c > 1 && c > g->groups) c >>= 1;
     g->chunks = c;
-    g->qpb = 4 / c;
-    g->blocks = (g->quads + g->qpb - 1) / g->qpb;
+    g->bpb = 4 / c;
+    g->blocks = (g->nblk + g->bpb - 1) / g->bpb;
     g->gmax = (g->groups + c - 1) / c;
     {
         /* the deepest supported ring that no wave's step count falls below */
@@ -327,8 +331,12 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     }
     const int64_t blob = ((int64_t)g->mt * (K + 16) + 1023) / 1024 * 1024;
     const int64_t xs = ((int64_t)g->mt * g->groups * 4 + 255) / 256 * 256;
-    const int64_t scb = (16 * (int64_t)g->gmax + 255) / 256 * 256;
-    const int64_t lds = blob + xs + 4 * scb;
+    /* weight scales: mxfp4a8 stages the workgroup's rows over the whole K (1 KB loads),
+     * fp8a8 each wave's rows over its chunk */
+    const int64_t rbw = 4 * (int64_t)g->qpw * g->bpb;
+    const int64_t scb = enc == ENC_MXFP4A8 ? (rbw * 4 * g->groups + 1023) / 1024 * 1024
+                                           : (16 * g->qpw * (int64_t)g->gmax + 255) / 256 * 256;
+    const int64_t lds = blob + xs + (enc == ENC_MXFP4A8 ? scb : 4 * scb);
     if (lds > kQuadMaxLds || g->blocks > 0x7FFFFFFF) return false;
     g->xs_off = (int)blob;
     g->sc_off = (int)(blob + xs);
@@ -388,7 +396,15 @@ int64_t env_quad_waves() {
     static const int64_t v = [] {
         const char* e = getenv("R3D_GFX950_QWAVES");
         const int64_t w = e ? (int64_t)atoll(e) : 0;
-        return w > 0 ? w : (int64_t)4096;
+        return w > 0 ? w : (int64_t)2048;
+    }();
+    return v;
+}
+
+int env_quad_qpw() {
+    static const int v = [] {
+        const char* e = getenv("R3D_GFX950_QPW");
+        return e && atoi(e) == 2 ? 2 : 1;
     }();
     return v;
 }
@@ -426,9 +442,9 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
     QuadGeom qg{};
     if (dec && quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &qg)) {
         snprintf(buf, (size_t)len,
-                 "arm=decode kernel=quad enc=%s M=%lld N=%lld K=%lld mt=%d chunks=%d waves=4 "
-                 "quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d",
-                 ename, (long long)P.M, (long long)P.N, (long long)P.K, qg.mt, qg.chunks,
+                 "arm=decode kernel=quad enc=%s M=%lld N=%lld K=%lld mt=%d qpw=%d chunks=%d "
+                 "waves=4 quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d",
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K, qg.mt, qg.qpw, qg.chunks,
                  (long long)qg.quads, (long long)qg.blocks, qg.groups, qg.depth, qg.lds, P.rblk);
     } else if (dec) {
         DecodeGeom g{};

@@ -50,19 +50,20 @@ struct DecodeGeom {
     int steps;               /* K / 128 */
 };
 
-/* Launch geometry of the quad decode GEMV (M <= 4): one wave per quad of 4 weight rows and
- * K chunk, 4 waves per workgroup (4 / chunks quads x chunks). */
+/* Launch geometry of the quad decode GEMV (M <= 4): one wave per block of qpw quads (4
+ * weight rows each) and K chunk, 4 waves per workgroup (4 / chunks blocks x chunks). */
 struct QuadGeom {
     int mt;                  /* activation rows of the instantiation: 1 or 4 */
-    int chunks;              /* waves per quad (split-K): 1, 2 or 4 */
-    int qpb;                 /* quads per workgroup: 4 / chunks */
+    int qpw;                 /* quads per wave: 1 or 2 */
+    int chunks;              /* waves per row block (split-K): 1, 2 or 4 */
+    int bpb;                 /* row blocks per workgroup: 4 / chunks */
     int groups;              /* K / 128 */
     int gmax;                /* most groups one chunk holds: ceil(groups / chunks) */
     int depth;               /* ring depth in K steps (<= every wave's step count) */
-    int64_t quads, blocks;
+    int64_t quads, nblk, blocks;   /* ceil(N/4); row blocks of 4 qpw rows; workgroups */
     int xs_off;              /* LDS: activation rows at 0 ([mt][K + 16], 1 KB rounded),
                                 a_scales ([mt][groups] f32) at xs_off */
-    int sc_off, sc_bytes;    /* LDS: per-wave weight scales */
+    int sc_off, sc_bytes;    /* LDS: weight scales (mxfp4a8: per workgroup; fp8a8: per wave) */
     int lds;                 /* dynamic LDS bytes per workgroup */
 };
 
@@ -108,8 +109,8 @@ void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGe
  * leaves the quad kernel. */
 constexpr int kQuadMaxLds = 48 * 1024;
 bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, QuadGeom* g);
-/* The quad kernel addresses a quad's 4 weight rows through one buffer resource: they must
- * span less than 2^31 bytes. */
+/* The quad kernel addresses a wave's (up to 8) weight rows through one buffer resource:
+ * they must span less than 2^31 bytes. */
 bool quad_fits(const GemmPlan& P);
 void tile_geom(int64_t M, int64_t N, TileGeom* g);
 /* mode: 0 = e4m3 activations with f32 scale per 128 (mxfp4a8), 1 = mxfp8 (mxfp4a16);
@@ -124,8 +125,9 @@ bool env_no_fp8a8();        /* R3D_NO_FP8A8: all fp8a8 rows */
 bool env_no_fp8_dec();      /* R3D_NO_FP8_DEC: the fp8a8 decode row */
 bool env_debug();           /* R3D_DEBUG_GEMM: one stderr line per distinct launch arm */
 int64_t env_splitk();       /* R3D_GFX950_SPLITK: force the decode chunk count (0 = policy) */
-int64_t env_quad_waves();   /* R3D_GFX950_QWAVES: waves the quad split aims for (default 4096) */
+int64_t env_quad_waves();   /* R3D_GFX950_QWAVES: waves the quad split aims for (default 2048) */
 int env_quad_depth(int enc);/* R3D_GFX950_QD: quad ring depth 1/2/4/8 (default 4) */
+int env_quad_qpw();         /* R3D_GFX950_QPW: quads per wave of the quad GEMV, 1 or 2 (default 1) */
 
 /* The decode rows' "splitk" tunable (RadArgs::tv): chunks per tile, 0 = the policy.  An
  * engine-chosen value wins over R3D_GFX950_SPLITK. */

@@ -97,6 +97,32 @@ def test_fp8_decode_small(gpu, M, rblk):
     _check(F8_DEC, "fp8a8", A, AS, B, BS, M, 200, 640, gpu, rblk=rblk)
 
 
+@pytest.mark.parametrize("pad,offset", [(4, 0), (0, 4), (12, 8)])
+def test_mxfp4_decode_scale_plane_layouts(gpu, pad, offset):
+    """The E8M0 plane as a padded-pitch and/or 4-byte (not 16-byte) aligned view: the decode
+    GEMV must stage it row by row instead of as one contiguous run, with the same result."""
+    import torch
+    gu = _gu()
+    M, N, K = 1, 300, 2560
+    A, AS, B, BS = _mx_case(M, N, K, 40 + pad + offset)
+    wide = np.zeros((N, K // 32 + pad), np.uint8)
+    wide[:, :K // 32] = BS
+    flat = np.concatenate([np.zeros(offset, np.uint8), wide.reshape(-1)])
+    gA, gAS, gB, gW = (gu.Guarded(x, gpu) for x in (A, AS, B, flat))
+    bs = gW.t[offset:].view(N, K // 32 + pad)[:, :K // 32]
+    gY = gu.y_buffer(M, N, gpu)
+    ops = R.GemmOperands(gA.t, gAS.t, gB.t, bs, gY.t, dtype="mxfp4a8", N=N, K=K)
+    rc = R.launch_row(MX_DEC, ops, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == R.RAD_OK
+    assert all(g.guards_intact() for g in (gA, gAS, gB, gW, gY))
+    Y = gY.t.cpu().numpy().view(np.uint16).reshape(M, N)
+    Yr, Yf, S = O.quant_dot_mxfp4a8(A, AS, B, BS)
+    S8 = O.group8_mag("mxfp4a8", A, AS, B, BS)
+    c = gu.compare(Y, Yr, Yf, S, K, S8)
+    assert c["sentinel_left"] == 0 and c["max_viol"] <= 1.0, c
+
+
 @pytest.mark.parametrize("N,K", [(17, 256), (1001, 4096), (4096, 1152), (6, 21504)])
 @pytest.mark.parametrize("rblk", [1, 128])
 def test_fp8_decode_shapes(gpu, N, K, rblk):
