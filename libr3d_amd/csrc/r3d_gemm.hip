@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include "r3d_gemm_kernels.h"
+#include "r3d_gemv_lines.h"
 #include "r3d_gemv_quad.h"
 #include "r3d_plan.h"
 #include "r3d_prefill.h"
@@ -105,10 +106,54 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
     return RAD_OK;
 }
 
+static int launch_lines(const GemmPlan& P, const LinesGeom& g, hipStream_t stream) {
+    const dim3 grid((unsigned)g.blocks), block(256);
+#define R3D_LINES(ENC_, MT_, TW_, D_)                                                        \
+    hipLaunchKernelGGL((gemv_lines_kernel<ENC_, MT_, TW_, D_>), grid, block, (size_t)g.lds,    \
+                       stream, P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K,        \
+                       g.chunks, P.rblk, g.gmax, g.wlds, P.a_pitch, P.as_pitch, P.b_pitch,    \
+                       P.bs_pitch, P.y_pitch)
+#define R3D_LINES_T(ENC_, MT_, D_)                                                           \
+    do {                                                                                     \
+        if (g.tw == 4) R3D_LINES(ENC_, MT_, 4, (D_ > 2 ? 2 : D_));                           \
+        else if (g.tw == 2) R3D_LINES(ENC_, MT_, 2, D_);                                     \
+        else R3D_LINES(ENC_, MT_, 1, D_);                                                    \
+    } while (0)
+#define R3D_LINES_D(ENC_, MT_)                                                               \
+    do {                                                                                     \
+        switch (g.depth) {                                                                   \
+        case 4: R3D_LINES_T(ENC_, MT_, 4); break;                                            \
+        case 2: R3D_LINES_T(ENC_, MT_, 2); break;                                            \
+        default: R3D_LINES_T(ENC_, MT_, 1); break;                                           \
+        }                                                                                    \
+    } while (0)
+    if (P.enc == ENC_MXFP4A8) {
+        if (g.mt == 8) R3D_LINES_D(ENC_MXFP4A8, 8);
+        else R3D_LINES_D(ENC_MXFP4A8, 16);
+    } else {
+        if (g.mt == 8) R3D_LINES_D(ENC_FP8A8, 8);
+        else R3D_LINES_D(ENC_FP8A8, 16);
+    }
+#undef R3D_LINES_T
+#undef R3D_LINES_D
+#undef R3D_LINES
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "libr3d_gfx950: line decode GEMV launch FAILED (%s)\n", hipGetErrorName(e));
+        return RAD_E_DEVICE;
+    }
+    debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 line decode GEMV" : "fp8a8 line decode GEMV",
+               192 + (P.enc << 4) + g.mt);
+    return RAD_OK;
+}
+
 static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) {
     QuadGeom qg{};
     if (quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg))
         return launch_quad(P, qg, stream);
+    LinesGeom lg{};
+    if (lines_fits(P) && lines_geom(P.enc, P.M, P.N, P.K, splitk, &lg))
+        return launch_lines(P, lg, stream);
     DecodeGeom g{};
     decode_geom(P.M, P.N, P.K, splitk, &g, gemv_wave_lds(P.enc, P.M <= 1 ? 1 : P.M <= 4 ? 4 : 16));
     const dim3 grid((unsigned)g.blocks), block((unsigned)(64 * g.waves));
@@ -216,7 +261,7 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
         return RAD_E_DEVICE;
     }
     debug_once(mode == PF_MX8 ? "mxfp4a16 prefill (mxfp8 quantiser + MFMA)" : "mxfp4a8 prefill",
-               128 + 8 * mode + g.wnf);
+               160 + 8 * mode + g.wnf);
     return RAD_OK;
 }
 

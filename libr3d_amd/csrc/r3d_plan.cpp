@@ -345,6 +345,63 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     return true;
 }
 
+bool lines_fits(const GemmPlan& P) {
+    const int64_t lim = (int64_t)1 << 31;
+    return 64 * P.b_pitch < lim && (P.M - 1) * P.a_pitch + P.K < lim;   /* up to 4 tiles */
+}
+
+/* Line geometry: tw tiles per wave (policy or R3D_GFX950_LTW), then split K until about
+ * env_lines_waves() waves are in flight (keeping >= 4 lines per chunk), or until a wave's
+ * scale tables fit the LDS budget. */
+bool lines_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, LinesGeom* g) {
+    if (M < 1 || M > 16 || N < 1 || K < 128 || K % 128 != 0) return false;
+    if (enc != ENC_MXFP4A8 && enc != ENC_FP8A8) return false;
+    if (force_chunks > 0 && force_chunks != 1 && force_chunks != 2 && force_chunks != 4)
+        return false;
+    const int G = enc == ENC_MXFP4A8 ? 2 : 1;
+    g->mt = M <= 8 ? 8 : 16;
+    g->groups = (int)(K / 128);
+    g->units = (g->groups + G - 1) / G;
+    g->tiles = (N + 15) / 16;
+    /* two tiles per wave halve the activation loads per weight byte; measured best on
+     * MI355X at the 27B-class shapes (M = 8..16) */
+    const int etw = env_lines_tw();
+    g->tw = etw == 1 || etw == 2 || etw == 4 ? etw : 2;
+    g->nblk = (g->tiles + g->tw - 1) / g->tw;
+    auto wlds_of = [&](int c) {
+        const int gm = G * ((g->units + c - 1) / c);
+        return (64 * gm + 255) / 256 * 256 + (64 * g->tw * gm + 255) / 256 * 256;
+    };
+    int c = 1;
+    if (force_chunks > 0) {
+        c = (int)force_chunks;
+    } else {
+        const int64_t target = env_lines_waves();
+        while (c < 4 && g->units >= 8 * c &&
+               (g->nblk * c < target || 4 * wlds_of(c) > kLinesMaxLds))
+            c *= 2;
+    }
+    while (c > 1 && c > g->units) c >>= 1;
+    g->chunks = c;
+    g->tpb = 4 / c;
+    g->blocks = (g->nblk + g->tpb - 1) / g->tpb;
+    g->gmax = G * ((g->units + c - 1) / c);
+    g->wlds = wlds_of(c);
+    const int fold = 4 * 1024 * g->tw;
+    g->lds = 4 * g->wlds > fold ? 4 * g->wlds : fold;
+    {
+        static const int kDepths[] = {4, 2, 1};
+        const int ns_min = g->units / c;
+        const int ed = env_lines_depth();
+        int want = ed > 0 ? ed : (g->tw >= 2 ? 2 : 4);   /* measured best */
+        if (g->tw >= 4 && want > 2) want = 2;             /* register budget */
+        g->depth = 1;
+        for (int d : kDepths)
+            if (d <= want && d <= ns_min) { g->depth = d; break; }
+    }
+    return g->lds <= kLinesMaxLds && g->blocks <= 0x7FFFFFFF;
+}
+
 void tile_geom(int64_t M, int64_t N, TileGeom* g) {
     g->bm = 128;
     g->bn = 128;
@@ -409,6 +466,31 @@ int env_quad_qpw() {
     return v;
 }
 
+int64_t env_lines_waves() {
+    static const int64_t v = [] {
+        const char* e = getenv("R3D_GFX950_LWAVES");
+        const int64_t w = e ? (int64_t)atoll(e) : 0;
+        return w > 0 ? w : (int64_t)4096;
+    }();
+    return v;
+}
+
+int env_lines_depth() {
+    static const int v = [] {
+        const char* e = getenv("R3D_GFX950_LD");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+int env_lines_tw() {
+    static const int v = [] {
+        const char* e = getenv("R3D_GFX950_LTW");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
 int env_quad_depth(int enc) {
     static const int v = [] {
         const char* e = getenv("R3D_GFX950_QD");
@@ -446,6 +528,13 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
                  "waves=4 quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d",
                  ename, (long long)P.M, (long long)P.N, (long long)P.K, qg.mt, qg.qpw, qg.chunks,
                  (long long)qg.quads, (long long)qg.blocks, qg.groups, qg.depth, qg.lds, P.rblk);
+    } else if (LinesGeom lg{}; dec && lines_fits(P) &&
+               lines_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &lg)) {
+        snprintf(buf, (size_t)len,
+                 "arm=decode kernel=lines enc=%s M=%lld N=%lld K=%lld mt=%d tw=%d chunks=%d waves=4 "
+                 "tiles=%lld blocks=%lld units=%d depth=%d lds=%d rblk=%d",
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K, lg.mt, lg.tw, lg.chunks,
+                 (long long)lg.tiles, (long long)lg.blocks, lg.units, lg.depth, lg.lds, P.rblk);
     } else if (dec) {
         DecodeGeom g{};
         decode_geom(P.M, P.N, P.K, decode_splitk(a), &g,

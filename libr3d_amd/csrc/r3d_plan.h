@@ -67,6 +67,22 @@ struct QuadGeom {
     int lds;                 /* dynamic LDS bytes per workgroup */
 };
 
+/* Launch geometry of the line GEMV (M <= 16): one wave per block of tw 16-row weight tiles
+ * and K chunk, 4 waves per workgroup (4 / chunks blocks x chunks); a unit is one 128-byte
+ * line of every row of the block (2 K groups at mxfp4a8, 1 at fp8a8). */
+struct LinesGeom {
+    int mt;                  /* activation rows of the instantiation: 8 or 16 */
+    int tw;                  /* 16-row tiles per wave: 1, 2 or 4 */
+    int chunks;              /* waves per row block (split-K): 1, 2 or 4 */
+    int tpb;                 /* row blocks (16 tw rows) per workgroup: 4 / chunks */
+    int groups, units;       /* K / 128; lines per row */
+    int gmax;                /* most K groups one chunk holds */
+    int depth;               /* ring depth in units (<= every wave's unit count) */
+    int wlds;                /* LDS bytes of one wave's scale tables */
+    int lds;                 /* dynamic LDS bytes per workgroup */
+    int64_t tiles, nblk, blocks;   /* ceil(N/16); row blocks of 16 tw rows; workgroups */
+};
+
 /* Launch geometry of the mxfp4 prefill GEMM (block-scaled MFMA, direct-to-LDS ring):
  * a workgroup of 8 waves (2 x 4) owns bn = 32 wnf weight rows x bm = 64 wmf tokens. */
 struct PrefillGeom {
@@ -112,6 +128,14 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
 /* The quad kernel addresses a wave's (up to 8) weight rows through one buffer resource:
  * they must span less than 2^31 bytes. */
 bool quad_fits(const GemmPlan& P);
+/* Line GEMV geometry; false when the shape is outside what it serves (M > 16, or a wave's
+ * scale tables over the LDS budget), and the 16-row GEMV runs instead.  force_chunks:
+ * 1/2/4 pin the split, anything else above 0 leaves the line kernel. */
+constexpr int kLinesMaxLds = 48 * 1024;
+bool lines_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, LinesGeom* g);
+/* The line kernel addresses a wave's (up to 64) weight rows and the whole activation plane through
+ * buffer resources: both must span less than 2^31 bytes. */
+bool lines_fits(const GemmPlan& P);
 void tile_geom(int64_t M, int64_t N, TileGeom* g);
 /* mode: 0 = e4m3 activations with f32 scale per 128 (mxfp4a8), 1 = mxfp8 (mxfp4a16);
  * ncu: compute units the launch can fill (tiles are sized so the last round of
@@ -128,6 +152,9 @@ int64_t env_splitk();       /* R3D_GFX950_SPLITK: force the decode chunk count (
 int64_t env_quad_waves();   /* R3D_GFX950_QWAVES: waves the quad split aims for (default 2048) */
 int env_quad_depth(int enc);/* R3D_GFX950_QD: quad ring depth 1/2/4/8 (default 4) */
 int env_quad_qpw();         /* R3D_GFX950_QPW: quads per wave of the quad GEMV, 1 or 2 (default 1) */
+int64_t env_lines_waves();  /* R3D_GFX950_LWAVES: waves the line GEMV's split aims for (default 4096) */
+int env_lines_depth();      /* R3D_GFX950_LD: line GEMV ring depth in units, 1/2/4 (0 = policy) */
+int env_lines_tw();         /* R3D_GFX950_LTW: 16-row tiles per wave of the line GEMV (0 = policy) */
 
 /* The decode rows' "splitk" tunable (RadArgs::tv): chunks per tile, 0 = the policy.  An
  * engine-chosen value wins over R3D_GFX950_SPLITK. */

@@ -97,6 +97,25 @@ def test_fp8_decode_small(gpu, M, rblk):
     _check(F8_DEC, "fp8a8", A, AS, B, BS, M, 200, 640, gpu, rblk=rblk)
 
 
+@pytest.mark.parametrize("N,K", [(17, 256), (40, 1152), (1001, 640), (300, 21504)])
+@pytest.mark.parametrize("M", [2, 5, 9, 16])
+def test_mxfp4_decode_lines_shapes(gpu, N, K, M):
+    """The 16-row line GEMV: ragged N, odd group counts (a half-used last line), and M = 2
+    at K = 21504, whose activation rows are too large for the quad GEMV's staging."""
+    A, AS, B, BS = _mx_case(M, N, K, 7 * N + K + M)
+    _check(MX_DEC, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+
+
+@pytest.mark.parametrize("N,K", [(17, 256), (1001, 640), (300, 21504)])
+@pytest.mark.parametrize("M", [2, 9, 16])
+@pytest.mark.parametrize("rblk", [1, 128])
+def test_fp8_decode_lines_shapes(gpu, N, K, M, rblk):
+    if rblk == 128 and N <= 128:
+        pytest.skip("one 128-row scale block: the grid is ambiguous and the plan refuses it")
+    A, AS, B, BS = _f8_case(M, N, K, 5 * N + K + M, rblk)
+    _check(F8_DEC, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk)
+
+
 @pytest.mark.parametrize("pad,offset", [(4, 0), (0, 4), (12, 8)])
 def test_mxfp4_decode_scale_plane_layouts(gpu, pad, offset):
     """The E8M0 plane as a padded-pitch and/or 4-byte (not 16-byte) aligned view: the decode
@@ -217,11 +236,12 @@ def test_decode_m_from_numel_y(gpu):
 
 @pytest.mark.parametrize("splitk", [1, 2, 4, 8])
 @pytest.mark.parametrize("dtype", ["mxfp4a8", "fp8a8"])
-def test_decode_splitk_deterministic(gpu, splitk, dtype):
+@pytest.mark.parametrize("M", [4, 16])
+def test_decode_splitk_deterministic(gpu, splitk, dtype, M):
     """Every chunk count (the decode rows' "splitk" tunable) stays in bound, and repeated
     calls are bit-identical (the LDS fold runs in chunk order)."""
     gu = _gu()
-    M, N, K = 4, 512, 2048
+    N, K = 512, 2048
     if dtype == "mxfp4a8":
         A, AS, B, BS = _mx_case(M, N, K, 77)
         row = MX_DEC
