@@ -157,7 +157,8 @@ def test_plan_accepts_and_derives_m_from_y():
     assert g["M"] == "3" and g["mt"] == "4"              # M = numel(y)/N; MT rounds up
 
 
-@pytest.mark.parametrize("M,mt", [(1, "1"), (2, "4"), (4, "4"), (5, "16"), (9, "16"), (16, "16")])
+@pytest.mark.parametrize("M,mt", [(1, "1"), (2, "4"), (4, "4"), (5, "8"), (8, "8"), (9, "16"),
+                                  (16, "16")])
 def test_mt_ladder_rounds_up(M, mt):
     ops, _ = _mx_ops(M=M)
     rc, d = R.describe("gemm_nt_q_mxfp4_decode", ops)
