@@ -1,6 +1,6 @@
-/* r3d_gemv_lines.h -- gfx950 decode GEMV for up to 16 activation rows (gemm_nt_q at
- * mxfp4a8 and fp8a8): M = 5..16, and M = 1..4 shapes whose whole-K activation rows are too
- * large for the quad GEMV's LDS staging.
+/* r3d_gemv_lines.h -- gfx950 decode GEMV for 5..16 activation rows (gemm_nt_q at mxfp4a8
+ * and fp8a8).  (MT = 8 also serves M <= 4 correctly; the launch policy sends those to the
+ * quad GEMV or the 16-row GEMV, measured faster there.)
  *
  * One wave owns a 16-row weight tile and one contiguous chunk of K; v_mfma_scale_f32_16x
  * 16x128_f8f6f4 takes the 16 weight rows as source A and 16 activation rows as source B,

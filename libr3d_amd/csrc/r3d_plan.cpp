@@ -354,7 +354,9 @@ bool lines_fits(const GemmPlan& P) {
  * env_lines_waves() waves are in flight (keeping >= 4 lines per chunk), or until a wave's
  * scale tables fit the LDS budget. */
 bool lines_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, LinesGeom* g) {
-    if (M < 1 || M > 16 || N < 1 || K < 128 || K % 128 != 0) return false;
+    /* M <= 4 shapes the quad GEMV cannot stage run faster on the 16-row GEMV's 4-row
+     * instantiation (measured on MI355X at K = 21504) */
+    if (M < 5 || M > 16 || N < 1 || K < 128 || K % 128 != 0) return false;
     if (enc != ENC_MXFP4A8 && enc != ENC_FP8A8) return false;
     if (force_chunks > 0 && force_chunks != 1 && force_chunks != 2 && force_chunks != 4)
         return false;

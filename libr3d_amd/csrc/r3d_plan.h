@@ -128,8 +128,8 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
 /* The quad kernel addresses a wave's (up to 8) weight rows through one buffer resource:
  * they must span less than 2^31 bytes. */
 bool quad_fits(const GemmPlan& P);
-/* Line GEMV geometry; false when the shape is outside what it serves (M > 16, or a wave's
- * scale tables over the LDS budget), and the 16-row GEMV runs instead.  force_chunks:
+/* Line GEMV geometry; false when the shape is outside what it serves (M outside 5..16, or a
+ * wave's scale tables over the LDS budget), and the 16-row GEMV runs instead.  force_chunks:
  * 1/2/4 pin the split, anything else above 0 leaves the line kernel. */
 constexpr int kLinesMaxLds = 48 * 1024;
 bool lines_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, LinesGeom* g);

@@ -174,13 +174,13 @@ def test_decode_band_bound_and_tile_any_m():
 
 def test_decode_geometry_policy():
     """M <= 4 runs the quad GEMV, split in K until ~2048 waves (>= 16 groups per chunk),
-    while its workgroup LDS (whole-K activation rows) stays <= 48 KB; else the line GEMV
-    (two 16-row tiles per wave), split until ~4096 waves (>= 4 lines per chunk); a pinned
-    split of 8 runs the 16-row GEMV."""
+    while its workgroup LDS (whole-K activation rows) stays <= 48 KB, else the 16-row GEMV;
+    M = 5..16 runs the line GEMV (two 16-row tiles per wave), split until ~4096 waves (>= 4
+    lines per chunk); a pinned split of 8 runs the 16-row GEMV."""
     for (M, N, K, kern, chunks) in [(1, 21504, 5376, "quad", "1"), (1, 5376, 21504, "quad", "2"),
                                     (1, 4096, 4096, "quad", "2"), (1, 1000, 4096, "quad", "4"),
                                     (1, 64, 256, "quad", "1"), (4, 8192, 5376, "quad", "1"),
-                                    (4, 5376, 21504, "lines", "4"), (16, 21504, 5376, "lines", "4"),
+                                    (4, 5376, 21504, "tile16", "2"), (16, 21504, 5376, "lines", "4"),
                                     (16, 5376, 21504, "lines", "4"), (8, 8192, 5376, "lines", "4"),
                                     (16, 64, 256, "lines", "1"), (16, 64, 2048, "lines", "2")]:
         ops, _ = _mx_ops(M=M, N=N, K=K)

@@ -100,8 +100,9 @@ def test_fp8_decode_small(gpu, M, rblk):
 @pytest.mark.parametrize("N,K", [(17, 256), (40, 1152), (1001, 640), (300, 21504)])
 @pytest.mark.parametrize("M", [2, 5, 9, 16])
 def test_mxfp4_decode_lines_shapes(gpu, N, K, M):
-    """The 16-row line GEMV: ragged N, odd group counts (a half-used last line), and M = 2
-    at K = 21504, whose activation rows are too large for the quad GEMV's staging."""
+    """The line GEMV (M = 5..16): ragged N, odd group counts (a half-used last line); M = 2
+    at K = 21504, whose activation rows are too large for the quad GEMV's staging, runs the
+    16-row GEMV."""
     A, AS, B, BS = _mx_case(M, N, K, 7 * N + K + M)
     _check(MX_DEC, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
 
