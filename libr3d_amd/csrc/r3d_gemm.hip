@@ -182,29 +182,11 @@ static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) 
     return RAD_OK;
 }
 
-/* The fp8a8 prefill tile. */
-static int launch_tile(const GemmPlan& P, hipStream_t stream) {
-    TileGeom g{};
-    tile_geom(P.M, P.N, &g);
-    if (g.grid_m > 65535) return RAD_E_SHAPE;
-    const dim3 grid((unsigned)g.grid_n, (unsigned)g.grid_m), block(256);
-    const int steps = (int)(P.K / 128);
-    hipLaunchKernelGGL((tile_kernel<ENC_FP8A8>), grid, block, 0, stream, P.A, P.AS, P.B,
-                       P.BS, P.Y, (int)P.M, (int)P.N, steps, P.rblk, P.a_pitch, P.as_pitch,
-                       P.b_pitch, P.bs_pitch, P.y_pitch);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        fprintf(stderr, "libr3d_gfx950: prefill tile launch FAILED (%s)\n", hipGetErrorName(e));
-        return RAD_E_DEVICE;
-    }
-    debug_once("fp8a8 prefill tile", 64 + P.enc);
-    return RAD_OK;
-}
-
-/* The mxfp4 prefill GEMM: mode PF_A8 reads A/AS as given (e4m3 + f32 per 128), mode
- * PF_MX8 reads the mxfp8 planes the quantiser left in P.scratch. */
+/* The prefill GEMM: mode PF_A8 reads A/AS as given (e4m3 + f32 per 128) against e2m1
+ * weights, PF_F8 the same activations against e4m3 weights with bf16 row scales, PF_MX8 the
+ * mxfp8 planes the quantiser left in P.scratch. */
 static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
-    const int mode = P.enc == ENC_MXFP4A16 ? PF_MX8 : PF_A8;
+    const int mode = P.enc == ENC_MXFP4A16 ? PF_MX8 : P.enc == ENC_FP8A8 ? PF_F8 : PF_A8;
     PrefillGeom g{};
     prefill_geom(P.M, P.N, P.K, mode, cu_count(), &g);
     if (g.tiles > 0x7FFFFFFF || g.grid_m > 0x7FFFFFFF) return RAD_E_SHAPE;
@@ -227,18 +209,20 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
     }
     /* the kernel addresses 256 rows of any operand with 32-bit lane offsets */
     const int64_t lim = (int64_t)1 << 31;
-    if (256 * a_pitch >= lim || 256 * P.b_pitch >= lim || 256 * P.bs_pitch >= lim ||
+    if (256 * a_pitch >= lim || 256 * P.b_pitch >= lim ||
+        256 * (mode == PF_F8 ? 2 * P.bs_pitch : P.bs_pitch) >= lim ||
         256 * (mode == PF_MX8 ? as_pitch : 4 * as_pitch) >= lim)
         return RAD_E_UNSUPPORTED;
     const dim3 grid((unsigned)g.tiles), block(512);
 #define R3D_PF(MODE_, WNF_, WMF_)                                                          \
-    static_assert(PrefillLayout<WNF_, WMF_, 3>::LDS == 3 * prefill_stage_bytes(WNF_, WMF_), \
+    static_assert(PrefillLayout<WNF_, WMF_, 3, MODE_ == PF_F8 ? 2 : 1>::LDS ==              \
+                      3 * prefill_stage_bytes(WNF_, WMF_, MODE_ == PF_F8 ? 2 : 1),          \
                   "host and kernel ring sizes differ");                                    \
     hipLaunchKernelGGL((prefill_kernel<MODE_, WNF_, WMF_>), grid, block,                    \
-                       (size_t)(PrefillLayout<WNF_, WMF_, 3>::LDS), stream, A, AS, P.B,     \
-                       (const uint8_t*)P.BS, P.Y, (int)P.M, (int)P.N, g.steps,             \
-                       (int)g.grid_m, (int)g.tiles, a_pitch, as_pitch, P.b_pitch,          \
-                       P.bs_pitch, P.y_pitch)
+                       (size_t)(PrefillLayout<WNF_, WMF_, 3, MODE_ == PF_F8 ? 2 : 1>::LDS),  \
+                       stream, A, AS, P.B, (const uint8_t*)P.BS, P.Y, (int)P.M, (int)P.N,  \
+                       g.steps, (int)g.grid_m, (int)g.tiles, P.rblk, a_pitch, as_pitch,     \
+                       P.b_pitch, P.bs_pitch, P.y_pitch)
     if (mode == PF_MX8) {
         switch (g.wnf) {
             case 8: R3D_PF(PF_MX8, 8, 4); break;
@@ -246,6 +230,8 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
             case 6: R3D_PF(PF_MX8, 6, 4); break;
             default: R3D_PF(PF_MX8, 4, 4); break;
         }
+    } else if (mode == PF_F8) {
+        R3D_PF(PF_F8, 4, 2);
     } else {
         switch (g.wnf) {
             case 8: R3D_PF(PF_A8, 8, 2); break;
@@ -260,7 +246,8 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
         fprintf(stderr, "libr3d_gfx950: prefill launch FAILED (%s)\n", hipGetErrorName(e));
         return RAD_E_DEVICE;
     }
-    debug_once(mode == PF_MX8 ? "mxfp4a16 prefill (mxfp8 quantiser + MFMA)" : "mxfp4a8 prefill",
+    debug_once(mode == PF_MX8 ? "mxfp4a16 prefill (mxfp8 quantiser + MFMA)"
+               : mode == PF_F8 ? "fp8a8 prefill" : "mxfp4a8 prefill",
                160 + 8 * mode + g.wnf);
     return RAD_OK;
 }
@@ -281,7 +268,7 @@ static int entry(const RadArgs* a, RadStream s, int enc, bool decode) {
     if (!chip_ok()) return RAD_E_UNSUPPORTED;
     hipStream_t stream = (hipStream_t)s;
     if (decode) return launch_decode(P, decode_splitk(a), stream);
-    return enc == ENC_FP8A8 ? launch_tile(P, stream) : launch_prefill(P, stream);
+    return launch_prefill(P, stream);
 }
 
 }  // namespace r3d

@@ -205,123 +205,6 @@ __global__ __launch_bounds__(512) void gemv_kernel(
     }
 }
 
-/* ---------------------------------------------------------------- prefill tile -----
- * 128 x 128 output tile per 256-thread workgroup (2 x 2 waves of 64 x 64), one 128-wide
- * K step per iteration staged through LDS.  Each step's MFMA results are scaled by
- * a_scale and added to f32 accumulators (the per-group flush), so the activation scale
- * is honoured exactly as in the decode kernel.  Rows past M / N stage zeros and are never
- * stored. */
-constexpr int kTileM = 128, kTileN = 128;
-constexpr int kWBytes = 64;                   /* mxfp4 bytes of one weight row per step */
-
-template <int ENC>
-__global__ __launch_bounds__(256) void tile_kernel(
-    const uint8_t* __restrict__ A, const float* __restrict__ AS,
-    const uint8_t* __restrict__ B, const void* __restrict__ BSv,
-    uint16_t* __restrict__ Y,
-    int M, int N, int steps, int rblk,
-    int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch) {
-    constexpr int WB = ENC == ENC_MXFP4A8 ? 64 : 128;        /* weight bytes per row-step */
-    constexpr int WP = WB + 16;                              /* padded LDS pitch */
-    constexpr int AP = 128 + 16;
-    __shared__ __attribute__((aligned(16))) uint8_t Ws[kTileN * WP];
-    __shared__ __attribute__((aligned(16))) uint8_t As[kTileM * AP];
-    __shared__ int Ss[kTileN];                               /* mxfp4: 4 E8M0 bytes per row */
-    __shared__ float SAs[kTileM];
-    __shared__ float SBs[kTileN];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wn = wave & 1, wm = wave >> 1;
-    const int q = lane >> 4, li = lane & 15;
-    const int64_t n0 = (int64_t)blockIdx.x * kTileN;
-    const int64_t m0 = (int64_t)blockIdx.y * kTileM;
-
-    r3d_f32x4 acc[4][4];
-    for (int a = 0; a < 4; ++a)
-        for (int b = 0; b < 4; ++b) acc[a][b] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    for (int s = 0; s < steps; ++s) {
-        /* stage weights: kTileN rows x WB bytes, 16 bytes per thread-iteration */
-        for (int idx = tid; idx < kTileN * (WB / 16); idx += 256) {
-            const int r = idx / (WB / 16), cpart = idx % (WB / 16);
-            const int64_t n = n0 + r;
-            r3d_i32x4 v = {0, 0, 0, 0};
-            if (n < N) v = r3d_ld16(B + n * b_pitch + (int64_t)s * WB + 16 * cpart);
-            *reinterpret_cast<r3d_i32x4*>(Ws + r * WP + 16 * cpart) = v;
-        }
-        for (int idx = tid; idx < kTileM * 8; idx += 256) {
-            const int r = idx >> 3, cpart = idx & 7;
-            const int64_t m = m0 + r;
-            r3d_i32x4 v = {0, 0, 0, 0};
-            if (m < M) v = r3d_ld16(A + m * a_pitch + (int64_t)s * 128 + 16 * cpart);
-            *reinterpret_cast<r3d_i32x4*>(As + r * AP + 16 * cpart) = v;
-        }
-        if (tid < kTileN) {
-            const int64_t n = n0 + tid;
-            const int64_t nc = n < N ? n : N - 1;
-            if (ENC == ENC_MXFP4A8) {
-                const uint8_t* bs = reinterpret_cast<const uint8_t*>(BSv) + nc * bs_pitch + 4 * (int64_t)s;
-                Ss[tid] = (int)bs[0] | ((int)bs[1] << 8) | ((int)bs[2] << 16) | ((int)bs[3] << 24);
-            } else {
-                const uint16_t* bs = reinterpret_cast<const uint16_t*>(BSv);
-                SBs[tid] = r3d_bf16_to_f32(bs[(nc / rblk) * bs_pitch + s]);
-            }
-        } else {
-            const int r = tid - kTileN;
-            const int64_t m = m0 + r;
-            SAs[r] = m < M ? AS[m * as_pitch + s] : 0.0f;
-        }
-        __syncthreads();
-
-        r3d_i32x8 bop[4];
-        float sam[4];
-        for (int mi = 0; mi < 4; ++mi) {
-            const int r = wm * 64 + mi * 16 + li;
-            const uint8_t* p = As + r * AP;
-            const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(p + 16 * q);
-            const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(p + 64 + 16 * q);
-            bop[mi] = r3d_i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            sam[mi] = SAs[r];
-        }
-        for (int ni = 0; ni < 4; ++ni) {
-            const int r = wn * 64 + ni * 16 + li;
-            if (ENC == ENC_MXFP4A8) {
-                const r3d_i32x4 w = *reinterpret_cast<const r3d_i32x4*>(Ws + r * WP + 16 * q);
-                const int scb = (Ss[r] >> (8 * q)) & 0xFF;
-                for (int mi = 0; mi < 4; ++mi) {
-                    const r3d_f32x4 d = r3d_mfma_fp4_fp8(w, scb, bop[mi], R3D_E8M0_ONE);
-                    for (int i = 0; i < 4; ++i) acc[ni][mi][i] = acc[ni][mi][i] + d[i] * sam[mi];
-                }
-            } else {
-                const uint8_t* p = Ws + r * WP;
-                const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(p + 16 * q);
-                const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(p + 64 + 16 * q);
-                const r3d_i32x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                float sbr[4];
-                for (int i = 0; i < 4; ++i) sbr[i] = SBs[wn * 64 + ni * 16 + 4 * q + i];
-                for (int mi = 0; mi < 4; ++mi) {
-                    const r3d_f32x4 d = r3d_mfma_fp8_fp8(w, bop[mi]);
-                    for (int i = 0; i < 4; ++i)
-                        acc[ni][mi][i] = acc[ni][mi][i] + (d[i] * sam[mi]) * sbr[i];
-                }
-            }
-        }
-        __syncthreads();
-    }
-
-    for (int ni = 0; ni < 4; ++ni)
-        for (int mi = 0; mi < 4; ++mi) {
-            const int64_t m = m0 + wm * 64 + mi * 16 + li;
-            if (m >= M) continue;
-            uint16_t* yrow = Y + m * y_pitch;
-            for (int i = 0; i < 4; ++i) {
-                const int64_t n = n0 + wn * 64 + ni * 16 + 4 * q + i;
-                if (n < N) yrow[n] = r3d_bf16_rne(acc[ni][mi][i]);
-            }
-        }
-}
-
 }  // namespace r3d
 
 #endif /* R3D_GEMM_KERNELS_H */

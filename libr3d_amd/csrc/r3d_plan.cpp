@@ -404,29 +404,29 @@ bool lines_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, 
     return g->lds <= kLinesMaxLds && g->blocks <= 0x7FFFFFFF;
 }
 
-void tile_geom(int64_t M, int64_t N, TileGeom* g) {
-    g->bm = 128;
-    g->bn = 128;
-    g->grid_m = (M + g->bm - 1) / g->bm;
-    g->grid_n = (N + g->bn - 1) / g->bn;
-}
-
 /* Prefill tile choice: 64 wmw tokens (4 fragments per wave in mxfp8 mode, where the
  * MFMA accumulates in place; 2 in the f32-a_scale mode, whose per-step flush needs a
  * second register set) by 32 wnf weight rows.  Workgroups run one per CU, so the launch
  * takes ceil(tiles / ncu) rounds; a round costs about wnf + 1/2 fragment-steps (the
  * fixed activation reads of a step).  The cheapest total wins, ties to the larger tile. */
 void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeom* g) {
+    /* e4m3 weights: two 8-register operand sets, the row scales and two f32 result sets per
+     * fragment hold the tile at 4 fragment pairs (at 6, 185 registers spill) */
     static const int kWnf[] = {8, 7, 6, 4};
+    static const int kWnfF8[] = {4};
     const int wmw = mode == PF_MX8 ? 4 : 2;
     if (ncu <= 0) ncu = 256;
-    int best = 8;
+    int best = 0;
     double best_cost = 0.0;
-    for (int w : kWnf) {
+    auto consider = [&](int w) {
         const int64_t tiles = ((N + 32 * w - 1) / (32 * w)) * ((M + 64 * wmw - 1) / (64 * wmw));
         const double cost = (double)((tiles + ncu - 1) / ncu) * (w + 0.5);
-        if (w == 8 || cost < best_cost) { best = w; best_cost = cost; }
-    }
+        if (best == 0 || cost < best_cost) { best = w; best_cost = cost; }
+    };
+    if (mode == PF_F8)
+        for (int w : kWnfF8) consider(w);
+    else
+        for (int w : kWnf) consider(w);
     g->wnf = best;
     g->wmf = wmw;
     g->nst = 3;
@@ -436,7 +436,7 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
     g->grid_n = (N + g->bn - 1) / g->bn;
     g->tiles = g->grid_m * g->grid_n;
     g->steps = (int)(K / 128);
-    g->lds = g->nst * prefill_stage_bytes(g->wnf, g->wmf);
+    g->lds = g->nst * prefill_stage_bytes(g->wnf, g->wmf, mode == PF_F8 ? 2 : 1);
 }
 
 bool env_no_mxfp4()   { static const bool v = getenv("R3D_NO_MXFP4") != nullptr;   return v; }
@@ -547,22 +547,16 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
                  ename, (long long)P.M, (long long)P.N, (long long)P.K,
                  g.mt, g.chunks, g.waves, (long long)g.tiles, (long long)g.blocks, g.steps,
                  P.rblk);
-    } else if (mx) {
+    } else {
+        const int mode = a16 ? PF_MX8 : mx ? PF_A8 : PF_F8;
         PrefillGeom g{};
-        prefill_geom(P.M, P.N, P.K, a16 ? PF_MX8 : PF_A8, 256, &g);
+        prefill_geom(P.M, P.N, P.K, mode, 256, &g);
         snprintf(buf, (size_t)len,
                  "arm=prefill enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d grid=%lldx%lld "
-                 "tiles=%lld nst=%d lds=%d steps=%d",
+                 "tiles=%lld nst=%d lds=%d steps=%d rblk=%d",
                  ename, (long long)P.M, (long long)P.N, (long long)P.K, g.bn, g.bm,
                  (long long)g.grid_n, (long long)g.grid_m, (long long)g.tiles, g.nst, g.lds,
-                 g.steps);
-    } else {
-        TileGeom g{};
-        tile_geom(P.M, P.N, &g);
-        snprintf(buf, (size_t)len,
-                 "arm=tile enc=%s M=%lld N=%lld K=%lld bm=%d bn=%d grid=%lldx%lld rblk=%d",
-                 ename, (long long)P.M, (long long)P.N, (long long)P.K,
-                 g.bm, g.bn, (long long)g.grid_n, (long long)g.grid_m, P.rblk);
+                 g.steps, P.rblk);
     }
     return RAD_OK;
 }

@@ -83,7 +83,7 @@ struct LinesGeom {
     int64_t tiles, nblk, blocks;   /* ceil(N/16); row blocks of 16 tw rows; workgroups */
 };
 
-/* Launch geometry of the mxfp4 prefill GEMM (block-scaled MFMA, direct-to-LDS ring):
+/* Launch geometry of the prefill GEMM (block-scaled MFMA, direct-to-LDS ring):
  * a workgroup of 8 waves (2 x 4) owns bn = 32 wnf weight rows x bm = 64 wmf tokens. */
 struct PrefillGeom {
     int wnf, wmf, nst;       /* 16-row fragments per wave along N / M; ring depth */
@@ -91,12 +91,6 @@ struct PrefillGeom {
     int64_t grid_m, grid_n, tiles;
     int steps;               /* K / 128 */
     int lds;                 /* dynamic LDS bytes per workgroup */
-};
-
-/* Launch geometry of the fp8a8 prefill tile. */
-struct TileGeom {
-    int bm, bn;              /* output tile of one workgroup */
-    int64_t grid_m, grid_n;
 };
 
 int64_t grid_block(int64_t ext, int64_t blocks);
@@ -136,8 +130,8 @@ bool lines_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, 
 /* The line kernel addresses a wave's (up to 64) weight rows and the whole activation plane through
  * buffer resources: both must span less than 2^31 bytes. */
 bool lines_fits(const GemmPlan& P);
-void tile_geom(int64_t M, int64_t N, TileGeom* g);
-/* mode: 0 = e4m3 activations with f32 scale per 128 (mxfp4a8), 1 = mxfp8 (mxfp4a16);
+/* mode: PF_A8 = e4m3 activations with f32 scale per 128 (mxfp4a8), PF_MX8 = mxfp8
+ * (mxfp4a16), PF_F8 = e4m3 activations and e4m3 weights with bf16 row scales (fp8a8);
  * ncu: compute units the launch can fill (tiles are sized so the last round of
  * workgroups is as full as possible). */
 void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeom* g);

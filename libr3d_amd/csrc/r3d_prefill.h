@@ -62,16 +62,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t r3d_rsrc(const void* base, int
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
 }
 
-/* Buffer load of `bytes` (16 or 4) per lane straight into LDS at lds + lane * bytes. */
+/* Buffer load of `bytes` (16, 4 or 2) per lane straight into LDS at lds + lane *
+ * max(bytes, 4). */
 template <int BYTES>
 __device__ __forceinline__ void r3d_buf_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff,
                                             uint32_t soff) {
-    static_assert(BYTES == 16 || BYTES == 4, "dwordx4 or dword loads");
+    static_assert(BYTES == 16 || BYTES == 4 || BYTES == 2, "dwordx4, dword or ushort loads");
     if constexpr (BYTES == 16)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
                                                  voff, soff, 0, 0);
-    else
+    else if constexpr (BYTES == 4)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
+                                                 voff, soff, 0, 0);
+    else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 2,
                                                  voff, soff, 0, 0);
 }
 
@@ -80,9 +84,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     const uint8_t* __restrict__ A, const void* __restrict__ ASv,
     const uint8_t* __restrict__ B, const uint8_t* __restrict__ BS,
     uint16_t* __restrict__ Y,
-    int M, int N, int steps, int grid_m, int tiles,
+    int M, int N, int steps, int grid_m, int tiles, int rblk,
     int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch) {
-    using L = PrefillLayout<WNF, WMW, 3>;
+    constexpr bool F8 = MODE == PF_F8;                   /* e4m3 weights, bf16 row scales */
+    constexpr int WH = F8 ? 2 : 1;                        /* 1 KB images per weight fragment */
+    constexpr int WB = 64 * WH;                           /* weight bytes per row per step */
+    using L = PrefillLayout<WNF, WMW, 3, WH>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
     const int lane = threadIdx.x & 63;
@@ -105,10 +112,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     const int64_t xs_pitch = MODE == PF_MX8 ? as_pitch : 4 * as_pitch;     /* bytes */
     const __amdgpu_buffer_rsrc_t rB = r3d_rsrc(B + n0 * b_pitch, (N - n0) * b_pitch);
     const __amdgpu_buffer_rsrc_t rA = r3d_rsrc(A + m0 * a_pitch, (M - m0) * a_pitch);
-    /* scales: waves 0-3 fetch the weight rows' E8M0 dwords, waves 4-7 the tokens' */
+    /* scales: waves 0-3 fetch the weight rows' scales (E8M0 dwords; e4m3 weights: the bf16
+     * of the row's scale row n / rblk), waves 4-7 the tokens' */
     const bool wsc = wave < 4;
+    const int64_t sr0 = F8 ? n0 / rblk : n0;             /* first scale row of the tile */
+    const int64_t srn = F8 ? (N - 1) / rblk + 1 : N;     /* scale rows */
+    const int64_t ws_pitch = F8 ? 2 * bs_pitch : bs_pitch;    /* bytes */
     const __amdgpu_buffer_rsrc_t rSX =
-        wsc ? r3d_rsrc(BS + n0 * bs_pitch, (N - n0) * bs_pitch)
+        wsc ? r3d_rsrc(BS + sr0 * ws_pitch, (srn - sr0) * ws_pitch)
             : r3d_rsrc(reinterpret_cast<const uint8_t*>(ASv) + m0 * xs_pitch, (M - m0) * xs_pitch);
     /* A plane load covers 16 rows x 64 bytes with four consecutive lanes on each row
      * (lane l: row l / 4), so every row is one 64-byte run; chunk l % 4 of the run is
@@ -120,11 +131,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     uint32_t woff[L::WLD];
 #pragma unroll
     for (int i = 0; i < L::WLD; ++i) {
-        const int f = wave + 8 * i;
-        const int fr = f < L::WFR ? f : L::WFR - 1;         /* pad slots reload the last */
-        int64_t n = n0 + 16 * fr + lr;
+        /* image j: fragment j / WH, 64-byte half j % WH (e4m3 rows are two halves) */
+        const int j = wave + 8 * i;
+        const int jr = j < WH * L::WFR ? j : WH * L::WFR - 1;    /* pad slots reload the last */
+        int64_t n = n0 + 16 * (jr / WH) + lr;
         if (n > N - 1) n = N - 1;
-        woff[i] = (uint32_t)((n - n0) * b_pitch + 16 * lc);
+        woff[i] = (uint32_t)((n - n0) * b_pitch + 64 * (jr % WH) + 16 * lc);
     }
     uint32_t sxoff;
     {
@@ -132,7 +144,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         if (wsc) {
             int64_t n = n0 + (r0 < L::BN ? r0 : L::BN - 1);
             if (n > N - 1) n = N - 1;
-            sxoff = (uint32_t)((n - n0) * bs_pitch);
+            sxoff = (uint32_t)(((F8 ? n / rblk : n) - sr0) * ws_pitch);
         } else {
             int64_t m = m0 + (r0 < L::BM ? r0 : L::BM - 1);
             if (m > M - 1) m = M - 1;
@@ -151,7 +163,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     /* load k (0 .. LOADS-1) of stage s into ring slot st */
     auto load = [&](int k, int s, uint8_t* st) {
         if (k < L::WLD)
-            r3d_buf_lds<16>(rB, st + L::W + 1024 * (wave + 8 * k), woff[k], 64 * s);
+            r3d_buf_lds<16>(rB, st + L::W + 1024 * (wave + 8 * k), woff[k], WB * s);
+        else if (k == L::WLD && F8 && wsc)
+            r3d_buf_lds<2>(rSX, st + sxdst, sxoff, 2 * s);        /* one bf16 per weight row */
         else if (k == L::WLD)
             r3d_buf_lds<4>(rSX, st + sxdst, sxoff, 4 * s);
         else
@@ -180,6 +194,15 @@ __global__ __launch_bounds__(512) void prefill_kernel(
 
     r3d_i32x4 wS[2][WNF];
     int xS[2][WNF];
+    /* PF_F8: the e4m3 weight operands and, per fragment, the bf16 scales (4-byte slots) of
+     * the lane's four result rows 4q .. 4q + 3; zero until the first step's are read, so
+     * the first (empty) deferred flush multiplies zeros */
+    r3d_i32x8 wF[2][WNF];
+    r3d_i32x4 sbF[2][WNF];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int a = 0; a < WNF; ++a) sbF[b][a] = r3d_i32x4{0, 0, 0, 0};
     r3d_i32x8 ar[4];
     int ax[4];
     float af[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -198,8 +221,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(
 #pragma unroll
         for (int ni = 0; ni < WNF; ++ni) {
             const int f = wn * WNF + ni;
-            wS[set][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 1024 * f + rd);
-            xS[set][ni] = st[L::S + 4 * (16 * f + li) + q];
+            if (F8) {
+                const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + rd);
+                const r3d_i32x4 hi =
+                    *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + 1024 + rd);
+                wF[set][ni] = r3d_i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                sbF[set][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::S + 4 * (16 * f + 4 * q));
+            } else {
+                wS[set][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 1024 * f + rd);
+                xS[set][ni] = st[L::S + 4 * (16 * f + li) + q];
+            }
         }
     };
     auto read_a = [&](const uint8_t* st, int mi) {
@@ -218,6 +249,22 @@ __global__ __launch_bounds__(512) void prefill_kernel(
 #pragma unroll
             for (int ni = 0; ni < WNF; ++ni)
                 r3d_mfma_mx_inplace(acc[ni][mi], wS[set][ni], xS[set][ni], ar[slot], ax[slot]);
+        } else if (F8) {
+            /* libref's (sub * sa) * sb flush (src/r3d_gemm_fp8a8.hip:9-15), deferred one
+             * group; the flushed group of group 0 is the previous step's last, whose weight
+             * scales are still in the other set (it is refilled only after this group) */
+            const int pm = mi == 0 ? WMW - 1 : mi - 1;
+            const int ps = mi == 0 ? set ^ 1 : set;
+#pragma unroll
+            for (int ni = 0; ni < WNF; ++ni) {
+                dq[mi & 1][ni] = r3d_mfma_fp8_fp8(wF[set][ni], ar[slot]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float sb = __uint_as_float((uint32_t)sbF[ps][ni][i] << 16);
+                    acc[ni][pm][i] = acc[ni][pm][i] + (dq[(mi + 1) & 1][ni][i] * sprev) * sb;
+                }
+            }
+            sprev = af[slot];
         } else {
             const int pm = mi == 0 ? WMW - 1 : mi - 1;         /* the group flushed now */
 #pragma unroll
@@ -291,12 +338,22 @@ __global__ __launch_bounds__(512) void prefill_kernel(
 #pragma unroll
             for (int b = 0; b < WMW; ++b) asm volatile("" : "+a"(acc[a][b]));
     } else {
-        /* the last group's results */
+        /* the last group's results (at e4m3 weights with the last step's weight set's
+         * scales: steps alternate sets starting from set 0) */
+        const int ls = (steps - 1) & 1;
 #pragma unroll
         for (int ni = 0; ni < WNF; ++ni)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                acc[ni][WMW - 1][i] = acc[ni][WMW - 1][i] + dq[(WMW - 1) & 1][ni][i] * sprev;
+            for (int i = 0; i < 4; ++i) {
+                if (F8) {
+                    const uint32_t sbb = (uint32_t)(ls ? sbF[1][ni][i] : sbF[0][ni][i]);
+                    const float sb = __uint_as_float(sbb << 16);
+                    acc[ni][WMW - 1][i] =
+                        acc[ni][WMW - 1][i] + (dq[(WMW - 1) & 1][ni][i] * sprev) * sb;
+                } else {
+                    acc[ni][WMW - 1][i] = acc[ni][WMW - 1][i] + dq[(WMW - 1) & 1][ni][i] * sprev;
+                }
+            }
     }
 
     /* ---- epilogue: lane holds Y[m0 + 16 g + li][n0 + 16 f + 4 q + i], i = 0..3.  The bf16

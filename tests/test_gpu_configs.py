@@ -84,6 +84,20 @@ def test_c3_mxfp4_prefill_sampled(gpu):
     _grade(Y[rows], A[rows], AS[rows], B, BS, K, "mxfp4a8")
 
 
+@pytest.mark.parametrize("rblk", [1, 128])
+def test_c3_shape_fp8a8_prefill_sampled(gpu, rblk):
+    """The fp8a8 generic row at config 3's shape (M=2048, K=5376, N=21504) on config 1's
+    weight law, both weight-scale grids."""
+    M, K, N = 2048, 5376, 21504
+    A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 35)
+    B, BS = synth.fp8_weights(N, K, 0x5EED + 36)
+    if rblk == 128:
+        BS = BS[::128].copy()                 # one scale row per 128 weight rows
+    Y = _run("gemm_nt_q_fp8a8", "fp8a8", A, AS, B, BS, M, N, K, gpu)
+    rows = np.sort(np.random.default_rng(5).choice(M, size=12, replace=False))
+    _grade(Y[rows], A[rows], AS[rows], B, BS, K, "fp8a8", rblk)
+
+
 def test_c4_lm_head_fp8(gpu):
     M, K, N = 4, 5376, 262144
     A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 40)

@@ -162,7 +162,8 @@ def test_mxfp4_tile(gpu, M, N, K):
     _check(MX_TILE, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (17, 200, 256), (130, 300, 384)])
+@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (17, 200, 256), (130, 300, 384),
+                                   (300, 1000, 1152), (257, 129, 640), (64, 520, 4096)])
 @pytest.mark.parametrize("rblk", [1, 128])
 def test_fp8_tile(gpu, M, N, K, rblk):
     A, AS, B, BS = _f8_case(M, N, K, 11 * M + N, rblk)
