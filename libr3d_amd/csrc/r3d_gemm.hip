@@ -232,12 +232,14 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
         }
     } else if (mode == PF_F8) {
         R3D_PF(PF_F8, 4, 2);
+    } else if (g.wmf == 2) {
+        R3D_PF(PF_A8, 4, 2);                            /* up to 128 tokens */
     } else {
         switch (g.wnf) {
-            case 8: R3D_PF(PF_A8, 8, 2); break;
-            case 7: R3D_PF(PF_A8, 7, 2); break;
-            case 6: R3D_PF(PF_A8, 6, 2); break;
-            default: R3D_PF(PF_A8, 4, 2); break;
+            case 8: R3D_PF(PF_A8, 8, 4); break;
+            case 7: R3D_PF(PF_A8, 7, 4); break;
+            case 6: R3D_PF(PF_A8, 6, 4); break;
+            default: R3D_PF(PF_A8, 4, 4); break;
         }
     }
 #undef R3D_PF

@@ -404,9 +404,9 @@ bool lines_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, 
     return g->lds <= kLinesMaxLds && g->blocks <= 0x7FFFFFFF;
 }
 
-/* Prefill tile choice: 64 wmw tokens (4 fragments per wave in mxfp8 mode, where the
- * MFMA accumulates in place; 2 in the f32-a_scale mode, whose per-step flush needs a
- * second register set) by 32 wnf weight rows.  Workgroups run one per CU, so the launch
+/* Prefill tile choice: 64 wmw tokens (4 fragments per wave; 2 with e4m3 weights, whose
+ * 8-register operands, row scales and flush results fill the register file at 4 x 2) by
+ * 32 wnf weight rows.  Workgroups run one per CU, so the launch
  * takes ceil(tiles / ncu) rounds; a round costs about wnf + 1/2 fragment-steps (the
  * fixed activation reads of a step).  The cheapest total wins, ties to the larger tile. */
 void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeom* g) {
@@ -414,7 +414,10 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
      * fragment hold the tile at 4 fragment pairs (at 6, 185 registers spill) */
     static const int kWnf[] = {8, 7, 6, 4};
     static const int kWnfF8[] = {4};
-    const int wmw = mode == PF_MX8 ? 4 : 2;
+    /* up to 128 tokens the f32-a_scale mode runs 2 token fragments per wave (the 4-fragment
+     * tile would leave most of its MFMAs on padding rows): 33 against 45 us at M = 8..64 */
+    const bool narrow = mode == PF_F8 || (mode == PF_A8 && M <= 128);
+    const int wmw = narrow ? 2 : 4;
     if (ncu <= 0) ncu = 256;
     int best = 0;
     double best_cost = 0.0;
@@ -423,7 +426,7 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
         const double cost = (double)((tiles + ncu - 1) / ncu) * (w + 0.5);
         if (best == 0 || cost < best_cost) { best = w; best_cost = cost; }
     };
-    if (mode == PF_F8)
+    if (narrow)
         for (int w : kWnfF8) consider(w);
     else
         for (int w : kWnf) consider(w);

@@ -161,7 +161,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         aoff[i] = (uint32_t)((m - m0) * a_pitch + 64 * (j & 1) + 16 * lc);
     }
     /* load k (0 .. LOADS-1) of stage s into ring slot st */
-    auto load = [&](int k, int s, uint8_t* st) {
+    auto load = [&](int k, int s, uint8_t* st) __attribute__((always_inline)) {
         if (k < L::WLD)
             r3d_buf_lds<16>(rB, st + L::W + 1024 * (wave + 8 * k), woff[k], WB * s);
         else if (k == L::WLD && F8 && wsc)
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     /* a stage's loads go out in WMW parts, one per fragment group, so the load issue
      * never stalls a wave for a whole stage at once */
     constexpr int kPer = (L::LOADS + WMW - 1) / WMW;
-    auto issue_part = [&](int part, int s, uint8_t* st) {
+    auto issue_part = [&](int part, int s, uint8_t* st) __attribute__((always_inline)) {
         const int sc = s < steps ? s : steps - 1;
 #pragma unroll
         for (int k = part * kPer; k < (part + 1) * kPer; ++k)
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
 
     /* this lane's operand chunk (row li, chunk q) inside any 1 KB fragment image */
     const int rd = 16 * (4 * li + (q ^ ((li >> 1) & 3)));
-    auto read_w = [&](const uint8_t* st, int set) {
+    auto read_w = [&](const uint8_t* st, int set) __attribute__((always_inline)) {
 #pragma unroll
         for (int ni = 0; ni < WNF; ++ni) {
             const int f = wn * WNF + ni;
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
             }
         }
     };
-    auto read_a = [&](const uint8_t* st, int mi) {
+    auto read_a = [&](const uint8_t* st, int mi) __attribute__((always_inline)) {
         const int g = wm * WMW + mi, slot = mi & 3;
         const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(st + L::A + 2048 * g + rd);
         const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(st + L::A + 2048 * g + 1024 + rd);
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         else
             af[slot] = *reinterpret_cast<const float*>(st + L::AS + 4 * (16 * g + li));
     };
-    auto group = [&](int mi, int set) {
+    auto group = [&](int mi, int set) __attribute__((always_inline)) {
         const int slot = mi & 3;
         if (MODE == PF_MX8) {
 #pragma unroll
@@ -277,6 +277,84 @@ __global__ __launch_bounds__(512) void prefill_kernel(
             sprev = af[slot];        /* this group's scale, kept past the slot's refill */
         }
     };
+    /* Flushed modes (PF_A8, PF_F8) with four token fragments per wave: ONE weight operand
+     * set -- fragment ni of step s + 1 is read into it right after the last group's MFMA on
+     * fragment ni of step s, WNF MFMAs before its first use -- and the MFMA results in a
+     * ring of RR, each flushed LAG MFMAs after its issue (past the result latency), so the
+     * registers of a second weight set and of two whole result sets go to the larger tile.
+     * The flush of MFMA t (index mi * WNF + ni in the step) uses its group's a_scale: the
+     * current group's, or sprev for the group before (the previous step's last group at
+     * mi = 0), and at e4m3 weights the row scales of its step's set. */
+    constexpr bool SS = MODE != PF_MX8 && WMW == 4;
+    constexpr int RR = 4, LAG = RR - 1;
+    static_assert(!SS || ((WMW * WNF) % RR == 0 && LAG < WNF), "result ring period");
+    r3d_f32x4 dqr[RR];
+#pragma unroll
+    for (int r = 0; r < RR; ++r) dqr[r] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto read_w1 = [&](const uint8_t* st, int ni, int sset) __attribute__((always_inline)) {
+        const int f = wn * WNF + ni;
+        if (F8) {
+            const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + rd);
+            const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + 1024 + rd);
+            wF[0][ni] = r3d_i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            sbF[sset][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::S + 4 * (16 * f + 4 * q));
+        } else {
+            wS[0][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 1024 * f + rd);
+            xS[0][ni] = st[L::S + 4 * (16 * f + li) + q];
+        }
+    };
+    auto flush1 = [&](int t, int mi, float scur, int set) __attribute__((always_inline)) {
+        const bool before = t < 0;                      /* the previous step's last group */
+        const int tt = before ? t + WMW * WNF : t;
+        const int nf = tt % WNF, mf = tt / WNF;
+        const float sv = (!before && mf == mi) ? scur : sprev;
+        const r3d_f32x4 d = dqr[tt % RR];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (F8) {
+                const int sbi = before ? (set ? sbF[0][nf][i] : sbF[1][nf][i])
+                                       : (set ? sbF[1][nf][i] : sbF[0][nf][i]);
+                const float sb = __uint_as_float((uint32_t)sbi << 16);
+                acc[nf][mf][i] = acc[nf][mf][i] + (d[i] * sv) * sb;
+            } else {
+                acc[nf][mf][i] = acc[nf][mf][i] + d[i] * sv;
+            }
+        }
+    };
+    auto group1 = [&](int mi, int set, const uint8_t* nxt) __attribute__((always_inline)) {
+        const int slot = mi & 3;
+        const float scur = af[slot];
+#pragma unroll
+        for (int ni = 0; ni < WNF; ++ni) {
+            const int t = mi * WNF + ni;
+            if (F8)
+                dqr[t % RR] = r3d_mfma_fp8_fp8(wF[0][ni], ar[slot]);
+            else
+                dqr[t % RR] = r3d_mfma_fp4_fp8(wS[0][ni], xS[0][ni], ar[slot], R3D_E8M0_ONE);
+            if (mi == WMW - 1) read_w1(nxt, ni, set ^ 1);
+            flush1(t - LAG, mi, scur, set);
+        }
+        sprev = scur;
+    };
+    auto step_ss = [&](int s, int set, uint8_t* cur, const uint8_t* nxt, uint8_t* prv) __attribute__((always_inline)) {
+#pragma unroll
+        for (int mi = 0; mi < WMW; ++mi) {
+            group1(mi, set, nxt);
+            if (mi + 2 < WMW) {
+                read_a(cur, mi + 2);
+                issue_part(mi + 2, s + 2, prv);
+            } else if (mi + 2 == WMW) {
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(L::LOADS) : "memory");
+                issue_part(0, s + 3, cur);
+                read_a(nxt, 0);
+            } else {
+                issue_part(1, s + 3, cur);
+                read_a(nxt, 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
     /* One K step on weight set `set` from ring slot cur (stage s); nxt and prv are the
      * slots of stages s + 1 and s - 1 (= s + 2).  At group WMW - 2 every read of stage s
      * has been issued: once this wave's reads are done and stage s + 1 has landed, the
@@ -284,7 +362,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(
      * are read from slot nxt into the other weight set.  Stage k's loads go out in the
      * WMW groups between the barriers of steps k - 3 and k - 2, so at each barrier exactly
      * one stage (LOADS loads) is younger than the one it waits for. */
-    auto step = [&](int s, int set, uint8_t* cur, const uint8_t* nxt, uint8_t* prv) {
+    auto step = [&](int s, int set, uint8_t* cur, const uint8_t* nxt, uint8_t* prv) __attribute__((always_inline)) {
+        if (SS) { step_ss(s, set, cur, nxt, prv); return; }
 #pragma unroll
         for (int mi = 0; mi < WMW; ++mi) {
             group(mi, set);
@@ -337,6 +416,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         for (int a = 0; a < WNF; ++a)
 #pragma unroll
             for (int b = 0; b < WMW; ++b) asm volatile("" : "+a"(acc[a][b]));
+    } else if (SS) {
+        /* the last LAG results of the last step (its last group; sprev is its scale) */
+        const int ls = (steps - 1) & 1;
+#pragma unroll
+        for (int t = WMW * WNF - LAG; t < WMW * WNF; ++t) flush1(t, WMW - 1, sprev, ls);
     } else {
         /* the last group's results (at e4m3 weights with the last step's weight set's
          * scales: steps alternate sets starting from set 0) */

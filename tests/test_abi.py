@@ -297,10 +297,17 @@ def test_prefill_tile_choice_fills_the_last_round():
     g = _geom(d)
     assert (g["arm"], g["bn"], g["bm"], g["tiles"], g["steps"]) == ("prefill", "224", "256", "768", "42")
     assert int(g["lds"]) <= 160 * 1024
-    # the f32-a_scale mode keeps 128-token tiles
+    # the f32-a_scale mode takes the same tile at config 3, 128-token tiles up to 128
+    # tokens; e4m3 weights run 128 x 128
     ops, _ = _mx_ops(M=2048, N=21504, K=5376)
     g = _geom(R.describe("gemm_nt_q_mxfp4", ops)[1])
-    assert (g["bn"], g["bm"]) == ("224", "128")
+    assert (g["bn"], g["bm"], g["tiles"]) == ("224", "256", "768")
+    ops, _ = _mx_ops(M=64, N=21504, K=5376)
+    g = _geom(R.describe("gemm_nt_q_mxfp4", ops)[1])
+    assert (g["bn"], g["bm"]) == ("128", "128")
+    ops, _ = _f8_ops(M=2048, N=21504, K=5376)
+    g = _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])
+    assert (g["arm"], g["bn"], g["bm"]) == ("prefill", "128", "128")
     # few tiles: the narrowest tile spreads the work over more CUs
     ops, _ = _mx_ops(M=256, N=4096, K=1024)
     g = _geom(R.describe("gemm_nt_q_mxfp4", ops)[1])
