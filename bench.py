@@ -250,7 +250,19 @@ def main():
                                        "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
         log("[bench] C3 mxfp4a8 prefill: %.1f us, %.1f TFLOP/s" % (kern * 1e6, tf))
         del c
+        # the same shape on the fp8a8 row (config 1's weight law)
+        A8, AS8 = synth.fp8_activations_per_token(M, K, 0x5EED + 35)
+        B8, BS8 = synth.fp8_weights(N, K, 0x5EED + 36)
+        c = Case("fp8a8", A8, AS8, B8, BS8, M, N, K, 1, dev)
+        wall, kern = time_case(c, "gemm_nt_q_fp8a8", 10, 3, stream)
+        tf = 2.0 * M * N * K / kern / 1e12
+        extra["c3_shape_fp8a8_prefill"] = {"M": M, "K": K, "N": N, "kernel_us": round(kern * 1e6, 1),
+                                           "TFLOPs": round(tf, 1),
+                                           "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
+        log("[bench] C3-shape fp8a8 prefill: %.1f us, %.1f TFLOP/s" % (kern * 1e6, tf))
+        del c
         torch.cuda.empty_cache()
+        extra.update(bench_quant(dev, stream))
         extra.update(bench_c4(dev, stream, steps=5))
     if extra:
         out["extra"] = extra
@@ -299,6 +311,38 @@ def bench_c3(dev, stream, steps=10, warmup=3):
                                     "TFLOPs": round(tf, 1),
                                     "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
                                     "includes": "bf16->mxfp8 quantiser + block-scaled MFMA GEMM"}}
+
+
+def bench_quant(dev, stream, steps=50):
+    """The quant_act_fp8 producer (bf16 in, e4m3 codes + f32 scale per 128 out) on the
+    configs' activation shapes: config 3's 2048 x 5376 and a decode step's 4 x 5376."""
+    import torch
+    import libr3d_amd as R
+    res = {}
+    for M in (2048, 4):
+        n, g = 5376, 128
+        x = torch.randn((M, n), device=dev, dtype=torch.float32).to(torch.bfloat16).view(torch.int16)
+        q = torch.empty((M, n), dtype=torch.uint8, device=dev)
+        s = torch.empty((M, n // g), dtype=torch.float32, device=dev)
+        ops = R.QuantActOperands(x, q, s, n=n, group=g, M=M, x_dtype="BF16")
+        f = R.row_launcher("quant_act_fp8_act")
+        for _ in range(3):
+            assert f(ops, stream) == 0
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            f(ops, stream)
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / steps
+        nb = M * n * 2 + M * n + M * (n // g) * 4
+        res["quant_act_fp8_M%d" % M] = {"n": n, "group": g, "kernel_us": round(t * 1e6, 2),
+                                         "GBps": round(nb / t / 1e9, 1),
+                                         "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
+        log("[bench] quant_act_fp8 M=%d n=%d: %.2f us, %.1f GB/s" % (M, n, t * 1e6, nb / t / 1e9))
+    return res
 
 
 def bench_c4(dev, stream, steps=5):

@@ -20,8 +20,9 @@ extern "C" {
 uint32_t rad_plugin_abi_version(void);
 const RadPluginInfo* rad_plugin_info(void);
 
-/* Op schemas this plugin declares: gemm_nt_q, parameters and operands exactly as
- * src/r3d_rows.cpp:186-210.  Replaces src/r3d_rows.cpp:2238-2247. */
+/* Op schemas this plugin declares: gemm_nt_q (src/r3d_rows.cpp:186-210) and quant_act_fp8
+ * (src/r3d_rows.cpp:615-625,985-990), parameters and operands exactly as there.
+ * Replaces src/r3d_rows.cpp:2238-2247. */
 int rad_kernel_schema_count(void);
 const RadOpSchema* rad_kernel_schema_at(int i);
 
@@ -60,6 +61,14 @@ int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s);
  * the M and K parameters, 0 when either is missing.  Same role as the reference's
  * src/r3d_gemm_fp8a8.hip:1249-1253. */
 int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a);
+
+/* quant_act_fp8, the activation producer of the fp8a8 / mxfp4a8 rows: per-(row, group)
+ * symmetric e4m3 codes of a bf16 or f32 activation, plain row-major, and the f32 dequant
+ * scale amax/448 per group.  Operands (x, q, scale); params M, n, group, dtype.  Replaces
+ * src/r3d_band.hip:460-487 (gates and refusal codes as there: RAD_E_INVAL for a missing
+ * operand, RAD_E_DTYPE, RAD_E_SHAPE, RAD_E_STRIDE; RAD_E_DEVICE for a failed launch).
+ * Asynchronous on `s`. */
+int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s);
 
 /* Host-only diagnostic with no counterpart in the reference: runs `row`'s preamble and
  * plan on `a` and writes the chosen arm and launch geometry (or the refusal) into buf.

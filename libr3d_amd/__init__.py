@@ -18,7 +18,7 @@ __all__ = [
     "RAD_OK", "RAD_E_UNSUPPORTED", "RAD_E_SHAPE", "RAD_E_STRIDE", "RAD_E_DTYPE",
     "RAD_E_INVAL", "RAD_E_DEVICE", "DT", "RadTensor", "RadParam", "RadArgs",
     "RadKernelInfo", "RadOpSchema", "lib", "lib_path", "rows", "schemas", "resolve",
-    "launch_row", "gemm_nt_q", "describe", "GemmOperands",
+    "launch_row", "gemm_nt_q", "describe", "GemmOperands", "QuantActOperands", "quant_act_fp8",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -286,6 +286,69 @@ class GemmOperands:
 
     def set_y(self, y):
         self._t[4].data = y.data_ptr()
+
+
+class QuantActOperands:
+    """Owns the ctypes RadArgs for one quant_act_fp8 call (src/r3d_band.hip:460-487).
+
+    x     float32 or bf16/int16 [M, n] (any view the band walk accepts; rank 1 is one row)
+    q     uint8 [M, n]                    e4m3 codes out
+    scale float32 [M, ceil(n / group)]    dequant scales out
+    x_dtype "F32" or "BF16" names x's element type (int16 tensors carry bf16 bits).
+    """
+
+    def __init__(self, x, q, scale, *, n, group, M=None, x_dtype=None, dtype=None,
+                 shapes=None, strides=None):
+        t = (RadTensor * 3)()
+        xdt = x_dtype or ("F32" if str(x.dtype).endswith("float32") else "BF16")
+        shapes = shapes or {}
+        strides = strides or {}
+        for i, (ten, dt) in enumerate(((x, xdt), (q, "F8E4M3"), (scale, "F32"))):
+            if ten is None:
+                t[i].data = None
+                t[i].rank = 0
+                continue
+            t[i].data = ten.data_ptr()
+            t[i].dtype = DT[dt]
+            shp = list(shapes.get(i, ten.shape))
+            std = list(strides.get(i, ten.stride()))
+            t[i].rank = len(shp)
+            for r, (s_, st) in enumerate(zip(shp, std)):
+                t[i].shape[r] = int(s_)
+                t[i].stride[r] = int(st)
+        self._t = t
+        params = [("n", int(n)), ("group", int(group)),
+                  ("dtype", dtype or ("f32" if xdt == "F32" else "bf16"))]
+        if M is not None:
+            params.append(("M", int(M)))
+        p = (RadParam * len(params))()
+        self._keep = []
+        for i, (k, v) in enumerate(params):
+            kb = k.encode()
+            self._keep.append(kb)
+            p[i].key = kb
+            if isinstance(v, str):
+                vb = v.encode()
+                self._keep.append(vb)
+                p[i].kind = RAD_P_STR
+                p[i].sval = vb
+            else:
+                p[i].kind = RAD_P_INT
+                p[i].ival = v
+        self._p = p
+        self.args = RadArgs(ctypes.cast(t, ctypes.POINTER(RadTensor)), 3,
+                            ctypes.cast(p, ctypes.POINTER(RadParam)), len(params),
+                            None, 0, None, 0, 0)
+
+
+def quant_act_fp8(x, q, scale, *, n, group=128, stream=None):
+    """Launch the quant_act_fp8 row on `stream` (a raw hipStream_t int, default the current
+    torch stream).  Returns the row's status."""
+    import torch
+    ops = QuantActOperands(x, q, scale, n=n, group=group, M=x.numel() // n)
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    return launch_row("quant_act_fp8_act", ops, stream)
 
 
 def row_launcher(row_name):

@@ -14,6 +14,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include "r3d_band.h"
 #include "r3d_gemm_kernels.h"
 #include "r3d_gemv_lines.h"
 #include "r3d_gemv_quad.h"
@@ -273,9 +274,45 @@ static int entry(const RadArgs* a, RadStream s, int enc, bool decode) {
     return launch_prefill(P, stream);
 }
 
+/* quant_act_fp8 (src/r3d_band.hip:460-487): the reference's gates, then one wave per
+ * (row, group). */
+static int quant_entry(const RadArgs* a, RadStream s) {
+    QuantPlan P{};
+    const int rc = plan_quant_act_fp8(a, &P);
+    if (rc) return rc;
+    if (!chip_ok()) return RAD_E_UNSUPPORTED;
+    const int64_t items = P.rows * P.ngrp;
+    const int64_t blocks = (items + 3) / 4;
+    if (blocks > 0x7FFFFFFF) return RAD_E_SHAPE;
+    const int eb = P.x_bf16 ? 2 : 4;
+    const bool pair = (P.g % 2) == 0 && (P.n % 2) == 0 && (P.x_pitch % 2) == 0 &&
+                      (P.q_pitch % 2) == 0 && ((uintptr_t)P.x % (2 * eb)) == 0 &&
+                      ((uintptr_t)P.q % 2) == 0;
+    hipStream_t stream = (hipStream_t)s;
+#define R3D_QA(B_, P_)                                                                      \
+    hipLaunchKernelGGL((quant_act_fp8_kernel<B_, P_>), dim3((unsigned)blocks), dim3(256), 0,  \
+                       stream, P.x, P.x_pitch, P.q, P.q_pitch, P.scale, P.s_pitch, P.n, P.g,  \
+                       P.ngrp, items)
+    if (P.x_bf16) {
+        if (pair) R3D_QA(true, true); else R3D_QA(true, false);
+    } else {
+        if (pair) R3D_QA(false, true); else R3D_QA(false, false);
+    }
+#undef R3D_QA
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "libr3d_gfx950: quant_act_fp8 launch FAILED (%s)\n", hipGetErrorName(e));
+        return RAD_E_DEVICE;
+    }
+    debug_once("quant_act_fp8", 250);
+    return RAD_OK;
+}
+
 }  // namespace r3d
 
 extern "C" {
+
+int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s) { return r3d::quant_entry(a, s); }
 
 int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s) {
     return r3d::entry(a, s, r3d::ENC_MXFP4A8, false);

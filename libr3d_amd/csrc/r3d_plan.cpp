@@ -442,6 +442,63 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
     g->lds = g->nst * prefill_stage_bytes(g->wnf, g->wmf, mode == PF_F8 ? 2 : 1);
 }
 
+int band_row_pitch(const RadTensor* t, int64_t cols, int64_t* pitch) {
+    if (!t || !t->data) return -1;
+    if (t->rank == 1) {
+        if (rad_tensor_numel(t) != cols || t->stride[0] != 1) return -2;
+        *pitch = 0;
+        return 0;
+    }
+    if (t->rank == 2) {
+        if (t->stride[1] != 1) return -3;
+        *pitch = t->shape[1] == cols ? t->stride[0] : cols;
+        return 0;
+    }
+    if (t->rank >= 3) {
+        if (t->stride[t->rank - 1] != 1) return -3;
+        if (t->shape[t->rank - 1] != cols) { *pitch = cols; return 0; }
+        for (int i = 0; i < (int)t->rank - 1; ++i)
+            if (t->stride[i] != t->shape[i + 1] * t->stride[i + 1]) return -4;
+        *pitch = cols;
+        return 0;
+    }
+    return -1;                                   /* rank 0 */
+}
+
+int plan_quant_act_fp8(const RadArgs* a, QuantPlan* P) {
+    const RadTensor* x = rad_arg_in(a, 0);
+    const RadTensor* q = rad_arg_in(a, 1);
+    const RadTensor* sc = rad_arg_in(a, 2);
+    if (!x || !q || !sc) return RAD_E_INVAL;
+    if (x->dtype != RAD_F32 && x->dtype != RAD_BF16) return RAD_E_DTYPE;
+    if (q->dtype != RAD_F8E4M3 || sc->dtype != RAD_F32) return RAD_E_DTYPE;
+    long long v = 0;
+    const int64_t n = rad_args_geti(a, "n", &v) ? (int64_t)v : (x->rank >= 2 ? x->shape[1] : 0);
+    if (n <= 0) return RAD_E_SHAPE;
+    const int64_t rows = rad_tensor_numel(x) / n;
+    if (rows <= 0 || rows > 0xffff) return RAD_E_SHAPE;
+    int64_t g = rad_args_geti(a, "group", &v) ? (int64_t)v : n;
+    if (g <= 0 || g > n) g = n;
+    const int64_t ngrp = (n + g - 1) / g;
+    if (ngrp > 0x7fffffffLL) return RAD_E_SHAPE;
+    if (rad_tensor_numel(q) < rows * n || rad_tensor_numel(sc) < rows * ngrp) return RAD_E_SHAPE;
+    int64_t xp = 0, qp = 0, sp = 0;
+    if (band_row_pitch(x, n, &xp) || band_row_pitch(q, n, &qp) || band_row_pitch(sc, ngrp, &sp))
+        return RAD_E_STRIDE;
+    P->x = (const uint8_t*)x->data;
+    P->q = (uint8_t*)q->data;
+    P->scale = (float*)sc->data;
+    P->x_bf16 = x->dtype == RAD_BF16;
+    P->rows = rows;
+    P->n = n;
+    P->g = g;
+    P->ngrp = ngrp;
+    P->x_pitch = xp;
+    P->q_pitch = qp;
+    P->s_pitch = sp;
+    return RAD_OK;
+}
+
 bool env_no_mxfp4()   { static const bool v = getenv("R3D_NO_MXFP4") != nullptr;   return v; }
 bool env_no_fp4_dec() { static const bool v = getenv("R3D_NO_FP4_DEC") != nullptr; return v; }
 bool env_no_fp8a8()   { static const bool v = getenv("R3D_NO_FP8A8") != nullptr;   return v; }
@@ -515,6 +572,18 @@ int64_t decode_splitk(const RadArgs* a) {
 
 int describe(const char* row, const RadArgs* a, char* buf, int len) {
     if (!row || !buf || len <= 0) return RAD_E_INVAL;
+    if (strstr(row, "quant_act_fp8") != nullptr) {
+        QuantPlan Q{};
+        const int rc = plan_quant_act_fp8(a, &Q);
+        if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
+        snprintf(buf, (size_t)len,
+                 "arm=band op=quant_act_fp8 x=%s rows=%lld n=%lld group=%lld ngrp=%lld "
+                 "x_pitch=%lld q_pitch=%lld s_pitch=%lld",
+                 Q.x_bf16 ? "bf16" : "f32", (long long)Q.rows, (long long)Q.n, (long long)Q.g,
+                 (long long)Q.ngrp, (long long)Q.x_pitch, (long long)Q.q_pitch,
+                 (long long)Q.s_pitch);
+        return RAD_OK;
+    }
     const bool a16 = strstr(row, "mxfp4a16") != nullptr;
     const bool mx = strstr(row, "mxfp4") != nullptr;
     const bool dec = strstr(row, "decode") != nullptr;

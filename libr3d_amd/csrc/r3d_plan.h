@@ -136,6 +136,28 @@ bool lines_fits(const GemmPlan& P);
  * workgroups is as full as possible). */
 void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeom* g);
 
+/* The band rows' operand walk (src/r3d_band.hip:419-449 of the reference): a rank-1 tensor
+ * of exactly `cols` unit-stride elements is one row read by every row (pitch 0); rank 2
+ * needs a unit inner stride and pitches by stride[0] when shape[1] == cols, else reads flat
+ * (pitch cols); rank >= 3 needs a unit inner stride and, when the last extent is cols,
+ * contiguous leading dimensions (pitch cols).  Returns 0 and sets *pitch (elements), or a
+ * negative code for a layout the walk refuses. */
+int band_row_pitch(const RadTensor* t, int64_t cols, int64_t* pitch);
+
+/* quant_act_fp8 launch plan (src/r3d_band.hip:460-487): operands x (f32 or bf16), q (e4m3),
+ * scale (f32); n from the param (default x's second extent), rows = numel(x) / n (at most
+ * 65535), group from the param clamped to [1, n] (absent or out of range: n).  Returns
+ * RAD_OK or the reference's refusal code. */
+struct QuantPlan {
+    const uint8_t* x;
+    uint8_t* q;
+    float* scale;
+    int x_bf16;
+    int64_t rows, n, g, ngrp;
+    int64_t x_pitch, q_pitch, s_pitch;        /* elements */
+};
+int plan_quant_act_fp8(const RadArgs* a, QuantPlan* P);
+
 /* Environment levers, read once per process (function-local statics). */
 bool env_no_mxfp4();        /* R3D_NO_MXFP4: all mxfp4a8 rows */
 bool env_no_fp4_dec();      /* R3D_NO_FP4_DEC: the mxfp4a8 decode row */

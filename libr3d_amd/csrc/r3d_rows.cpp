@@ -1,14 +1,15 @@
-/* r3d_rows.cpp -- plugin identity, the gemm_nt_q op schema and the gfx950 row table of
+/* r3d_rows.cpp -- plugin identity, the op schemas and the gfx950 row table of
  * libr3d_gfx950, behind radiance's kernel-plugin ABI 26 (src/r3d_rows.cpp:14-27,
  * 2238-2278 of the reference).  Pure host C++.
  *
  * Rows (resolver: per op and band, the highest-priority row whose constraints hold;
  * src/r3d_rows.cpp:1165-1177):
- *   gemm_nt_q_mxfp4          prio 1000  dtype IN mxfp4a8, K DIV 128      prefill tile
+ *   gemm_nt_q_mxfp4          prio 1000  dtype IN mxfp4a8, K DIV 128      prefill GEMM
  *   gemm_nt_q_mxfp4_decode   prio 1100  + M LE 16                         decode GEMV
  *   gemm_nt_q_fp8a8          prio 1000  dtype IN fp8a8, K DIV 128, group EQ 128
  *   gemm_nt_q_fp8a8_decode   prio 1100  + M LE 16
  *   gemm_nt_q_mxfp4a16       prio 1000  dtype IN mxfp4a16, K DIV 128     bf16-in prefill
+ *   quant_act_fp8_act        prio 1000  n GE 1, dtype IN f32 bf16          activation producer
  * gemm_nt_q_mxfp4a16 has no counterpart in the reference: it takes bf16 activations (no
  * a_scale), quantises them to mxfp8 (e4m3 + E8M0 per 32 of K) in the launch scratch its
  * hook sizes, and runs the prefill GEMM with both block scales inside the MFMA.
@@ -37,6 +38,7 @@ int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s);
 int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a);
+int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s);
 }
 
 namespace {
@@ -64,11 +66,34 @@ const RadOperandSpec kGemmNtQOperands[] = {
     {"b_ref", RAD_OPD_WEIGHT, 1},
 };
 
+/* quant_act_fp8's schema, as the reference declares it (src/r3d_rows.cpp:615-625). */
+const RadParamSpec kQuantActParams[] = {
+    {"M", RAD_P_INT, RAD_REQUIRED, 0},
+    {"n", RAD_P_INT, RAD_REQUIRED, 0},
+    {"group", RAD_P_INT, RAD_REQUIRED, 0},
+    {"dtype", RAD_P_STR, RAD_REQUIRED, 0},
+};
+const RadOperandSpec kQuantActOperands[] = {
+    {"x", RAD_OPD_IN, 0},
+    {"q", RAD_OPD_OUT, 0},
+    {"scale", RAD_OPD_OUT, 0},
+};
+
 const RadOpSchema kSchemas[] = {
     {"gemm_nt_q", kGemmNtQParams, 8, kGemmNtQOperands, 7,
      "Y[M,N] = A[M,K] . dequant(B)[N,K]^T with block-scaled operands; `dtype` names the "
      "operand combination (mxfp4a8: e4m3 A + f32 a_scale per 128 of K, e2m1 B + E8M0 per "
      "32; fp8a8: e4m3 A + f32 a_scale, e4m3 B + bf16 scale per 128 x 128 tile or per row)."},
+    {"quant_act_fp8", kQuantActParams, 4, kQuantActOperands, 3,
+     "per-(row, `group`-column) symmetric E4M3 quantisation of a token-major activation, "
+     "plain row-major; the scale is amax/448, a dequant multiplier (the GEMMs multiply both "
+     "scales and never divide)."},
+};
+
+/* the band rows' constraint (src/r3d_rows.cpp:1262-1265) */
+const RadConstraint cBandMn[] = {
+    {"n", RAD_C_GE, 1, nullptr},
+    {"dtype", RAD_C_IN, 0, "f32 bf16"},
 };
 
 const RadConstraint cMxfp4Tile[] = {
@@ -108,7 +133,7 @@ const RadTunable tSplitK[] = {
 
 const RadKernelInfo kRows[] = {
     {"gemm_nt_q_mxfp4", "gemm_nt_q", "gemm",
-     "mxfp4a8 prefill GEMM on gfx950 block-scaled MFMA: up to 256 weight rows x 128 tokens "
+     "mxfp4a8 prefill GEMM on gfx950 block-scaled MFMA: up to 256 weight rows x 256 tokens "
      "per workgroup, a three-deep direct-to-LDS ring, e2m1 weights with their E8M0 scales "
      "fed to v_mfma_scale_f32_16x16x128_f8f6f4 as is, e4m3 activations, one MFMA per "
      "128-of-K activation group scaled by a_scale in f32",
@@ -120,9 +145,9 @@ const RadKernelInfo kRows[] = {
      nullptr, nullptr, r3d_rad_gemm_nt_q, nullptr, nullptr, nullptr, nullptr, nullptr},
 
     {"gemm_nt_q_mxfp4_decode", "gemm_nt_q", "gemm",
-     "mxfp4a8 decode-band GEMV on gfx950: one wave per 16-row weight tile and K chunk, "
-     "16-byte non-temporal loads of the nibble plane straight into the MFMA's fp4 operand "
-     "with the E8M0 bytes as its scale operand, split-K folded through LDS in chunk order",
+     "mxfp4a8 decode-band GEMV on gfx950: M <= 4 one wave per 4 weight rows (whole 128-byte "
+     "lines straight into the MFMA's fp4 operand, E8M0 bytes as its scale operand), M 5..16 "
+     "one wave per 32 rows; split-K folded through LDS in chunk order",
      "M <= 16 (decode and speculative verify; widened from the reference's 8); K a multiple "
      "of 128; N any (dead rows clamp their loads and never store); M derives from numel(y)/N",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), e2m1 b with E8M0 b_scale per (row, 32 K), "
@@ -132,8 +157,9 @@ const RadKernelInfo kRows[] = {
      nullptr},
 
     {"gemm_nt_q_fp8a8", "gemm_nt_q", "gemm",
-     "fp8a8 prefill tile on gfx950 MFMA: 128x128 output tile, e4m3 on both operands, one MFMA "
-     "per 128-of-K scale group flushed as (sub * a_scale) * b_scale in the oracle's order",
+     "fp8a8 prefill GEMM on gfx950 block-scaled MFMA: 128x128 output tile over a three-deep "
+     "direct-to-LDS ring, e4m3 on both operands, one MFMA per 128-of-K scale group flushed as "
+     "(sub * a_scale) * b_scale in the oracle's order",
      "K a multiple of 128; 16-byte aligned A/B bases and pitches; b_scale either the 128x128 "
      "block grid or a per-row grid; M derives from numel(y)/N",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), fp8_e4m3 b with bf16 scale per 128x128 "
@@ -142,8 +168,8 @@ const RadKernelInfo kRows[] = {
      nullptr, nullptr, r3d_rad_gemm_nt_q_fp8, nullptr, nullptr, nullptr, nullptr, nullptr},
 
     {"gemm_nt_q_fp8a8_decode", "gemm_nt_q", "gemm",
-     "fp8a8 decode-band GEMV on gfx950: one wave per 16-row weight tile and K chunk, two "
-     "16-byte non-temporal loads per lane per 128-of-K group into the MFMA's fp8 operand, "
+     "fp8a8 decode-band GEMV on gfx950: M <= 4 one wave per 4 weight rows (two whole-line "
+     "loads per 128-of-K group into the MFMA's fp8 operand), M 5..16 one wave per 32 rows; "
      "(sub * a_scale) * b_scale per group, split-K folded through LDS in chunk order",
      "M <= 16; K a multiple of 128; N any; b_scale either the 128x128 block grid or a per-row "
      "grid",
@@ -166,6 +192,15 @@ const RadKernelInfo kRows[] = {
      RAD_DOMAIN_DEVICE, kPrioTile, cMxfp4A16, 2, nullptr, 0, nullptr,
      nullptr, nullptr, r3d_rad_gemm_nt_q_mxfp4a16, r3d_rad_gemm_nt_q_mxfp4a16_scratch,
      nullptr, nullptr, nullptr, nullptr},
+
+    {"quant_act_fp8_act", "quant_act_fp8", "band",
+     "per-group symmetric E4M3 quantisation of an activation, plain row-major, on gfx950: one "
+     "wave per (row, group), v_max_f32 maximum over the group, v_cvt_pk_fp8_f32 encode",
+     "f32/bf16 inputs; the scale is amax/448, a dequant multiplier; group clamped to n; at "
+     "most 65535 rows",
+     "activation in, f8e4m3 codes and f32 group scales out",
+     RAD_DOMAIN_DEVICE, kPrioTile, cBandMn, 2, nullptr, 0, nullptr,
+     nullptr, nullptr, r3d_rad_quant_act_fp8, nullptr, nullptr, nullptr, nullptr, nullptr},
 };
 
 bool row_hidden(const RadKernelInfo& k) {
@@ -188,7 +223,8 @@ uint32_t rad_plugin_abi_version(void) { return RAD_ABI_VERSION; }
 const RadPluginInfo* rad_plugin_info(void) {
     static const RadPluginInfo info = {
         RAD_PLUGIN_KERNEL, "libr3d_gfx950", "0.1.0",
-        "radiance gemm_nt_q rows (mxfp4a8, fp8a8, mxfp4a16) for AMD Instinct MI355X (CDNA4)",
+        "radiance gemm_nt_q rows (mxfp4a8, fp8a8, mxfp4a16) and the quant_act_fp8 producer for "
+        "AMD Instinct MI355X (CDNA4)",
         "gfx950",
     };
     return &info;

@@ -34,7 +34,10 @@ def test_plugin_identity_and_schema():
     info = L.rad_plugin_info().contents
     assert info.targets == b"gfx950" and info.kind == 1
     sch = R.schemas()
-    assert [s["op"] for s in sch] == ["gemm_nt_q"]
+    assert [s["op"] for s in sch] == ["gemm_nt_q", "quant_act_fp8"]
+    q = sch[1]                              # src/r3d_rows.cpp:615-625, verbatim
+    assert [(p[0], p[2]) for p in q["params"]] == [("M", 0), ("n", 0), ("group", 0), ("dtype", 0)]
+    assert [(o[0], o[1], o[2]) for o in q["operands"]] == [("x", 0, 0), ("q", 1, 0), ("scale", 1, 0)]
     s = sch[0]
     assert [p[0] for p in s["params"]] == ["M", "N", "K", "group", "dtype", "pb1", "pb2", "split_n"]
     assert [p[2] for p in s["params"]] == [0, 0, 0, 0, 0, 1, 1, 1]          # required / optional
@@ -46,7 +49,12 @@ def test_plugin_identity_and_schema():
 def test_rows_and_resolver():
     rows = {r["name"]: r for r in R.rows()}
     assert set(rows) == {"gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", "gemm_nt_q_fp8a8",
-                         "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4a16"}
+                         "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4a16", "quant_act_fp8_act"}
+    qa = lambda **kw: R.resolve("quant_act_fp8", kw)["name"] if R.resolve("quant_act_fp8", kw) else None
+    assert qa(M=4, n=5376, group=128, dtype="bf16") == "quant_act_fp8_act"
+    assert qa(M=4, n=5376, group=128, dtype="f32") == "quant_act_fp8_act"
+    assert qa(M=4, n=5376, group=128, dtype="f16") is None
+    assert qa(M=4, n=0, group=128, dtype="bf16") is None
     assert rows["gemm_nt_q_mxfp4_decode"]["priority"] == 1100
     assert rows["gemm_nt_q_mxfp4"]["priority"] == 1000
     q = lambda **kw: R.resolve("gemm_nt_q", kw)["name"] if R.resolve("gemm_nt_q", kw) else None
@@ -74,20 +82,24 @@ print(json.dumps(sorted(r["name"] for r in R.rows())))
 A16 = "gemm_nt_q_mxfp4a16"
 
 
+QA = "quant_act_fp8_act"
+
+
 @pytest.mark.parametrize("env,expect", [
-    ({}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16]),
-    ({"R3D_NO_MXFP4": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode"]),
-    ({"R3D_NO_FP4_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", A16]),
-    ({"R3D_NO_FP8A8": "1"}, ["gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16]),
-    ({"R3D_NO_FP8_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16]),
-    ({"R3D_NO_FP8_DEC": "", "R3D_NO_FP4_DEC": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", A16]),
+    ({}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
+    ({"R3D_NO_MXFP4": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", QA]),
+    ({"R3D_NO_FP4_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", A16, QA]),
+    ({"R3D_NO_FP8A8": "1"}, ["gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
+    ({"R3D_NO_FP8_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
+    ({"R3D_NO_FP8_DEC": "", "R3D_NO_FP4_DEC": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", A16, QA]),
     ({"R3D_MXFP4_Q8X": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4",
-                              "gemm_nt_q_mxfp4_decode", A16]),
-    ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, []),
+                              "gemm_nt_q_mxfp4_decode", A16, QA]),
+    ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, [QA]),
 ])
 def test_kill_switch_matrix(env, expect):
     """Presence-tested levers hide rows at registration (the value does not matter: an
-    empty or "0" value still counts as set); R3D_MXFP4_Q8X is inert here."""
+    empty or "0" value still counts as set); R3D_MXFP4_Q8X is inert here; the band row has
+    no lever."""
     e = {k: v for k, v in os.environ.items() if not k.startswith("R3D_")}
     e.update(env)
     out = subprocess.run([sys.executable, "-c", _ROWS_SCRIPT % ROOT], env=e, capture_output=True,
@@ -341,3 +353,70 @@ def test_resolver_routes_a16_to_its_row():
     r = R.resolve("gemm_nt_q", {"dtype": "mxfp4a16", "M": 2048, "N": 21504, "K": 5376, "group": 32})
     assert r["name"] == "gemm_nt_q_mxfp4a16"
     assert R.resolve("gemm_nt_q", {"dtype": "mxfp4a16", "M": 4, "N": 64, "K": 320, "group": 32}) is None
+
+
+# ------------------------------------------------------------------ quant_act_fp8 plan
+def _qa(x, q, s, **kw):
+    return R.QuantActOperands(FakeT(x), FakeT(q) if q is not None else None,
+                              FakeT(s) if s is not None else None, **kw)
+
+
+@pytest.mark.parametrize("case,rc", [
+    ("ok", R.RAD_OK), ("no_scale", R.RAD_E_INVAL), ("x_f16", R.RAD_E_DTYPE),
+    ("q_u8", R.RAD_E_DTYPE), ("n0", R.RAD_E_SHAPE), ("rows", R.RAD_E_SHAPE),
+    ("q_short", R.RAD_E_SHAPE), ("x_col_stride", R.RAD_E_STRIDE),
+])
+def test_quant_act_plan_refusals(case, rc):
+    """The reference's gates and codes (src/r3d_band.hip:463-481), on the host."""
+    M, n = 4, 256
+    x = _aligned((M, n), np.uint16)
+    q = _aligned((M, n), np.uint8)
+    s = _aligned((M, 2), np.float32)
+    kw = dict(n=n, group=128, M=M, x_dtype="BF16")
+    if case == "no_scale":
+        ops = _qa(x, q, None, **kw)
+    else:
+        ops = _qa(x, q, s, **kw)
+        if case == "x_f16":
+            ops._t[0].dtype = R.DT["F16"]
+        elif case == "q_u8":
+            ops._t[1].dtype = R.DT["U8"]
+        elif case == "n0":
+            ops._p[0].ival = 0
+        elif case == "rows":
+            ops._t[0].shape[0] = 70000                      # rows above 65535
+            ops._t[1].shape[0] = 70000
+        elif case == "q_short":
+            ops._t[1].shape[0] = 3
+        elif case == "x_col_stride":
+            ops._t[0].stride[1] = 2
+    got, d = R.describe("quant_act_fp8_act", ops)
+    assert got == rc, d
+
+
+def test_quant_act_plan_walk():
+    """Group clamp, ragged groups and the band row walk (src/r3d_band.hip:419-449): a
+    wider-row view pitches by its row stride, a rank-1 x is one row (pitch 0), a view
+    whose shape[1] differs from n reads flat."""
+    x = _aligned((3, 300), np.float32)
+    q = _aligned((3, 300), np.uint8)
+    s = _aligned((3, 3), np.float32)
+    g = _geom(R.describe("quant_act_fp8_act", _qa(x, q, s, n=300, group=128, M=3))[1])
+    assert (g["x"], g["rows"], g["group"], g["ngrp"], g["x_pitch"]) == ("f32", "3", "128", "3", "300")
+    g = _geom(R.describe("quant_act_fp8_act", _qa(x, q, s, n=300, group=1000, M=3))[1])
+    assert (g["group"], g["ngrp"]) == ("300", "1")
+    g = _geom(R.describe("quant_act_fp8_act", _qa(x, q, s, n=300, group=0, M=3))[1])
+    assert g["group"] == "300"
+    wide = _aligned((3, 320), np.uint16)
+    ops = R.QuantActOperands(FakeT(wide), FakeT(q), FakeT(s), n=300, group=128, M=3,
+                             x_dtype="BF16", shapes={0: (3, 300)}, strides={0: (320, 1)})
+    g = _geom(R.describe("quant_act_fp8_act", ops)[1])
+    assert (g["x"], g["x_pitch"], g["q_pitch"]) == ("bf16", "320", "300")
+    one = _aligned((300,), np.uint16)
+    ops = R.QuantActOperands(FakeT(one), FakeT(q), FakeT(s), n=300, group=128, M=1, x_dtype="BF16")
+    g = _geom(R.describe("quant_act_fp8_act", ops)[1])
+    assert (g["rows"], g["x_pitch"]) == ("1", "0")
+    ops = R.QuantActOperands(FakeT(wide), FakeT(q), FakeT(s), n=300, group=128, M=3,
+                             x_dtype="BF16", shapes={0: (3, 320)}, strides={0: (320, 1)})
+    g = _geom(R.describe("quant_act_fp8_act", ops)[1])
+    assert g["x_pitch"] == "300"                              # shape[1] != n: flat walk
