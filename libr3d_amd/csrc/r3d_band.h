@@ -9,13 +9,31 @@
  * scale is a correctly rounded f32 multiply and divide (hipcc's default), and a second
  * pass encodes with v_cvt_pk_fp8_f32 (the same code as the oracle's encoder on every
  * clamped input; NaN fixed up).  With even groups, pitches and aligned bases each lane
- * moves two elements per pass (4 or 8 bytes in, 2 bytes out), else one. */
+ * moves two elements per pass (4 or 8 bytes in, 2 bytes out), else one.  The common case
+ * (groups of 8..512 that tile the rows, aligned rows) takes the vector kernel below. */
 #ifndef R3D_BAND_H
 #define R3D_BAND_H
 
 #include "r3d_device.h"
 
 namespace r3d {
+
+/* Four f32 (already inside +-448) -> four e4m3 codes, a in the low byte: two
+ * v_cvt_pk_fp8_f32, then NaN inputs are set to 0x7F with their sign.  On MI355X this is
+ * round-to-nearest-even e4m3 (the oracle's encoder) for every one of the 2^32 inputs after
+ * the +-448 clamp (checked exhaustively on the device; the conversion alone differs only on
+ * NaNs). */
+__device__ __forceinline__ uint32_t r3d_e4m3x4_rne(float a, float b, float c, float d) {
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+    const float x[4] = {a, b, c, d};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t nan = ((__float_as_uint(x[i]) >> 24) & 0x80u) | 0x7Fu;
+        w = x[i] != x[i] ? (w & ~(0xFFu << (8 * i))) | (nan << (8 * i)) : w;
+    }
+    return w;
+}
 
 /* Two f32 (already inside +-448) -> two e4m3 codes in the low 16 bits, a in the low byte:
  * one v_cvt_pk_fp8_f32, then NaN inputs set to 0x7F with their sign (the conversion
@@ -100,6 +118,65 @@ __global__ __launch_bounds__(256) void quant_act_fp8_kernel(
         } else {
             const float v = r3d_band_ld<BF16>(x, xb + i);
             qr[i] = (uint8_t)r3d_e4m3x2_rne(r3d_band_clamp448(v * inv), 0.0f);
+        }
+    }
+}
+
+/* Vector path: one workgroup per row, each thread 8 consecutive elements (one chunk) per
+ * pass, its U chunks 256 chunks apart loaded before the first is used; the L = group / 8
+ * lanes of a group (a power of two <= 64, so groups never straddle a wave) take the
+ * maximum by log2(L) xor-shuffles.  Needs group % 8 == 0, n % group == 0, 16-byte aligned
+ * x rows and 8-byte aligned q rows (the launch checks). */
+constexpr int kQaU = 4;
+
+template <bool BF16, int L>
+__global__ __launch_bounds__(256) void quant_act_fp8_vec_kernel(
+    const uint8_t* __restrict__ x, int64_t x_pitch, uint8_t* __restrict__ q, int64_t q_pitch,
+    float* __restrict__ sc, int64_t s_pitch, int64_t n) {
+    const int64_t row = blockIdx.x;
+    const int64_t chunks = n >> 3;
+    const uint8_t* xr = x + row * x_pitch * (BF16 ? 2 : 4);
+    uint8_t* qr = q + row * q_pitch;
+    float* sr = sc + row * s_pitch;
+    for (int64_t c0 = threadIdx.x; c0 - threadIdx.x < chunks; c0 += 256 * kQaU) {
+        float v[kQaU][8];
+#pragma unroll
+        for (int u = 0; u < kQaU; ++u) {
+            /* a thread past the row's end re-reads its last chunk: the lanes of a group
+             * leave the shuffles together, and nothing of it is stored */
+            const int64_t c = c0 + 256 * u < chunks ? c0 + 256 * u : chunks - 1;
+            if (BF16) {
+                const r3d_i32x4 w = *reinterpret_cast<const r3d_i32x4*>(xr + 16 * c);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[u][2 * i] = __uint_as_float((uint32_t)w[i] << 16);
+                    v[u][2 * i + 1] = __uint_as_float((uint32_t)w[i] & 0xFFFF0000u);
+                }
+            } else {
+                const float4 a = *reinterpret_cast<const float4*>(xr + 32 * c);
+                const float4 b = *reinterpret_cast<const float4*>(xr + 32 * c + 16);
+                v[u][0] = a.x; v[u][1] = a.y; v[u][2] = a.z; v[u][3] = a.w;
+                v[u][4] = b.x; v[u][5] = b.y; v[u][6] = b.z; v[u][7] = b.w;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kQaU; ++u) {
+            const int64_t c = c0 + 256 * u;
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[u][i]));
+#pragma unroll
+            for (int off = L / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            if (c >= chunks) continue;
+            const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+            const float inv = 1.0f / s;
+            if ((c & (L - 1)) == 0) sr[c / L] = s;
+            float cv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cv[i] = r3d_band_clamp448(v[u][i] * inv);
+            const uint32_t lo = r3d_e4m3x4_rne(cv[0], cv[1], cv[2], cv[3]);
+            const uint32_t hi = r3d_e4m3x4_rne(cv[4], cv[5], cv[6], cv[7]);
+            *reinterpret_cast<uint2*>(qr + 8 * c) = make_uint2(lo, hi);
         }
     }
 }

@@ -285,10 +285,36 @@ static int quant_entry(const RadArgs* a, RadStream s) {
     const int64_t blocks = (items + 3) / 4;
     if (blocks > 0x7FFFFFFF) return RAD_E_SHAPE;
     const int eb = P.x_bf16 ? 2 : 4;
+    const int lanes = (int)(P.g / 8);
+    const bool vec = P.g % 8 == 0 && lanes >= 1 && lanes <= 64 && (lanes & (lanes - 1)) == 0 &&
+                     P.n % P.g == 0 && ((uintptr_t)P.x % 16) == 0 && (P.x_pitch * eb) % 16 == 0 &&
+                     ((uintptr_t)P.q % 8) == 0 && P.q_pitch % 8 == 0;
+    hipStream_t stream = (hipStream_t)s;
+    if (vec) {
+#define R3D_QV(B_, L_)                                                                      \
+    hipLaunchKernelGGL((quant_act_fp8_vec_kernel<B_, L_>), dim3((unsigned)P.rows), dim3(256), \
+                       0, stream, P.x, P.x_pitch, P.q, P.q_pitch, P.scale, P.s_pitch, P.n)
+#define R3D_QVL(B_)                                                                         \
+    switch (lanes) {                                                                        \
+        case 1: R3D_QV(B_, 1); break;   case 2: R3D_QV(B_, 2); break;                       \
+        case 4: R3D_QV(B_, 4); break;   case 8: R3D_QV(B_, 8); break;                       \
+        case 16: R3D_QV(B_, 16); break; case 32: R3D_QV(B_, 32); break;                     \
+        default: R3D_QV(B_, 64); break;                                                     \
+    }
+        if (P.x_bf16) { R3D_QVL(true); } else { R3D_QVL(false); }
+#undef R3D_QVL
+#undef R3D_QV
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) {
+            fprintf(stderr, "libr3d_gfx950: quant_act_fp8 launch FAILED (%s)\n", hipGetErrorName(e));
+            return RAD_E_DEVICE;
+        }
+        debug_once("quant_act_fp8 (vector)", 251);
+        return RAD_OK;
+    }
     const bool pair = (P.g % 2) == 0 && (P.n % 2) == 0 && (P.x_pitch % 2) == 0 &&
                       (P.q_pitch % 2) == 0 && ((uintptr_t)P.x % (2 * eb)) == 0 &&
                       ((uintptr_t)P.q % 2) == 0;
-    hipStream_t stream = (hipStream_t)s;
 #define R3D_QA(B_, P_)                                                                      \
     hipLaunchKernelGGL((quant_act_fp8_kernel<B_, P_>), dim3((unsigned)blocks), dim3(256), 0,  \
                        stream, P.x, P.x_pitch, P.q, P.q_pitch, P.scale, P.s_pitch, P.n, P.g,  \

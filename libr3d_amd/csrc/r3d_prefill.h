@@ -42,6 +42,7 @@
 #ifndef R3D_PREFILL_H
 #define R3D_PREFILL_H
 
+#include "r3d_band.h"
 #include "r3d_device.h"
 #include "r3d_prefill_layout.h"
 
@@ -485,7 +486,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(
 /* f32 -> e4m3 code, round to nearest even, saturating at +-448, NaN -> 0x7F with the sign.
  * Branch-free (selects only): on MI355X it gives the same code as the step-by-step form
  * (exponent / mantissa split, explicit subnormal shift and tie test) for every one of the
- * 2^32 inputs after the quantiser's +-448 clamp (checked exhaustively on the device). */
+ * 2^32 inputs after the quantiser's +-448 clamp (checked exhaustively on the device); the
+ * kernels encode with r3d_e4m3x4_rne (r3d_band.h), checked equal to it on all inputs. */
 __device__ __forceinline__ uint32_t r3d_e4m3_rne(float f) {
     const uint32_t u = __float_as_uint(f);
     const uint32_t s = (u >> 24) & 0x80u;
@@ -504,22 +506,6 @@ __device__ __forceinline__ uint32_t r3d_e4m3_rne(float f) {
     r = r > 0x7Eu ? 0x7Eu : r;
     r = a > 0x7F800000u ? 0x7Fu : r;
     return s | r;
-}
-
-/* Four f32 (already inside +-448) -> four e4m3 codes, a in the low byte: two
- * v_cvt_pk_fp8_f32, then NaN inputs are set to 0x7F with their sign.  On MI355X this is
- * the same code as r3d_e4m3_rne for every one of the 2^32 inputs after the +-448 clamp
- * (checked exhaustively on the device; the conversion alone differs only on NaNs). */
-__device__ __forceinline__ uint32_t r3d_e4m3x4_rne(float a, float b, float c, float d) {
-    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
-    w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
-    const float x[4] = {a, b, c, d};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t nan = ((__float_as_uint(x[i]) >> 24) & 0x80u) | 0x7Fu;
-        w = x[i] != x[i] ? (w & ~(0xFFu << (8 * i))) | (nan << (8 * i)) : w;
-    }
-    return w;
 }
 
 /* Each thread converts 8 consecutive elements (one 16-byte load) and four lanes share a

@@ -2,9 +2,10 @@
 producer (src/r3d_band.hip:117-153; oracle/r3d_oracle.c r3d_ref_quant_act_fp8), through
 the C ABI: codes and scales bit-exact, red zones intact, every output written.
 
-Covers bf16 and f32 inputs, the two-element and one-element lane paths (even / odd sizes
-and offsets), ragged last groups, a group past n (clamped to n), strided and rank-1
-views, and the special values: NaN (never the group maximum, encoded 0x7F with its sign),
+Covers bf16 and f32 inputs, the vector path (groups of 8..512 tiling aligned rows: every
+group width it instantiates) and the two-element and one-element lane paths (ragged,
+even / odd sizes and offsets), a group past n (clamped to n), strided and rank-1 views,
+and the special values: NaN (never the group maximum, encoded 0x7F with its sign),
 +-Inf (scale Inf, finite codes 0, Inf codes NaN), signed zeros, subnormals, an all-zero
 group (scale 1) and a lone non-zero element.
 """
@@ -63,7 +64,8 @@ def _bf16(a):
 @pytest.mark.parametrize("M,n,group", [(1, 5376, 128), (4, 5376, 128), (17, 4096, 128),
                                        (3, 200, 128), (2, 256, 32), (5, 384, 64),
                                        (3, 300, 1000), (2, 7, 128), (3, 131, 16),
-                                       (2048, 5376, 128)])
+                                       (2, 1024, 8), (3, 2048, 16), (2, 1024, 256),
+                                       (2, 2048, 512), (2048, 5376, 128)])
 def test_quant_act_fp8_bf16(gpu, M, n, group):
     rng = np.random.default_rng(M * 7 + n + group)
     x = _bf16(rng.standard_normal((M, n), dtype=np.float32) * np.float32(3.0))
