@@ -263,6 +263,7 @@ def main():
         del c
         torch.cuda.empty_cache()
         extra.update(bench_quant(dev, stream))
+        extra.update(bench_fused_decode(dev, stream, ksteps))
         extra.update(bench_c4(dev, stream, steps=5))
     if extra:
         out["extra"] = extra
@@ -342,6 +343,69 @@ def bench_quant(dev, stream, steps=50):
                                          "GBps": round(nb / t / 1e9, 1),
                                          "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
         log("[bench] quant_act_fp8 M=%d n=%d: %.2f us, %.1f GB/s" % (M, n, t * 1e6, nb / t / 1e9))
+    return res
+
+
+def bench_fused_decode(dev, stream, steps=50):
+    """A decode call fed bf16 activations, two ways, cold weights: the quant_act_fp8 row then
+    the decode row (two launches), and the decode row taking the bf16 rows itself (the
+    producer fused into its LDS staging, one launch; M = 1 only).  Config 1's shape (fp8a8) and
+    config 2's gate_up (mxfp4a8)."""
+    import torch
+    import libr3d_amd as R
+    from libr3d_amd import synth
+    res = {}
+    for name, dtype, M, K, N in (("c1_fp8a8_M1", "fp8a8", 1, 5376, 21504),
+                                 ("c2_mxfp4_gate_up_M1", "mxfp4a8", 1, 5376, 21504)):
+        if dtype == "fp8a8":
+            B, BS = synth.fp8_weights(N, K, 0x5EED + 11)
+            BS = BS.view(np.int16)
+            row, nb = "gemm_nt_q_fp8a8_decode", f8_bytes(M, N, K)
+        else:
+            B, BS = synth.mxfp4_weights(N, K, 0x5EED + 21 + K)
+            row, nb = "gemm_nt_q_mxfp4_decode", mx_bytes(M, N, K)
+        copies = copies_for(B.nbytes + BS.nbytes)
+        bs = [torch.from_numpy(B).to(dev)]
+        bss = [torch.from_numpy(BS).to(dev)]
+        for _ in range(copies - 1):
+            bs.append(bs[0].clone())
+            bss.append(bss[0].clone())
+        x = torch.randn((M, K), device=dev, dtype=torch.float32).to(torch.bfloat16).view(torch.int16)
+        q = torch.empty((M, K), dtype=torch.uint8, device=dev)
+        sc = torch.empty((M, K // 128), dtype=torch.float32, device=dev)
+        y = torch.empty((M, N), dtype=torch.int16, device=dev)
+        qa = R.QuantActOperands(x, q, sc, n=K, group=128, M=M, x_dtype="BF16")
+        two = [R.GemmOperands(q, sc, b, s_, y, dtype=dtype, N=N, K=K) for b, s_ in zip(bs, bss)]
+        one = [R.GemmOperands(x, None, b, s_, y, dtype=dtype, N=N, K=K) for b, s_ in zip(bs, bss)]
+        fq, fg = R.row_launcher("quant_act_fp8_act"), R.row_launcher(row)
+
+        def timed(body):
+            for i in range(10):
+                body(i)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for i in range(steps):
+                body(i)
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e-3 / steps
+
+        def unfused(i):
+            assert fq(qa, stream) == 0 and fg(two[i % copies], stream) == 0
+
+        def fused(i):
+            assert fg(one[i % copies], stream) == 0
+
+        t2, t1 = timed(unfused), timed(fused)
+        res["fused_decode_" + name] = {
+            "M": M, "K": K, "N": N, "two_launch_us": round(t2 * 1e6, 2),
+            "fused_us": round(t1 * 1e6, 2), "GBps_fused": round(nb / t1 / 1e9, 1)}
+        log("[bench] bf16-fed decode %s: quant + GEMV %.2f us, fused %.2f us" % (
+            name, t2 * 1e6, t1 * 1e6))
+        del bs, bss, one, two
+        torch.cuda.empty_cache()
     return res
 
 

@@ -200,6 +200,8 @@ class GemmOperands:
 
     a      uint8 [M, K]           e4m3 codes (mxfp4a16: bf16/int16 [M, K])
     a_scale float32 [M, K/128]    (mxfp4a16: None)
+           The decode rows also take a bf16/int16 `a` with a_scale None: the GEMV quantises
+           it with quant_act_fp8's arithmetic (groups of 128) on the way into its LDS.
     b      uint8 [N, K/2] (mxfp4a8/a16: packed e2m1, low nibble = even k) or [N, K] (fp8a8)
     b_scale uint8 [N, K/32] E8M0 (mxfp4) or bf16/int16 [N or N/128, K/128] (fp8a8)
     y      bf16/int16 [M, N]
@@ -228,7 +230,8 @@ class GemmOperands:
                 t[i].shape[r] = int(s_)
                 t[i].stride[r] = int(st)
 
-        fill(0, a, "BF16" if dtype == "mxfp4a16" else "F8E4M3")
+        fused = a is not None and a_scale is None and a.element_size() == 2
+        fill(0, a, "BF16" if dtype == "mxfp4a16" or fused else "F8E4M3")
         fill(1, a_scale, "F32")
         if mx:
             # FP4 counts nibbles: [N, K] with strides {K, 1}

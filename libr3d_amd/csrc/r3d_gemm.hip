@@ -68,17 +68,16 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
     /* mxfp4 scale rows contiguous (pitch = K/32) in a 16-byte aligned plane: 1 KB staging loads */
     const int sc16 = P.enc == ENC_MXFP4A8 && P.bs_pitch == P.K / 32 &&
                      ((uintptr_t)P.BS & 15) == 0;
+    if (P.xq && g.mt != 1) return RAD_E_UNSUPPORTED;    /* the fused producer is MT = 1 only */
+#define R3D_QUAD1(ENC_, MT_, Q_, D_, X_)                                                    \
+    hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, Q_, D_, X_>), grid, block, (size_t)g.lds, \
+                       stream, P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K,       \
+                       g.chunks, P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, sc16,        \
+                       P.a_pitch, P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch)
 #define R3D_QUAD(ENC_, MT_, D_)                                                              \
-    if (g.qpw == 2)                                                                          \
-        hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, 2, D_>), grid, block, (size_t)g.lds,   \
-                           stream, P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K,   \
-                           g.chunks, P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, sc16,    \
-                           P.a_pitch, P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch);          \
-    else                                                                                     \
-    hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, 1, D_>), grid, block, (size_t)g.lds, stream, \
-                       P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K, g.chunks,      \
-                       P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, sc16, P.a_pitch,       \
-                       P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch)
+    if (P.xq) R3D_QUAD1(ENC_, MT_, 1, D_, (MT_ == 1));                                       \
+    else if (g.qpw == 2) R3D_QUAD1(ENC_, MT_, 2, D_, 0);                                     \
+    else R3D_QUAD1(ENC_, MT_, 1, D_, 0)
 #define R3D_QUAD_D(ENC_, MT_)                                                                \
     do {                                                                                     \
         switch (g.depth) {                                                                   \
@@ -97,13 +96,14 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
     }
 #undef R3D_QUAD_D
 #undef R3D_QUAD
+#undef R3D_QUAD1
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         fprintf(stderr, "libr3d_gfx950: quad decode GEMV launch FAILED (%s)\n", hipGetErrorName(e));
         return RAD_E_DEVICE;
     }
     debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 quad decode GEMV" : "fp8a8 quad decode GEMV",
-               128 + (P.enc << 4) + g.mt);
+               128 + (P.enc << 4) + g.mt + 2 * P.xq);
     return RAD_OK;
 }
 
@@ -152,6 +152,7 @@ static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) 
     QuadGeom qg{};
     if (quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg))
         return launch_quad(P, qg, stream);
+    if (P.xq) return RAD_E_UNSUPPORTED;     /* fused bf16 activations: the quad GEMV only */
     LinesGeom lg{};
     if (lines_fits(P) && lines_geom(P.enc, P.M, P.N, P.K, splitk, &lg))
         return launch_lines(P, lg, stream);

@@ -44,6 +44,7 @@
 #ifndef R3D_GEMV_QUAD_H
 #define R3D_GEMV_QUAD_H
 
+#include "r3d_band.h"
 #include "r3d_device.h"
 #include "r3d_plan.h"
 
@@ -99,7 +100,7 @@ __device__ __forceinline__ void r3d_quad_dma(const void* g, uint32_t lds) {
 }
 #pragma clang diagnostic pop
 
-template <int ENC, int MT, int QPW, int D>
+template <int ENC, int MT, int QPW, int D, int XQ = 0>
 __global__ __launch_bounds__(256) void gemv_quad_kernel(
     const uint8_t* A, const float* AS, const uint8_t* B, const void* BSv,
     uint16_t* __restrict__ Y,
@@ -164,8 +165,8 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
         }
     }
     /* ... then the workgroup's activation rows ([MT][K + 16] bytes, whole K) and a_scales
-     * ([MT][groups] f32), shared by its 4 waves */
-    {
+     * ([MT][groups] f32), shared by its 4 waves (XQ: quantised here, below) */
+    if (!XQ) {
         const int xp = K + 16;
         const int nx = (MT * xp + 1023) >> 10;
         for (int i = wave; i < nx; i += 4) {
@@ -222,6 +223,66 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
         return v;
     };
 
+    /* XQ: the activations arrive as bf16 rows (A, a_pitch bytes) and are quantised into the
+     * same LDS images with quant_act_fp8's arithmetic over groups of 128 (src/r3d_band.hip:
+     * 117-153): amax = max |x| (NaN never wins), sc = amax > 0 ? amax / 448 : 1 (as
+     * amax * (1/448)), q = e4m3_rne(clamp(x * (1 / sc), +-448)) -- the codes and scales the
+     * quant_act_fp8 row writes, so the products are those of the unfused pair.  A lane takes
+     * one 16-byte chunk (8 values) of the [MT][K / 8] chunk space per block of 64 chunks; a
+     * group is 16 consecutive chunks, i.e. 16 lanes, reduced by 4 xor-shuffles.  Wave w
+     * takes blocks w, w + 4, ...; XU blocks per batch, the first batch's loads issued
+     * before the weight ring is primed (so waiting for them never waits for weights).  One
+     * batch covers K <= 8192; a longer K takes more batches, whose loads wait behind the
+     * ring's.  MT = 1 only: every workgroup re-reads the bf16 rows (twice the bytes of the
+     * e4m3 images) and re-quantises them, which at MT = 4 costs more than the separate
+     * producer launch it saves. */
+    static_assert(!XQ || MT == 1, "the fused producer is built for one activation row");
+    constexpr int XU = XQ ? 4 : 1;
+    const int cpr = K >> 3, nchunk = MT * cpr;
+    const int nxb = (nchunk + 63) >> 6;
+    r3d_i32x4 xv[XU];
+    auto xq_load = [&](int batch) {
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int c0 = 64 * (wave + 4 * (batch * XU + u)) + lane;
+            const int c = c0 < nchunk ? c0 : nchunk - 1;
+            const int t = c / cpr, k = 8 * (c - t * cpr);
+            const int tm = t < M ? t : M - 1;
+            xv[u] = *reinterpret_cast<const r3d_i32x4*>(A + (int64_t)tm * a_pitch + 2 * k);
+        }
+    };
+    auto xq_store = [&](int batch) {
+        float* xst = reinterpret_cast<float*>(smem + xs_off);
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int c = 64 * (wave + 4 * (batch * XU + u)) + lane;
+            float v[8];
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[2 * i] = __uint_as_float((uint32_t)xv[u][i] << 16);
+                v[2 * i + 1] = __uint_as_float((uint32_t)xv[u][i] & 0xFFFF0000u);
+                amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
+            }
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            if (c < nchunk) {                              /* whole 16-lane groups */
+                const int t = c / cpr, k = 8 * (c - t * cpr);
+                const float sc = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+                const float inv = 1.0f / sc;
+                float cv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) cv[i] = r3d_band_clamp448(v[i] * inv);
+                *reinterpret_cast<uint2*>(smem + t * (K + 16) + k) =
+                    make_uint2(r3d_e4m3x4_rne(cv[0], cv[1], cv[2], cv[3]),
+                               r3d_e4m3x4_rne(cv[4], cv[5], cv[6], cv[7]));
+                if ((lane & 15) == 0) xst[t * groups + (k >> 7)] = sc;
+            }
+        }
+    };
+    if (XQ) xq_load(0);
+    __builtin_amdgcn_sched_barrier(0);
+
     /* Scheduling barriers keep each step's loads in step order, in the prologue as in the
      * loop, so every wait is "the oldest step's loads".  The launch picks D <= ns. */
     Step ring[D];
@@ -230,9 +291,19 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
         ring[d] = load(d);
         __builtin_amdgcn_sched_barrier(0);
     }
-    /* this wave's LDS loads are all but the newest D*LPS loads in flight: wait for them,
-     * then meet the other waves */
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(D * LPS) : "memory");
+    if (XQ) {
+        for (int b = 0;;) {
+            xq_store(b);
+            if (++b * 4 * XU >= nxb) break;
+            xq_load(b);
+        }
+        /* the quantised rows are this wave's LDS writes: publish them with the staging */
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(D * LPS) : "memory");
+    } else {
+        /* this wave's LDS loads are all but the newest D*LPS loads in flight: wait for
+         * them, then meet the other waves */
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(D * LPS) : "memory");
+    }
 
     /* ---- 3. consume: B operand, a_scale and weight scales from LDS.  These are ordinary
      * LDS reads: the compiler knows nothing of the LDS fill (inline asm above), so it

@@ -52,7 +52,9 @@ int entry_preamble(const RadArgs* a, int enc, int64_t m_max, int64_t* M, int64_t
     const RadTensor* ASUM = rad_arg_in(a, 5);
     const RadTensor* BREF = rad_arg_in(a, 6);
     if (!A || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
-    if (enc == ENC_MXFP4A16 ? AS != nullptr : AS == nullptr) return RAD_E_UNSUPPORTED;
+    /* a decode row takes bf16 activations without a_scale: the fused quant_act_fp8 */
+    const bool fused = m_max > 0 && enc != ENC_MXFP4A16 && AS == nullptr && A->dtype == RAD_BF16;
+    if (enc == ENC_MXFP4A16 ? AS != nullptr : (AS == nullptr && !fused)) return RAD_E_UNSUPPORTED;
     if (ASUM) return RAD_E_UNSUPPORTED;                 /* no zero point at any encoding */
     if (enc == ENC_FP8A8 && BREF) return RAD_E_UNSUPPORTED;   /* b_ref: e2m1 weights only */
     if (Y->dtype != RAD_BF16) return RAD_E_UNSUPPORTED;
@@ -79,9 +81,13 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     const RadTensor* B  = rad_arg_in(a, 2);
     const RadTensor* BS = rad_arg_in(a, 3);
     const RadTensor* Y  = rad_arg_in(a, 4);
-    if (!A || !AS || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
-    if (A->dtype != RAD_F8E4M3 || B->dtype != RAD_FP4E2M1 || Y->dtype != RAD_BF16 ||
-        AS->dtype != RAD_F32 || (BS->dtype != RAD_E8M0 && BS->dtype != RAD_U8))
+    /* AS absent with bf16 A: the decode rows' fused producer (the preamble let it through
+     * only there) */
+    const bool xq = A && !AS && A->dtype == RAD_BF16;
+    if (!A || (!AS && !xq) || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
+    if ((xq ? A->dtype != RAD_BF16 : A->dtype != RAD_F8E4M3) || B->dtype != RAD_FP4E2M1 ||
+        Y->dtype != RAD_BF16 || (!xq && AS->dtype != RAD_F32) ||
+        (BS->dtype != RAD_E8M0 && BS->dtype != RAD_U8))
         return RAD_E_UNSUPPORTED;
 
     long long K = 0;
@@ -89,27 +95,29 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     if (N <= 0 || K <= 0 || M <= 0) return RAD_E_SHAPE;
     if (M > kDimMax || N > kDimMax || K > kDimMax) return RAD_E_SHAPE;
     if (rad_tensor_numel(A) < M * K || rad_tensor_numel(B) < N * K) return RAD_E_SHAPE;
+    if (xq && M != 1) return RAD_E_UNSUPPORTED;    /* fused producer: M = 1 only */
 
     /* Scale grids derived from the operands, then pinned to b 32 / a 128. */
     if (BS->rank != 2 || BS->stride[1] != 1 || BS->shape[0] < N) return RAD_E_UNSUPPORTED;
-    if (AS->rank != 2 || AS->stride[1] != 1 || AS->shape[0] < M) return RAD_E_UNSUPPORTED;
-    const int64_t bs_cols = BS->shape[1], as_cols = AS->shape[1];
+    if (!xq && (AS->rank != 2 || AS->stride[1] != 1 || AS->shape[0] < M)) return RAD_E_UNSUPPORTED;
+    const int64_t bs_cols = BS->shape[1], as_cols = xq ? (K + 127) / 128 : AS->shape[1];
     if (grid_block(K, bs_cols) != 32 || grid_block(K, as_cols) != 128) return RAD_E_UNSUPPORTED;
     if (bs_cols != (K + 31) / 32 || as_cols != (K + 127) / 128) return RAD_E_UNSUPPORTED;
-    if (rad_tensor_numel(AS) < M * as_cols) return RAD_E_SHAPE;
+    if (!xq && rad_tensor_numel(AS) < M * as_cols) return RAD_E_SHAPE;
 
     if (!inner_contig(A) || !inner_contig(B) || !inner_contig(Y)) return RAD_E_STRIDE;
     if ((K & 1) || row_stride(B, K) != K) return RAD_E_STRIDE;   /* nibble rows packed */
 
     /* gfx950 gates: whole 128-wide MFMA steps, 16-byte operand walks. */
     if (K % 128) return RAD_E_UNSUPPORTED;
-    const int64_t a_pitch = row_stride(A, K);
+    const int64_t a_pitch = row_stride(A, K) * (xq ? 2 : 1);     /* bytes */
     if (!aligned16(A->data) || !aligned16(B->data) || (a_pitch & 15)) return RAD_E_UNSUPPORTED;
     if ((uintptr_t)BS->data & 3) return RAD_E_UNSUPPORTED;      /* dword scale walk */
 
     P->enc = ENC_MXFP4A8;
+    P->xq = xq;
     P->A = (const uint8_t*)A->data;
-    P->AS = (const float*)AS->data;
+    P->AS = xq ? nullptr : (const float*)AS->data;
     P->B = (const uint8_t*)B->data;
     P->BS = BS->data;
     P->Y = (uint16_t*)Y->data;
@@ -117,7 +125,7 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     P->a_pitch = a_pitch;
     P->b_pitch = K / 2;
     P->y_pitch = row_stride(Y, N);
-    P->as_pitch = row_stride(AS, as_cols);
+    P->as_pitch = xq ? as_cols : row_stride(AS, as_cols);
     P->bs_pitch = row_stride(BS, bs_cols);
     if (P->bs_pitch & 3) return RAD_E_UNSUPPORTED;               /* dword scale walk */
     P->as_cols = (int)as_cols;
@@ -205,9 +213,10 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
     const RadTensor* B  = rad_arg_in(a, 2);
     const RadTensor* BS = rad_arg_in(a, 3);
     const RadTensor* Y  = rad_arg_in(a, 4);
-    if (!A || !AS || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
-    if (A->dtype != RAD_F8E4M3 || B->dtype != RAD_F8E4M3 || AS->dtype != RAD_F32 ||
-        BS->dtype != RAD_BF16 || Y->dtype != RAD_BF16)
+    const bool xq = A && !AS && A->dtype == RAD_BF16;       /* the decode rows' fused producer */
+    if (!A || (!AS && !xq) || !B || !BS || !Y) return RAD_E_UNSUPPORTED;
+    if ((xq ? A->dtype != RAD_BF16 : A->dtype != RAD_F8E4M3) || B->dtype != RAD_F8E4M3 ||
+        (!xq && AS->dtype != RAD_F32) || BS->dtype != RAD_BF16 || Y->dtype != RAD_BF16)
         return RAD_E_UNSUPPORTED;
 
     long long N = 0, K = 0;
@@ -217,13 +226,14 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
     if (M <= 0) return RAD_E_SHAPE;
     if (M > kDimMax || N > kDimMax || K > kDimMax) return RAD_E_SHAPE;
     if (rad_tensor_numel(A) < M * K || rad_tensor_numel(B) < N * K) return RAD_E_SHAPE;
+    if (xq && M != 1) return RAD_E_UNSUPPORTED;    /* fused producer: M = 1 only */
 
     if (BS->rank != 2 || BS->stride[1] != 1) return RAD_E_UNSUPPORTED;
-    if (AS->rank != 2 || AS->stride[1] != 1 || AS->shape[0] < M) return RAD_E_UNSUPPORTED;
-    const int64_t bs_cols = BS->shape[1], as_cols = AS->shape[1];
+    if (!xq && (AS->rank != 2 || AS->stride[1] != 1 || AS->shape[0] < M)) return RAD_E_UNSUPPORTED;
+    const int64_t bs_cols = BS->shape[1], as_cols = xq ? (K + 127) / 128 : AS->shape[1];
     if (grid_block(K, bs_cols) != 128 || grid_block(K, as_cols) != 128) return RAD_E_UNSUPPORTED;
     if (bs_cols != (K + 127) / 128 || as_cols != (K + 127) / 128) return RAD_E_SHAPE;
-    if (rad_tensor_numel(AS) < M * as_cols) return RAD_E_SHAPE;
+    if (!xq && rad_tensor_numel(AS) < M * as_cols) return RAD_E_SHAPE;
     int rblk;
     if (BS->shape[0] >= N) {
         if (BS->shape[0] != N) return RAD_E_SHAPE;
@@ -240,13 +250,14 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
 
     if (!inner_contig(A) || !inner_contig(B) || !inner_contig(Y)) return RAD_E_STRIDE;
 
-    const int64_t a_pitch = row_stride(A, K), b_pitch = row_stride(B, K);
+    const int64_t a_pitch = row_stride(A, K) * (xq ? 2 : 1), b_pitch = row_stride(B, K);
     if (!aligned16(A->data) || !aligned16(B->data) || (a_pitch & 15) || (b_pitch & 15))
         return RAD_E_UNSUPPORTED;
 
     P->enc = ENC_FP8A8;
+    P->xq = xq;
     P->A = (const uint8_t*)A->data;
-    P->AS = (const float*)AS->data;
+    P->AS = xq ? nullptr : (const float*)AS->data;
     P->B = (const uint8_t*)B->data;
     P->BS = BS->data;
     P->Y = (uint16_t*)Y->data;
@@ -254,7 +265,7 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
     P->a_pitch = a_pitch;
     P->b_pitch = b_pitch;
     P->y_pitch = row_stride(Y, N);
-    P->as_pitch = row_stride(AS, as_cols);
+    P->as_pitch = xq ? as_cols : row_stride(AS, as_cols);
     P->bs_pitch = row_stride(BS, bs_cols);
     P->as_cols = (int)as_cols;
     P->bs_cols = (int)bs_cols;
@@ -599,9 +610,14 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
     if (dec && quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &qg)) {
         snprintf(buf, (size_t)len,
                  "arm=decode kernel=quad enc=%s M=%lld N=%lld K=%lld mt=%d qpw=%d chunks=%d "
-                 "waves=4 quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d",
+                 "waves=4 quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d xq=%d",
                  ename, (long long)P.M, (long long)P.N, (long long)P.K, qg.mt, qg.qpw, qg.chunks,
-                 (long long)qg.quads, (long long)qg.blocks, qg.groups, qg.depth, qg.lds, P.rblk);
+                 (long long)qg.quads, (long long)qg.blocks, qg.groups, qg.depth, qg.lds, P.rblk,
+                 P.xq);
+    } else if (dec && P.xq) {
+        snprintf(buf, (size_t)len, "refused rc=%d (fused bf16 activations need the quad GEMV)",
+                 RAD_E_UNSUPPORTED);
+        return RAD_E_UNSUPPORTED;
     } else if (LinesGeom lg{}; dec && lines_fits(P) &&
                lines_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &lg)) {
         snprintf(buf, (size_t)len,

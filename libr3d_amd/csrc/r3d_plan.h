@@ -27,6 +27,9 @@ struct GemmPlan {
                                                                 (mxfp4a16 A: elements) */
     int as_cols, bs_cols;
     int rblk;                /* fp8a8 weight-scale rows per scale row: 1 or 128 */
+    int xq;                  /* decode rows at M = 1: A is a bf16 row (a_pitch bytes), AS
+                                absent -- quantised in the kernel with quant_act_fp8's
+                                arithmetic */
     uint8_t* scratch;        /* mxfp4a16: e4m3 codes [M, K] then E8M0 [M, K/32] */
 };
 
@@ -105,9 +108,10 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P);
  * scratch of at least mxfp4a16_scratch_bytes(M, K), 16-byte aligned. */
 int plan_mxfp4a16(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P);
 
-/* The shared entry preamble: operands present (a_scale except at mxfp4a16), a_sum (and
- * for fp8a8 b_ref) refused, Y bf16 and inner-contiguous, N from the schema parameter,
- * M = numel(Y)/N (never the M parameter), and the band's own M bound when `m_max` > 0. */
+/* The shared entry preamble: operands present (a_scale except at mxfp4a16, and at the
+ * decode rows when `a` is bf16: the fused producer), a_sum (and for fp8a8 b_ref) refused, Y
+ * bf16 and inner-contiguous, N from the schema parameter, M = numel(Y)/N (never the M
+ * parameter), and the band's own M bound when `m_max` > 0 (a decode row). */
 int entry_preamble(const RadArgs* a, int enc, int64_t m_max, int64_t* M, int64_t* N);
 
 /* wave_lds: LDS bytes one wave needs (0 = unknown: assume it fits 8 waves per workgroup). */

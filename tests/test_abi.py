@@ -128,6 +128,9 @@ class FakeT:
     def numel(self):
         return self.arr.size
 
+    def element_size(self):
+        return self.arr.itemsize
+
 
 def _aligned(shape, dtype):
     n = int(np.prod(shape)) * np.dtype(dtype).itemsize
@@ -273,6 +276,52 @@ def test_fp8_plan_refusals(case, rc):
     assert got == rc, (case, d)
     if rc == R.RAD_OK:
         assert _geom(d)["rblk"] == str(rblk)
+
+
+def _xq_ops(dtype, M, N, K, pitch=None, rblk=1, a_dt=np.uint16, **kw):
+    """Decode operands with bf16 activations and no a_scale (the fused producer)."""
+    a = FakeT(_aligned((M, pitch or K), a_dt))
+    if pitch:
+        a.shape, a.arr = (M, K), a.arr
+        a.stride = lambda dim=None, p=pitch: (p, 1) if dim is None else (p, 1)[dim]
+    if dtype == "mxfp4a8":
+        b = FakeT(_aligned((N, K // 2), np.uint8))
+        bs = FakeT(_aligned((N, K // 32), np.uint8))
+    else:
+        b = FakeT(_aligned((N, K), np.uint8))
+        bs = FakeT(_aligned((N if rblk == 1 else (N + 127) // 128, K // 128), np.uint16))
+    y = FakeT(_aligned((M, N), np.uint16))
+    return R.GemmOperands(a, None, b, bs, y, dtype=dtype, N=N, K=K, **kw)
+
+
+@pytest.mark.parametrize("dtype,row", [("mxfp4a8", "gemm_nt_q_mxfp4_decode"),
+                                       ("fp8a8", "gemm_nt_q_fp8a8_decode")])
+def test_fused_producer_plan(dtype, row):
+    """bf16 activations without a_scale: accepted by the decode row at M = 1 (the quad GEMV
+    quantises the row in its LDS staging), refused everywhere else so the engine runs the
+    producer first."""
+    for M, N, K in [(1, 21504, 5376), (1, 64, 256), (1, 5376, 21504), (1, 2048, 16384)]:
+        rc, d = R.describe(row, _xq_ops(dtype, M, N, K))
+        assert rc == R.RAD_OK, (M, N, K, d)
+        g = _geom(d)
+        assert g["kernel"] == "quad" and g["xq"] == "1", d
+    if dtype == "fp8a8":
+        rc, d = R.describe(row, _xq_ops(dtype, 1, 512, 1024, rblk=128))
+        assert rc == R.RAD_OK and _geom(d)["rblk"] == "128", d
+    rc, d = R.describe(row, _xq_ops(dtype, 1, 256, 512, pitch=512 + 64))
+    assert rc == R.RAD_OK, d
+    refused = [
+        _xq_ops(dtype, 4, 5376, 5376),                        # M > 1
+        _xq_ops(dtype, 2, 64, 256),
+        _xq_ops(dtype, 8, 512, 1024),
+        _xq_ops(dtype, 1, 512, 1024, tunables=[("splitk", 8)]),
+        _xq_ops(dtype, 1, 256, 512, pitch=512 + 4),           # pitch not 16 bytes
+        _xq_ops(dtype, 1, 256, 512, a_dt=np.float32),         # f32 activations
+    ]
+    for ops in refused:
+        assert R.describe(row, ops)[0] == R.RAD_E_UNSUPPORTED
+    tile = "gemm_nt_q_mxfp4" if dtype == "mxfp4a8" else "gemm_nt_q_fp8a8"
+    assert R.describe(tile, _xq_ops(dtype, 64, 512, 1024))[0] == R.RAD_E_UNSUPPORTED
 
 
 def test_entries_refuse_without_gfx950():
