@@ -39,13 +39,16 @@ const RadKernelInfo* rad_kernel_at(int i);
 int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s);
 
 /* gemm_nt_q at mxfp4a8, decode band M <= 16.  Replaces src/r3d_gemm_mxfp4.hip:1712-2170
- * (r3d_rad_gemm_nt_q_mxfp4_decode and its q8x sibling share this one row here). */
+ * (r3d_rad_gemm_nt_q_mxfp4_decode and its q8x sibling share this one row here).  Beyond the
+ * reference: at M = 1 it also takes a bf16 activation row with a_scale absent and quantises
+ * it as quant_act_fp8 does (src/r3d_band.hip:117-153) before the products. */
 int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s);
 
 /* gemm_nt_q at fp8a8, prefill row.  Replaces src/r3d_gemm_fp8a8.hip:1054-1099. */
 int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s);
 
-/* gemm_nt_q at fp8a8, decode band M <= 16.  Replaces src/r3d_gemm_fp8a8.hip:1101-1130. */
+/* gemm_nt_q at fp8a8, decode band M <= 16.  Replaces src/r3d_gemm_fp8a8.hip:1101-1130.
+ * Takes a bf16 activation row at M = 1 as the mxfp4a8 decode entry does. */
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
 
 /* gemm_nt_q at dtype "mxfp4a16", prefill row (any M).  No counterpart in the reference:
