@@ -73,6 +73,18 @@ int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a);
  * Asynchronous on `s`. */
 int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s);
 
+/* gated_quant_fp8: silu(gate) * up (or sigmoid(gate) * up), narrowed to bf16, then the
+ * quant_act_fp8 quantiser.  Replaces src/r3d_band.hip:489-547 (r3d_rad_gated_quant_fp8). */
+int r3d_rad_gated_quant_fp8(const RadArgs* a, RadStream s);
+
+/* gemm_nt_q_gated at fp8a8: the fp8a8 GEMM into the launch scratch, then gated_quant_fp8
+ * over it.  Replaces src/r3d_gemm_fp8a8.hip:1163-1241 (r3d_rad_gemm_nt_q_gated_fp8). */
+int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s);
+
+/* The gated row's scratch hook: 64 * N * 2 bytes (0 without N).  Replaces
+ * src/r3d_gemm_fp8a8.hip:1246-1253 (r3d_rad_gemm_nt_q_gated_fp8_scratch). */
+int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a);
+
 /* Host-only diagnostic with no counterpart in the reference: runs `row`'s preamble and
  * plan on `a` and writes the chosen arm and launch geometry (or the refusal) into buf.
  * Launches nothing, touches no device memory.  Returns the plan's status code. */

@@ -19,6 +19,7 @@ __all__ = [
     "RAD_E_INVAL", "RAD_E_DEVICE", "DT", "RadTensor", "RadParam", "RadArgs",
     "RadKernelInfo", "RadOpSchema", "lib", "lib_path", "rows", "schemas", "resolve",
     "launch_row", "gemm_nt_q", "describe", "GemmOperands", "QuantActOperands", "quant_act_fp8",
+    "GatedQuantOperands", "GatedGemmOperands",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -342,6 +343,106 @@ class QuantActOperands:
         self.args = RadArgs(ctypes.cast(t, ctypes.POINTER(RadTensor)), 3,
                             ctypes.cast(p, ctypes.POINTER(RadParam)), len(params),
                             None, 0, None, 0, 0)
+
+
+class _Args:
+    """ctypes RadArgs over operands [(tensor or None, element type name, shape, stride)]
+    (shape / stride None: the tensor's own) and params [(key, int | float | str)]."""
+
+    def __init__(self, operands, params):
+        t = (RadTensor * len(operands))()
+        for i, (ten, dt, shp, std) in enumerate(operands):
+            if ten is None:
+                t[i].data = None
+                t[i].rank = 0
+                continue
+            t[i].data = ten.data_ptr()
+            t[i].dtype = DT[dt]
+            shp = list(shp if shp is not None else ten.shape)
+            std = list(std if std is not None else ten.stride())
+            t[i].rank = len(shp)
+            for r, (s_, st) in enumerate(zip(shp, std)):
+                t[i].shape[r] = int(s_)
+                t[i].stride[r] = int(st)
+        self._t = t
+        p = (RadParam * max(1, len(params)))()
+        self._keep = []
+        for i, (k, v) in enumerate(params):
+            kb = k.encode()
+            self._keep.append(kb)
+            p[i].key = kb
+            if isinstance(v, str):
+                vb = v.encode()
+                self._keep.append(vb)
+                p[i].kind = RAD_P_STR
+                p[i].sval = vb
+            elif isinstance(v, float):
+                p[i].kind = RAD_P_F64
+                p[i].dval = v
+            else:
+                p[i].kind = RAD_P_INT
+                p[i].ival = int(v)
+        self._p = p
+        self.args = RadArgs(ctypes.cast(t, ctypes.POINTER(RadTensor)), len(operands),
+                            ctypes.cast(p, ctypes.POINTER(RadParam)), len(params),
+                            None, 0, None, 0, 0)
+
+    def set_scratch(self, scratch, nbytes=None):
+        """Hand `scratch` (a device tensor) to the launch as RadArgs::scratch."""
+        self.args.scratch = scratch.data_ptr()
+        self.args.scratch_bytes = int(nbytes if nbytes is not None
+                                      else scratch.numel() * scratch.element_size())
+
+
+def _elt(x, default="BF16"):
+    return "F32" if str(x.dtype).endswith("float32") else default
+
+
+class GatedQuantOperands(_Args):
+    """One gated_quant_fp8 call (src/r3d_band.hip:492-541).
+
+    gate_up float32 or bf16/int16 [M, 2n]   gate columns [0, n), up columns [n, 2n)
+    q       uint8 [M, n]                      e4m3 codes out
+    scale   float32 [M, ceil(n / group)]      dequant scales out
+    out     optional float32 or bf16/int16 [M, n]: the gated value h
+    act     "silu" (default when absent) or "sigmoid"
+    """
+
+    def __init__(self, gate_up, q, scale, out=None, *, n, group=128, act=None, M=None,
+                 dtype=None, shapes=None, strides=None):
+        shapes, strides = shapes or {}, strides or {}
+        gdt = _elt(gate_up)
+        ops = [(gate_up, gdt), (q, "F8E4M3"), (scale, "F32"),
+               (out, _elt(out) if out is not None else "BF16")]
+        super().__init__([(x, dt, shapes.get(i), strides.get(i)) for i, (x, dt) in enumerate(ops)],
+                         [("n", n), ("group", group),
+                          ("dtype", dtype or ("f32" if gdt == "F32" else "bf16"))] +
+                         ([("act", act)] if act is not None else []) +
+                         ([("M", M)] if M is not None else []))
+
+
+class GatedGemmOperands(_Args):
+    """One gemm_nt_q_gated call at fp8a8 (src/r3d_gemm_fp8a8.hip:1166-1241).
+
+    a uint8 [M, K] e4m3, a_scale float32 [M, K/128], b uint8 [N, K] e4m3 (N = 2n: gate rows
+    then up rows), b_scale bf16/int16 [N or N/128, K/128], q uint8 [M, n], scale float32
+    [M, n/group], out optional float32 or bf16/int16 [M, n]; the launch scratch (the row's
+    hook sizes it) holds the [M, N] bf16 gate_up plane.
+    """
+
+    def __init__(self, a, a_scale, b, b_scale, q, scale, out=None, *, N, K, act="silu",
+                 group=128, M=None, a_sum=None, scratch=None):
+        ops = [(a, "F8E4M3"), (a_scale, "F32"), (b, "F8E4M3"), (b_scale, "BF16"),
+               (q, "F8E4M3"), (scale, "F32"),
+               (out, _elt(out) if out is not None else "BF16")]
+        if a_sum is not None:
+            ops.append((a_sum, "F32"))
+        super().__init__([(x, dt, None, None) for x, dt in ops],
+                         [("N", N), ("K", K), ("group", group), ("dtype", "fp8a8")] +
+                         ([("act", act)] if act is not None else []) +
+                         ([("M", M)] if M is not None else []))
+        if scratch is not None:
+            self.set_scratch(scratch)
 
 
 def quant_act_fp8(x, q, scale, *, n, group=128, stream=None):

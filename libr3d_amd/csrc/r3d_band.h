@@ -1,6 +1,7 @@
-/* r3d_band.h -- the quant_act_fp8 producer on gfx950: per-(row, group) symmetric e4m3
- * quantisation of a bf16 or f32 activation, plain row-major codes and an f32 dequant
- * scale per group (src/r3d_band.hip:117-153 of the reference):
+/* r3d_band.h -- the activation producers on gfx950: quant_act_fp8 and gated_quant_fp8
+ * (below).  quant_act_fp8 is per-(row, group) symmetric e4m3 quantisation of a bf16 or f32
+ * activation, plain row-major codes and an f32 dequant scale per group
+ * (src/r3d_band.hip:117-153 of the reference):
  *     amax = max |x| over the group (NaN never wins; 0 when the group has none)
  *     sc   = amax > 0 ? amax * (1/448) : 1          (stored)
  *     q    = e4m3_rne(clamp(x * (1 / sc), +-448))   (NaN -> 0x7F with its sign)
@@ -177,6 +178,150 @@ __global__ __launch_bounds__(256) void quant_act_fp8_vec_kernel(
             const uint32_t lo = r3d_e4m3x4_rne(cv[0], cv[1], cv[2], cv[3]);
             const uint32_t hi = r3d_e4m3x4_rne(cv[4], cv[5], cv[6], cv[7]);
             *reinterpret_cast<uint2*>(qr + 8 * c) = make_uint2(lo, hi);
+        }
+    }
+}
+
+/* ---- gated_quant_fp8 (src/r3d_band.hip:155-201 of the reference): per element
+ *     h = bf16(act(gate) * up),  act(x) = silu ? x * sigmoid(x) : sigmoid(x)
+ *     sigmoid(x) = 1 / (1 + f32(exp_f64(-x)))        (exp in double, narrowed once)
+ * with bf16() round-to-nearest-even (a NaN keeps its sign and top payload bits, quieted),
+ * then quant_act_fp8's quantiser over each group of h.  The optional gated output is h
+ * (bf16, exact) or h widened (f32). */
+__device__ __forceinline__ uint32_t r3d_band_bf16_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float r3d_gated_h(float gt, float up, int silu) {
+    const float e = (float)exp(-(double)gt);
+    const float sg = 1.0f / (1.0f + e);
+    const float t = silu ? gt * sg : sg;
+    return __uint_as_float(r3d_band_bf16_bits(t * up) << 16);
+}
+
+/* One wave per (row, group), two passes (the gated value is recomputed for the encode pass:
+ * the same instructions on the same inputs, so the same bits).  Pitches in elements; ob is
+ * null when the gated output is not asked for. */
+template <bool BF16>
+__global__ __launch_bounds__(256) void gated_quant_fp8_kernel(
+    const uint8_t* __restrict__ gu, int64_t gu_pitch, uint8_t* __restrict__ q, int64_t q_pitch,
+    float* __restrict__ sc, int64_t s_pitch, uint8_t* __restrict__ ob, int ob_bf16,
+    int64_t ob_pitch, int64_t n, int64_t g, int64_t ngrp, int64_t items, int silu) {
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= items) return;                            /* wave-uniform */
+    const int lane = threadIdx.x & 63;
+    const int64_t row = item / ngrp, gi = item - row * ngrp;
+    const int64_t k0 = gi * g;
+    const int64_t len = n - k0 < g ? n - k0 : g;
+    const int64_t gb = row * gu_pitch + k0;
+    float amax = 0.0f;
+    for (int64_t i = lane; i < len; i += 64) {
+        const float h = r3d_gated_h(r3d_band_ld<BF16>(gu, gb + i), r3d_band_ld<BF16>(gu, gb + n + i),
+                                    silu);
+        amax = fmaxf(amax, fabsf(h));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+    if (lane == 0) sc[row * s_pitch + gi] = s;
+    const float inv = 1.0f / s;
+    for (int64_t i = lane; i < len; i += 64) {
+        const float h = r3d_gated_h(r3d_band_ld<BF16>(gu, gb + i), r3d_band_ld<BF16>(gu, gb + n + i),
+                                    silu);
+        if (ob) {
+            if (ob_bf16)
+                reinterpret_cast<uint16_t*>(ob)[row * ob_pitch + k0 + i] =
+                    (uint16_t)(__float_as_uint(h) >> 16);
+            else
+                reinterpret_cast<float*>(ob)[row * ob_pitch + k0 + i] = h;
+        }
+        q[row * q_pitch + k0 + i] = (uint8_t)r3d_e4m3x2_rne(r3d_band_clamp448(h * inv), 0.0f);
+    }
+}
+
+/* Groups of 8..512 tiling the rows (n % g == 0), aligned operands: one workgroup per row,
+ * 8 elements per lane per chunk (16-byte gate and up loads at bf16), L = g / 8 lanes per
+ * group reducing the maximum by xor-shuffles; codes leave 8 bytes per lane, the gated
+ * output 16 (bf16) or 32 (f32). */
+template <bool BF16, int L>
+__global__ __launch_bounds__(256) void gated_quant_fp8_vec_kernel(
+    const uint8_t* __restrict__ gu, int64_t gu_pitch, uint8_t* __restrict__ q, int64_t q_pitch,
+    float* __restrict__ sc, int64_t s_pitch, uint8_t* __restrict__ ob, int ob_bf16,
+    int64_t ob_pitch, int64_t n, int silu) {
+    constexpr int EB = BF16 ? 2 : 4;
+    constexpr int U = 2;
+    const int64_t row = blockIdx.x;
+    const int64_t chunks = n >> 3;
+    const uint8_t* gr = gu + row * gu_pitch * EB;
+    const uint8_t* ur = gr + n * EB;
+    uint8_t* qr = q + row * q_pitch;
+    float* sr = sc + row * s_pitch;
+    for (int64_t c0 = threadIdx.x; c0 - threadIdx.x < chunks; c0 += 256 * U) {
+        float gv[U][8], uv[U][8];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            /* a thread past the row's end re-reads its last chunk; nothing of it is stored */
+            const int64_t c = c0 + 256 * u < chunks ? c0 + 256 * u : chunks - 1;
+            if (BF16) {
+                const r3d_i32x4 a = *reinterpret_cast<const r3d_i32x4*>(gr + 16 * c);
+                const r3d_i32x4 b = *reinterpret_cast<const r3d_i32x4*>(ur + 16 * c);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    gv[u][2 * i] = __uint_as_float((uint32_t)a[i] << 16);
+                    gv[u][2 * i + 1] = __uint_as_float((uint32_t)a[i] & 0xFFFF0000u);
+                    uv[u][2 * i] = __uint_as_float((uint32_t)b[i] << 16);
+                    uv[u][2 * i + 1] = __uint_as_float((uint32_t)b[i] & 0xFFFF0000u);
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float4 a = *reinterpret_cast<const float4*>(gr + 32 * c + 16 * h);
+                    const float4 b = *reinterpret_cast<const float4*>(ur + 32 * c + 16 * h);
+                    gv[u][4 * h] = a.x; gv[u][4 * h + 1] = a.y; gv[u][4 * h + 2] = a.z;
+                    gv[u][4 * h + 3] = a.w;
+                    uv[u][4 * h] = b.x; uv[u][4 * h + 1] = b.y; uv[u][4 * h + 2] = b.z;
+                    uv[u][4 * h + 3] = b.w;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + 256 * u;
+            float h[8];
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                h[i] = r3d_gated_h(gv[u][i], uv[u][i], silu);
+                amax = fmaxf(amax, fabsf(h[i]));
+            }
+#pragma unroll
+            for (int off = L / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            if (c >= chunks) continue;
+            const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+            const float inv = 1.0f / s;
+            if ((c & (L - 1)) == 0) sr[c / L] = s;
+            float cv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cv[i] = r3d_band_clamp448(h[i] * inv);
+            *reinterpret_cast<uint2*>(qr + 8 * c) =
+                make_uint2(r3d_e4m3x4_rne(cv[0], cv[1], cv[2], cv[3]),
+                           r3d_e4m3x4_rne(cv[4], cv[5], cv[6], cv[7]));
+            if (ob) {
+                if (ob_bf16) {
+                    r3d_i32x4 o;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[i] = (int)((__float_as_uint(h[2 * i]) >> 16) |
+                                     (__float_as_uint(h[2 * i + 1]) & 0xFFFF0000u));
+                    *reinterpret_cast<r3d_i32x4*>(ob + 2 * (row * ob_pitch + 8 * c)) = o;
+                } else {
+                    float* of = reinterpret_cast<float*>(ob) + row * ob_pitch + 8 * c;
+                    *reinterpret_cast<float4*>(of) = make_float4(h[0], h[1], h[2], h[3]);
+                    *reinterpret_cast<float4*>(of + 4) = make_float4(h[4], h[5], h[6], h[7]);
+                }
+            }
         }
     }
 }

@@ -335,11 +335,90 @@ static int quant_entry(const RadArgs* a, RadStream s) {
     return RAD_OK;
 }
 
+/* gated_quant_fp8's kernels over a plan: the vector kernel where its gates hold, else one
+ * wave per (row, group). */
+static int launch_gated(const GatedPlan& P, hipStream_t stream) {
+    const int eb = P.gu_bf16 ? 2 : 4, ob_eb = P.ob_bf16 ? 2 : 4;
+    const int lanes = (int)(P.g / 8);
+    const bool vec = P.g % 8 == 0 && lanes >= 1 && lanes <= 64 && (lanes & (lanes - 1)) == 0 &&
+                     P.n % P.g == 0 && ((uintptr_t)P.gu % 16) == 0 &&
+                     (P.gu_pitch * eb) % 16 == 0 && ((uintptr_t)P.q % 8) == 0 &&
+                     P.q_pitch % 8 == 0 &&
+                     (!P.ob || (((uintptr_t)P.ob % 16) == 0 && (P.ob_pitch * ob_eb) % 16 == 0));
+    if (vec) {
+#define R3D_GV(B_, L_)                                                                      \
+    hipLaunchKernelGGL((gated_quant_fp8_vec_kernel<B_, L_>), dim3((unsigned)P.rows),          \
+                       dim3(256), 0, stream, P.gu, P.gu_pitch, P.q, P.q_pitch, P.scale,       \
+                       P.s_pitch, P.ob, P.ob_bf16, P.ob_pitch, P.n, P.silu)
+#define R3D_GVL(B_)                                                                         \
+    switch (lanes) {                                                                        \
+        case 1: R3D_GV(B_, 1); break;   case 2: R3D_GV(B_, 2); break;                       \
+        case 4: R3D_GV(B_, 4); break;   case 8: R3D_GV(B_, 8); break;                       \
+        case 16: R3D_GV(B_, 16); break; case 32: R3D_GV(B_, 32); break;                     \
+        default: R3D_GV(B_, 64); break;                                                     \
+    }
+        if (P.gu_bf16) { R3D_GVL(true); } else { R3D_GVL(false); }
+#undef R3D_GVL
+#undef R3D_GV
+    } else {
+        const int64_t items = P.rows * P.ngrp;
+        const int64_t blocks = (items + 3) / 4;
+        if (blocks > 0x7FFFFFFF) return RAD_E_SHAPE;
+#define R3D_GQ(B_)                                                                          \
+    hipLaunchKernelGGL((gated_quant_fp8_kernel<B_>), dim3((unsigned)blocks), dim3(256), 0,    \
+                       stream, P.gu, P.gu_pitch, P.q, P.q_pitch, P.scale, P.s_pitch, P.ob,    \
+                       P.ob_bf16, P.ob_pitch, P.n, P.g, P.ngrp, items, P.silu)
+        if (P.gu_bf16) R3D_GQ(true); else R3D_GQ(false);
+#undef R3D_GQ
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "libr3d_gfx950: gated_quant_fp8 launch FAILED (%s)\n", hipGetErrorName(e));
+        return RAD_E_DEVICE;
+    }
+    debug_once(vec ? "gated_quant_fp8 (vector)" : "gated_quant_fp8", vec ? 253 : 252);
+    return RAD_OK;
+}
+
+/* gated_quant_fp8 (src/r3d_band.hip:492-541): the reference's gates, then the kernels. */
+static int gated_entry(const RadArgs* a, RadStream s) {
+    GatedPlan P{};
+    const int rc = plan_gated_quant_fp8(a, &P);
+    if (rc) return rc;
+    if (!chip_ok()) return RAD_E_UNSUPPORTED;
+    return launch_gated(P, (hipStream_t)s);
+}
+
+/* gemm_nt_q_gated at fp8a8 (src/r3d_gemm_fp8a8.hip:1166-1241): the fp8a8 GEMM writes the
+ * [M, 2n] bf16 gate_up plane into the launch scratch -- the arm the gemm_nt_q rows would
+ * run at this M (the decode GEMVs up to M = 16 while the fp8a8 decode row is registered,
+ * else the prefill pipeline) -- then gated_quant_fp8's kernels close it into codes and
+ * scales on the same stream: the two ops' composition, byte for byte. */
+static int gemm_gated_entry(const RadArgs* a, RadStream s) {
+    GemmPlan G{};
+    GatedPlan E{};
+    int rc = plan_gemm_gated(a, &G, &E);
+    if (rc) return rc;
+    if (!chip_ok()) return RAD_E_UNSUPPORTED;
+    hipStream_t stream = (hipStream_t)s;
+    const bool dec = G.M <= 16 && !env_no_fp8_dec();
+    rc = dec ? launch_decode(G, decode_splitk(a), stream) : launch_prefill(G, stream);
+    if (rc) return rc;
+    return launch_gated(E, stream);
+}
+
 }  // namespace r3d
 
 extern "C" {
 
 int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s) { return r3d::quant_entry(a, s); }
+int r3d_rad_gated_quant_fp8(const RadArgs* a, RadStream s) { return r3d::gated_entry(a, s); }
+int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s) {
+    return r3d::gemm_gated_entry(a, s);
+}
+int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a) {
+    return r3d::gemm_gated_scratch_bytes(a);
+}
 
 int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s) {
     return r3d::entry(a, s, r3d::ENC_MXFP4A8, false);

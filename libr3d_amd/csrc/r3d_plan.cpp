@@ -510,6 +510,131 @@ int plan_quant_act_fp8(const RadArgs* a, QuantPlan* P) {
     return RAD_OK;
 }
 
+int plan_gated_quant_fp8(const RadArgs* a, GatedPlan* P) {
+    const RadTensor* gu = rad_arg_in(a, 0);
+    const RadTensor* q = rad_arg_in(a, 1);
+    const RadTensor* sc = rad_arg_in(a, 2);
+    const RadTensor* ob = rad_arg_in(a, 3);
+    if (!gu || !q || !sc) return RAD_E_INVAL;
+    if (gu->dtype != RAD_F32 && gu->dtype != RAD_BF16) return RAD_E_DTYPE;
+    if (q->dtype != RAD_F8E4M3 || sc->dtype != RAD_F32) return RAD_E_DTYPE;
+    if (ob && ob->dtype != RAD_F32 && ob->dtype != RAD_BF16) return RAD_E_DTYPE;
+    long long v = 0;
+    const int64_t n = rad_args_geti(a, "n", &v) ? (int64_t)v
+                                                : (gu->rank >= 2 ? gu->shape[1] / 2 : 0);
+    if (n <= 0) return RAD_E_SHAPE;
+    const char* act = rad_args_gets(a, "act");
+    int64_t g = rad_args_geti(a, "group", &v) ? (int64_t)v : n;
+    if (g <= 0 || g > n) g = n;
+    const int64_t ngrp = (n + g - 1) / g;
+    const int64_t rows = rad_tensor_numel(gu) / (2 * n);
+    if (rows <= 0 || rows > 0xffff) return RAD_E_SHAPE;
+    if (rad_tensor_numel(q) < rows * n || rad_tensor_numel(sc) < rows * ngrp) return RAD_E_SHAPE;
+    if (ob && rad_tensor_numel(ob) < rows * n) return RAD_E_SHAPE;
+    int64_t gp = 0, qp = 0, sp = 0, op = 0;
+    if (band_row_pitch(gu, 2 * n, &gp) || band_row_pitch(q, n, &qp) ||
+        band_row_pitch(sc, ngrp, &sp) || (ob && band_row_pitch(ob, n, &op)))
+        return RAD_E_STRIDE;
+    P->gu = (const uint8_t*)gu->data;
+    P->q = (uint8_t*)q->data;
+    P->scale = (float*)sc->data;
+    P->ob = ob ? (uint8_t*)ob->data : nullptr;
+    P->gu_bf16 = gu->dtype == RAD_BF16;
+    P->ob_bf16 = ob && ob->dtype == RAD_BF16;
+    P->silu = !act || strcmp(act, "sigmoid") != 0;
+    P->rows = rows;
+    P->n = n;
+    P->g = g;
+    P->ngrp = ngrp;
+    P->gu_pitch = gp;
+    P->q_pitch = qp;
+    P->s_pitch = sp;
+    P->ob_pitch = op;
+    return RAD_OK;
+}
+
+int64_t gemm_gated_scratch_bytes(const RadArgs* a) {
+    long long N = 0;
+    if (!rad_args_geti(a, "N", &N) || N <= 0 || N > (1LL << 34)) return 0;
+    return 64 * (int64_t)N * 2;
+}
+
+int plan_gemm_gated(const RadArgs* a, GemmPlan* G, GatedPlan* E) {
+    if (env_no_fp8a8()) return RAD_E_UNSUPPORTED;
+    const RadTensor* A = rad_arg_in(a, 0);
+    const RadTensor* AS = rad_arg_in(a, 1);
+    const RadTensor* B = rad_arg_in(a, 2);
+    const RadTensor* BS = rad_arg_in(a, 3);
+    const RadTensor* Q = rad_arg_in(a, 4);
+    const RadTensor* SC = rad_arg_in(a, 5);
+    const RadTensor* OB = rad_arg_in(a, 6);
+    if (!A || !AS || !B || !BS || !Q || !SC) return RAD_E_UNSUPPORTED;
+    if (rad_arg_in(a, 7)) return RAD_E_UNSUPPORTED;              /* a_sum */
+    if (Q->dtype != RAD_F8E4M3 || SC->dtype != RAD_F32) return RAD_E_UNSUPPORTED;
+    if (OB && OB->dtype != RAD_BF16 && OB->dtype != RAD_F32) return RAD_E_UNSUPPORTED;
+    /* act is required here: a row may compile one gate only */
+    const char* act = rad_args_gets(a, "act");
+    if (!act || (strcmp(act, "silu") != 0 && strcmp(act, "sigmoid") != 0))
+        return RAD_E_UNSUPPORTED;
+    long long N = 0;
+    if (!rad_args_geti(a, "N", &N) || N <= 0 || (N & 1)) return RAD_E_SHAPE;
+    const int64_t n = N / 2;
+    long long gv = 0;
+    int64_t g = rad_args_geti(a, "group", &gv) && gv > 0 ? (int64_t)gv : n;
+    if (g > n) g = n;
+    const int64_t ngrp = (n + g - 1) / g;
+    const int64_t qn = rad_tensor_numel(Q);
+    if (qn <= 0 || qn % n) return RAD_E_SHAPE;
+    const int64_t M = qn / n;
+    if (M > 0xffff) return RAD_E_SHAPE;
+    if (rad_tensor_numel(SC) < M * ngrp) return RAD_E_SHAPE;
+    if (OB && rad_tensor_numel(OB) < M * n) return RAD_E_SHAPE;
+
+    /* the GEMM over the gate_up plane, with the scratch as its y */
+    if (!a->scratch || a->scratch_bytes < M * N * 2 || ((uintptr_t)a->scratch & 15))
+        return RAD_E_UNSUPPORTED;
+    RadArgs ga = *a;
+    RadTensor gt[5];
+    for (int i = 0; i < 4; ++i) gt[i] = a->t[i];
+    memset(&gt[4], 0, sizeof gt[4]);
+    gt[4].data = a->scratch;
+    gt[4].dtype = RAD_BF16;
+    gt[4].rank = 2;
+    gt[4].shape[0] = M;
+    gt[4].shape[1] = N;
+    gt[4].stride[0] = N;
+    gt[4].stride[1] = 1;
+    ga.t = gt;
+    ga.n_t = 5;
+    int64_t gm = 0, gn = 0;
+    int rc = entry_preamble(&ga, ENC_FP8A8, 0, &gm, &gn);
+    if (rc) return rc;
+    rc = plan_fp8a8(&ga, gm, G);
+    if (rc) return rc;
+    if (G->N != N) return RAD_E_SHAPE;
+
+    int64_t qp = 0, sp = 0, op = 0;
+    if (band_row_pitch(Q, n, &qp) || band_row_pitch(SC, ngrp, &sp) ||
+        (OB && band_row_pitch(OB, n, &op)))
+        return RAD_E_STRIDE;
+    E->gu = (const uint8_t*)a->scratch;
+    E->q = (uint8_t*)Q->data;
+    E->scale = (float*)SC->data;
+    E->ob = OB ? (uint8_t*)OB->data : nullptr;
+    E->gu_bf16 = 1;
+    E->ob_bf16 = OB && OB->dtype == RAD_BF16;
+    E->silu = strcmp(act, "sigmoid") != 0;
+    E->rows = M;
+    E->n = n;
+    E->g = g;
+    E->ngrp = ngrp;
+    E->gu_pitch = N;
+    E->q_pitch = qp;
+    E->s_pitch = sp;
+    E->ob_pitch = op;
+    return RAD_OK;
+}
+
 bool env_no_mxfp4()   { static const bool v = getenv("R3D_NO_MXFP4") != nullptr;   return v; }
 bool env_no_fp4_dec() { static const bool v = getenv("R3D_NO_FP4_DEC") != nullptr; return v; }
 bool env_no_fp8a8()   { static const bool v = getenv("R3D_NO_FP8A8") != nullptr;   return v; }
@@ -593,6 +718,32 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
                  Q.x_bf16 ? "bf16" : "f32", (long long)Q.rows, (long long)Q.n, (long long)Q.g,
                  (long long)Q.ngrp, (long long)Q.x_pitch, (long long)Q.q_pitch,
                  (long long)Q.s_pitch);
+        return RAD_OK;
+    }
+    if (strstr(row, "gemm_nt_q_gated") != nullptr) {
+        GemmPlan G{};
+        GatedPlan E{};
+        const int rc = plan_gemm_gated(a, &G, &E);
+        if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
+        snprintf(buf, (size_t)len,
+                 "arm=gated gemm=%s M=%lld N=%lld K=%lld n=%lld group=%lld act=%s ob=%s rblk=%d",
+                 G.M <= 16 && !env_no_fp8_dec() ? "decode" : "prefill", (long long)G.M,
+                 (long long)G.N, (long long)G.K, (long long)E.n, (long long)E.g,
+                 E.silu ? "silu" : "sigmoid", E.ob ? (E.ob_bf16 ? "bf16" : "f32") : "none",
+                 G.rblk);
+        return RAD_OK;
+    }
+    if (strstr(row, "gated_quant_fp8") != nullptr) {
+        GatedPlan E{};
+        const int rc = plan_gated_quant_fp8(a, &E);
+        if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
+        snprintf(buf, (size_t)len,
+                 "arm=band op=gated_quant_fp8 gate_up=%s rows=%lld n=%lld group=%lld ngrp=%lld "
+                 "act=%s ob=%s gu_pitch=%lld q_pitch=%lld s_pitch=%lld ob_pitch=%lld",
+                 E.gu_bf16 ? "bf16" : "f32", (long long)E.rows, (long long)E.n, (long long)E.g,
+                 (long long)E.ngrp, E.silu ? "silu" : "sigmoid",
+                 E.ob ? (E.ob_bf16 ? "bf16" : "f32") : "none", (long long)E.gu_pitch,
+                 (long long)E.q_pitch, (long long)E.s_pitch, (long long)E.ob_pitch);
         return RAD_OK;
     }
     const bool a16 = strstr(row, "mxfp4a16") != nullptr;

@@ -162,6 +162,31 @@ struct QuantPlan {
 };
 int plan_quant_act_fp8(const RadArgs* a, QuantPlan* P);
 
+/* gated_quant_fp8 launch plan (src/r3d_band.hip:492-541): gate_up (f32 or bf16, [rows, 2n]:
+ * gate columns [0, n), up columns [n, 2n)), q (e4m3), scale (f32), optional out_bf16 (f32
+ * or bf16); n from the param (default half of gate_up's second extent); act "sigmoid"
+ * selects sigmoid(gate) * up, anything else (or absent) silu(gate) * up; group as
+ * quant_act_fp8's.  Returns RAD_OK or the reference's refusal code. */
+struct GatedPlan {
+    const uint8_t* gu;
+    uint8_t* q;
+    float* scale;
+    uint8_t* ob;                              /* null: no gated output */
+    int gu_bf16, ob_bf16, silu;
+    int64_t rows, n, g, ngrp;
+    int64_t gu_pitch, q_pitch, s_pitch, ob_pitch;   /* elements */
+};
+int plan_gated_quant_fp8(const RadArgs* a, GatedPlan* P);
+
+/* gemm_nt_q_gated at fp8a8 (src/r3d_gemm_fp8a8.hip:1166-1241): operands a, a_scale, b,
+ * b_scale, q, scale, out_bf16?, a_sum? (refused); params N (= 2n, even), K, group, dtype,
+ * act (required: silu or sigmoid).  M = numel(q) / n.  The GEMM writes the [M, N] bf16
+ * gate_up plane into the launch scratch (at least M*N*2 bytes, 16-byte aligned, else
+ * RAD_E_UNSUPPORTED) -- G is the fp8a8 plan for that plane -- and E is gated_quant_fp8's
+ * plan over it.  Returns RAD_OK or the reference's refusal code. */
+int plan_gemm_gated(const RadArgs* a, GemmPlan* G, GatedPlan* E);
+int64_t gemm_gated_scratch_bytes(const RadArgs* a);   /* 64 * N * 2, or 0 without N */
+
 /* Environment levers, read once per process (function-local statics). */
 bool env_no_mxfp4();        /* R3D_NO_MXFP4: all mxfp4a8 rows */
 bool env_no_fp4_dec();      /* R3D_NO_FP4_DEC: the mxfp4a8 decode row */

@@ -10,6 +10,9 @@
  *   gemm_nt_q_fp8a8_decode   prio 1100  + M LE 16
  *   gemm_nt_q_mxfp4a16       prio 1000  dtype IN mxfp4a16, K DIV 128     bf16-in prefill
  *   quant_act_fp8_act        prio 1000  n GE 1, dtype IN f32 bf16          activation producer
+ *   gated_quant_fp8_act      prio 1000  n GE 1, dtype IN f32 bf16          gated producer
+ *   gemm_nt_q_gated_fp8a8    prio 1000  dtype IN fp8a8, M LE 64, K DIV 128, group EQ 128,
+ *                                       act IN silu sigmoid              GEMM + gated producer
  * gemm_nt_q_mxfp4a16 has no counterpart in the reference: it takes bf16 activations (no
  * a_scale), quantises them to mxfp8 (e4m3 + E8M0 per 32 of K) in the launch scratch its
  * hook sizes, and runs the prefill GEMM with both block scales inside the MFMA.
@@ -21,7 +24,8 @@
  * Kill switches act HERE, at registration (src/r3d_rows.cpp:2197-2236): an issue-time
  * refusal is an engine abort, so a lever hides rows and the band re-resolves.
  *   R3D_NO_MXFP4   hides every mxfp4 row;    R3D_NO_FP4_DEC  the mxfp4a8 decode row;
- *   R3D_NO_FP8A8   hides both fp8a8 rows;    R3D_NO_FP8_DEC  the fp8a8 decode row.
+ *   R3D_NO_FP8A8   hides the fp8a8 rows (and the gated row); R3D_NO_FP8_DEC  the fp8a8
+ *                  decode row (the gated row then runs its GEMM on the prefill pipeline).
  * Presence-tested (getenv != null), read once.  R3D_MXFP4_Q8X is accepted and inert:
  * this library has no repacked-plane arm for it to withdraw.
  */
@@ -39,6 +43,9 @@ int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s);
 int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a);
 int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s);
+int r3d_rad_gated_quant_fp8(const RadArgs* a, RadStream s);
+int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s);
+int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a);
 }
 
 namespace {
@@ -79,6 +86,41 @@ const RadOperandSpec kQuantActOperands[] = {
     {"scale", RAD_OPD_OUT, 0},
 };
 
+/* gemm_nt_q_gated's schema (src/r3d_rows.cpp:212-230 of the reference): `act` required, N
+ * the weight's rows (twice the gated width), outputs the quantiser's codes and scales. */
+const RadParamSpec kGemmGatedParams[] = {
+    {"M", RAD_P_INT, RAD_REQUIRED, 0},
+    {"N", RAD_P_INT, RAD_REQUIRED, 0},
+    {"K", RAD_P_INT, RAD_REQUIRED, 0},
+    {"group", RAD_P_INT, RAD_REQUIRED, 0},
+    {"dtype", RAD_P_STR, RAD_REQUIRED, 0},
+    {"act", RAD_P_STR, RAD_REQUIRED, 0},
+};
+const RadOperandSpec kGemmGatedOperands[] = {
+    {"a", RAD_OPD_IN, 0},
+    {"a_scale", RAD_OPD_IN, 0},
+    {"b", RAD_OPD_WEIGHT, 0},
+    {"b_scale", RAD_OPD_WEIGHT, 0},
+    {"q", RAD_OPD_OUT, 0},
+    {"scale", RAD_OPD_OUT, 0},
+    {"out_bf16", RAD_OPD_OUT, 1},
+};
+
+/* gated_quant_fp8's schema (src/r3d_rows.cpp:626-637 of the reference). */
+const RadParamSpec kGatedParams[] = {
+    {"M", RAD_P_INT, RAD_REQUIRED, 0},
+    {"n", RAD_P_INT, RAD_REQUIRED, 0},
+    {"group", RAD_P_INT, RAD_REQUIRED, 0},
+    {"dtype", RAD_P_STR, RAD_REQUIRED, 0},
+    {"act", RAD_P_STR, RAD_OPTIONAL, 0},
+};
+const RadOperandSpec kGatedOperands[] = {
+    {"gate_up", RAD_OPD_IN, 0},
+    {"q", RAD_OPD_OUT, 0},
+    {"scale", RAD_OPD_OUT, 0},
+    {"out_bf16", RAD_OPD_OUT, 1},
+};
+
 const RadOpSchema kSchemas[] = {
     {"gemm_nt_q", kGemmNtQParams, 8, kGemmNtQOperands, 7,
      "Y[M,N] = A[M,K] . dequant(B)[N,K]^T with block-scaled operands; `dtype` names the "
@@ -88,6 +130,13 @@ const RadOpSchema kSchemas[] = {
      "per-(row, `group`-column) symmetric E4M3 quantisation of a token-major activation, "
      "plain row-major; the scale is amax/448, a dequant multiplier (the GEMMs multiply both "
      "scales and never divide)."},
+    {"gemm_nt_q_gated", kGemmGatedParams, 6, kGemmGatedOperands, 7,
+     "gemm_nt_q over a [2n, K] gate_up weight plane closed by gated_quant_fp8: the outputs are "
+     "the quantiser's E4M3 codes, its scale per (row, `group` columns) and optionally the bf16 "
+     "gated product; byte-identical to gemm_nt_q followed by gated_quant_fp8."},
+    {"gated_quant_fp8", kGatedParams, 5, kGatedOperands, 4,
+     "silu(gate)*up or sigmoid(gate)*up (gate the first n columns of each row, up the next "
+     "n), narrowed to bf16, then quant_act_fp8's quantiser, in one pass."},
 };
 
 /* the band rows' constraint (src/r3d_rows.cpp:1262-1265) */
@@ -119,6 +168,16 @@ const RadConstraint cFp8Decode[] = {
     {"M", RAD_C_LE, 16, nullptr},
     {"K", RAD_C_DIV, 128, nullptr},
     {"group", RAD_C_EQ, 128, nullptr},
+};
+
+/* the gated GEMM row (src/r3d_rows.cpp:1114-1125): the scratch is sized at the band's M
+ * bound */
+const RadConstraint cFp8Gated[] = {
+    {"dtype", RAD_C_IN, 0, "fp8a8"},
+    {"M", RAD_C_LE, 64, nullptr},
+    {"K", RAD_C_DIV, 128, nullptr},
+    {"group", RAD_C_EQ, 128, nullptr},
+    {"act", RAD_C_IN, 0, "silu sigmoid"},
 };
 
 enum { kPrioTile = 1000, kPrioDecode = 1100 };
@@ -201,6 +260,29 @@ const RadKernelInfo kRows[] = {
      "activation in, f8e4m3 codes and f32 group scales out",
      RAD_DOMAIN_DEVICE, kPrioTile, cBandMn, 2, nullptr, 0, nullptr,
      nullptr, nullptr, r3d_rad_quant_act_fp8, nullptr, nullptr, nullptr, nullptr, nullptr},
+
+    {"gated_quant_fp8_act", "gated_quant_fp8", "band",
+     "silu(gate)*up or sigmoid(gate)*up fused with quant_act_fp8's quantiser on gfx950: one "
+     "workgroup per row with 8 elements a lane for groups of 8..512 that tile the row, else "
+     "one wave per (row, group) recomputing the gated value for its encode pass",
+     "f32/bf16 gate_up [M, 2n]; the gated value narrows to bf16 once (exp in double, as the "
+     "reference's sigmoid); group clamped to n; at most 65535 rows",
+     "f32/bf16 gate_up in, f8e4m3 codes, f32 scales, optional bf16/f32 gated output",
+     RAD_DOMAIN_DEVICE, kPrioTile, cBandMn, 2, nullptr, 0, nullptr,
+     nullptr, nullptr, r3d_rad_gated_quant_fp8, nullptr, nullptr, nullptr, nullptr, nullptr},
+
+    {"gemm_nt_q_gated_fp8a8", "gemm_nt_q_gated", "gemm",
+     "the fp8a8 GEMM (decode GEMV up to M = 16, the prefill pipeline above) writing its bf16 "
+     "gate_up plane into the launch scratch, closed by the gated_quant_fp8 kernels on the same "
+     "stream -- the byte-identical composition of the two rows",
+     "M <= 64 (the scratch is sized at the band's bound, 64*N*2 bytes, 16-byte aligned); K a "
+     "multiple of 128; N = 2n; M derives from numel(q)/n",
+     "fp8_e4m3 a with f32 a_scale per (row, 128 K), fp8_e4m3 b with bf16 scale per 128x128 "
+     "tile (or per row), e4m3 q + f32 scale out, optional bf16/f32 gated product; act silu "
+     "or sigmoid; a_sum refused",
+     RAD_DOMAIN_DEVICE, kPrioTile, cFp8Gated, 5, nullptr, 0, nullptr,
+     nullptr, nullptr, r3d_rad_gemm_nt_q_gated_fp8, r3d_rad_gemm_nt_q_gated_fp8_scratch,
+     nullptr, nullptr, nullptr, nullptr},
 };
 
 bool row_hidden(const RadKernelInfo& k) {
@@ -210,6 +292,7 @@ bool row_hidden(const RadKernelInfo& k) {
     if (!strcmp(k.name, "gemm_nt_q_mxfp4a16")) return no_mx;
     if (!strcmp(k.name, "gemm_nt_q_mxfp4_decode")) return no_mx || no_mxd;
     if (!strcmp(k.name, "gemm_nt_q_fp8a8")) return no_f8;
+    if (!strcmp(k.name, "gemm_nt_q_gated_fp8a8")) return no_f8;
     if (!strcmp(k.name, "gemm_nt_q_fp8a8_decode")) return no_f8 || no_f8d;
     return false;
 }
@@ -223,7 +306,8 @@ uint32_t rad_plugin_abi_version(void) { return RAD_ABI_VERSION; }
 const RadPluginInfo* rad_plugin_info(void) {
     static const RadPluginInfo info = {
         RAD_PLUGIN_KERNEL, "libr3d_gfx950", "0.1.0",
-        "radiance gemm_nt_q rows (mxfp4a8, fp8a8, mxfp4a16) and the quant_act_fp8 producer for "
+        "radiance gemm_nt_q rows (mxfp4a8, fp8a8, mxfp4a16), gemm_nt_q_gated (fp8a8) and the "
+        "quant_act_fp8 / gated_quant_fp8 producers for "
         "AMD Instinct MI355X (CDNA4)",
         "gfx950",
     };

@@ -114,6 +114,25 @@ def quant_act_fp8(x, group=128):
     return q, sc
 
 
+def gated_quant_fp8(gu, n=None, group=128, act="silu"):
+    """gu: bf16 bits (uint16) or float32, [M, 2n] -> (codes uint8 [M, n], scale f32
+    [M, ceil(n/group)], gated value bf16 bits uint16 [M, n]); act "sigmoid" or silu."""
+    is_bf16 = gu.dtype == np.uint16
+    gu = np.ascontiguousarray(gu, np.uint16 if is_bf16 else np.float32)
+    M, n2 = gu.shape
+    n = n2 // 2 if n is None else n
+    ng = (n + group - 1) // group
+    q = np.empty((M, n), np.uint8)
+    sc = np.empty((M, ng), np.float32)
+    out = np.empty((M, n), np.uint16)
+    _lib().r3d_ref_gated_quant_fp8(gu.ctypes.data_as(ctypes.c_void_p), ctypes.c_int(int(is_bf16)),
+                                   _i64(M), _i64(n), _i64(n2), _i64(group),
+                                   ctypes.c_int(0 if act == "sigmoid" else 1), _p(q, _u8p),
+                                   _i64(n), _p(sc, _f32p), _i64(ng),
+                                   out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), _i64(n))
+    return q, sc, out
+
+
 def quant_dot_mxfp4a8(A, AS, B, BS, nthreads=1):
     """-> (Y bf16 bits uint16 [M,N], Yf f32 accumulator, S f32 magnitude sum)."""
     A = np.ascontiguousarray(A, np.uint8)

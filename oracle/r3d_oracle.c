@@ -20,6 +20,11 @@
  *                   scale 1 and code 0, |dequant - x| <= half an e4m3 ulp relative,
  *                   NaN inputs encode to the NaN code; and an independent numpy
  *                   float32 evaluation of the reference's step order.
+ *   gated_quant_fp8 closed forms: sigmoid(0) = 1/2 exactly, so act=sigmoid with a zero
+ *                   gate quantises up/2; a gate of 30 has sigmoid 1 in f32, so silu
+ *                   quantises bf16(30 * up); both through quant_act_fp8 (gate/up order,
+ *                   the act switch and the bf16 narrowing fail them when wrong); plus a
+ *                   numpy evaluation (float64 exp) on random and special gates, and NaN.
  *   quant_dot       float64 brute force within the bound 2*K*2^-24*S + ulp_bf16;
  *                   single-nonzero closed forms; K=32 / K=128 single-group forms;
  *                   power-of-two scale exactness (a_scale linearity); 0xFF scale
@@ -170,6 +175,47 @@ void r3d_ref_quant_act_fp8(const void* x, int x_is_bf16, int64_t M, int64_t K,
             const float inv = 1.0f / sc;
             for (int64_t k = k0; k < k1; ++k) {
                 float c = ld_act(x, x_is_bf16, m * x_pitch + k) * inv;
+                if (c > 448.0f) c = 448.0f;
+                if (c < -448.0f) c = -448.0f;
+                q[m * q_pitch + k] = r3d_ref_f32_to_e4m3(c);
+            }
+        }
+    }
+}
+
+/* gated_quant_fp8 (src/r3d_band.hip:155-201; the sigmoid at :46-47): per element
+ * h = bf16(act(gate) * up) with sigmoid(x) = 1 / (1 + (float)exp((double)-x)) and
+ * act(x) = silu ? x * sigmoid(x) : sigmoid(x); then quant_act_fp8's quantiser over each
+ * group of h (h recomputed for the encode pass, as there); `out` (nullable) receives h's
+ * bf16 bits.  gate_up rows: gate at [0, n), up at [n, 2n), row pitch gu_pitch. */
+static inline float ref_gated_h(const void* gu, int bf16, int64_t i, int64_t n, int silu) {
+    const float gt = ld_act(gu, bf16, i), up = ld_act(gu, bf16, i + n);
+    const float e = (float)exp(-(double)gt);
+    const float sg = 1.0f / (1.0f + e);
+    const float t = silu ? gt * sg : sg;
+    return r3d_ref_bf16_to_f32(r3d_ref_f32_to_bf16(t * up));
+}
+
+void r3d_ref_gated_quant_fp8(const void* gu, int gu_is_bf16, int64_t M, int64_t n,
+                             int64_t gu_pitch, int64_t group, int silu, uint8_t* q,
+                             int64_t q_pitch, float* scale, int64_t s_pitch, uint16_t* out,
+                             int64_t out_pitch) {
+    const int64_t ng = (n + group - 1) / group;
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t g = 0; g < ng; ++g) {
+            const int64_t k0 = g * group, k1 = (k0 + group < n) ? k0 + group : n;
+            float amax = 0.0f;
+            for (int64_t k = k0; k < k1; ++k) {
+                const float a = fabsf(ref_gated_h(gu, gu_is_bf16, m * gu_pitch + k, n, silu));
+                if (a > amax) amax = a;
+            }
+            const float sc = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+            scale[m * s_pitch + g] = sc;
+            const float inv = 1.0f / sc;
+            for (int64_t k = k0; k < k1; ++k) {
+                const float h = ref_gated_h(gu, gu_is_bf16, m * gu_pitch + k, n, silu);
+                if (out) out[m * out_pitch + k] = r3d_ref_f32_to_bf16(h);
+                float c = h * inv;
                 if (c > 448.0f) c = 448.0f;
                 if (c < -448.0f) c = -448.0f;
                 q[m * q_pitch + k] = r3d_ref_f32_to_e4m3(c);

@@ -51,6 +51,14 @@ void r3d_ref_quant_act_fp8(const void* x, int x_is_bf16, int64_t M, int64_t K,
                            int64_t x_pitch, int64_t group, uint8_t* q, int64_t q_pitch,
                            float* scale, int64_t s_pitch);
 
+/* gated_quant_fp8: gate_up [M, 2n] (bf16 when gu_is_bf16, else f32), row pitch gu_pitch;
+ * silu selects x*sigmoid(x) over sigmoid(x); codes q [M, n], scales [M, ceil(n/group)];
+ * out (nullable) the gated value's bf16 bits [M, n]. */
+void r3d_ref_gated_quant_fp8(const void* gu, int gu_is_bf16, int64_t M, int64_t n,
+                             int64_t gu_pitch, int64_t group, int silu, uint8_t* q,
+                             int64_t q_pitch, float* scale, int64_t s_pitch, uint16_t* out,
+                             int64_t out_pitch);
+
 /* quant_dot at mxfp4a8.
  *   A  [M, K] e4m3 (pitch a_pitch bytes), AS [M, ceil(K/128)] f32 (pitch as_pitch)
  *   B  [N, K/2] packed e2m1, low nibble = even k (pitch K/2 bytes)

@@ -34,7 +34,18 @@ def test_plugin_identity_and_schema():
     info = L.rad_plugin_info().contents
     assert info.targets == b"gfx950" and info.kind == 1
     sch = R.schemas()
-    assert [s["op"] for s in sch] == ["gemm_nt_q", "quant_act_fp8"]
+    assert [s["op"] for s in sch] == ["gemm_nt_q", "quant_act_fp8", "gemm_nt_q_gated",
+                                      "gated_quant_fp8"]
+    gg, gq = sch[2], sch[3]                 # src/r3d_rows.cpp:215-230 and :626-637, verbatim
+    assert [(p[0], p[2]) for p in gg["params"]] == [("M", 0), ("N", 0), ("K", 0), ("group", 0),
+                                                    ("dtype", 0), ("act", 0)]
+    assert [(o[0], o[1], o[2]) for o in gg["operands"]] == [
+        ("a", 0, 0), ("a_scale", 0, 0), ("b", 3, 0), ("b_scale", 3, 0), ("q", 1, 0),
+        ("scale", 1, 0), ("out_bf16", 1, 1)]
+    assert [(p[0], p[2]) for p in gq["params"]] == [("M", 0), ("n", 0), ("group", 0),
+                                                    ("dtype", 0), ("act", 1)]
+    assert [(o[0], o[1], o[2]) for o in gq["operands"]] == [
+        ("gate_up", 0, 0), ("q", 1, 0), ("scale", 1, 0), ("out_bf16", 1, 1)]
     q = sch[1]                              # src/r3d_rows.cpp:615-625, verbatim
     assert [(p[0], p[2]) for p in q["params"]] == [("M", 0), ("n", 0), ("group", 0), ("dtype", 0)]
     assert [(o[0], o[1], o[2]) for o in q["operands"]] == [("x", 0, 0), ("q", 1, 0), ("scale", 1, 0)]
@@ -49,7 +60,18 @@ def test_plugin_identity_and_schema():
 def test_rows_and_resolver():
     rows = {r["name"]: r for r in R.rows()}
     assert set(rows) == {"gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", "gemm_nt_q_fp8a8",
-                         "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4a16", "quant_act_fp8_act"}
+                         "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4a16", "quant_act_fp8_act",
+                         "gated_quant_fp8_act", "gemm_nt_q_gated_fp8a8"}
+    gq = lambda **kw: (R.resolve("gated_quant_fp8", kw) or {}).get("name")
+    assert gq(M=1, n=10752, group=128, dtype="bf16") == "gated_quant_fp8_act"
+    assert gq(M=1, n=10752, group=128, dtype="f16") is None
+    gg = lambda **kw: (R.resolve("gemm_nt_q_gated", kw) or {}).get("name")
+    ok = dict(dtype="fp8a8", M=64, N=21504, K=5376, group=128, act="silu")
+    assert gg(**ok) == "gemm_nt_q_gated_fp8a8"
+    assert gg(**dict(ok, act="sigmoid")) == "gemm_nt_q_gated_fp8a8"
+    assert gg(**dict(ok, M=65)) is None and gg(**dict(ok, act="gelu")) is None
+    assert gg(**dict(ok, K=5377)) is None and gg(**dict(ok, dtype="mxfp4a8")) is None
+    assert rows["gemm_nt_q_gated_fp8a8"]["scratch"]
     qa = lambda **kw: R.resolve("quant_act_fp8", kw)["name"] if R.resolve("quant_act_fp8", kw) else None
     assert qa(M=4, n=5376, group=128, dtype="bf16") == "quant_act_fp8_act"
     assert qa(M=4, n=5376, group=128, dtype="f32") == "quant_act_fp8_act"
@@ -83,18 +105,24 @@ A16 = "gemm_nt_q_mxfp4a16"
 
 
 QA = "quant_act_fp8_act"
+GQ = "gated_quant_fp8_act"
+GG = "gemm_nt_q_gated_fp8a8"
 
 
 @pytest.mark.parametrize("env,expect", [
-    ({}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
-    ({"R3D_NO_MXFP4": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", QA]),
-    ({"R3D_NO_FP4_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4", A16, QA]),
-    ({"R3D_NO_FP8A8": "1"}, ["gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
-    ({"R3D_NO_FP8_DEC": "1"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
-    ({"R3D_NO_FP8_DEC": "", "R3D_NO_FP4_DEC": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_mxfp4", A16, QA]),
-    ({"R3D_MXFP4_Q8X": "0"}, ["gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4",
-                              "gemm_nt_q_mxfp4_decode", A16, QA]),
-    ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, [QA]),
+    ({}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG, "gemm_nt_q_mxfp4",
+          "gemm_nt_q_mxfp4_decode", A16, QA]),
+    ({"R3D_NO_MXFP4": "1"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG, QA]),
+    ({"R3D_NO_FP4_DEC": "1"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG,
+                               "gemm_nt_q_mxfp4", A16, QA]),
+    ({"R3D_NO_FP8A8": "1"}, [GQ, "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
+    ({"R3D_NO_FP8_DEC": "1"}, [GQ, "gemm_nt_q_fp8a8", GG, "gemm_nt_q_mxfp4",
+                               "gemm_nt_q_mxfp4_decode", A16, QA]),
+    ({"R3D_NO_FP8_DEC": "", "R3D_NO_FP4_DEC": "0"}, [GQ, "gemm_nt_q_fp8a8", GG,
+                                                     "gemm_nt_q_mxfp4", A16, QA]),
+    ({"R3D_MXFP4_Q8X": "0"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG,
+                              "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
+    ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, [GQ, QA]),
 ])
 def test_kill_switch_matrix(env, expect):
     """Presence-tested levers hide rows at registration (the value does not matter: an
@@ -469,3 +497,89 @@ def test_quant_act_plan_walk():
                              x_dtype="BF16", shapes={0: (3, 320)}, strides={0: (320, 1)})
     g = _geom(R.describe("quant_act_fp8_act", ops)[1])
     assert g["x_pitch"] == "300"                              # shape[1] != n: flat walk
+
+
+# ------------------------------------------------------------------ gated rows (host only)
+def _gated_ops(M=4, n=1024, K=512, rblk=128, out=True, scratch=True, act="silu", **kw):
+    N = 2 * n
+    a = FakeT(_aligned((M, K), np.uint8))
+    s = FakeT(_aligned((M, K // 128), np.float32))
+    b = FakeT(_aligned((N, K), np.uint8))
+    bs = FakeT(_aligned((N if rblk == 1 else (N + 127) // 128, K // 128), np.uint16))
+    q = FakeT(_aligned((M, n), np.uint8))
+    sc = FakeT(_aligned((M, n // 128), np.float32))
+    ob = FakeT(_aligned((M, n), np.uint16)) if out else None
+    ops = R.GatedGemmOperands(a, s, b, bs, q, sc, ob, N=N, K=K, act=act, **kw)
+    need = R.lib().r3d_rad_gemm_nt_q_gated_fp8_scratch(ctypes.byref(ops.args))
+    assert need == 64 * N * 2
+    if scratch:
+        buf = FakeT(_aligned((need,), np.uint8))
+        ops.set_scratch(buf, need if scratch is True else scratch)
+        ops._buf = buf
+    return ops
+
+
+def test_gated_gemm_plan_and_refusals():
+    """The gated row's gates (src/r3d_gemm_fp8a8.hip:1166-1219): GEMM arm by M (decode GEMV
+    to 16, the prefill pipeline above), act required, N even, M from numel(q)/n, scratch
+    at least M*N*2 bytes."""
+    G = "gemm_nt_q_gated_fp8a8"
+    for M, arm in ((1, "decode"), (16, "decode"), (17, "prefill"), (64, "prefill")):
+        rc, d = R.describe(G, _gated_ops(M=M))
+        assert rc == R.RAD_OK, d
+        g = _geom(d)
+        assert g["gemm"] == arm and g["M"] == str(M) and g["n"] == "1024" and g["ob"] == "bf16", d
+    rc, d = R.describe(G, _gated_ops(M=2, rblk=1, out=False, act="sigmoid"))
+    assert rc == R.RAD_OK and _geom(d)["act"] == "sigmoid" and _geom(d)["ob"] == "none", d
+    assert R.describe(G, _gated_ops(act=None))[0] == R.RAD_E_UNSUPPORTED
+    assert R.describe(G, _gated_ops(act="gelu"))[0] == R.RAD_E_UNSUPPORTED
+    assert R.describe(G, _gated_ops(scratch=False))[0] == R.RAD_E_UNSUPPORTED
+    assert R.describe(G, _gated_ops(M=4, scratch=4 * 2048 * 2 - 2))[0] == R.RAD_E_UNSUPPORTED
+    assert R.describe(G, _gated_ops(M=4, scratch=4 * 2048 * 2))[0] == R.RAD_OK
+    ops = _gated_ops()
+    ops._p[0].ival = 2047                                   # N odd
+    assert R.describe(G, ops)[0] == R.RAD_E_SHAPE
+    ops = _gated_ops()
+    ops._t[4].shape[1] = 1000                               # numel(q) not a multiple of n
+    assert R.describe(G, ops)[0] == R.RAD_E_SHAPE
+    ops = _gated_ops()
+    ops._t[1].data = None                                   # a_scale absent
+    assert R.describe(G, ops)[0] == R.RAD_E_UNSUPPORTED
+
+
+def _gq_ops(M=3, n=512, group=128, gu_dt=np.uint16, out_dt=np.uint16, act=None, pitch=None):
+    gu = FakeT(_aligned((M, pitch or 2 * n), gu_dt))
+    if pitch:
+        gu.shape = (M, 2 * n)
+        gu.stride = lambda dim=None, p=pitch: (p, 1) if dim is None else (p, 1)[dim]
+    q = FakeT(_aligned((M, n), np.uint8))
+    sc = FakeT(_aligned((M, (n + group - 1) // group), np.float32))
+    ob = FakeT(_aligned((M, n), out_dt)) if out_dt is not None else None
+    return R.GatedQuantOperands(gu, q, sc, ob, n=n, group=group, act=act, M=M)
+
+
+def test_gated_quant_plan_and_refusals():
+    G = "gated_quant_fp8_act"
+    rc, d = R.describe(G, _gq_ops())
+    g = _geom(d)
+    assert rc == R.RAD_OK and g["act"] == "silu" and g["ob"] == "bf16" and g["gu_pitch"] == "1024", d
+    g = _geom(R.describe(G, _gq_ops(act="sigmoid", gu_dt=np.float32, out_dt=np.float32))[1])
+    assert g["act"] == "sigmoid" and g["gate_up"] == "f32" and g["ob"] == "f32"
+    g = _geom(R.describe(G, _gq_ops(act="tanh", out_dt=None))[1])   # any other act: silu
+    assert g["act"] == "silu" and g["ob"] == "none"
+    g = _geom(R.describe(G, _gq_ops(n=300, group=1000))[1])          # group clamps to n
+    assert g["group"] == "300" and g["ngrp"] == "1"
+    g = _geom(R.describe(G, _gq_ops(pitch=1100))[1])
+    assert g["gu_pitch"] == "1100"
+    ops = _gq_ops()
+    ops._t[0].dtype = R.DT["F8E4M3"]
+    assert R.describe(G, ops)[0] == R.RAD_E_DTYPE
+    ops = _gq_ops()
+    ops._t[3].dtype = R.DT["F8E4M3"]                        # out_bf16 not f32/bf16
+    assert R.describe(G, ops)[0] == R.RAD_E_DTYPE
+    ops = _gq_ops()
+    ops._t[1].data = None
+    assert R.describe(G, ops)[0] == R.RAD_E_INVAL
+    ops = _gq_ops()
+    ops._t[2].shape[1] = 3                                   # too few scales
+    assert R.describe(G, ops)[0] == R.RAD_E_SHAPE

@@ -174,6 +174,74 @@ def test_quant_act_fp8_matches_numpy_float32_steps():
     assert np.array_equal(q, q2)
 
 
+# ------------------------------------------------------------------ gated_quant_fp8
+def _same_nan_class(a, b):
+    na, nb = (a & 0x7F80) == 0x7F80, (b & 0x7F80) == 0x7F80   # bf16 Inf/NaN exponent
+    nan_a, nan_b = na & ((a & 0x7F) != 0), nb & ((b & 0x7F) != 0)
+    assert np.array_equal(nan_a, nan_b)
+    assert np.array_equal(a[~nan_a], b[~nan_b])
+
+
+def test_gated_quant_fp8_closed_forms():
+    """sigmoid(0) = 1/2 exactly, so act=sigmoid with a zero gate gives h = up/2; a gate of
+    30 has sigmoid 1 in f32 (exp(-30) is below half an ulp of 1), so silu gives
+    h = bf16(30 * up).  Both must equal quant_act_fp8 of that h, with gate/up taken from
+    the right halves."""
+    rng = np.random.default_rng(77)
+    M, n = 3, 512
+    up = synth.bf16_bits((rng.standard_normal((M, n)) * 2).astype(np.float32))
+    upf = O.bf16_to_f32(up)
+    gu = np.concatenate([np.zeros((M, n), np.uint16), up], axis=1)
+    q, s, o = O.gated_quant_fp8(gu, group=128, act="sigmoid")
+    half = synth.bf16_bits(upf * np.float32(0.5))
+    assert np.array_equal(o, half)
+    qr, sr = O.quant_act_fp8(half, 128)
+    assert np.array_equal(q, qr) and np.array_equal(s.view(np.uint32), sr.view(np.uint32))
+    # silu with a zero gate is exactly zero: every group all-zero, scale 1, code 0
+    q, s, o = O.gated_quant_fp8(gu, group=128, act="silu")
+    assert not o.any() or set(np.unique(o & 0x7FFF)) == {0}
+    assert (s == 1.0).all() and not (q & 0x7F).any()
+    g30 = synth.bf16_bits(np.full((M, n), 30.0, np.float32))
+    q, s, o = O.gated_quant_fp8(np.concatenate([g30, up], axis=1), group=64, act="silu")
+    h = synth.bf16_bits(np.float32(30.0) * upf)
+    assert np.array_equal(o, h)
+    qr, sr = O.quant_act_fp8(h, 64)
+    assert np.array_equal(q, qr) and np.array_equal(s, sr)
+    # swapped halves (gate = up values, up = 30) differ: the order is pinned
+    q2, _, o2 = O.gated_quant_fp8(np.concatenate([up, g30], axis=1), group=64, act="silu")
+    assert not np.array_equal(o2, o)
+
+
+@pytest.mark.parametrize("act", ["silu", "sigmoid"])
+@pytest.mark.parametrize("f32_in", [False, True])
+def test_gated_quant_fp8_numpy_eval(act, f32_in):
+    """numpy evaluation of the gated step (exp in float64, narrowed to float32, then float32
+    arithmetic and torch's RNE bf16), on random gates and the special ones (+-0, +-30,
+    +-88, +-100, +-inf, NaN), then quant_act_fp8 on the result."""
+    rng = np.random.default_rng(91 if f32_in else 90)
+    M, n = 4, 384
+    gt = (rng.standard_normal((M, n)) * 4).astype(np.float32)
+    sp = np.array([0.0, -0.0, 30, -30, 88, -88, 100, -100, np.inf, -np.inf, np.nan],
+                  np.float32)
+    gt[0, :sp.size] = sp
+    upf = (rng.standard_normal((M, n)) * 3).astype(np.float32)
+    if f32_in:
+        gu = np.concatenate([gt, upf], axis=1)
+        gtf, uf = gt, upf
+    else:
+        gu = synth.bf16_bits(np.concatenate([gt, upf], axis=1))
+        gtf, uf = O.bf16_to_f32(gu[:, :n]), O.bf16_to_f32(gu[:, n:])
+    with np.errstate(over="ignore", invalid="ignore"):
+        e = np.exp(-gtf.astype(np.float64)).astype(np.float32)
+        sg = np.float32(1.0) / (np.float32(1.0) + e)
+        t = gtf * sg if act == "silu" else sg
+        h = synth.bf16_bits((t * uf).astype(np.float32))
+    q, s, o = O.gated_quant_fp8(gu, group=128, act=act)
+    _same_nan_class(o, h)
+    qr, sr = O.quant_act_fp8(o, 128)
+    assert np.array_equal(q, qr) and np.array_equal(s.view(np.uint32), sr.view(np.uint32))
+
+
 # ------------------------------------------------------------------ quant_dot
 def _mx(M, N, K, seed, lo=115, hi=139):
     rng = np.random.default_rng(seed)
