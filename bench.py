@@ -264,6 +264,7 @@ def main():
         torch.cuda.empty_cache()
         extra.update(bench_quant(dev, stream))
         extra.update(bench_fused_decode(dev, stream, ksteps))
+        extra.update(bench_gated(dev, stream, ksteps))
         extra.update(bench_c4(dev, stream, steps=5))
     if extra:
         out["extra"] = extra
@@ -406,6 +407,76 @@ def bench_fused_decode(dev, stream, steps=50):
             name, t2 * 1e6, t1 * 1e6))
         del bs, bss, one, two
         torch.cuda.empty_cache()
+    return res
+
+
+def bench_gated(dev, stream, steps=50):
+    """gemm_nt_q_gated at fp8a8 on config 1's plane read as a gate_up pair (N = 2n = 21504,
+    K = 5376, per-row weight scales, cold), silu: the gated row against its two rows
+    (gemm_nt_q, then gated_quant_fp8) at M = 1 and 4 -- the same kernels, so the gap is the
+    host work of the second row's launch."""
+    import torch
+    import libr3d_amd as R
+    from libr3d_amd import synth
+    res = {}
+    K, N = 5376, 21504
+    n = N // 2
+    B, BS = synth.fp8_weights(N, K, 0x5EED + 11)
+    copies = copies_for(B.nbytes)
+    bs = [torch.from_numpy(B).to(dev)]
+    bss = [torch.from_numpy(BS.view(np.int16)).to(dev)]
+    for _ in range(copies - 1):
+        bs.append(bs[0].clone())
+        bss.append(bss[0].clone())
+    for M in (1, 4):
+        A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 40 + M)
+        a, as_ = torch.from_numpy(A).to(dev), torch.from_numpy(AS).to(dev)
+        q = torch.empty((M, n), dtype=torch.uint8, device=dev)
+        sc = torch.empty((M, n // 128), dtype=torch.float32, device=dev)
+        y = torch.empty((M, N), dtype=torch.int16, device=dev)
+        scratch = torch.empty(64 * N * 2, dtype=torch.uint8, device=dev)
+        fused = []
+        for b, s_ in zip(bs, bss):
+            o = R.GatedGemmOperands(a, as_, b, s_, q, sc, None, N=N, K=K, act="silu", M=M)
+            o.set_scratch(scratch)
+            fused.append(o)
+        gemm = [R.GemmOperands(a, as_, b, s_, y, dtype="fp8a8", N=N, K=K) for b, s_ in zip(bs, bss)]
+        gq = R.GatedQuantOperands(y, q, sc, None, n=n, group=128, act="silu", M=M)
+        fg, fd, fq = (R.row_launcher(r) for r in
+                      ("gemm_nt_q_gated_fp8a8", "gemm_nt_q_fp8a8_decode", "gated_quant_fp8_act"))
+
+        def timed(body):
+            for i in range(10):
+                body(i)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for i in range(steps):
+                body(i)
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e-3 / steps
+
+        def one(i):
+            assert fg(fused[i % copies], stream) == 0
+
+        def two(i):
+            assert fd(gemm[i % copies], stream) == 0 and fq(gq, stream) == 0
+
+        def prod(i):
+            assert fq(gq, stream) == 0
+
+        t1, t2, tp = timed(one), timed(two), timed(prod)
+        nb = f8_bytes(M, N, K)
+        res["gated_fp8a8_c1_plane_M%d" % M] = {
+            "M": M, "K": K, "N": N, "gated_row_us": round(t1 * 1e6, 2),
+            "two_rows_us": round(t2 * 1e6, 2), "gated_quant_fp8_us": round(tp * 1e6, 2),
+            "GBps_gated_row": round(nb / t1 / 1e9, 1)}
+        log("[bench] gated fp8a8 M=%d: row %.2f us, gemm_nt_q + gated_quant_fp8 %.2f us "
+            "(producer alone %.2f us)" % (M, t1 * 1e6, t2 * 1e6, tp * 1e6))
+    del bs, bss
+    torch.cuda.empty_cache()
     return res
 
 

@@ -241,8 +241,9 @@ __global__ __launch_bounds__(256) void gated_quant_fp8_kernel(
     }
 }
 
-/* Groups of 8..512 tiling the rows (n % g == 0), aligned operands: one workgroup per row,
- * 8 elements per lane per chunk (16-byte gate and up loads at bf16), L = g / 8 lanes per
+/* Groups of 8..512 tiling the rows (n % g == 0), aligned operands: grid (ceil(chunks / 256),
+ * rows), one 8-element chunk per lane (16-byte gate and up loads at bf16) -- the exp in
+ * double makes this ALU-heavy, so a row spreads over workgroups -- with L = g / 8 lanes per
  * group reducing the maximum by xor-shuffles; codes leave 8 bytes per lane, the gated
  * output 16 (bf16) or 32 (f32). */
 template <bool BF16, int L>
@@ -251,77 +252,65 @@ __global__ __launch_bounds__(256) void gated_quant_fp8_vec_kernel(
     float* __restrict__ sc, int64_t s_pitch, uint8_t* __restrict__ ob, int ob_bf16,
     int64_t ob_pitch, int64_t n, int silu) {
     constexpr int EB = BF16 ? 2 : 4;
-    constexpr int U = 2;
-    const int64_t row = blockIdx.x;
+    const int64_t row = blockIdx.y;
     const int64_t chunks = n >> 3;
     const uint8_t* gr = gu + row * gu_pitch * EB;
     const uint8_t* ur = gr + n * EB;
-    uint8_t* qr = q + row * q_pitch;
-    float* sr = sc + row * s_pitch;
-    for (int64_t c0 = threadIdx.x; c0 - threadIdx.x < chunks; c0 += 256 * U) {
-        float gv[U][8], uv[U][8];
+    /* a lane past the row's end re-reads its last chunk (its group's lanes leave the
+     * shuffles together) and stores nothing */
+    const int64_t c0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t c = c0 < chunks ? c0 : chunks - 1;
+    float gv[8], uv[8];
+    if (BF16) {
+        const r3d_i32x4 a = *reinterpret_cast<const r3d_i32x4*>(gr + 16 * c);
+        const r3d_i32x4 b = *reinterpret_cast<const r3d_i32x4*>(ur + 16 * c);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            /* a thread past the row's end re-reads its last chunk; nothing of it is stored */
-            const int64_t c = c0 + 256 * u < chunks ? c0 + 256 * u : chunks - 1;
-            if (BF16) {
-                const r3d_i32x4 a = *reinterpret_cast<const r3d_i32x4*>(gr + 16 * c);
-                const r3d_i32x4 b = *reinterpret_cast<const r3d_i32x4*>(ur + 16 * c);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    gv[u][2 * i] = __uint_as_float((uint32_t)a[i] << 16);
-                    gv[u][2 * i + 1] = __uint_as_float((uint32_t)a[i] & 0xFFFF0000u);
-                    uv[u][2 * i] = __uint_as_float((uint32_t)b[i] << 16);
-                    uv[u][2 * i + 1] = __uint_as_float((uint32_t)b[i] & 0xFFFF0000u);
-                }
-            } else {
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const float4 a = *reinterpret_cast<const float4*>(gr + 32 * c + 16 * h);
-                    const float4 b = *reinterpret_cast<const float4*>(ur + 32 * c + 16 * h);
-                    gv[u][4 * h] = a.x; gv[u][4 * h + 1] = a.y; gv[u][4 * h + 2] = a.z;
-                    gv[u][4 * h + 3] = a.w;
-                    uv[u][4 * h] = b.x; uv[u][4 * h + 1] = b.y; uv[u][4 * h + 2] = b.z;
-                    uv[u][4 * h + 3] = b.w;
-                }
-            }
+        for (int i = 0; i < 4; ++i) {
+            gv[2 * i] = __uint_as_float((uint32_t)a[i] << 16);
+            gv[2 * i + 1] = __uint_as_float((uint32_t)a[i] & 0xFFFF0000u);
+            uv[2 * i] = __uint_as_float((uint32_t)b[i] << 16);
+            uv[2 * i + 1] = __uint_as_float((uint32_t)b[i] & 0xFFFF0000u);
         }
+    } else {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t c = c0 + 256 * u;
-            float h[8];
-            float amax = 0.0f;
+        for (int h = 0; h < 2; ++h) {
+            const float4 a = *reinterpret_cast<const float4*>(gr + 32 * c + 16 * h);
+            const float4 b = *reinterpret_cast<const float4*>(ur + 32 * c + 16 * h);
+            gv[4 * h] = a.x; gv[4 * h + 1] = a.y; gv[4 * h + 2] = a.z; gv[4 * h + 3] = a.w;
+            uv[4 * h] = b.x; uv[4 * h + 1] = b.y; uv[4 * h + 2] = b.z; uv[4 * h + 3] = b.w;
+        }
+    }
+    float h[8];
+    float amax = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                h[i] = r3d_gated_h(gv[u][i], uv[u][i], silu);
-                amax = fmaxf(amax, fabsf(h[i]));
-            }
+    for (int i = 0; i < 8; ++i) {
+        h[i] = r3d_gated_h(gv[i], uv[i], silu);
+        amax = fmaxf(amax, fabsf(h[i]));
+    }
 #pragma unroll
-            for (int off = L / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-            if (c >= chunks) continue;
-            const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
-            const float inv = 1.0f / s;
-            if ((c & (L - 1)) == 0) sr[c / L] = s;
-            float cv[8];
+    for (int off = L / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if (c0 >= chunks) return;
+    const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+    const float inv = 1.0f / s;
+    if ((c & (L - 1)) == 0) sc[row * s_pitch + c / L] = s;
+    float cv[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) cv[i] = r3d_band_clamp448(h[i] * inv);
-            *reinterpret_cast<uint2*>(qr + 8 * c) =
-                make_uint2(r3d_e4m3x4_rne(cv[0], cv[1], cv[2], cv[3]),
-                           r3d_e4m3x4_rne(cv[4], cv[5], cv[6], cv[7]));
-            if (ob) {
-                if (ob_bf16) {
-                    r3d_i32x4 o;
+    for (int i = 0; i < 8; ++i) cv[i] = r3d_band_clamp448(h[i] * inv);
+    *reinterpret_cast<uint2*>(q + row * q_pitch + 8 * c) =
+        make_uint2(r3d_e4m3x4_rne(cv[0], cv[1], cv[2], cv[3]),
+                   r3d_e4m3x4_rne(cv[4], cv[5], cv[6], cv[7]));
+    if (ob) {
+        if (ob_bf16) {
+            r3d_i32x4 o;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        o[i] = (int)((__float_as_uint(h[2 * i]) >> 16) |
-                                     (__float_as_uint(h[2 * i + 1]) & 0xFFFF0000u));
-                    *reinterpret_cast<r3d_i32x4*>(ob + 2 * (row * ob_pitch + 8 * c)) = o;
-                } else {
-                    float* of = reinterpret_cast<float*>(ob) + row * ob_pitch + 8 * c;
-                    *reinterpret_cast<float4*>(of) = make_float4(h[0], h[1], h[2], h[3]);
-                    *reinterpret_cast<float4*>(of + 4) = make_float4(h[4], h[5], h[6], h[7]);
-                }
-            }
+            for (int i = 0; i < 4; ++i)
+                o[i] = (int)((__float_as_uint(h[2 * i]) >> 16) |
+                             (__float_as_uint(h[2 * i + 1]) & 0xFFFF0000u));
+            *reinterpret_cast<r3d_i32x4*>(ob + 2 * (row * ob_pitch + 8 * c)) = o;
+        } else {
+            float* of = reinterpret_cast<float*>(ob) + row * ob_pitch + 8 * c;
+            *reinterpret_cast<float4*>(of) = make_float4(h[0], h[1], h[2], h[3]);
+            *reinterpret_cast<float4*>(of + 4) = make_float4(h[4], h[5], h[6], h[7]);
         }
     }
 }

@@ -346,10 +346,11 @@ static int launch_gated(const GatedPlan& P, hipStream_t stream) {
                      P.q_pitch % 8 == 0 &&
                      (!P.ob || (((uintptr_t)P.ob % 16) == 0 && (P.ob_pitch * ob_eb) % 16 == 0));
     if (vec) {
+        const dim3 grid((unsigned)((P.n / 8 + 255) / 256), (unsigned)P.rows);
 #define R3D_GV(B_, L_)                                                                      \
-    hipLaunchKernelGGL((gated_quant_fp8_vec_kernel<B_, L_>), dim3((unsigned)P.rows),          \
-                       dim3(256), 0, stream, P.gu, P.gu_pitch, P.q, P.q_pitch, P.scale,       \
-                       P.s_pitch, P.ob, P.ob_bf16, P.ob_pitch, P.n, P.silu)
+    hipLaunchKernelGGL((gated_quant_fp8_vec_kernel<B_, L_>), grid, dim3(256), 0, stream,      \
+                       P.gu, P.gu_pitch, P.q, P.q_pitch, P.scale, P.s_pitch, P.ob, P.ob_bf16, \
+                       P.ob_pitch, P.n, P.silu)
 #define R3D_GVL(B_)                                                                         \
     switch (lanes) {                                                                        \
         case 1: R3D_GV(B_, 1); break;   case 2: R3D_GV(B_, 2); break;                       \
