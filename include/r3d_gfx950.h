@@ -77,6 +77,11 @@ int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s);
  * quant_act_fp8 quantiser.  Replaces src/r3d_band.hip:489-547 (r3d_rad_gated_quant_fp8). */
 int r3d_rad_gated_quant_fp8(const RadArgs* a, RadStream s);
 
+/* rmsnorm_quant_fp8: RMS norm (after an optional residual add written back) and the fp8
+ * group quantiser over the bf16 normed row.  Replaces src/r3d_more.hip:479-539
+ * (r3d_rad_rmsnorm_quant_fp8). */
+int r3d_rad_rmsnorm_quant_fp8(const RadArgs* a, RadStream s);
+
 /* gemm_nt_q_gated at fp8a8: the fp8a8 GEMM into the launch scratch, then gated_quant_fp8
  * over it.  Replaces src/r3d_gemm_fp8a8.hip:1163-1241 (r3d_rad_gemm_nt_q_gated_fp8). */
 int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s);

@@ -4,6 +4,7 @@
  *   rad_arg_in(a, i)      the i-th operand, or null when absent (index past n_t or null
  *                         data pointer);
  *   rad_args_geti/gets    look a parameter up by key, 1 when found with that kind;
+ *   rad_args_getf_or      an F64 parameter by key, else the fallback;
  *   rad_tensor_numel      product of the shape (0 for a null tensor).
  */
 #ifndef RAD_PLUGIN_H
@@ -33,6 +34,16 @@ static inline const char* rad_args_gets(const RadArgs* a, const char* key) {
         if (a->p[i].key && strcmp(a->p[i].key, key) == 0 && a->p[i].kind == RAD_P_STR)
             return a->p[i].sval;
     return 0;
+}
+
+/* A float parameter by key, or `fb` when absent or not an F64 (call sites
+ * src/r3d_band.hip:565, src/r3d_more.hip:361). */
+static inline double rad_args_getf_or(const RadArgs* a, const char* key, double fb) {
+    if (!a || !a->p) return fb;
+    for (int i = 0; i < a->n_p; ++i)
+        if (a->p[i].key && strcmp(a->p[i].key, key) == 0 && a->p[i].kind == RAD_P_F64)
+            return a->p[i].dval;
+    return fb;
 }
 
 static inline long long rad_tensor_numel(const RadTensor* t) {

@@ -19,7 +19,7 @@ __all__ = [
     "RAD_E_INVAL", "RAD_E_DEVICE", "DT", "RadTensor", "RadParam", "RadArgs",
     "RadKernelInfo", "RadOpSchema", "lib", "lib_path", "rows", "schemas", "resolve",
     "launch_row", "gemm_nt_q", "describe", "GemmOperands", "QuantActOperands", "quant_act_fp8",
-    "GatedQuantOperands", "GatedGemmOperands",
+    "GatedQuantOperands", "GatedGemmOperands", "RmsNormQuantOperands",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -418,6 +418,26 @@ class GatedQuantOperands(_Args):
                          [("n", n), ("group", group),
                           ("dtype", dtype or ("f32" if gdt == "F32" else "bf16"))] +
                          ([("act", act)] if act is not None else []) +
+                         ([("M", M)] if M is not None else []))
+
+
+class RmsNormQuantOperands(_Args):
+    """One rmsnorm_quant_fp8 call (src/r3d_more.hip:482-539).
+
+    x        bf16/int16 [M, n]
+    residual optional bf16/int16 [M, n], updated in place with bf16(residual + x)
+    w        float32 or bf16/int16 [n] (rank 1)
+    q        uint8 [M, n] e4m3 codes out; scale float32 [M, ceil(n / group)] out
+    out      optional float32 or bf16/int16 [M, n]: the normed bf16 values
+    """
+
+    def __init__(self, x, residual, w, q, scale, out=None, *, n, eps=1e-6, group=128,
+                 wadd=None, M=None, w_dtype=None):
+        ops = [(x, "BF16"), (residual, "BF16"), (w, w_dtype or _elt(w)), (q, "F8E4M3"),
+               (scale, "F32"), (out, _elt(out) if out is not None else "BF16")]
+        super().__init__([(t, dt, None, None) for t, dt in ops],
+                         [("n", n), ("eps", float(eps)), ("group", group), ("dtype", "bf16")] +
+                         ([("wadd", float(wadd))] if wadd is not None else []) +
                          ([("M", M)] if M is not None else []))
 
 

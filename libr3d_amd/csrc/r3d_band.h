@@ -1,5 +1,5 @@
-/* r3d_band.h -- the activation producers on gfx950: quant_act_fp8 and gated_quant_fp8
- * (below).  quant_act_fp8 is per-(row, group) symmetric e4m3 quantisation of a bf16 or f32
+/* r3d_band.h -- the activation producers on gfx950: quant_act_fp8, gated_quant_fp8 and
+ * rmsnorm_quant_fp8 (below).  quant_act_fp8 is per-(row, group) symmetric e4m3 quantisation of a bf16 or f32
  * activation, plain row-major codes and an f32 dequant scale per group
  * (src/r3d_band.hip:117-153 of the reference):
  *     amax = max |x| over the group (NaN never wins; 0 when the group has none)
@@ -312,6 +312,84 @@ __global__ __launch_bounds__(256) void gated_quant_fp8_vec_kernel(
             *reinterpret_cast<float4*>(of) = make_float4(h[0], h[1], h[2], h[3]);
             *reinterpret_cast<float4*>(of + 4) = make_float4(h[4], h[5], h[6], h[7]);
         }
+    }
+}
+
+/* ---- rmsnorm_quant_fp8 (src/r3d_more.hip:241-330 of the reference), one workgroup of 256
+ * lanes per row, the row's bf16 values staged in LDS:
+ *   1. with a residual: y = bf16(residual + x) is stored back and squared; else x is.
+ *      Lane t sums the squares of elements t, t + 256, ... in that order (separately
+ *      rounded multiply and add: the reference builds this file without contraction);
+ *      the 256 partials then fold exactly as the reference's 32-lane warps do -- a
+ *      shuffle-down tree inside each 32-lane half (offsets 16, 8, 4, 2, 1), and the eight
+ *      half sums added in order -- so the sum is bit-identical.
+ *   2. rs = 1 / sqrt(sum / n + eps);  h = bf16((src * rs) * (w + wadd)), the normed value
+ *      out_bf16 carries and the quantiser sees.
+ *   3. quant_act_fp8's quantiser over each group of h (one wave per group here; the
+ *      maximum is order-free). */
+template <bool WBF16>
+__global__ __launch_bounds__(256) void rmsnorm_quant_fp8_kernel(
+    const uint16_t* __restrict__ x, int64_t x_pitch, uint16_t* __restrict__ res, int64_t r_pitch,
+    const uint8_t* __restrict__ w, uint8_t* __restrict__ q, int64_t q_pitch,
+    float* __restrict__ sc, int64_t s_pitch, uint8_t* __restrict__ ob, int ob_bf16,
+    int64_t ob_pitch, int n, int g, int ngrp, float eps, float wadd) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t s_h[];
+    __shared__ float s_part[8];
+    __shared__ float s_rs;
+    const int t = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const uint16_t* xr = x + row * x_pitch;
+    uint16_t* rr = res ? res + row * r_pitch : nullptr;
+    float ss = 0.0f;
+    for (int i = t; i < n; i += 256) {
+        float v = __uint_as_float((uint32_t)xr[i] << 16);
+        if (rr) {
+            const uint32_t hb = r3d_band_bf16_bits(__fadd_rn(__uint_as_float((uint32_t)rr[i] << 16), v));
+            rr[i] = (uint16_t)hb;
+            s_h[i] = (uint16_t)hb;
+            v = __uint_as_float(hb << 16);
+        }
+        ss = __fadd_rn(ss, __fmul_rn(v, v));
+    }
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) ss = __fadd_rn(ss, __shfl_down(ss, off, 32));
+    if ((t & 31) == 0) s_part[t >> 5] = ss;
+    __syncthreads();
+    if (t == 0) {
+        float r = s_part[0];
+        for (int k = 1; k < 8; ++k) r = __fadd_rn(r, s_part[k]);
+        s_rs = 1.0f / sqrtf(__fadd_rn(r / (float)n, eps));
+    }
+    __syncthreads();
+    const float rs = s_rs;
+    for (int i = t; i < n; i += 256) {
+        const float src = rr ? __uint_as_float((uint32_t)s_h[i] << 16)
+                             : __uint_as_float((uint32_t)xr[i] << 16);
+        const float wv = __fadd_rn(WBF16 ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(w)[i] << 16)
+                                         : reinterpret_cast<const float*>(w)[i],
+                                   wadd);
+        const uint32_t h = r3d_band_bf16_bits(__fmul_rn(__fmul_rn(src, rs), wv));
+        if (ob) {
+            if (ob_bf16) reinterpret_cast<uint16_t*>(ob)[row * ob_pitch + i] = (uint16_t)h;
+            else reinterpret_cast<float*>(ob)[row * ob_pitch + i] = __uint_as_float(h << 16);
+        }
+        s_h[i] = (uint16_t)h;
+    }
+    __syncthreads();
+    const int wave = t >> 6, lane = t & 63;
+    for (int gi = wave; gi < ngrp; gi += 4) {                 /* wave-uniform */
+        const int k0 = gi * g, len = n - k0 < g ? n - k0 : g;
+        float amax = 0.0f;
+        for (int i = lane; i < len; i += 64)
+            amax = fmaxf(amax, fabsf(__uint_as_float((uint32_t)s_h[k0 + i] << 16)));
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+        if (lane == 0) sc[row * s_pitch + gi] = s;
+        const float inv = 1.0f / s;
+        for (int i = lane; i < len; i += 64)
+            q[row * q_pitch + k0 + i] = (uint8_t)r3d_e4m3x2_rne(
+                r3d_band_clamp448(__uint_as_float((uint32_t)s_h[k0 + i] << 16) * inv), 0.0f);
     }
 }
 

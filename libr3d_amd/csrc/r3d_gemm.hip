@@ -381,6 +381,32 @@ static int launch_gated(const GatedPlan& P, hipStream_t stream) {
     return RAD_OK;
 }
 
+/* rmsnorm_quant_fp8 (src/r3d_more.hip:482-539): the reference's gates, then one workgroup
+ * per row with the row staged in LDS. */
+static int rms_entry(const RadArgs* a, RadStream s) {
+    RmsPlan P{};
+    const int rc = plan_rmsnorm_quant_fp8(a, &P);
+    if (rc) return rc;
+    if (!chip_ok()) return RAD_E_UNSUPPORTED;
+    hipStream_t stream = (hipStream_t)s;
+    const size_t lds = (size_t)((P.n * 2 + 15) / 16 * 16);
+#define R3D_RMS(W_)                                                                         \
+    hipLaunchKernelGGL((rmsnorm_quant_fp8_kernel<W_>), dim3((unsigned)P.rows), dim3(256), lds,  \
+                       stream, reinterpret_cast<const uint16_t*>(P.x), P.x_pitch,             \
+                       reinterpret_cast<uint16_t*>(P.res), P.r_pitch, P.w, P.q, P.q_pitch,    \
+                       P.scale, P.s_pitch, P.ob, P.ob_bf16, P.ob_pitch, (int)P.n, (int)P.g,   \
+                       (int)P.ngrp, P.eps, P.wadd)
+    if (P.w_bf16) R3D_RMS(true); else R3D_RMS(false);
+#undef R3D_RMS
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "libr3d_gfx950: rmsnorm_quant_fp8 launch FAILED (%s)\n", hipGetErrorName(e));
+        return RAD_E_DEVICE;
+    }
+    debug_once("rmsnorm_quant_fp8", 254);
+    return RAD_OK;
+}
+
 /* gated_quant_fp8 (src/r3d_band.hip:492-541): the reference's gates, then the kernels. */
 static int gated_entry(const RadArgs* a, RadStream s) {
     GatedPlan P{};
@@ -414,6 +440,7 @@ extern "C" {
 
 int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s) { return r3d::quant_entry(a, s); }
 int r3d_rad_gated_quant_fp8(const RadArgs* a, RadStream s) { return r3d::gated_entry(a, s); }
+int r3d_rad_rmsnorm_quant_fp8(const RadArgs* a, RadStream s) { return r3d::rms_entry(a, s); }
 int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s) {
     return r3d::gemm_gated_entry(a, s);
 }

@@ -553,6 +553,62 @@ int plan_gated_quant_fp8(const RadArgs* a, GatedPlan* P) {
     return RAD_OK;
 }
 
+int plan_rmsnorm_quant_fp8(const RadArgs* a, RmsPlan* P) {
+    if (!a || a->n_t < 5) return RAD_E_INVAL;
+    const RadTensor* x = rad_arg_in(a, 0);
+    const RadTensor* res = rad_arg_in(a, 1);
+    const RadTensor* w = rad_arg_in(a, 2);
+    const RadTensor* q = rad_arg_in(a, 3);
+    const RadTensor* sc = rad_arg_in(a, 4);
+    const RadTensor* ob = rad_arg_in(a, 5);
+    if (!x || !w || !q || !sc) return RAD_E_INVAL;
+    if (x->dtype != RAD_BF16) return RAD_E_DTYPE;
+    if (res && res->dtype != RAD_BF16) return RAD_E_DTYPE;
+    if (w->dtype != RAD_F32 && w->dtype != RAD_BF16) return RAD_E_DTYPE;
+    if (q->dtype != RAD_F8E4M3 || sc->dtype != RAD_F32) return RAD_E_DTYPE;
+    if (ob && ob->dtype != RAD_F32 && ob->dtype != RAD_BF16) return RAD_E_DTYPE;
+    long long v = 0;
+    const int64_t n = rad_args_geti(a, "n", &v) ? (int64_t)v
+                                                : (w->rank ? w->shape[w->rank - 1] : 0);
+    if (n <= 0 || n > 30720) return RAD_E_SHAPE;
+    int64_t g = rad_args_geti(a, "group", &v) ? (int64_t)v : 0;
+    if (g <= 0 || g > n) g = n;
+    const int64_t ngrp = (n + g - 1) / g;
+    const int64_t rows = rad_tensor_numel(x) / n;
+    if (rows <= 0 || rows > 0xffff) return RAD_E_SHAPE;
+    if (rad_tensor_numel(q) < rows * n || rad_tensor_numel(sc) < rows * ngrp ||
+        rad_tensor_numel(w) < n)
+        return RAD_E_SHAPE;
+    if (res && rad_tensor_numel(res) < rows * n) return RAD_E_SHAPE;
+    if (ob && rad_tensor_numel(ob) < rows * n) return RAD_E_SHAPE;
+    int64_t xp = 0, rp = 0, qp = 0, sp = 0, op = 0;
+    if (band_row_pitch(x, n, &xp)) return RAD_E_STRIDE;
+    if (res && band_row_pitch(res, n, &rp)) return RAD_E_STRIDE;
+    if (w->rank != 1 || w->stride[0] != 1) return RAD_E_STRIDE;
+    if (band_row_pitch(q, n, &qp) || band_row_pitch(sc, ngrp, &sp)) return RAD_E_STRIDE;
+    if (ob && band_row_pitch(ob, n, &op)) return RAD_E_STRIDE;
+    P->x = (const uint8_t*)x->data;
+    P->res = res ? (uint8_t*)res->data : nullptr;
+    P->w = (const uint8_t*)w->data;
+    P->q = (uint8_t*)q->data;
+    P->scale = (float*)sc->data;
+    P->ob = ob ? (uint8_t*)ob->data : nullptr;
+    P->w_bf16 = w->dtype == RAD_BF16;
+    P->ob_bf16 = ob && ob->dtype == RAD_BF16;
+    P->rows = rows;
+    P->n = n;
+    P->g = g;
+    P->ngrp = ngrp;
+    P->x_pitch = xp;
+    P->r_pitch = rp;
+    P->q_pitch = qp;
+    P->s_pitch = sp;
+    P->ob_pitch = op;
+    P->eps = (float)rad_args_getf_or(a, "eps", 1e-6);
+    P->wadd = (float)rad_args_getf_or(a, "wadd", 0.0);
+    return RAD_OK;
+}
+
 int64_t gemm_gated_scratch_bytes(const RadArgs* a) {
     long long N = 0;
     if (!rad_args_geti(a, "N", &N) || N <= 0 || N > (1LL << 34)) return 0;
@@ -718,6 +774,19 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
                  Q.x_bf16 ? "bf16" : "f32", (long long)Q.rows, (long long)Q.n, (long long)Q.g,
                  (long long)Q.ngrp, (long long)Q.x_pitch, (long long)Q.q_pitch,
                  (long long)Q.s_pitch);
+        return RAD_OK;
+    }
+    if (strstr(row, "rmsnorm_quant_fp8") != nullptr) {
+        RmsPlan R{};
+        const int rc = plan_rmsnorm_quant_fp8(a, &R);
+        if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
+        snprintf(buf, (size_t)len,
+                 "arm=band op=rmsnorm_quant_fp8 rows=%lld n=%lld group=%lld ngrp=%lld w=%s "
+                 "residual=%d ob=%s eps=%.9g wadd=%.9g x_pitch=%lld q_pitch=%lld s_pitch=%lld",
+                 (long long)R.rows, (long long)R.n, (long long)R.g, (long long)R.ngrp,
+                 R.w_bf16 ? "bf16" : "f32", R.res != nullptr,
+                 R.ob ? (R.ob_bf16 ? "bf16" : "f32") : "none", (double)R.eps, (double)R.wadd,
+                 (long long)R.x_pitch, (long long)R.q_pitch, (long long)R.s_pitch);
         return RAD_OK;
     }
     if (strstr(row, "gemm_nt_q_gated") != nullptr) {

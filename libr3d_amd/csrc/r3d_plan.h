@@ -178,6 +178,26 @@ struct GatedPlan {
 };
 int plan_gated_quant_fp8(const RadArgs* a, GatedPlan* P);
 
+/* rmsnorm_quant_fp8 launch plan (src/r3d_more.hip:482-521): x (bf16), optional residual
+ * (bf16, updated in place: the fused add form), w (f32 or bf16, rank 1), q (e4m3), scale
+ * (f32), optional out_bf16 (f32 or bf16); n from the param (default w's extent, at most
+ * 30720: the row is staged in LDS), group clamped to [1, n] (absent: n), eps (F64, default
+ * 1e-6) and wadd (F64, default 0) narrowed to f32.  Returns RAD_OK or the reference's
+ * refusal code. */
+struct RmsPlan {
+    const uint8_t* x;
+    uint8_t* res;                             /* null: no residual */
+    const uint8_t* w;
+    uint8_t* q;
+    float* scale;
+    uint8_t* ob;                              /* null: no normed output */
+    int w_bf16, ob_bf16;
+    int64_t rows, n, g, ngrp;
+    int64_t x_pitch, r_pitch, q_pitch, s_pitch, ob_pitch;   /* elements */
+    float eps, wadd;
+};
+int plan_rmsnorm_quant_fp8(const RadArgs* a, RmsPlan* P);
+
 /* gemm_nt_q_gated at fp8a8 (src/r3d_gemm_fp8a8.hip:1166-1241): operands a, a_scale, b,
  * b_scale, q, scale, out_bf16?, a_sum? (refused); params N (= 2n, even), K, group, dtype,
  * act (required: silu or sigmoid).  M = numel(q) / n.  The GEMM writes the [M, N] bf16

@@ -11,6 +11,7 @@
  *   gemm_nt_q_mxfp4a16       prio 1000  dtype IN mxfp4a16, K DIV 128     bf16-in prefill
  *   quant_act_fp8_act        prio 1000  n GE 1, dtype IN f32 bf16          activation producer
  *   gated_quant_fp8_act      prio 1000  n GE 1, dtype IN f32 bf16          gated producer
+ *   rmsnorm_quant_fp8        prio 1000  n DIV 4, group EQ 128, dtype IN bf16  norm producer
  *   gemm_nt_q_gated_fp8a8    prio 1000  dtype IN fp8a8, M LE 64, K DIV 128, group EQ 128,
  *                                       act IN silu sigmoid              GEMM + gated producer
  * gemm_nt_q_mxfp4a16 has no counterpart in the reference: it takes bf16 activations (no
@@ -44,6 +45,7 @@ int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s);
 int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a);
 int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s);
 int r3d_rad_gated_quant_fp8(const RadArgs* a, RadStream s);
+int r3d_rad_rmsnorm_quant_fp8(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s);
 int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a);
 }
@@ -121,6 +123,24 @@ const RadOperandSpec kGatedOperands[] = {
     {"out_bf16", RAD_OPD_OUT, 1},
 };
 
+/* rmsnorm_quant_fp8's schema (src/r3d_rows.cpp:700-716 of the reference). */
+const RadParamSpec kRmsParams[] = {
+    {"M", RAD_P_INT, RAD_REQUIRED, 0},
+    {"n", RAD_P_INT, RAD_REQUIRED, 0},
+    {"eps", RAD_P_F64, RAD_REQUIRED, 0},
+    {"group", RAD_P_INT, RAD_REQUIRED, 0},
+    {"dtype", RAD_P_STR, RAD_REQUIRED, 0},
+    {"wadd", RAD_P_F64, RAD_OPTIONAL, 0},
+};
+const RadOperandSpec kRmsOperands[] = {
+    {"x", RAD_OPD_IN, 0},
+    {"residual", RAD_OPD_INOUT, 1},
+    {"w", RAD_OPD_WEIGHT, 0},
+    {"q", RAD_OPD_OUT, 0},
+    {"scale", RAD_OPD_OUT, 0},
+    {"out_bf16", RAD_OPD_OUT, 1},
+};
+
 const RadOpSchema kSchemas[] = {
     {"gemm_nt_q", kGemmNtQParams, 8, kGemmNtQOperands, 7,
      "Y[M,N] = A[M,K] . dequant(B)[N,K]^T with block-scaled operands; `dtype` names the "
@@ -137,6 +157,10 @@ const RadOpSchema kSchemas[] = {
     {"gated_quant_fp8", kGatedParams, 5, kGatedOperands, 4,
      "silu(gate)*up or sigmoid(gate)*up (gate the first n columns of each row, up the next "
      "n), narrowed to bf16, then quant_act_fp8's quantiser, in one pass."},
+    {"rmsnorm_quant_fp8", kRmsParams, 6, kRmsOperands, 6,
+     "RMS norm (optionally after a residual add that is written back) and the fp8 group "
+     "quantiser in one pass over the row; the bf16 normed values are what the codes are "
+     "taken over, and out_bf16 carries them when present."},
 };
 
 /* the band rows' constraint (src/r3d_rows.cpp:1262-1265) */
@@ -178,6 +202,13 @@ const RadConstraint cFp8Gated[] = {
     {"K", RAD_C_DIV, 128, nullptr},
     {"group", RAD_C_EQ, 128, nullptr},
     {"act", RAD_C_IN, 0, "silu sigmoid"},
+};
+
+/* the rmsnorm producer's row (src/r3d_rows.cpp:1419-1423) */
+const RadConstraint cRmsQuant[] = {
+    {"n", RAD_C_DIV, 4, nullptr},
+    {"group", RAD_C_EQ, 128, nullptr},
+    {"dtype", RAD_C_IN, 0, "bf16"},
 };
 
 enum { kPrioTile = 1000, kPrioDecode = 1100 };
@@ -271,6 +302,17 @@ const RadKernelInfo kRows[] = {
      RAD_DOMAIN_DEVICE, kPrioTile, cBandMn, 2, nullptr, 0, nullptr,
      nullptr, nullptr, r3d_rad_gated_quant_fp8, nullptr, nullptr, nullptr, nullptr, nullptr},
 
+    {"rmsnorm_quant_fp8", "rmsnorm_quant_fp8", "quant",
+     "RMS norm and the fp8 group quantiser on gfx950: one workgroup of 256 lanes per row, the "
+     "row staged in LDS as bf16, the sum of squares folded in the reference's order (lane "
+     "strides of 256, 32-lane shuffle trees, eight partials in order), one wave per group",
+     "n <= 30720 (the row in LDS); w rank 1; with a residual the bf16-narrowed sum is stored "
+     "before the variance reads it; at most 65535 rows",
+     "bf16 in (and residual), f32/bf16 w, fp8_e4m3 codes with an f32 per-group scale, "
+     "optional bf16/f32 out_bf16",
+     RAD_DOMAIN_DEVICE, kPrioTile, cRmsQuant, 3, nullptr, 0, nullptr,
+     nullptr, nullptr, r3d_rad_rmsnorm_quant_fp8, nullptr, nullptr, nullptr, nullptr, nullptr},
+
     {"gemm_nt_q_gated_fp8a8", "gemm_nt_q_gated", "gemm",
      "the fp8a8 GEMM (decode GEMV up to M = 16, the prefill pipeline above) writing its bf16 "
      "gate_up plane into the launch scratch, closed by the gated_quant_fp8 kernels on the same "
@@ -307,7 +349,7 @@ const RadPluginInfo* rad_plugin_info(void) {
     static const RadPluginInfo info = {
         RAD_PLUGIN_KERNEL, "libr3d_gfx950", "0.1.0",
         "radiance gemm_nt_q rows (mxfp4a8, fp8a8, mxfp4a16), gemm_nt_q_gated (fp8a8) and the "
-        "quant_act_fp8 / gated_quant_fp8 producers for "
+        "quant_act_fp8 / gated_quant_fp8 / rmsnorm_quant_fp8 producers for "
         "AMD Instinct MI355X (CDNA4)",
         "gfx950",
     };

@@ -133,6 +133,29 @@ def gated_quant_fp8(gu, n=None, group=128, act="silu"):
     return q, sc, out
 
 
+def rmsnorm_quant_fp8(x, w, group=128, eps=1e-6, wadd=0.0, residual=None):
+    """x: bf16 bits uint16 [M, n]; w: bf16 bits uint16 or float32 [n]; residual: optional
+    bf16 bits [M, n] -> (codes uint8 [M, n], scale f32 [M, ceil(n/group)], normed bf16 bits
+    uint16 [M, n], residual after the call or None)."""
+    x = np.ascontiguousarray(x, np.uint16)
+    M, n = x.shape
+    w_bf16 = w.dtype == np.uint16
+    w = np.ascontiguousarray(w, np.uint16 if w_bf16 else np.float32)
+    ng = (n + group - 1) // group
+    q = np.empty((M, n), np.uint8)
+    sc = np.empty((M, ng), np.float32)
+    out = np.empty((M, n), np.uint16)
+    res = None if residual is None else np.array(residual, np.uint16, copy=True)
+    u16p = ctypes.POINTER(ctypes.c_uint16)
+    _lib().r3d_ref_rmsnorm_quant_fp8(
+        x.ctypes.data_as(u16p), _i64(M), _i64(n), _i64(n),
+        res.ctypes.data_as(u16p) if res is not None else None, _i64(n),
+        w.ctypes.data_as(ctypes.c_void_p), ctypes.c_int(int(w_bf16)), _i64(group),
+        ctypes.c_float(eps), ctypes.c_float(wadd), _p(q, _u8p), _i64(n), _p(sc, _f32p), _i64(ng),
+        out.ctypes.data_as(u16p), _i64(n))
+    return q, sc, out, res
+
+
 def quant_dot_mxfp4a8(A, AS, B, BS, nthreads=1):
     """-> (Y bf16 bits uint16 [M,N], Yf f32 accumulator, S f32 magnitude sum)."""
     A = np.ascontiguousarray(A, np.uint8)

@@ -25,6 +25,12 @@
  *                   quantises bf16(30 * up); both through quant_act_fp8 (gate/up order,
  *                   the act switch and the bf16 narrowing fail them when wrong); plus a
  *                   numpy evaluation (float64 exp) on random and special gates, and NaN.
+ *   rmsnorm_quant_fp8  integer-valued rows whose squares sum exactly in f32 in any order
+ *                   (so the fold order drops out) against a numpy float32 evaluation;
+ *                   the residual form equals the plain form on the written-back sum;
+ *                   a power-of-two constant row has the closed form rs = 1/sqrt(c^2+eps).
+ *                   The fold order itself is the reference kernel's, restated here and
+ *                   met bit for bit by the device kernel's real shuffles.
  *   quant_dot       float64 brute force within the bound 2*K*2^-24*S + ulp_bf16;
  *                   single-nonzero closed forms; K=32 / K=128 single-group forms;
  *                   power-of-two scale exactness (a_scale linearity); 0xFF scale
@@ -222,6 +228,67 @@ void r3d_ref_gated_quant_fp8(const void* gu, int gu_is_bf16, int64_t M, int64_t 
             }
         }
     }
+}
+
+/* rmsnorm_quant_fp8 (src/r3d_more.hip:241-330), in the reference kernel's arithmetic
+ * order: 256 lanes, lane t summing the squares of elements t, t+256, ... (multiply and add
+ * separately rounded: that file is built with -ffp-contract=off); each 32-lane warp folded
+ * by __shfl_down with offsets 16..1 (a lane whose source is past the warp adds its own
+ * value, as the intrinsic returns it); the 8 warp sums added in order; then
+ * rs = 1 / sqrtf(sum / n + eps).  With a residual, y = bf16(residual + x) is written back
+ * first and squared.  h = bf16((src * rs) * (w + wadd)); `out` (nullable) gets h's bits;
+ * quant_act_fp8's quantiser over each group of h. */
+void r3d_ref_rmsnorm_quant_fp8(const uint16_t* x, int64_t M, int64_t n, int64_t x_pitch,
+                               uint16_t* res, int64_t r_pitch, const void* w, int w_is_bf16,
+                               int64_t group, float eps, float wadd, uint8_t* q,
+                               int64_t q_pitch, float* scale, int64_t s_pitch, uint16_t* out,
+                               int64_t out_pitch) {
+    uint16_t* hs = (uint16_t*)malloc((size_t)n * sizeof(uint16_t));
+    if (!hs) return;
+    const int64_t ng = (n + group - 1) / group;
+    for (int64_t m = 0; m < M; ++m) {
+        const uint16_t* xr = x + m * x_pitch;
+        uint16_t* rr = res ? res + m * r_pitch : 0;
+        float lane[256];
+        for (int t = 0; t < 256; ++t) {
+            float ss = 0.0f;
+            for (int64_t i = t; i < n; i += 256) {
+                float v = r3d_ref_bf16_to_f32(xr[i]);
+                if (rr) {
+                    const uint16_t hb = r3d_ref_f32_to_bf16(r3d_ref_bf16_to_f32(rr[i]) + v);
+                    rr[i] = hb;
+                    hs[i] = hb;
+                    v = r3d_ref_bf16_to_f32(hb);
+                }
+                const float sq = v * v;
+                ss = ss + sq;
+            }
+            lane[t] = ss;
+        }
+        float warp[8];
+        for (int wv = 0; wv < 8; ++wv) {
+            float* l = lane + 32 * wv;
+            for (int off = 16; off > 0; off >>= 1) {
+                float nx[32];
+                for (int i = 0; i < 32; ++i) nx[i] = l[i] + (i + off < 32 ? l[i + off] : l[i]);
+                memcpy(l, nx, sizeof nx);
+            }
+            warp[wv] = l[0];
+        }
+        float r = warp[0];
+        for (int k = 1; k < 8; ++k) r = r + warp[k];
+        const float rs = 1.0f / sqrtf(r / (float)n + eps);
+        for (int64_t i = 0; i < n; ++i) {
+            const float src = rr ? r3d_ref_bf16_to_f32(hs[i]) : r3d_ref_bf16_to_f32(xr[i]);
+            const float wv = (w_is_bf16 ? r3d_ref_bf16_to_f32(((const uint16_t*)w)[i])
+                                        : ((const float*)w)[i]) + wadd;
+            const float t1 = src * rs;
+            hs[i] = r3d_ref_f32_to_bf16(t1 * wv);
+            if (out) out[m * out_pitch + i] = hs[i];
+        }
+        r3d_ref_quant_act_fp8(hs, 1, 1, n, n, group, q + m * q_pitch, n, scale + m * s_pitch, ng);
+    }
+    free(hs);
 }
 
 #ifdef _OPENMP

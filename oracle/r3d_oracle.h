@@ -59,6 +59,15 @@ void r3d_ref_gated_quant_fp8(const void* gu, int gu_is_bf16, int64_t M, int64_t 
                              int64_t q_pitch, float* scale, int64_t s_pitch, uint16_t* out,
                              int64_t out_pitch);
 
+/* rmsnorm_quant_fp8: x bf16 [M, n] (row pitch x_pitch); res (nullable) bf16 [M, n] updated
+ * with bf16(res + x); w [n] (bf16 when w_is_bf16, else f32); codes q [M, n], scales
+ * [M, ceil(n/group)]; out (nullable) the normed values' bf16 bits [M, n]. */
+void r3d_ref_rmsnorm_quant_fp8(const uint16_t* x, int64_t M, int64_t n, int64_t x_pitch,
+                               uint16_t* res, int64_t r_pitch, const void* w, int w_is_bf16,
+                               int64_t group, float eps, float wadd, uint8_t* q,
+                               int64_t q_pitch, float* scale, int64_t s_pitch, uint16_t* out,
+                               int64_t out_pitch);
+
 /* quant_dot at mxfp4a8.
  *   A  [M, K] e4m3 (pitch a_pitch bytes), AS [M, ceil(K/128)] f32 (pitch as_pitch)
  *   B  [N, K/2] packed e2m1, low nibble = even k (pitch K/2 bytes)

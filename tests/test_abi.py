@@ -35,7 +35,13 @@ def test_plugin_identity_and_schema():
     assert info.targets == b"gfx950" and info.kind == 1
     sch = R.schemas()
     assert [s["op"] for s in sch] == ["gemm_nt_q", "quant_act_fp8", "gemm_nt_q_gated",
-                                      "gated_quant_fp8"]
+                                      "gated_quant_fp8", "rmsnorm_quant_fp8"]
+    rq = sch[4]                             # src/r3d_rows.cpp:701-716, verbatim
+    assert [(p[0], p[1], p[2]) for p in rq["params"]] == [
+        ("M", 0, 0), ("n", 0, 0), ("eps", 2, 0), ("group", 0, 0), ("dtype", 1, 0), ("wadd", 2, 1)]
+    assert [(o[0], o[1], o[2]) for o in rq["operands"]] == [
+        ("x", 0, 0), ("residual", 2, 1), ("w", 3, 0), ("q", 1, 0), ("scale", 1, 0),
+        ("out_bf16", 1, 1)]
     gg, gq = sch[2], sch[3]                 # src/r3d_rows.cpp:215-230 and :626-637, verbatim
     assert [(p[0], p[2]) for p in gg["params"]] == [("M", 0), ("N", 0), ("K", 0), ("group", 0),
                                                     ("dtype", 0), ("act", 0)]
@@ -61,7 +67,11 @@ def test_rows_and_resolver():
     rows = {r["name"]: r for r in R.rows()}
     assert set(rows) == {"gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", "gemm_nt_q_fp8a8",
                          "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4a16", "quant_act_fp8_act",
-                         "gated_quant_fp8_act", "gemm_nt_q_gated_fp8a8"}
+                         "gated_quant_fp8_act", "gemm_nt_q_gated_fp8a8", "rmsnorm_quant_fp8"}
+    rq = lambda **kw: (R.resolve("rmsnorm_quant_fp8", kw) or {}).get("name")
+    assert rq(M=4, n=5376, eps=1e-6, group=128, dtype="bf16") == "rmsnorm_quant_fp8"
+    assert rq(M=4, n=5378, eps=1e-6, group=128, dtype="bf16") is None      # n DIV 4
+    assert rq(M=4, n=5376, eps=1e-6, group=64, dtype="bf16") is None
     gq = lambda **kw: (R.resolve("gated_quant_fp8", kw) or {}).get("name")
     assert gq(M=1, n=10752, group=128, dtype="bf16") == "gated_quant_fp8_act"
     assert gq(M=1, n=10752, group=128, dtype="f16") is None
@@ -107,22 +117,23 @@ A16 = "gemm_nt_q_mxfp4a16"
 QA = "quant_act_fp8_act"
 GQ = "gated_quant_fp8_act"
 GG = "gemm_nt_q_gated_fp8a8"
+RQ = "rmsnorm_quant_fp8"
 
 
 @pytest.mark.parametrize("env,expect", [
     ({}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG, "gemm_nt_q_mxfp4",
-          "gemm_nt_q_mxfp4_decode", A16, QA]),
-    ({"R3D_NO_MXFP4": "1"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG, QA]),
+          "gemm_nt_q_mxfp4_decode", A16, QA, RQ]),
+    ({"R3D_NO_MXFP4": "1"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG, QA, RQ]),
     ({"R3D_NO_FP4_DEC": "1"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG,
-                               "gemm_nt_q_mxfp4", A16, QA]),
-    ({"R3D_NO_FP8A8": "1"}, [GQ, "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
+                               "gemm_nt_q_mxfp4", A16, QA, RQ]),
+    ({"R3D_NO_FP8A8": "1"}, [GQ, "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA, RQ]),
     ({"R3D_NO_FP8_DEC": "1"}, [GQ, "gemm_nt_q_fp8a8", GG, "gemm_nt_q_mxfp4",
-                               "gemm_nt_q_mxfp4_decode", A16, QA]),
+                               "gemm_nt_q_mxfp4_decode", A16, QA, RQ]),
     ({"R3D_NO_FP8_DEC": "", "R3D_NO_FP4_DEC": "0"}, [GQ, "gemm_nt_q_fp8a8", GG,
-                                                     "gemm_nt_q_mxfp4", A16, QA]),
+                                                     "gemm_nt_q_mxfp4", A16, QA, RQ]),
     ({"R3D_MXFP4_Q8X": "0"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG,
-                              "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA]),
-    ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, [GQ, QA]),
+                              "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA, RQ]),
+    ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, [GQ, QA, RQ]),
 ])
 def test_kill_switch_matrix(env, expect):
     """Presence-tested levers hide rows at registration (the value does not matter: an
@@ -583,3 +594,46 @@ def test_gated_quant_plan_and_refusals():
     ops = _gq_ops()
     ops._t[2].shape[1] = 3                                   # too few scales
     assert R.describe(G, ops)[0] == R.RAD_E_SHAPE
+
+
+def _rms_ops(M=3, n=512, group=128, res=True, out=True, w_dt=np.float32, **kw):
+    x = FakeT(_aligned((M, n), np.uint16))
+    r = FakeT(_aligned((M, n), np.uint16)) if res else None
+    w = FakeT(_aligned((n,), w_dt))
+    q = FakeT(_aligned((M, n), np.uint8))
+    sc = FakeT(_aligned((M, (n + group - 1) // group), np.float32))
+    ob = FakeT(_aligned((M, n), np.uint16)) if out else None
+    return R.RmsNormQuantOperands(x, r, w, q, sc, ob, n=n, group=group, M=M, **kw)
+
+
+def test_rmsnorm_quant_plan_and_refusals():
+    """src/r3d_more.hip:482-521's gates: bf16 x (and residual), f32/bf16 w of rank 1, n at
+    most 30720, group clamped, eps / wadd from F64 params."""
+    G = "rmsnorm_quant_fp8"
+    rc, d = R.describe(G, _rms_ops(eps=1e-5, wadd=1.0))
+    g = _geom(d)
+    assert rc == R.RAD_OK and g["residual"] == "1" and g["ob"] == "bf16" and g["w"] == "f32", d
+    assert float(g["eps"]) == np.float32(1e-5) and float(g["wadd"]) == 1.0
+    g = _geom(R.describe(G, _rms_ops(res=False, out=False, w_dt=np.uint16))[1])
+    assert g["residual"] == "0" and g["ob"] == "none" and g["w"] == "bf16" and float(g["eps"]) == np.float32(1e-6)
+    g = _geom(R.describe(G, _rms_ops(n=300, group=1000))[1])
+    assert g["group"] == "300" and g["ngrp"] == "1"
+    assert R.describe(G, _rms_ops(n=30720))[0] == R.RAD_OK
+    assert R.describe(G, _rms_ops(n=30724))[0] == R.RAD_E_SHAPE
+    ops = _rms_ops()
+    ops._t[0].dtype = R.DT["F32"]
+    assert R.describe(G, ops)[0] == R.RAD_E_DTYPE                        # x must be bf16
+    ops = _rms_ops()
+    ops._t[1].dtype = R.DT["F32"]
+    assert R.describe(G, ops)[0] == R.RAD_E_DTYPE                        # residual bf16
+    ops = _rms_ops()
+    ops._t[2].rank = 2
+    ops._t[2].shape[0], ops._t[2].shape[1] = 1, 512
+    ops._t[2].stride[0], ops._t[2].stride[1] = 512, 1
+    assert R.describe(G, ops)[0] == R.RAD_E_STRIDE                       # w rank 1
+    ops = _rms_ops()
+    ops._t[3].data = None
+    assert R.describe(G, ops)[0] == R.RAD_E_INVAL
+    ops = _rms_ops()
+    ops.args.n_t = 4
+    assert R.describe(G, ops)[0] == R.RAD_E_INVAL                        # n_t < 5

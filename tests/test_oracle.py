@@ -242,6 +242,47 @@ def test_gated_quant_fp8_numpy_eval(act, f32_in):
     assert np.array_equal(q, qr) and np.array_equal(s.view(np.uint32), sr.view(np.uint32))
 
 
+# ------------------------------------------------------------------ rmsnorm_quant_fp8
+@pytest.mark.parametrize("w_bf16", [False, True])
+@pytest.mark.parametrize("n", [5376, 300, 30720])
+def test_rmsnorm_quant_fp8_exact_sums(n, w_bf16):
+    """Integer-valued rows in [-8, 8]: every square and partial sum is exact in f32, so the
+    sum (hence rs) is the same in any order; the oracle must then equal a numpy float32
+    evaluation of rs = 1/sqrt(ss/n + eps), h = bf16((x * rs) * (w + wadd)), and the
+    quantiser over h."""
+    rng = np.random.default_rng(n + w_bf16)
+    M = 3
+    xf = rng.integers(-8, 9, size=(M, n)).astype(np.float32)
+    x = synth.bf16_bits(xf)
+    wf = (1.0 + 0.25 * rng.standard_normal(n)).astype(np.float32)
+    w = synth.bf16_bits(wf) if w_bf16 else wf
+    wv = (O.bf16_to_f32(w) if w_bf16 else wf).astype(np.float32)
+    eps, wadd = np.float32(1e-6), np.float32(0.5)
+    q, s, out, _ = O.rmsnorm_quant_fp8(x, w, group=128, eps=float(eps), wadd=float(wadd))
+    ss = (xf.astype(np.float64) ** 2).sum(axis=1).astype(np.float32)   # exact
+    rs = np.float32(1.0) / np.sqrt(ss / np.float32(n) + eps, dtype=np.float32)
+    h = synth.bf16_bits((xf * rs[:, None]).astype(np.float32) * (wv + wadd))
+    assert np.array_equal(out, h)
+    qr, sr = O.quant_act_fp8(h, 128)
+    assert np.array_equal(q, qr) and np.array_equal(s, sr)
+
+
+def test_rmsnorm_quant_fp8_residual_and_closed_form():
+    rng = np.random.default_rng(4)
+    M, n = 2, 1024
+    x = synth.bf16_bits(rng.standard_normal((M, n)).astype(np.float32))
+    r0 = synth.bf16_bits(rng.standard_normal((M, n)).astype(np.float32))
+    w = synth.bf16_bits(np.ones(n, np.float32))
+    q, s, out, r1 = O.rmsnorm_quant_fp8(x, w, residual=r0)
+    assert np.array_equal(r1, synth.bf16_bits(O.bf16_to_f32(r0) + O.bf16_to_f32(x)))
+    q2, s2, out2, _ = O.rmsnorm_quant_fp8(r1, w)        # the plain form on the written sum
+    assert np.array_equal(q, q2) and np.array_equal(s, s2) and np.array_equal(out, out2)
+    # a constant row c = 2: ss = 4n exactly, rs = 1/sqrt(4 + eps) -> h = bf16(2 * rs)
+    xc = synth.bf16_bits(np.full((1, n), 2.0, np.float32))
+    _, _, oc, _ = O.rmsnorm_quant_fp8(xc, w, eps=0.0)
+    assert (O.bf16_to_f32(oc) == 1.0).all()
+
+
 # ------------------------------------------------------------------ quant_dot
 def _mx(M, N, K, seed, lo=115, hi=139):
     rng = np.random.default_rng(seed)
