@@ -344,6 +344,26 @@ def bench_quant(dev, stream, steps=50):
                                          "GBps": round(nb / t / 1e9, 1),
                                          "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
         log("[bench] quant_act_fp8 M=%d n=%d: %.2f us, %.1f GB/s" % (M, n, t * 1e6, nb / t / 1e9))
+        # rmsnorm_quant_fp8 on the same rows, with a residual and the bf16 normed output
+        r = torch.randn((M, n), device=dev, dtype=torch.float32).to(torch.bfloat16).view(torch.int16)
+        w = torch.ones(n, dtype=torch.float32, device=dev)
+        o = torch.empty((M, n), dtype=torch.int16, device=dev)
+        rops = R.RmsNormQuantOperands(x, r, w, q, s, o, n=n, group=g, M=M)
+        fr = R.row_launcher("rmsnorm_quant_fp8")
+        for _ in range(3):
+            assert fr(rops, stream) == 0
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fr(rops, stream)
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / steps
+        nb = M * n * 2 * 4 + n * 4 + M * n + M * (n // g) * 4    # x, residual in/out, out, w, q, s
+        res["rmsnorm_quant_fp8_M%d" % M] = {"n": n, "group": g, "kernel_us": round(t * 1e6, 2),
+                                             "GBps": round(nb / t / 1e9, 1)}
+        log("[bench] rmsnorm_quant_fp8 (+residual, +out) M=%d n=%d: %.2f us, %.1f GB/s"
+            % (M, n, t * 1e6, nb / t / 1e9))
     return res
 
 

@@ -317,17 +317,20 @@ __global__ __launch_bounds__(256) void gated_quant_fp8_vec_kernel(
 
 /* ---- rmsnorm_quant_fp8 (src/r3d_more.hip:241-330 of the reference), one workgroup of 256
  * lanes per row, the row's bf16 values staged in LDS:
- *   1. with a residual: y = bf16(residual + x) is stored back and squared; else x is.
- *      Lane t sums the squares of elements t, t + 256, ... in that order (separately
- *      rounded multiply and add: the reference builds this file without contraction);
- *      the 256 partials then fold exactly as the reference's 32-lane warps do -- a
- *      shuffle-down tree inside each 32-lane half (offsets 16, 8, 4, 2, 1), and the eight
- *      half sums added in order -- so the sum is bit-identical.
+ *   0. stage the row: with a residual, y = bf16(residual + x) is stored back and staged;
+ *      else x is staged (16-byte loads and stores when VEC, else element by element --
+ *      every load independent, so all are in flight together).
+ *   1. lane t sums the squares of staged elements t, t + 256, ... in that order (separately
+ *      rounded multiply and add: the reference builds this file without contraction); the
+ *      256 partials then fold exactly as the reference's 32-lane warps do -- a shuffle-down
+ *      tree inside each 32-lane half (offsets 16, 8, 4, 2, 1), and the eight half sums added
+ *      in order -- so the sum is bit-identical.
  *   2. rs = 1 / sqrt(sum / n + eps);  h = bf16((src * rs) * (w + wadd)), the normed value
- *      out_bf16 carries and the quantiser sees.
- *   3. quant_act_fp8's quantiser over each group of h (one wave per group here; the
- *      maximum is order-free). */
-template <bool WBF16>
+ *      out_bf16 carries and the quantiser sees (elementwise, any lane order).
+ *   3. quant_act_fp8's quantiser over each group of h: VQ -- groups of 8..512 tiling the
+ *      row -- L = g / 8 lanes per group, 8 values a lane, xor-shuffle maximum; else one wave
+ *      per group.  The maximum is order-free. */
+template <bool WBF16, bool VEC, int L>
 __global__ __launch_bounds__(256) void rmsnorm_quant_fp8_kernel(
     const uint16_t* __restrict__ x, int64_t x_pitch, uint16_t* __restrict__ res, int64_t r_pitch,
     const uint8_t* __restrict__ w, uint8_t* __restrict__ q, int64_t q_pitch,
@@ -340,15 +343,51 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_fp8_kernel(
     const int64_t row = blockIdx.x;
     const uint16_t* xr = x + row * x_pitch;
     uint16_t* rr = res ? res + row * r_pitch : nullptr;
+    auto bf = [](uint32_t b) { return __uint_as_float(b << 16); };
+    constexpr int U = 4;                        /* chunks a lane loads before using any */
+    const int nc = n >> 3;
+    if (VEC) {
+        for (int c0 = t; c0 < nc; c0 += 256 * U) {
+            r3d_i32x4 v[U], a[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + 256 * u < nc ? c0 + 256 * u : nc - 1;
+                v[u] = *reinterpret_cast<const r3d_i32x4*>(xr + 8 * c);
+                if (rr) a[u] = *reinterpret_cast<const r3d_i32x4*>(rr + 8 * c);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + 256 * u;
+                if (c >= nc) break;
+                if (rr) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t lo = r3d_band_bf16_bits(__fadd_rn(
+                            bf((uint32_t)a[u][i] & 0xFFFFu), bf((uint32_t)v[u][i] & 0xFFFFu)));
+                        const uint32_t hi = r3d_band_bf16_bits(__fadd_rn(
+                            bf((uint32_t)a[u][i] >> 16), bf((uint32_t)v[u][i] >> 16)));
+                        v[u][i] = (int)(lo | (hi << 16));
+                    }
+                    *reinterpret_cast<r3d_i32x4*>(rr + 8 * c) = v[u];
+                }
+                *reinterpret_cast<r3d_i32x4*>(s_h + 8 * c) = v[u];
+            }
+        }
+    } else {
+#pragma unroll 4
+        for (int i = t; i < n; i += 256) {
+            uint32_t hb = xr[i];
+            if (rr) {
+                hb = r3d_band_bf16_bits(__fadd_rn(bf(rr[i]), bf(hb)));
+                rr[i] = (uint16_t)hb;
+            }
+            s_h[i] = (uint16_t)hb;
+        }
+    }
+    __syncthreads();
     float ss = 0.0f;
     for (int i = t; i < n; i += 256) {
-        float v = __uint_as_float((uint32_t)xr[i] << 16);
-        if (rr) {
-            const uint32_t hb = r3d_band_bf16_bits(__fadd_rn(__uint_as_float((uint32_t)rr[i] << 16), v));
-            rr[i] = (uint16_t)hb;
-            s_h[i] = (uint16_t)hb;
-            v = __uint_as_float(hb << 16);
-        }
+        const float v = bf(s_h[i]);
         ss = __fadd_rn(ss, __fmul_rn(v, v));
     }
 #pragma unroll
@@ -362,34 +401,112 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_fp8_kernel(
     }
     __syncthreads();
     const float rs = s_rs;
-    for (int i = t; i < n; i += 256) {
-        const float src = rr ? __uint_as_float((uint32_t)s_h[i] << 16)
-                             : __uint_as_float((uint32_t)xr[i] << 16);
-        const float wv = __fadd_rn(WBF16 ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(w)[i] << 16)
-                                         : reinterpret_cast<const float*>(w)[i],
-                                   wadd);
-        const uint32_t h = r3d_band_bf16_bits(__fmul_rn(__fmul_rn(src, rs), wv));
-        if (ob) {
-            if (ob_bf16) reinterpret_cast<uint16_t*>(ob)[row * ob_pitch + i] = (uint16_t)h;
-            else reinterpret_cast<float*>(ob)[row * ob_pitch + i] = __uint_as_float(h << 16);
+    auto wval = [&](int i) {
+        return __fadd_rn(WBF16 ? bf(reinterpret_cast<const uint16_t*>(w)[i])
+                               : reinterpret_cast<const float*>(w)[i], wadd);
+    };
+    if (VEC) {
+        for (int c0 = t; c0 < nc; c0 += 256 * U) {
+            float wv[U][8];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {               /* the batch's w loads first */
+                const int c = c0 + 256 * u < nc ? c0 + 256 * u : nc - 1;
+                if (WBF16) {
+                    const r3d_i32x4 a = *reinterpret_cast<const r3d_i32x4*>(w + 16 * c);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        wv[u][2 * i] = bf((uint32_t)a[i] & 0xFFFFu);
+                        wv[u][2 * i + 1] = bf((uint32_t)a[i] >> 16);
+                    }
+                } else {
+                    const float4 a = *reinterpret_cast<const float4*>(w + 32 * c);
+                    const float4 b = *reinterpret_cast<const float4*>(w + 32 * c + 16);
+                    wv[u][0] = a.x; wv[u][1] = a.y; wv[u][2] = a.z; wv[u][3] = a.w;
+                    wv[u][4] = b.x; wv[u][5] = b.y; wv[u][6] = b.z; wv[u][7] = b.w;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + 256 * u;
+                if (c >= nc) break;
+                const r3d_i32x4 v = *reinterpret_cast<const r3d_i32x4*>(s_h + 8 * c);
+                r3d_i32x4 o;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t lo = r3d_band_bf16_bits(__fmul_rn(
+                        __fmul_rn(bf((uint32_t)v[i] & 0xFFFFu), rs), __fadd_rn(wv[u][2 * i], wadd)));
+                    const uint32_t hi = r3d_band_bf16_bits(__fmul_rn(
+                        __fmul_rn(bf((uint32_t)v[i] >> 16), rs), __fadd_rn(wv[u][2 * i + 1], wadd)));
+                    o[i] = (int)(lo | (hi << 16));
+                }
+                if (ob) {
+                    if (ob_bf16) {
+                        *reinterpret_cast<r3d_i32x4*>(ob + 2 * (row * ob_pitch + 8 * c)) = o;
+                    } else {
+                        float* of = reinterpret_cast<float*>(ob) + row * ob_pitch + 8 * c;
+                        *reinterpret_cast<float4*>(of) =
+                            make_float4(bf((uint32_t)o[0] & 0xFFFFu), bf((uint32_t)o[0] >> 16),
+                                        bf((uint32_t)o[1] & 0xFFFFu), bf((uint32_t)o[1] >> 16));
+                        *reinterpret_cast<float4*>(of + 4) =
+                            make_float4(bf((uint32_t)o[2] & 0xFFFFu), bf((uint32_t)o[2] >> 16),
+                                        bf((uint32_t)o[3] & 0xFFFFu), bf((uint32_t)o[3] >> 16));
+                    }
+                }
+                *reinterpret_cast<r3d_i32x4*>(s_h + 8 * c) = o;
+            }
         }
-        s_h[i] = (uint16_t)h;
+    } else {
+        for (int i = t; i < n; i += 256) {
+            const uint32_t h = r3d_band_bf16_bits(__fmul_rn(__fmul_rn(bf(s_h[i]), rs), wval(i)));
+            if (ob) {
+                if (ob_bf16) reinterpret_cast<uint16_t*>(ob)[row * ob_pitch + i] = (uint16_t)h;
+                else reinterpret_cast<float*>(ob)[row * ob_pitch + i] = bf(h);
+            }
+            s_h[i] = (uint16_t)h;
+        }
     }
     __syncthreads();
-    const int wave = t >> 6, lane = t & 63;
-    for (int gi = wave; gi < ngrp; gi += 4) {                 /* wave-uniform */
-        const int k0 = gi * g, len = n - k0 < g ? n - k0 : g;
-        float amax = 0.0f;
-        for (int i = lane; i < len; i += 64)
-            amax = fmaxf(amax, fabsf(__uint_as_float((uint32_t)s_h[k0 + i] << 16)));
+    if (L > 0) {
+        /* groups of 8 L values tiling the row: L lanes a group, 8 values a lane */
+        for (int c0 = t; c0 - t < nc; c0 += 256) {
+            const int c = c0 < nc ? c0 : nc - 1;
+            const r3d_i32x4 v = *reinterpret_cast<const r3d_i32x4*>(s_h + 8 * c);
+            float h[8];
+            float amax = 0.0f;
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-        const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
-        if (lane == 0) sc[row * s_pitch + gi] = s;
-        const float inv = 1.0f / s;
-        for (int i = lane; i < len; i += 64)
-            q[row * q_pitch + k0 + i] = (uint8_t)r3d_e4m3x2_rne(
-                r3d_band_clamp448(__uint_as_float((uint32_t)s_h[k0 + i] << 16) * inv), 0.0f);
+            for (int i = 0; i < 4; ++i) {
+                h[2 * i] = bf((uint32_t)v[i] & 0xFFFFu);
+                h[2 * i + 1] = bf((uint32_t)v[i] >> 16);
+                amax = fmaxf(amax, fmaxf(fabsf(h[2 * i]), fabsf(h[2 * i + 1])));
+            }
+#pragma unroll
+            for (int off = L / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            if (c0 >= nc) continue;
+            const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+            if ((c & (L - 1)) == 0) sc[row * s_pitch + c / L] = s;
+            const float inv = 1.0f / s;
+            float cv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cv[i] = r3d_band_clamp448(h[i] * inv);
+            *reinterpret_cast<uint2*>(q + row * q_pitch + 8 * c) =
+                make_uint2(r3d_e4m3x4_rne(cv[0], cv[1], cv[2], cv[3]),
+                           r3d_e4m3x4_rne(cv[4], cv[5], cv[6], cv[7]));
+        }
+    } else {
+        const int wave = t >> 6, lane = t & 63;
+        for (int gi = wave; gi < ngrp; gi += 4) {             /* wave-uniform */
+            const int k0 = gi * g, len = n - k0 < g ? n - k0 : g;
+            float amax = 0.0f;
+            for (int i = lane; i < len; i += 64) amax = fmaxf(amax, fabsf(bf(s_h[k0 + i])));
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+            if (lane == 0) sc[row * s_pitch + gi] = s;
+            const float inv = 1.0f / s;
+            for (int i = lane; i < len; i += 64)
+                q[row * q_pitch + k0 + i] = (uint8_t)r3d_e4m3x2_rne(
+                    r3d_band_clamp448(bf(s_h[k0 + i]) * inv), 0.0f);
+        }
     }
 }
 

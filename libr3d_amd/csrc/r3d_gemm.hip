@@ -390,13 +390,34 @@ static int rms_entry(const RadArgs* a, RadStream s) {
     if (!chip_ok()) return RAD_E_UNSUPPORTED;
     hipStream_t stream = (hipStream_t)s;
     const size_t lds = (size_t)((P.n * 2 + 15) / 16 * 16);
-#define R3D_RMS(W_)                                                                         \
-    hipLaunchKernelGGL((rmsnorm_quant_fp8_kernel<W_>), dim3((unsigned)P.rows), dim3(256), lds,  \
-                       stream, reinterpret_cast<const uint16_t*>(P.x), P.x_pitch,             \
-                       reinterpret_cast<uint16_t*>(P.res), P.r_pitch, P.w, P.q, P.q_pitch,    \
-                       P.scale, P.s_pitch, P.ob, P.ob_bf16, P.ob_pitch, (int)P.n, (int)P.g,   \
-                       (int)P.ngrp, P.eps, P.wadd)
-    if (P.w_bf16) R3D_RMS(true); else R3D_RMS(false);
+    const int ob_eb = P.ob_bf16 ? 2 : 4;
+    auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    /* 16-byte row walks: 8-element chunks tiling every row, aligned bases and pitches */
+    const bool vec = P.n % 8 == 0 && a16(P.x) && P.x_pitch % 8 == 0 &&
+                     (!P.res || (a16(P.res) && P.r_pitch % 8 == 0)) && a16(P.w) &&
+                     (!P.ob || (a16(P.ob) && (P.ob_pitch * ob_eb) % 16 == 0));
+    /* vector quantiser: groups of 8..512 tiling the row, 8-byte code stores */
+    const int lanes = (int)(P.g / 8);
+    const bool vq = vec && P.g % 8 == 0 && lanes >= 1 && lanes <= 64 &&
+                    (lanes & (lanes - 1)) == 0 && P.n % P.g == 0 &&
+                    ((uintptr_t)P.q % 8) == 0 && P.q_pitch % 8 == 0;
+#define R3D_RMS(W_, V_, L_)                                                                 \
+    hipLaunchKernelGGL((rmsnorm_quant_fp8_kernel<W_, V_, L_>), dim3((unsigned)P.rows),        \
+                       dim3(256), lds, stream, reinterpret_cast<const uint16_t*>(P.x),        \
+                       P.x_pitch, reinterpret_cast<uint16_t*>(P.res), P.r_pitch, P.w, P.q,    \
+                       P.q_pitch, P.scale, P.s_pitch, P.ob, P.ob_bf16, P.ob_pitch, (int)P.n,  \
+                       (int)P.g, (int)P.ngrp, P.eps, P.wadd)
+#define R3D_RMSL(W_)                                                                        \
+    if (!vec) { R3D_RMS(W_, false, 0); }                                                    \
+    else if (!vq) { R3D_RMS(W_, true, 0); }                                                 \
+    else switch (lanes) {                                                                   \
+        case 1: R3D_RMS(W_, true, 1); break;   case 2: R3D_RMS(W_, true, 2); break;         \
+        case 4: R3D_RMS(W_, true, 4); break;   case 8: R3D_RMS(W_, true, 8); break;         \
+        case 16: R3D_RMS(W_, true, 16); break; case 32: R3D_RMS(W_, true, 32); break;       \
+        default: R3D_RMS(W_, true, 64); break;                                              \
+    }
+    if (P.w_bf16) { R3D_RMSL(true) } else { R3D_RMSL(false) }
+#undef R3D_RMSL
 #undef R3D_RMS
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
