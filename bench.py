@@ -31,7 +31,7 @@ ROTATE_BYTES = 1.1 * 2 ** 30
 # script (--quick), FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 -- the factors a plain 256 MiB
 # device copy reads on the same counters (bench.py --copy-calib).  Re-measured whenever
 # the decode kernel changes; profiles/gemv_quad_fp8a8_c1_pmc_traffic.md has the numbers.
-HEADLINE_TRAFFIC_BYTES = 117731328
+HEADLINE_TRAFFIC_BYTES = 117642240
 
 
 def log(*a):
@@ -202,7 +202,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": HEADLINE_TRAFFIC_BYTES,
-                     "kernel": "r3d::gemv_quad_kernel<1, 1, 1, 4> (fp8a8, MT=1, one quad per wave, 4-step ring)",
+                     "kernel": "r3d::gemv_quad_kernel<1, 1, 1, 4, 0, 8> (fp8a8, MT=1, one quad per wave, 4-step ring, 8 waves a workgroup)",
                      "kernel_us": round(kern * 1e6, 3)},
     }
 

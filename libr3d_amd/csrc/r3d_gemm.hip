@@ -64,19 +64,24 @@ static void debug_once(const char* what, int key) {
 }
 
 static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream) {
-    const dim3 grid((unsigned)g.blocks), block(256);
+    const dim3 grid((unsigned)g.blocks), block((unsigned)(64 * g.wv));
     /* mxfp4 scale rows contiguous (pitch = K/32) in a 16-byte aligned plane: 1 KB staging loads */
     const int sc16 = P.enc == ENC_MXFP4A8 && P.bs_pitch == P.K / 32 &&
                      ((uintptr_t)P.BS & 15) == 0;
     if (P.xq && g.mt != 1) return RAD_E_UNSUPPORTED;    /* the fused producer is MT = 1 only */
-#define R3D_QUAD1(ENC_, MT_, Q_, D_, X_)                                                    \
-    hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, Q_, D_, X_>), grid, block, (size_t)g.lds, \
+    if ((g.wv != 4 && g.wv != 8) || (g.qpw == 2 && g.wv != 4)) return RAD_E_UNSUPPORTED;
+#define R3D_QUAD1(ENC_, MT_, Q_, D_, X_) R3D_QUADW(ENC_, MT_, Q_, D_, X_, 4)
+#define R3D_QUADW(ENC_, MT_, Q_, D_, X_, W_)                                                \
+    hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, Q_, D_, X_, W_>), grid, block,          \
+                       (size_t)g.lds,                                                        \
                        stream, P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K,       \
                        g.chunks, P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, sc16,        \
                        P.a_pitch, P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch)
 #define R3D_QUAD(ENC_, MT_, D_)                                                              \
-    if (P.xq) R3D_QUAD1(ENC_, MT_, 1, D_, (MT_ == 1));                                       \
+    if (P.xq && g.wv == 8) R3D_QUADW(ENC_, MT_, 1, D_, (MT_ == 1), 8);                       \
+    else if (P.xq) R3D_QUAD1(ENC_, MT_, 1, D_, (MT_ == 1));                                  \
     else if (g.qpw == 2) R3D_QUAD1(ENC_, MT_, 2, D_, 0);                                     \
+    else if (g.wv == 8) R3D_QUADW(ENC_, MT_, 1, D_, 0, 8);                                   \
     else R3D_QUAD1(ENC_, MT_, 1, D_, 0)
 #define R3D_QUAD_D(ENC_, MT_)                                                                \
     do {                                                                                     \
@@ -97,6 +102,7 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
 #undef R3D_QUAD_D
 #undef R3D_QUAD
 #undef R3D_QUAD1
+#undef R3D_QUADW
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         fprintf(stderr, "libr3d_gfx950: quad decode GEMV launch FAILED (%s)\n", hipGetErrorName(e));

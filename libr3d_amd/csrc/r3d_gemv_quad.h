@@ -8,7 +8,8 @@
  * direct global->LDS loads issued before the ring is primed.
  *
  * Work split: one wave owns a quad (4 consecutive weight rows) and one contiguous chunk of
- * the 128-wide K groups; a workgroup is 4 waves = (4 / chunks) quads x chunks, so every
+ * the 128-wide K groups; a workgroup is WV (4 or 8) waves = (WV / chunks) quads x chunks --
+ * eight halve the staging bytes per weight row -- so every
  * chunk of a quad sits in the same workgroup and the partials fold through LDS in a fixed
  * order (deterministic).
  *
@@ -100,8 +101,8 @@ __device__ __forceinline__ void r3d_quad_dma(const void* g, uint32_t lds) {
 }
 #pragma clang diagnostic pop
 
-template <int ENC, int MT, int QPW, int D, int XQ = 0>
-__global__ __launch_bounds__(256) void gemv_quad_kernel(
+template <int ENC, int MT, int QPW, int D, int XQ = 0, int WV = 4>
+__global__ __launch_bounds__(64 * WV) void gemv_quad_kernel(
     const uint8_t* A, const float* AS, const uint8_t* B, const void* BSv,
     uint16_t* __restrict__ Y,
     int M, int N, int K, int chunks, int rblk, int gmax, int xs_off, int sc_off, int sc_bytes,
@@ -114,7 +115,7 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int groups = K >> 7;
-    const int bpb = 4 / chunks;                           /* row blocks per workgroup */
+    const int bpb = WV / chunks;                          /* row blocks per workgroup */
     const int bi = wave / chunks, c = wave % chunks;
     const int64_t n0 = ((int64_t)blockIdx.x * bpb + bi) * RB;
     const int g0 = (int)((int64_t)groups * c / chunks);
@@ -139,13 +140,13 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
             /* the workgroup's rows are one contiguous, 16-byte aligned run of the plane:
              * 1 KB per load (lanes past the run reload its last 16 bytes into padding) */
             const int blk = rbw * 4 * groups;
-            for (int i = wave; i < (sc_bytes >> 10); i += 4) {
+            for (int i = wave; i < (sc_bytes >> 10); i += WV) {
                 const int o = 1024 * i + 16 * lane < blk - 16 ? 1024 * i + 16 * lane : blk - 16;
                 r3d_quad_dma<16>(BS8 + wn0 * bs_pitch + o, scl + 1024 * i);
             }
         } else {
             const int nd = rbw * groups;                  /* dwords */
-            for (int h = wave; h < (sc_bytes >> 8); h += 4) {
+            for (int h = wave; h < (sc_bytes >> 8); h += WV) {
                 int e = lane + 64 * h;
                 if (e > nd - 1) e = nd - 1;
                 const int r = e / groups, d = e - r * groups;
@@ -165,11 +166,11 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
         }
     }
     /* ... then the workgroup's activation rows ([MT][K + 16] bytes, whole K) and a_scales
-     * ([MT][groups] f32), shared by its 4 waves (XQ: quantised here, below) */
+     * ([MT][groups] f32), shared by its WV waves (XQ: quantised here, below) */
     if (!XQ) {
         const int xp = K + 16;
         const int nx = (MT * xp + 1023) >> 10;
-        for (int i = wave; i < nx; i += 4) {
+        for (int i = wave; i < nx; i += WV) {
             const int b = 1024 * i + 16 * lane;
             int t = b / xp, k = b - t * xp;
             if (t > MT - 1) { t = MT - 1; k = K - 16; }
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
             r3d_quad_dma<16>(A + (int64_t)tm * a_pitch + k, lds0 + 1024 * i);
         }
         const int nxs = (MT * groups + 63) >> 6;
-        for (int h = wave; h < nxs; h += 4) {
+        for (int h = wave; h < nxs; h += WV) {
             const int e = lane + 64 * h;
             int t = e / groups, g = e - t * groups;
             if (t > MT - 1) { t = MT - 1; g = groups - 1; }
@@ -244,7 +245,7 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
     auto xq_load = [&](int batch) {
 #pragma unroll
         for (int u = 0; u < XU; ++u) {
-            const int c0 = 64 * (wave + 4 * (batch * XU + u)) + lane;
+            const int c0 = 64 * (wave + WV * (batch * XU + u)) + lane;
             const int c = c0 < nchunk ? c0 : nchunk - 1;
             const int t = c / cpr, k = 8 * (c - t * cpr);
             const int tm = t < M ? t : M - 1;
@@ -255,7 +256,7 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
         float* xst = reinterpret_cast<float*>(smem + xs_off);
 #pragma unroll
         for (int u = 0; u < XU; ++u) {
-            const int c = 64 * (wave + 4 * (batch * XU + u)) + lane;
+            const int c = 64 * (wave + WV * (batch * XU + u)) + lane;
             float v[8];
             float amax = 0.0f;
 #pragma unroll
@@ -294,7 +295,7 @@ __global__ __launch_bounds__(256) void gemv_quad_kernel(
     if (XQ) {
         for (int b = 0;;) {
             xq_store(b);
-            if (++b * 4 * XU >= nxb) break;
+            if (++b * WV * XU >= nxb) break;
             xq_load(b);
         }
         /* the quantised rows are this wave's LDS writes: publish them with the staging */

@@ -328,7 +328,14 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     }
     while (c > 1 && c > g->groups) c >>= 1;
     g->chunks = c;
-    g->bpb = 4 / c;
+    /* eight waves share one activation staging: measured on MI355X, a gain at MT = 4 (the
+     * staging is four rows; 2-4 % on config 2/4 shapes) and for fp8a8 at MT = 1 without a
+     * K split (1.5 % at config 1), a loss for mxfp4a8 at MT = 1 (the long-K split shape
+     * most: 13.2 -> 15.5 us); two quads a wave keep four waves */
+    const int wv_env = env_quad_wv();
+    g->wv = g->qpw == 2 ? 4 : wv_env ? wv_env
+          : (g->mt == 4 || (enc == ENC_FP8A8 && c == 1)) ? 8 : 4;
+    g->bpb = g->wv / c;
     g->blocks = (g->nblk + g->bpb - 1) / g->bpb;
     g->gmax = (g->groups + c - 1) / c;
     {
@@ -347,7 +354,9 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     const int64_t rbw = 4 * (int64_t)g->qpw * g->bpb;
     const int64_t scb = enc == ENC_MXFP4A8 ? (rbw * 4 * g->groups + 1023) / 1024 * 1024
                                            : (16 * g->qpw * (int64_t)g->gmax + 255) / 256 * 256;
-    const int64_t lds = blob + xs + (enc == ENC_MXFP4A8 ? scb : 4 * scb);
+    int64_t lds = blob + xs + (enc == ENC_MXFP4A8 ? scb : (int64_t)g->wv * scb);
+    const int64_t fold = (int64_t)g->wv * g->qpw * 256;   /* the fold reuses the blob's start */
+    if (lds < fold) lds = fold;
     if (lds > kQuadMaxLds || g->blocks > 0x7FFFFFFF) return false;
     g->xs_off = (int)blob;
     g->sc_off = (int)(blob + xs);
@@ -720,6 +729,15 @@ int env_quad_qpw() {
     return v;
 }
 
+int env_quad_wv() {
+    static const int v = [] {
+        const char* e = getenv("R3D_GFX950_QWV");
+        const int w = e ? atoi(e) : 0;
+        return w == 4 || w == 8 ? w : 0;
+    }();
+    return v;
+}
+
 int64_t env_lines_waves() {
     static const int64_t v = [] {
         const char* e = getenv("R3D_GFX950_LWAVES");
@@ -830,8 +848,9 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
     if (dec && quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &qg)) {
         snprintf(buf, (size_t)len,
                  "arm=decode kernel=quad enc=%s M=%lld N=%lld K=%lld mt=%d qpw=%d chunks=%d "
-                 "waves=4 quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d xq=%d",
+                 "waves=%d quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d xq=%d",
                  ename, (long long)P.M, (long long)P.N, (long long)P.K, qg.mt, qg.qpw, qg.chunks,
+                 qg.wv,
                  (long long)qg.quads, (long long)qg.blocks, qg.groups, qg.depth, qg.lds, P.rblk,
                  P.xq);
     } else if (dec && P.xq) {

@@ -58,8 +58,9 @@ struct DecodeGeom {
 struct QuadGeom {
     int mt;                  /* activation rows of the instantiation: 1 or 4 */
     int qpw;                 /* quads per wave: 1 or 2 */
+    int wv;                  /* waves per workgroup: 4 or 8 */
     int chunks;              /* waves per row block (split-K): 1, 2 or 4 */
-    int bpb;                 /* row blocks per workgroup: 4 / chunks */
+    int bpb;                 /* row blocks per workgroup: wv / chunks */
     int groups;              /* K / 128 */
     int gmax;                /* most groups one chunk holds: ceil(groups / chunks) */
     int depth;               /* ring depth in K steps (<= every wave's step count) */
@@ -217,6 +218,7 @@ int64_t env_splitk();       /* R3D_GFX950_SPLITK: force the decode chunk count (
 int64_t env_quad_waves();   /* R3D_GFX950_QWAVES: waves the quad split aims for (default 2048) */
 int env_quad_depth(int enc);/* R3D_GFX950_QD: quad ring depth 1/2/4/8 (default 4) */
 int env_quad_qpw();         /* R3D_GFX950_QPW: quads per wave of the quad GEMV, 1 or 2 (default 1) */
+int env_quad_wv();          /* R3D_GFX950_QWV: waves per quad-GEMV workgroup, 4 or 8 (0: policy) */
 int64_t env_lines_waves();  /* R3D_GFX950_LWAVES: waves the line GEMV's split aims for (default 4096) */
 int env_lines_depth();      /* R3D_GFX950_LD: line GEMV ring depth in units, 1/2/4 (0 = policy) */
 int env_lines_tw();         /* R3D_GFX950_LTW: 16-row tiles per wave of the line GEMV (0 = policy) */

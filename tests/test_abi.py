@@ -242,6 +242,14 @@ def test_decode_geometry_policy():
         assert rc == R.RAD_OK, d
         g = _geom(d)
         assert g["kernel"] == kern and g["chunks"] == chunks, (M, N, K, d)
+    # waves per quad workgroup: 8 at MT = 4 and for fp8a8 at MT = 1 without a K split
+    for (mk, M, N, K, wv) in [(_mx_ops, 1, 21504, 5376, "4"), (_mx_ops, 4, 21504, 5376, "8"),
+                              (_f8_ops, 1, 21504, 5376, "8"), (_f8_ops, 1, 4096, 4096, "4"),
+                              (_f8_ops, 3, 2048, 5376, "8")]:
+        ops, _ = mk(M=M, N=N, K=K)
+        rc, d = R.describe("gemm_nt_q_mxfp4_decode" if mk is _mx_ops else
+                           "gemm_nt_q_fp8a8_decode", ops)
+        assert rc == R.RAD_OK and _geom(d)["waves"] == wv, (M, N, K, d)
     ops, _ = _mx_ops(M=1, N=21504, K=5376, tunables=[("splitk", 2)])
     g = _geom(R.describe("gemm_nt_q_mxfp4_decode", ops)[1])
     assert g["kernel"] == "quad" and g["chunks"] == "2"
