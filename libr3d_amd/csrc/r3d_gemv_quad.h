@@ -233,8 +233,8 @@ __global__ __launch_bounds__(64 * WV) void gemv_quad_kernel(
      * group is 16 consecutive chunks, i.e. 16 lanes, reduced by 4 xor-shuffles.  Wave w
      * takes blocks w, w + 4, ...; XU blocks per batch, the first batch's loads issued
      * before the weight ring is primed (so waiting for them never waits for weights).  One
-     * batch covers K <= 8192; a longer K takes more batches, whose loads wait behind the
-     * ring's.  MT = 1 only: every workgroup re-reads the bf16 rows (twice the bytes of the
+     * batch covers K <= 2048 * WV; a longer K takes more batches, whose loads wait behind
+     * the ring's.  MT = 1 only: every workgroup re-reads the bf16 rows (twice the bytes of the
      * e4m3 images) and re-quantises them, which at MT = 4 costs more than the separate
      * producer launch it saves. */
     static_assert(!XQ || MT == 1, "the fused producer is built for one activation row");
