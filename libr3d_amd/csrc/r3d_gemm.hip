@@ -194,6 +194,21 @@ static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) 
  * weights, PF_F8 the same activations against e4m3 weights with bf16 row scales, PF_MX8 the
  * mxfp8 planes the quantiser left in P.scratch. */
 static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
+    /* the skinny band on a narrow N: 16-row passes of the decode GEMVs (each output row is
+     * the same arithmetic either way) */
+    if (const int passes = skinny_passes(P.enc, P.M, P.N, cu_count())) {
+        for (int p = 0; p < passes; ++p) {
+            GemmPlan S = P;
+            const int64_t m0 = 16 * (int64_t)p;
+            S.M = P.M - m0 < 16 ? P.M - m0 : 16;
+            S.A = P.A + m0 * P.a_pitch;
+            S.AS = P.AS + m0 * P.as_pitch;
+            S.Y = P.Y + m0 * P.y_pitch;
+            const int rc = launch_decode(S, 0, stream);
+            if (rc) return rc;
+        }
+        return RAD_OK;
+    }
     const int mode = P.enc == ENC_MXFP4A16 ? PF_MX8 : P.enc == ENC_FP8A8 ? PF_F8 : PF_A8;
     PrefillGeom g{};
     prefill_geom(P.M, P.N, P.K, mode, cu_count(), &g);

@@ -462,6 +462,15 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
     g->lds = g->nst * prefill_stage_bytes(g->wnf, g->wmf, mode == PF_F8 ? 2 : 1);
 }
 
+int skinny_passes(int enc, int64_t M, int64_t N, int ncu) {
+    if ((enc != ENC_MXFP4A8 && enc != ENC_FP8A8) || M < 17 || M > 64) return 0;
+    if (ncu <= 0) ncu = 256;
+    const int64_t tiles = (N + 127) / 128;            /* the narrow (128 x 128) prefill tile */
+    const int64_t act = tiles < ncu ? tiles : ncu;
+    const int passes = (int)((M + 15) / 16);
+    return passes * act < 200 ? passes : 0;
+}
+
 int band_row_pitch(const RadTensor* t, int64_t cols, int64_t* pitch) {
     if (!t || !t->data) return -1;
     if (t->rank == 1) {
@@ -874,6 +883,10 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
                  ename, (long long)P.M, (long long)P.N, (long long)P.K,
                  g.mt, g.chunks, g.waves, (long long)g.tiles, (long long)g.blocks, g.steps,
                  P.rblk);
+    } else if (const int passes = skinny_passes(P.enc, P.M, P.N, 256)) {
+        snprintf(buf, (size_t)len,
+                 "arm=skinny enc=%s M=%lld N=%lld K=%lld passes=%d (16-row decode GEMV passes)",
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K, passes);
     } else {
         const int mode = a16 ? PF_MX8 : mx ? PF_A8 : PF_F8;
         PrefillGeom g{};

@@ -141,6 +141,13 @@ bool lines_fits(const GemmPlan& P);
  * workgroups is as full as possible). */
 void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeom* g);
 
+/* The skinny band (M = 17..64) on the tile rows: the number of 16-row passes of the decode
+ * GEMVs to run instead of the prefill pipeline, or 0.  The prefill tile spans 128 weight
+ * rows, so a narrow N leaves most CUs idle on a weight-bound problem (measured per active
+ * tile ~12.5 GB/s), while each line-GEMV pass streams the whole plane at ~2.5 TB/s: passes
+ * win while passes x min(tiles, CUs) < 200. */
+int skinny_passes(int enc, int64_t M, int64_t N, int ncu);
+
 /* The band rows' operand walk (src/r3d_band.hip:419-449 of the reference): a rank-1 tensor
  * of exactly `cols` unit-stride elements is one row read by every row (pitch 0); rank 2
  * needs a unit inner stride and pitches by stride[0] when shape[1] == cols, else reads flat

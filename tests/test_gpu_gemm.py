@@ -156,14 +156,17 @@ def test_fp8_decode_shapes(gpu, N, K, rblk):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 128, 128), (17, 200, 256), (64, 256, 512),
-                                   (130, 300, 384), (256, 512, 1024)])
+                                   (130, 300, 384), (256, 512, 1024),
+                                   (48, 1000, 4096), (63, 520, 2048),   # skinny: 16-row passes
+                                   (32, 21504, 512)])                   # skinny, wide N: prefill
 def test_mxfp4_tile(gpu, M, N, K):
     A, AS, B, BS = _mx_case(M, N, K, 7 * M + N)
     _check(MX_TILE, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 128, 128), (17, 200, 256), (130, 300, 384),
-                                   (300, 1000, 1152), (257, 129, 640), (64, 520, 4096)])
+                                   (300, 1000, 1152), (257, 129, 640), (64, 520, 4096),
+                                   (40, 1000, 2048), (32, 21504, 512)])
 @pytest.mark.parametrize("rblk", [1, 128])
 def test_fp8_tile(gpu, M, N, K, rblk):
     A, AS, B, BS = _f8_case(M, N, K, 11 * M + N, rblk)
