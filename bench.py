@@ -265,6 +265,7 @@ def main():
         extra.update(bench_quant(dev, stream))
         extra.update(bench_fused_decode(dev, stream, ksteps))
         extra.update(bench_gated(dev, stream, ksteps))
+        extra.update(bench_skinny(dev, stream, ksteps))
         extra.update(bench_c4(dev, stream, steps=5))
     if extra:
         out["extra"] = extra
@@ -496,6 +497,32 @@ def bench_gated(dev, stream, steps=50):
         log("[bench] gated fp8a8 M=%d: row %.2f us, gemm_nt_q + gated_quant_fp8 %.2f us "
             "(producer alone %.2f us)" % (M, t1 * 1e6, t2 * 1e6, tp * 1e6))
     del bs, bss
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_skinny(dev, stream, steps=50):
+    """The skinny band (M = 17..64) on the mxfp4a8 tile row at config 2's shapes, cold: the
+    row's own dispatch (16-row decode passes on a narrow N, else the prefill pipeline)."""
+    import torch
+    import libr3d_amd as R
+    from libr3d_amd import synth
+    res = {}
+    for name, (K, N) in (("gate_up", (5376, 21504)), ("down", (21504, 5376)),
+                         ("qkv", (5376, 8192))):
+        B, BS = synth.mxfp4_weights(N, K, 0x5EED + 21 + K)
+        for M in (17, 32, 64):
+            _, A, AS = synth.activations(M, K, 0x5EED + 50 + M)
+            c = Case("mxfp4a8", A, AS, B, BS, M, N, K, copies_for(B.nbytes + BS.nbytes), dev)
+            wall, kern = time_case(c, "gemm_nt_q_mxfp4", steps, 10, stream)
+            nb = mx_bytes(M, N, K)
+            arm = R.describe("gemm_nt_q_mxfp4", c.ops[0])[1].split()[0]
+            res["skinny_mxfp4_%s_M%d" % (name, M)] = {
+                "K": K, "N": N, "us": round(kern * 1e6, 2), "GBps": round(nb / kern / 1e9, 1),
+                "frac_hbm": round(nb / kern / 1e9 / HBM_PEAK_GBS, 4), "arm": arm}
+            log("[bench] skinny %s M=%d: %.2f us, %.1f GB/s (%s)" % (name, M, kern * 1e6,
+                                                                  nb / kern / 1e9, arm))
+            del c
     torch.cuda.empty_cache()
     return res
 
