@@ -113,8 +113,11 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
     return RAD_OK;
 }
 
-static int launch_lines(const GemmPlan& P, const LinesGeom& g, hipStream_t stream) {
-    const dim3 grid((unsigned)g.blocks), block(256);
+/* passes > 1: P.M = 17..64 rows in 16-row passes side by side (grid.y), each pass exactly a
+ * 16-row call's arithmetic; g is the 16-row geometry */
+static int launch_lines(const GemmPlan& P, const LinesGeom& g, hipStream_t stream,
+                        int passes = 1) {
+    const dim3 grid((unsigned)g.blocks, (unsigned)passes), block(256);
 #define R3D_LINES(ENC_, MT_, TW_, D_)                                                        \
     hipLaunchKernelGGL((gemv_lines_kernel<ENC_, MT_, TW_, D_>), grid, block, (size_t)g.lds,    \
                        stream, P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K,        \
@@ -197,6 +200,11 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
     /* the skinny band on a narrow N: 16-row passes of the decode GEMVs (each output row is
      * the same arithmetic either way) */
     if (const int passes = skinny_passes(P.enc, P.M, P.N, cu_count())) {
+        GemmPlan S = P;
+        S.M = 16;
+        LinesGeom lg{};
+        if (lines_fits(S) && lines_geom(P.enc, 16, P.N, P.K, 0, &lg) && lg.mt == 16)
+            return launch_lines(P, lg, stream, passes);      /* all passes in one launch */
         for (int p = 0; p < passes; ++p) {
             GemmPlan S = P;
             const int64_t m0 = 16 * (int64_t)p;

@@ -78,6 +78,15 @@ __global__ __launch_bounds__(256) void gemv_lines_kernel(
     constexpr int LPU = 2 * TW + G * (MT == 16 ? 2 : 1);   /* loads per unit */
     constexpr int RW = 16 * TW;                            /* weight rows per wave */
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    /* grid.y > 1 (the skinny band): workgroup row y computes activation rows
+     * [16 y, 16 y + 16) of a taller A -- the same arithmetic as a 16-row call */
+    {
+        const int m0 = 16 * (int)blockIdx.y;
+        A += m0 * a_pitch;
+        AS += m0 * as_pitch;
+        Y += m0 * y_pitch;
+        M = M - m0 < 16 ? M - m0 : 16;
+    }
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

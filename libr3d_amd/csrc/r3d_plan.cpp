@@ -464,11 +464,16 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
 
 int skinny_passes(int enc, int64_t M, int64_t N, int ncu) {
     if ((enc != ENC_MXFP4A8 && enc != ENC_FP8A8) || M < 17 || M > 64) return 0;
+    static const int lever = [] {
+        const char* e = getenv("R3D_GFX950_SKINNY");
+        return e ? (atoi(e) ? 1 : 0) : -1;
+    }();
+    if (lever >= 0) return lever ? (int)((M + 15) / 16) : 0;
     if (ncu <= 0) ncu = 256;
     const int64_t tiles = (N + 127) / 128;            /* the narrow (128 x 128) prefill tile */
     const int64_t act = tiles < ncu ? tiles : ncu;
     const int passes = (int)((M + 15) / 16);
-    return passes * act < 200 ? passes : 0;
+    return passes * act < 300 ? passes : 0;
 }
 
 int band_row_pitch(const RadTensor* t, int64_t cols, int64_t* pitch) {

@@ -143,9 +143,11 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
 
 /* The skinny band (M = 17..64) on the tile rows: the number of 16-row passes of the decode
  * GEMVs to run instead of the prefill pipeline, or 0.  The prefill tile spans 128 weight
- * rows, so a narrow N leaves most CUs idle on a weight-bound problem (measured per active
- * tile ~12.5 GB/s), while each line-GEMV pass streams the whole plane at ~2.5 TB/s: passes
- * win while passes x min(tiles, CUs) < 200. */
+ * rows, so a narrow N leaves most CUs idle on a weight-bound problem (~12.5 GB/s per active
+ * tile, measured), while the line GEMV runs the passes side by side in one launch (the
+ * repeated weight reads mostly hit the caches): passes win while
+ * passes x min(tiles, CUs) < 300 (measured on MI355X at config 2's shapes).
+ * R3D_GFX950_SKINNY=0 / 1 turns the passes off / on for every skinny shape. */
 int skinny_passes(int enc, int64_t M, int64_t N, int ncu);
 
 /* The band rows' operand walk (src/r3d_band.hip:419-449 of the reference): a rank-1 tensor

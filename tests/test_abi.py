@@ -221,14 +221,15 @@ def test_mt_ladder_rounds_up(M, mt):
 
 def test_decode_band_bound_and_tile_any_m():
     """The decode rows stop at M = 16; the tile rows take any M: the skinny band (17..64)
-    on a narrow N runs 16-row decode-GEMV passes while passes x min(tiles, 256) < 200, the
+    on a narrow N runs 16-row decode-GEMV passes while passes x min(tiles, 256) < 300, the
     rest the prefill pipeline."""
     ops, _ = _mx_ops(M=17)
     assert R.describe("gemm_nt_q_mxfp4_decode", ops)[0] == R.RAD_E_UNSUPPORTED
     for mk, row in ((_mx_ops, "gemm_nt_q_mxfp4"), (_f8_ops, "gemm_nt_q_fp8a8")):
         for M, N, K, arm, passes in [(17, 64, 256, "skinny", "2"), (64, 5376, 21504, "skinny", "4"),
                                      (48, 8192, 5376, "skinny", "3"),
-                                     (64, 8192, 5376, "prefill", None),
+                                     (64, 8192, 5376, "skinny", "4"),
+                                     (17, 21504, 5376, "prefill", None),
                                      (32, 21504, 5376, "prefill", None),
                                      (65, 5376, 21504, "prefill", None)]:
             rc, d = R.describe(row, mk(M=M, N=N, K=K)[0])
