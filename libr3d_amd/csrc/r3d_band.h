@@ -182,6 +182,49 @@ __global__ __launch_bounds__(256) void quant_act_fp8_vec_kernel(
     }
 }
 
+/* Few rows (decode): the same quantiser with one 8-element chunk per lane on a
+ * (ceil(chunks / 256), rows) grid, so a row spreads over workgroups instead of one
+ * workgroup walking it. */
+template <bool BF16, int L>
+__global__ __launch_bounds__(256) void quant_act_fp8_spread_kernel(
+    const uint8_t* __restrict__ x, int64_t x_pitch, uint8_t* __restrict__ q, int64_t q_pitch,
+    float* __restrict__ sc, int64_t s_pitch, int64_t n) {
+    const int64_t row = blockIdx.y;
+    const int64_t chunks = n >> 3;
+    const uint8_t* xr = x + row * x_pitch * (BF16 ? 2 : 4);
+    const int64_t c0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t c = c0 < chunks ? c0 : chunks - 1;   /* past the end: re-read, store nothing */
+    float v[8];
+    if (BF16) {
+        const r3d_i32x4 w = *reinterpret_cast<const r3d_i32x4*>(xr + 16 * c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float((uint32_t)w[i] << 16);
+            v[2 * i + 1] = __uint_as_float((uint32_t)w[i] & 0xFFFF0000u);
+        }
+    } else {
+        const float4 a = *reinterpret_cast<const float4*>(xr + 32 * c);
+        const float4 b = *reinterpret_cast<const float4*>(xr + 32 * c + 16);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if (c0 >= chunks) return;
+    const float s = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
+    const float inv = 1.0f / s;
+    if ((c & (L - 1)) == 0) sc[row * s_pitch + c / L] = s;
+    float cv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cv[i] = r3d_band_clamp448(v[i] * inv);
+    *reinterpret_cast<uint2*>(q + row * q_pitch + 8 * c) =
+        make_uint2(r3d_e4m3x4_rne(cv[0], cv[1], cv[2], cv[3]),
+                   r3d_e4m3x4_rne(cv[4], cv[5], cv[6], cv[7]));
+}
+
 /* ---- gated_quant_fp8 (src/r3d_band.hip:155-201 of the reference): per element
  *     h = bf16(act(gate) * up),  act(x) = silu ? x * sigmoid(x) : sigmoid(x)
  *     sigmoid(x) = 1 / (1 + f32(exp_f64(-x)))        (exp in double, narrowed once)

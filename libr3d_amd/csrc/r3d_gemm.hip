@@ -321,7 +321,14 @@ static int quant_entry(const RadArgs* a, RadStream s) {
                      ((uintptr_t)P.q % 8) == 0 && P.q_pitch % 8 == 0;
     hipStream_t stream = (hipStream_t)s;
     if (vec) {
+        /* few rows: spread each row over workgroups, one chunk a lane */
+        const bool spread = P.rows <= 64;
+        const dim3 sgrid((unsigned)((P.n / 8 + 255) / 256), (unsigned)P.rows);
 #define R3D_QV(B_, L_)                                                                      \
+    if (spread)                                                                             \
+        hipLaunchKernelGGL((quant_act_fp8_spread_kernel<B_, L_>), sgrid, dim3(256), 0, stream, \
+                           P.x, P.x_pitch, P.q, P.q_pitch, P.scale, P.s_pitch, P.n);          \
+    else                                                                                    \
     hipLaunchKernelGGL((quant_act_fp8_vec_kernel<B_, L_>), dim3((unsigned)P.rows), dim3(256), \
                        0, stream, P.x, P.x_pitch, P.q, P.q_pitch, P.scale, P.s_pitch, P.n)
 #define R3D_QVL(B_)                                                                         \
