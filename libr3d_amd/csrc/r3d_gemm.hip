@@ -159,7 +159,7 @@ static int launch_lines(const GemmPlan& P, const LinesGeom& g, hipStream_t strea
 
 static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) {
     QuadGeom qg{};
-    if (quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg))
+    if (quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg, P.xq))
         return launch_quad(P, qg, stream);
     if (P.xq) return RAD_E_UNSUPPORTED;     /* fused bf16 activations: the quad GEMV only */
     LinesGeom lg{};

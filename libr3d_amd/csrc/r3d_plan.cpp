@@ -310,7 +310,8 @@ bool quad_fits(const GemmPlan& P) { return 8 * P.b_pitch < ((int64_t)1 << 31); }
 
 /* Quad geometry: split K until about env_quad_waves() waves are in flight, keeping >= 16
  * groups per chunk. */
-bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, QuadGeom* g) {
+bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, QuadGeom* g,
+               int xq) {
     if (M < 1 || M > 4 || N < 1 || K < 128 || K % 128 != 0) return false;
     if (force_chunks > 0 && force_chunks != 1 && force_chunks != 2 && force_chunks != 4)
         return false;
@@ -331,10 +332,11 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     /* eight waves share one activation staging: measured on MI355X, a gain at MT = 4 (the
      * staging is four rows; 2-4 % on config 2/4 shapes) and for fp8a8 at MT = 1 without a
      * K split (1.5 % at config 1), a loss for mxfp4a8 at MT = 1 (the long-K split shape
-     * most: 13.2 -> 15.5 us); two quads a wave keep four waves */
+     * most: 13.2 -> 15.5 us) except with the fused producer, whose bf16 re-read it halves
+     * (15.0 -> 14.4 us at config 2's gate_up); two quads a wave keep four waves */
     const int wv_env = env_quad_wv();
     g->wv = g->qpw == 2 ? 4 : wv_env ? wv_env
-          : (g->mt == 4 || (enc == ENC_FP8A8 && c == 1)) ? 8 : 4;
+          : (g->mt == 4 || (enc == ENC_FP8A8 && c == 1) || xq) ? 8 : 4;
     g->bpb = g->wv / c;
     g->blocks = (g->nblk + g->bpb - 1) / g->bpb;
     g->gmax = (g->groups + c - 1) / c;
@@ -859,7 +861,7 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
     rc = a16 ? plan_mxfp4a16(a, M, N, &P) : mx ? plan_mxfp4a8(a, M, N, &P) : plan_fp8a8(a, M, &P);
     if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
     QuadGeom qg{};
-    if (dec && quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &qg)) {
+    if (dec && quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &qg, P.xq)) {
         snprintf(buf, (size_t)len,
                  "arm=decode kernel=quad enc=%s M=%lld N=%lld K=%lld mt=%d qpw=%d chunks=%d "
                  "waves=%d quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d xq=%d",

@@ -123,7 +123,8 @@ void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGe
  * runs instead.  force_chunks: 1/2/4 pin the split, anything else above 0
  * leaves the quad kernel. */
 constexpr int kQuadMaxLds = 48 * 1024;
-bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, QuadGeom* g);
+bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, QuadGeom* g,
+               int xq = 0);
 /* The quad kernel addresses a wave's (up to 8) weight rows through one buffer resource:
  * they must span less than 2^31 bytes. */
 bool quad_fits(const GemmPlan& P);

@@ -362,7 +362,7 @@ def test_fused_producer_plan(dtype, row):
         rc, d = R.describe(row, _xq_ops(dtype, M, N, K))
         assert rc == R.RAD_OK, (M, N, K, d)
         g = _geom(d)
-        assert g["kernel"] == "quad" and g["xq"] == "1", d
+        assert g["kernel"] == "quad" and g["xq"] == "1" and g["waves"] == "8", d
     if dtype == "fp8a8":
         rc, d = R.describe(row, _xq_ops(dtype, 1, 512, 1024, rblk=128))
         assert rc == R.RAD_OK and _geom(d)["rblk"] == "128", d
