@@ -202,7 +202,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": HEADLINE_TRAFFIC_BYTES,
-                     "kernel": "r3d::gemv_quad_kernel<1, 1, 1, 4, 0, 8> (fp8a8, MT=1, one quad per wave, 4-step ring, 8 waves a workgroup)",
+                     "kernel": "r3d::gemv_quad_kernel<1, 1, 1, 4, 0, 7> (fp8a8, MT=1, one quad per wave, 4-step ring, 7 waves a workgroup)",
                      "kernel_us": round(kern * 1e6, 3)},
     }
 

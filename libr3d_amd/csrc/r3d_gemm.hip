@@ -69,7 +69,9 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
     const int sc16 = P.enc == ENC_MXFP4A8 && P.bs_pitch == P.K / 32 &&
                      ((uintptr_t)P.BS & 15) == 0;
     if (P.xq && g.mt != 1) return RAD_E_UNSUPPORTED;    /* the fused producer is MT = 1 only */
-    if ((g.wv != 4 && g.wv != 8) || (g.qpw == 2 && g.wv != 4)) return RAD_E_UNSUPPORTED;
+    if ((g.wv != 4 && g.wv != 7 && g.wv != 8) || (g.qpw == 2 && g.wv != 4) ||
+        (g.wv == 7 && (g.chunks != 1 || P.xq)))
+        return RAD_E_UNSUPPORTED;
 #define R3D_QUAD1(ENC_, MT_, Q_, D_, X_) R3D_QUADW(ENC_, MT_, Q_, D_, X_, 4)
 #define R3D_QUADW(ENC_, MT_, Q_, D_, X_, W_)                                                \
     hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, Q_, D_, X_, W_>), grid, block,          \
@@ -82,6 +84,7 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
     else if (P.xq) R3D_QUAD1(ENC_, MT_, 1, D_, (MT_ == 1));                                  \
     else if (g.qpw == 2) R3D_QUAD1(ENC_, MT_, 2, D_, 0);                                     \
     else if (g.wv == 8) R3D_QUADW(ENC_, MT_, 1, D_, 0, 8);                                   \
+    else if (g.wv == 7) R3D_QUADW(ENC_, MT_, 1, D_, 0, 7);                                   \
     else R3D_QUAD1(ENC_, MT_, 1, D_, 0)
 #define R3D_QUAD_D(ENC_, MT_)                                                                \
     do {                                                                                     \

@@ -337,6 +337,13 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     const int wv_env = env_quad_wv();
     g->wv = g->qpw == 2 ? 4 : wv_env ? wv_env
           : (g->mt == 4 || (enc == ENC_FP8A8 && c == 1) || xq) ? 8 : 4;
+    if (g->wv == 8 && c == 1 && !xq && !wv_env) {
+        /* seven waves when that evens the workgroups over the CUs: the most waves any CU
+         * holds, ceil(blocks / 256) x waves, is what the stream waits for (config 1: 768
+         * workgroups of 7 = 21 a CU against 672 of 8 = 24) */
+        const int64_t b8 = (g->nblk + 7) / 8, b7 = (g->nblk + 6) / 7;
+        if (((b7 + 255) / 256) * 7 < ((b8 + 255) / 256) * 8) g->wv = 7;
+    }
     g->bpb = g->wv / c;
     g->blocks = (g->nblk + g->bpb - 1) / g->bpb;
     g->gmax = (g->groups + c - 1) / c;
@@ -749,7 +756,7 @@ int env_quad_wv() {
     static const int v = [] {
         const char* e = getenv("R3D_GFX950_QWV");
         const int w = e ? atoi(e) : 0;
-        return w == 4 || w == 8 ? w : 0;
+        return w == 4 || w == 7 || w == 8 ? w : 0;
     }();
     return v;
 }
