@@ -337,12 +337,14 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     const int wv_env = env_quad_wv();
     g->wv = g->qpw == 2 ? 4 : wv_env ? wv_env
           : (g->mt == 4 || (enc == ENC_FP8A8 && c == 1) || xq) ? 8 : 4;
-    if (g->wv == 8 && c == 1 && !xq && !wv_env) {
+    if (g->qpw == 1 && c == 1 && !xq && !wv_env) {
         /* seven waves when that evens the workgroups over the CUs: the most waves any CU
          * holds, ceil(blocks / 256) x waves, is what the stream waits for (config 1: 768
-         * workgroups of 7 = 21 a CU against 672 of 8 = 24) */
-        const int64_t b8 = (g->nblk + 7) / 8, b7 = (g->nblk + 6) / 7;
-        if (((b7 + 255) / 256) * 7 < ((b8 + 255) / 256) * 8) g->wv = 7;
+         * workgroups of 7 = 21 a CU against 672 of 8 = 24; config 2's gate_up at M = 1:
+         * against 1344 of 4, also 24) */
+        const int w0 = g->wv;
+        const int64_t b0 = (g->nblk + w0 - 1) / w0, b7 = (g->nblk + 6) / 7;
+        if (((b7 + 255) / 256) * 7 < ((b0 + 255) / 256) * w0) g->wv = 7;
     }
     g->bpb = g->wv / c;
     g->blocks = (g->nblk + g->bpb - 1) / g->bpb;

@@ -255,7 +255,8 @@ def test_decode_geometry_policy():
         assert g["kernel"] == kern and g["chunks"] == chunks, (M, N, K, d)
     # waves per quad workgroup: 8 at MT = 4 and for fp8a8 at MT = 1 without a K split
     # (seven when that evens the workgroups over 256 CUs without a K split)
-    for (mk, M, N, K, wv) in [(_mx_ops, 1, 21504, 5376, "4"), (_mx_ops, 4, 21504, 5376, "7"),
+    for (mk, M, N, K, wv) in [(_mx_ops, 1, 21504, 5376, "7"), (_mx_ops, 1, 8192, 5376, "4"),
+                              (_mx_ops, 1, 5376, 21504, "4"), (_mx_ops, 4, 21504, 5376, "7"),
                               (_f8_ops, 1, 21504, 5376, "7"), (_f8_ops, 1, 16384, 5376, "8"),
                               (_f8_ops, 1, 4096, 4096, "4"), (_f8_ops, 3, 2048, 5376, "8")]:
         ops, _ = mk(M=M, N=N, K=K)
