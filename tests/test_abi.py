@@ -254,7 +254,11 @@ def test_decode_geometry_policy():
         g = _geom(d)
         assert g["kernel"] == kern and g["chunks"] == chunks, (M, N, K, d)
     # waves per quad workgroup: 8 at MT = 4 and for fp8a8 at MT = 1 without a K split
-    # (seven when that evens the workgroups over 256 CUs without a K split)
+    # (seven when that evens the workgroups over 256 CUs without a K split; the ragged
+    # shapes the GPU tests run at seven waves)
+    for (mk, row, M, N) in [(_f8_ops, "gemm_nt_q_fp8a8_decode", 1, 8227),
+                            (_mx_ops, "gemm_nt_q_mxfp4_decode", 3, 8354)]:
+        assert _geom(R.describe(row, mk(M=M, N=N, K=1024)[0])[1])["waves"] == "7"
     for (mk, M, N, K, wv) in [(_mx_ops, 1, 21504, 5376, "7"), (_mx_ops, 1, 8192, 5376, "4"),
                               (_mx_ops, 1, 5376, 21504, "4"), (_mx_ops, 4, 21504, 5376, "7"),
                               (_f8_ops, 1, 21504, 5376, "7"), (_f8_ops, 1, 16384, 5376, "8"),

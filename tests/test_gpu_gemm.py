@@ -90,6 +90,20 @@ def test_mxfp4_decode_shapes(gpu, N, K):
         _check(MX_DEC, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
 
 
+@pytest.mark.parametrize("dtype,M,N", [("fp8a8", 1, 8227), ("fp8a8", 1, 8301),
+                                       ("mxfp4a8", 3, 8354), ("mxfp4a8", 3, 8477)])
+def test_decode_seven_wave_ragged(gpu, dtype, M, N):
+    """Seven-wave quad workgroups (chosen where they even the grid over the CUs) with a last
+    workgroup of fewer quads and a partial last quad."""
+    K = 1024
+    row = MX_DEC if dtype == "mxfp4a8" else F8_DEC
+    if dtype == "mxfp4a8":
+        A, AS, B, BS = _mx_case(M, N, K, N + M)
+    else:
+        A, AS, B, BS = _f8_case(M, N, K, N + M, 1)
+    _check(row, dtype, A, AS, B, BS, M, N, K, gpu)
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 7, 8, 9, 15, 16])
 @pytest.mark.parametrize("rblk", [1, 128])
 def test_fp8_decode_small(gpu, M, rblk):
