@@ -142,6 +142,9 @@ def main():
                     help="only run a plain 256 MiB device copy (counter calibration for PMC runs)")
     ap.add_argument("--c3-only", action="store_true",
                     help="only time config 3 (mxfp4a16 prefill) and print its JSON (for profiling)")
+    ap.add_argument("--case", default=None,
+                    help="only run one named workload and print its JSON line (for profiling): "
+                         + ", ".join(CASES))
     args = ap.parse_args()
     if args.copy_calib:
         import torch
@@ -165,6 +168,9 @@ def main():
     stream = torch.cuda.current_stream().cuda_stream
     if args.c3_only:
         print(json.dumps(bench_c3(dev, stream, steps=args.steps, warmup=args.warmup)), flush=True)
+        return
+    if args.case:
+        print(json.dumps(run_case(args.case, dev, stream, args.steps, args.warmup)), flush=True)
         return
 
     # ---- headline: config 1, fp8a8 decode GEMV, cold
@@ -236,8 +242,16 @@ def main():
                 log("[bench] C2 %s M=%d: %.2f us, %.1f GB/s (%.1f%%)" % (
                     name, M, kern * 1e6, gbs, 100 * gbs / HBM_PEAK_GBS))
                 del c
-        # C3 as configured: bf16 activations quantised in-library to mxfp8, mxfp4a16 row
+        # C3 as configured: bf16 activations quantised in-library to mxfp8, mxfp4a16 row;
+        # its GEMM kernel alone carries the compute roofline
         extra.update(bench_c3(dev, stream))
+        g = run_case("c3_a16_gemm", dev, stream, 10, 3)
+        out["roofline_c3"] = {"bound": "mfma", "achieved": g["TFLOPs"], "peak": FP8_PEAK_TFLOPS,
+                              "unit": "TFLOP/s", "frac": g["frac_fp8_peak"], "flops": g["flops"],
+                              "kernel": g["kernel"], "kernel_us": g["kernel_us"],
+                              "note": "config 3's GEMM alone (stage 2 of gemm_nt_q_mxfp4a16), "
+                                      "dense fp8-rate peak: an fp4 x fp8 scaled MFMA issues "
+                                      "at the fp8 rate"}
         # C3 on the reference's activation contract (e4m3 + f32 per 128): mxfp4a8 row
         M, K, N = 2048, 5376, 21504
         _, A, AS = synth.activations(M, K, 0x5EED + 30)
@@ -274,6 +288,113 @@ def main():
         log("[bench] CPU baseline (oracle, bounded sample) ...")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
+
+
+CASES = (["c0", "c1", "c3_a16", "c3_a16_quant", "c3_a16_gemm", "c3_a8", "c3_f8", "lm_head_M4"] +
+         ["c2_%s_M%d" % (s, m) for s in ("gate_up", "down", "qkv") for m in (1, 4, 16)] +
+         ["c4_%s_M4" % s for s in ("q", "kv", "o")] +
+         ["skinny_%s_M%d" % (s, m) for s in ("gate_up", "down", "qkv") for m in (17, 32, 64)])
+C2_SHAPES = {"gate_up": (5376, 21504), "down": (21504, 5376), "qkv": (5376, 8192)}
+C4_SHAPES = {"q": (5376, 4096), "kv": (5376, 2048), "o": (4096, 5376)}
+
+
+def run_case(name, dev, stream, steps, warmup):
+    """One named workload, cold where its weights exceed the cache (rotated copies), timed
+    with HIP events on the launch stream: kernel (or op) microseconds and the rate against
+    its roofline.  The names are the profiling targets of profiles/."""
+    import torch
+    import libr3d_amd as R
+    from libr3d_amd import synth
+    if name not in CASES:
+        raise SystemExit("unknown case %r; one of: %s" % (name, ", ".join(CASES)))
+    res = {"case": name, "steps": steps}
+    if name.startswith("c3_a16"):
+        M, K, N = 2048, 5376, 21504
+        rng = np.random.default_rng(0x5EED + 32)
+        X = synth.bf16_bits(rng.standard_normal((M, K), dtype=np.float32))
+        B, BS = synth.mxfp4_weights(N, K, 0x5EED + 31)
+        x = torch.from_numpy(X.view(np.int16)).to(dev)
+        b, bs = torch.from_numpy(B).to(dev), torch.from_numpy(BS).to(dev)
+        y = torch.empty((M, N), dtype=torch.int16, device=dev)
+        ops = R.GemmOperands(x, None, b, bs, y, dtype="mxfp4a16", N=N, K=K, group=32, M=M)
+        scratch = torch.empty(R.row_scratch_bytes("gemm_nt_q_mxfp4a16", ops), dtype=torch.uint8,
+                              device=dev)
+        ops.set_scratch(scratch)
+        stage = {"c3_a16": 0, "c3_a16_quant": 1, "c3_a16_gemm": 2}[name]
+        assert R.mxfp4a16_stage(ops, 1, stream) == 0           # the planes the GEMM reads
+        for _ in range(warmup):
+            assert R.mxfp4a16_stage(ops, stage, stream) == 0
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            R.mxfp4a16_stage(ops, stage, stream)
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / steps
+        fl = 2.0 * M * N * K
+        res.update({"M": M, "K": K, "N": N, "kernel_us": round(t * 1e6, 2), "flops": fl})
+        if stage == 1:
+            nb = M * K * 2 + M * K + M * K // 32
+            res.update({"kernel": "r3d::quant_mx8_kernel", "GBps": round(nb / t / 1e9, 1),
+                        "frac_hbm": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)})
+        else:
+            d = R.describe("gemm_nt_q_mxfp4a16", ops)[1]
+            bn = int(d.split("bn=")[1].split()[0])
+            res.update({"kernel": "r3d::prefill_kernel<1, %d, 4>" % (bn // 32)
+                        + (" (+ r3d::quant_mx8_kernel)" if stage == 0 else ""),
+                        "TFLOPs": round(fl / t / 1e12, 1),
+                        "frac_fp8_peak": round(fl / t / 1e12 / FP8_PEAK_TFLOPS, 4)})
+        return res
+    if name in ("c3_a8", "c3_f8"):
+        M, K, N = 2048, 5376, 21504
+        if name == "c3_a8":
+            _, A, AS = synth.activations(M, K, 0x5EED + 30)
+            B, BS = synth.mxfp4_weights(N, K, 0x5EED + 31)
+            c, row = Case("mxfp4a8", A, AS, B, BS, M, N, K, 1, dev), "gemm_nt_q_mxfp4"
+        else:
+            A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 35)
+            B, BS = synth.fp8_weights(N, K, 0x5EED + 36)
+            c, row = Case("fp8a8", A, AS, B, BS, M, N, K, 1, dev), "gemm_nt_q_fp8a8"
+        wall, kern = time_case(c, row, steps, warmup, stream)
+        fl = 2.0 * M * N * K
+        res.update({"M": M, "K": K, "N": N, "row": row, "kernel_us": round(kern * 1e6, 2),
+                    "flops": fl, "TFLOPs": round(fl / kern / 1e12, 1),
+                    "frac_fp8_peak": round(fl / kern / 1e12 / FP8_PEAK_TFLOPS, 4),
+                    "plan": R.describe(row, c.ops[0])[1]})
+        return res
+    # bandwidth-bound workloads
+    if name == "c1" or name == "lm_head_M4":
+        M, K, N = (1, 5376, 21504) if name == "c1" else (4, 5376, 262144)
+        A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 10 if name == "c1" else 0x5EED + 40)
+        B, BS = synth.fp8_weights(N, K, 0x5EED + 11 if name == "c1" else 0x5EED + 41)
+        dtype, row, nb = "fp8a8", "gemm_nt_q_fp8a8_decode", f8_bytes(M, N, K)
+    else:
+        if name == "c0":
+            M, K, N, seed = 1, 4096, 4096, 0x5EED
+        elif name.startswith("c2_") or name.startswith("skinny_"):
+            shape, m = name.split("_", 1)[1].rsplit("_M", 1)
+            M = int(m)
+            K, N = C2_SHAPES[shape]
+            seed = 0x5EED + 20 + M if name.startswith("c2_") else 0x5EED + 50 + M
+        else:
+            shape = name[3:].rsplit("_M", 1)[0]
+            M = 4
+            K, N = C4_SHAPES[shape]
+            seed = 0x5EED + 50 + K
+        _, A, AS = synth.activations(M, K, seed)
+        B, BS = synth.mxfp4_weights(N, K, 0x5EED + 21 + K)
+        dtype, nb = "mxfp4a8", mx_bytes(M, N, K)
+        row = "gemm_nt_q_mxfp4" if name.startswith("skinny_") else "gemm_nt_q_mxfp4_decode"
+    copies = 1 if name == "c0" else copies_for(B.nbytes + BS.nbytes)
+    c = Case(dtype, A, AS, B, BS, M, N, K, copies, dev)
+    wall, kern = time_case(c, row, steps, warmup, stream)
+    res.update({"M": M, "K": K, "N": N, "row": row, "bytes": nb, "copies": copies,
+                "kernel_us": round(kern * 1e6, 3), "GBps": round(nb / kern / 1e9, 1),
+                "frac_hbm": round(nb / kern / 1e9 / HBM_PEAK_GBS, 4),
+                "GBps_wall": round(nb * steps / wall / 1e9, 1),
+                "plan": R.describe(row, c.ops[0])[1]})
+    return res
 
 
 def bench_c3(dev, stream, steps=10, warmup=3):

@@ -95,6 +95,20 @@ int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a);
  * Launches nothing, touches no device memory.  Returns the plan's status code. */
 int r3d_gfx950_describe(const char* row, const RadArgs* a, char* buf, int len);
 
+/* Diagnostic with no counterpart in the reference: one stage of a gemm_nt_q_mxfp4a16 call
+ * on `s`, for timing and checking the stages apart.  stage 0 = the whole call (as the
+ * row's launch), 1 = the mxfp8 quantiser alone (fills RadArgs::scratch), 2 = the
+ * block-scaled GEMM alone on the planes already in RadArgs::scratch.  Same gates and
+ * refusal codes as the row; RAD_E_INVAL for another stage; RAD_E_UNSUPPORTED where the
+ * call would take the skinny band's decode passes (no quantiser stage there). */
+int r3d_gfx950_mxfp4a16_stage(const RadArgs* a, RadStream s, int stage);
+
+/* Build identity with no counterpart in the reference: the SHA-256 (hex) of the sources
+ * this library was compiled from -- every file under libr3d_amd/csrc and include, in name
+ * order, each as "<relative path>\n<bytes>" -- so a test harness can tell whether the
+ * binary it loaded was built from the tree beside it. */
+const char* r3d_gfx950_build_id(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,7 +19,8 @@ __all__ = [
     "RAD_E_INVAL", "RAD_E_DEVICE", "DT", "RadTensor", "RadParam", "RadArgs",
     "RadKernelInfo", "RadOpSchema", "lib", "lib_path", "rows", "schemas", "resolve",
     "launch_row", "gemm_nt_q", "describe", "GemmOperands", "QuantActOperands", "quant_act_fp8",
-    "GatedQuantOperands", "GatedGemmOperands", "RmsNormQuantOperands",
+    "GatedQuantOperands", "GatedGemmOperands", "RmsNormQuantOperands", "build_id",
+    "check_build_id", "mxfp4a16_stage",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -127,12 +128,40 @@ def lib():
         L.r3d_gfx950_describe.restype = ctypes.c_int
         L.r3d_gfx950_describe.argtypes = [ctypes.c_char_p, ctypes.POINTER(RadArgs),
                                           ctypes.c_char_p, ctypes.c_int]
+        L.r3d_gfx950_mxfp4a16_stage.restype = ctypes.c_int
+        L.r3d_gfx950_mxfp4a16_stage.argtypes = [ctypes.POINTER(RadArgs), ctypes.c_void_p,
+                                                ctypes.c_int]
+        L.r3d_gfx950_build_id.restype = ctypes.c_char_p
+        L.r3d_gfx950_build_id.argtypes = []
         _LIB = L
     return _LIB
 
 
 def _s(b):
     return b.decode() if isinstance(b, bytes) else b
+
+
+def build_id():
+    """The SHA-256 of the sources the loaded library was compiled from."""
+    return _s(lib().r3d_gfx950_build_id())
+
+
+def check_build_id():
+    """Raise unless the loaded library was built from the sources beside this module (a
+    stale binary would test or benchmark other code than the tree holds)."""
+    from libr3d_amd import build as B
+    got, want = build_id(), B.source_id()
+    if got != want:
+        raise RuntimeError("libr3d_gfx950.so is stale: built from sources %s, tree holds %s "
+                           "(rebuild: python -m libr3d_amd.build)" % (got[:16], want[:16]))
+    return got
+
+
+def mxfp4a16_stage(ops, stage, stream=0):
+    """One stage of a gemm_nt_q_mxfp4a16 call (0 whole, 1 quantiser, 2 GEMM on the planes
+    already in the scratch); returns the status."""
+    return lib().r3d_gfx950_mxfp4a16_stage(ctypes.byref(ops.args), ctypes.c_void_p(stream),
+                                           int(stage))
 
 
 def rows():

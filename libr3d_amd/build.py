@@ -6,6 +6,7 @@ hipcc compiles the HIP kernels for --offload-arch=gfx950 with packed-fp32 code
 generation switched off; the host C++ (row table, plans) goes into the same shared
 object.  The oracle (oracle/Makefile) is test infrastructure and is built beside it.
 """
+import hashlib
 import os
 import shutil
 import subprocess
@@ -36,9 +37,27 @@ def _run(cmd, cwd=None):
     return out
 
 
+def source_id():
+    """SHA-256 (hex) of every file under libr3d_amd/csrc and include, in name order, each
+    hashed as "<path relative to the repo root>\n<bytes>" -- the identity the library
+    reports through r3d_gfx950_build_id()."""
+    h = hashlib.sha256()
+    files = []
+    for d in (CSRC, os.path.join(ROOT, "include")):
+        for name in os.listdir(d):
+            p = os.path.join(d, name)
+            if os.path.isfile(p):
+                files.append(os.path.relpath(p, ROOT).replace(os.sep, "/"))
+    for rel in sorted(files):
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(rel.encode() + b"\n" + f.read())
+    return h.hexdigest()
+
+
 def build_library():
     tmp = LIB + ".tmp"
-    cmd = [HIPCC] + FLAGS + [os.path.join(CSRC, s) for s in SOURCES] + ["-o", tmp]
+    cmd = ([HIPCC] + FLAGS + ['-DR3D_BUILD_ID="%s"' % source_id()] +
+           [os.path.join(CSRC, s) for s in SOURCES] + ["-o", tmp])
     out = _run(cmd)
     if out.strip():
         sys.stderr.write(out + "\n")
@@ -54,9 +73,21 @@ def build_oracle():
     return os.path.join(ROOT, "oracle", "libr3d_oracle.so")
 
 
+def build_harness():
+    """The C engine-side test harness (tests/c_abi): compiled against the public headers and
+    linked against the library just built and the oracle."""
+    make = shutil.which("make")
+    if make is None:
+        raise RuntimeError("make not found")
+    _run([make, "-s", "-B", "-C", os.path.join(ROOT, "tests", "c_abi")])
+    return os.path.join(ROOT, "tests", "c_abi", "abi_harness")
+
+
 def build_all():
     build_oracle()
-    return build_library()
+    lib = build_library()
+    build_harness()
+    return lib
 
 
 if __name__ == "__main__":

@@ -198,8 +198,9 @@ static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) 
 
 /* The prefill GEMM: mode PF_A8 reads A/AS as given (e4m3 + f32 per 128) against e2m1
  * weights, PF_F8 the same activations against e4m3 weights with bf16 row scales, PF_MX8 the
- * mxfp8 planes the quantiser left in P.scratch. */
-static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
+ * mxfp8 planes the quantiser left in P.scratch.  stage (mxfp4a16 only): 0 both launches, 1
+ * the quantiser alone, 2 the GEMM alone on the planes already in the scratch. */
+static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0) {
     /* the skinny band on a narrow N: 16-row passes of the decode GEMVs (each output row is
      * the same arithmetic either way) */
     if (const int passes = skinny_passes(P.enc, P.M, P.N, cu_count())) {
@@ -233,9 +234,14 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream) {
         uint8_t* SX = P.scratch + qbytes;
         const int64_t qblocks = P.M;                     /* one workgroup per row */
         if (qblocks > 0x7FFFFFFF) return RAD_E_SHAPE;
-        hipLaunchKernelGGL(quant_mx8_kernel, dim3((unsigned)qblocks), dim3(256), 0, stream,
-                           reinterpret_cast<const uint16_t*>(P.A), P.a_pitch, Q, P.K, SX,
-                           P.K / 32, P.M, (int)P.K);
+        if (stage != 2)
+            hipLaunchKernelGGL(quant_mx8_kernel, dim3((unsigned)qblocks), dim3(256), 0, stream,
+                               reinterpret_cast<const uint16_t*>(P.A), P.a_pitch, Q, P.K, SX,
+                               P.K / 32, P.M, (int)P.K);
+        if (stage == 1) {
+            const hipError_t e = hipGetLastError();
+            return e == hipSuccess ? RAD_OK : RAD_E_DEVICE;
+        }
         A = Q;
         AS = SX;
         a_pitch = P.K;
@@ -531,6 +537,20 @@ int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s) {
 }
 int r3d_gfx950_describe(const char* row, const RadArgs* a, char* buf, int len) {
     return r3d::describe(row, a, buf, len);
+}
+int r3d_gfx950_mxfp4a16_stage(const RadArgs* a, RadStream s, int stage) {
+    if (stage < 0 || stage > 2) return RAD_E_INVAL;
+    if (r3d::env_no_mxfp4()) return RAD_E_UNSUPPORTED;
+    int64_t M = 0, N = 0;
+    int rc = r3d::entry_preamble(a, r3d::ENC_MXFP4A16, 0, &M, &N);
+    if (rc) return rc;
+    r3d::GemmPlan P{};
+    rc = r3d::plan_mxfp4a16(a, M, N, &P);
+    if (rc) return rc;
+    if (!r3d::chip_ok()) return RAD_E_UNSUPPORTED;
+    /* the skinny band's decode-GEMV passes have no quantiser stage */
+    if (r3d::skinny_passes(P.enc, P.M, P.N, r3d::cu_count())) return RAD_E_UNSUPPORTED;
+    return r3d::launch_prefill(P, (hipStream_t)s, stage);
 }
 
 }  /* extern "C" */

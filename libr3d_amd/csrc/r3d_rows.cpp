@@ -377,4 +377,11 @@ const RadKernelInfo* rad_kernel_at(int i) {
     return nullptr;
 }
 
+/* The build script passes the sources' SHA-256 as R3D_BUILD_ID; a compile without it
+ * reports "unknown". */
+#ifndef R3D_BUILD_ID
+#define R3D_BUILD_ID "unknown"
+#endif
+const char* r3d_gfx950_build_id(void) { return R3D_BUILD_ID; }
+
 }  /* extern "C" */

@@ -1,0 +1,263 @@
+/* abi_harness.c -- a C engine-side caller of libr3d_gfx950.so, compiled against
+ * include/rad_abi.h and include/r3d_gfx950.h and linked against the library itself, so the
+ * header's prototypes and the binary's exports must agree at build time.  Test
+ * infrastructure (it also links the CPU oracle as the checker); modelled on the
+ * reference's dlopen harness (tools/probe_m4_entry.cpp:24-97): hand-built RadTensor /
+ * RadParam / RadArgs, a launch through the row table, the oracle on the host.
+ *
+ *   abi_harness layout   JSON: sizeof / offsetof of every ABI structure (no GPU)
+ *   abi_harness table    JSON: ABI version, plugin identity, schemas and rows (no GPU)
+ *   abi_harness run      one mxfp4a8 decode launch (M = 3) and one fp8a8 prefill launch
+ *                        (M = 130) on the GPU, each through RadKernelInfo::launch and the
+ *                        named export, checked against the oracle; exit 0 when both pass
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "r3d_gfx950.h"
+#include "rad_abi.h"
+#include "r3d_oracle.h"
+
+#define FIELD(T, f) printf("\"%s.%s\": [%zu, %zu], ", #T, #f, offsetof(T, f), sizeof(((T*)0)->f))
+
+static int layout(void) {
+    printf("{");
+    printf("\"sizeof.RadTensor\": %zu, ", sizeof(RadTensor));
+    FIELD(RadTensor, data); FIELD(RadTensor, dtype); FIELD(RadTensor, rank);
+    FIELD(RadTensor, shape); FIELD(RadTensor, stride);
+    printf("\"sizeof.RadParam\": %zu, ", sizeof(RadParam));
+    FIELD(RadParam, kind); FIELD(RadParam, key); FIELD(RadParam, ival); FIELD(RadParam, ihi);
+    FIELD(RadParam, sval); FIELD(RadParam, dval);
+    printf("\"sizeof.RadTunableValue\": %zu, ", sizeof(RadTunableValue));
+    FIELD(RadTunableValue, name); FIELD(RadTunableValue, value);
+    printf("\"sizeof.RadArgs\": %zu, ", sizeof(RadArgs));
+    FIELD(RadArgs, t); FIELD(RadArgs, n_t); FIELD(RadArgs, p); FIELD(RadArgs, n_p);
+    FIELD(RadArgs, tv); FIELD(RadArgs, n_tv); FIELD(RadArgs, scratch);
+    FIELD(RadArgs, scratch_bytes); FIELD(RadArgs, flags);
+    printf("\"sizeof.RadConstraint\": %zu, ", sizeof(RadConstraint));
+    FIELD(RadConstraint, key); FIELD(RadConstraint, op); FIELD(RadConstraint, ival);
+    FIELD(RadConstraint, sval);
+    printf("\"sizeof.RadKernelInfo\": %zu, ", sizeof(RadKernelInfo));
+    FIELD(RadKernelInfo, name); FIELD(RadKernelInfo, op); FIELD(RadKernelInfo, family);
+    FIELD(RadKernelInfo, summary); FIELD(RadKernelInfo, limits); FIELD(RadKernelInfo, formats);
+    FIELD(RadKernelInfo, domain); FIELD(RadKernelInfo, priority);
+    FIELD(RadKernelInfo, constraints); FIELD(RadKernelInfo, n_constraints);
+    FIELD(RadKernelInfo, tunables); FIELD(RadKernelInfo, n_tunables);
+    FIELD(RadKernelInfo, replaces); FIELD(RadKernelInfo, init); FIELD(RadKernelInfo, fini);
+    FIELD(RadKernelInfo, launch); FIELD(RadKernelInfo, scratch); FIELD(RadKernelInfo, layout);
+    FIELD(RadKernelInfo, relayout); FIELD(RadKernelInfo, opd_shape);
+    FIELD(RadKernelInfo, unrelayout);
+    printf("\"sizeof.RadParamSpec\": %zu, ", sizeof(RadParamSpec));
+    FIELD(RadParamSpec, key); FIELD(RadParamSpec, kind); FIELD(RadParamSpec, req);
+    FIELD(RadParamSpec, role);
+    printf("\"sizeof.RadOperandSpec\": %zu, ", sizeof(RadOperandSpec));
+    FIELD(RadOperandSpec, name); FIELD(RadOperandSpec, role); FIELD(RadOperandSpec, optional);
+    printf("\"sizeof.RadOpSchema\": %zu, ", sizeof(RadOpSchema));
+    FIELD(RadOpSchema, op); FIELD(RadOpSchema, params); FIELD(RadOpSchema, n_params);
+    FIELD(RadOpSchema, operands); FIELD(RadOpSchema, n_operands); FIELD(RadOpSchema, prose);
+    printf("\"sizeof.RadPluginInfo\": %zu, ", sizeof(RadPluginInfo));
+    FIELD(RadPluginInfo, kind); FIELD(RadPluginInfo, name); FIELD(RadPluginInfo, version);
+    FIELD(RadPluginInfo, description); FIELD(RadPluginInfo, targets);
+    printf("\"RAD_MAX_RANK\": %d}\n", RAD_MAX_RANK);
+    return 0;
+}
+
+/* Every declared export, referenced by name: the link fails if the binary lacks one. */
+static const void* const kExports[] = {
+    (const void*)rad_plugin_abi_version, (const void*)rad_plugin_info,
+    (const void*)rad_kernel_schema_count, (const void*)rad_kernel_schema_at,
+    (const void*)rad_kernel_count, (const void*)rad_kernel_at,
+    (const void*)r3d_rad_gemm_nt_q, (const void*)r3d_rad_gemm_nt_q_mxfp4_decode,
+    (const void*)r3d_rad_gemm_nt_q_fp8, (const void*)r3d_rad_gemm_nt_q_fp8_decode,
+    (const void*)r3d_rad_gemm_nt_q_mxfp4a16, (const void*)r3d_rad_gemm_nt_q_mxfp4a16_scratch,
+    (const void*)r3d_rad_quant_act_fp8, (const void*)r3d_rad_gated_quant_fp8,
+    (const void*)r3d_rad_rmsnorm_quant_fp8, (const void*)r3d_rad_gemm_nt_q_gated_fp8,
+    (const void*)r3d_rad_gemm_nt_q_gated_fp8_scratch, (const void*)r3d_gfx950_describe,
+    (const void*)r3d_gfx950_mxfp4a16_stage, (const void*)r3d_gfx950_build_id,
+};
+
+static int table(void) {
+    const RadPluginInfo* pi = rad_plugin_info();
+    printf("{\"abi\": %u, \"exports\": %zu, \"build_id\": \"%s\", ", rad_plugin_abi_version(),
+           sizeof kExports / sizeof kExports[0], r3d_gfx950_build_id());
+    printf("\"plugin\": [%d, \"%s\", \"%s\"], \"schemas\": [", pi->kind, pi->name, pi->targets);
+    for (int i = 0; i < rad_kernel_schema_count(); ++i) {
+        const RadOpSchema* s = rad_kernel_schema_at(i);
+        printf("%s[\"%s\", %d, %d]", i ? ", " : "", s->op, s->n_params, s->n_operands);
+    }
+    printf("], \"rows\": [");
+    for (int i = 0; i < rad_kernel_count(); ++i) {
+        const RadKernelInfo* k = rad_kernel_at(i);
+        printf("%s[\"%s\", \"%s\", %d, %d, %d]", i ? ", " : "", k->name, k->op, k->priority,
+               k->n_constraints, k->launch != NULL);
+    }
+    printf("]}\n");
+    return 0;
+}
+
+/* ------------------------------------------------------------------ GPU run */
+static uint32_t g_lcg = 777u;
+static uint32_t rnd(void) { g_lcg = g_lcg * 1664525u + 1013904223u; return g_lcg >> 8; }
+static uint8_t rnd_e4m3(void) {                 /* NaN-free e4m3 code */
+    uint8_t c = (uint8_t)rnd();
+    return (c & 0x7F) == 0x7F ? (uint8_t)(c & 0xFE) : c;
+}
+static float bf16f(uint16_t h) { uint32_t u = (uint32_t)h << 16; float f; memcpy(&f, &u, 4); return f; }
+
+#define CK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { \
+    fprintf(stderr, "%s failed: %s\n", #x, hipGetErrorName(e_)); exit(2); } } while (0)
+
+static void* to_dev(const void* h, size_t n) {
+    void* d = NULL;
+    CK(hipMalloc(&d, n ? n : 1));
+    CK(hipMemcpy(d, h, n, hipMemcpyHostToDevice));
+    return d;
+}
+
+static RadLaunchFn row_launch(const char* name) {
+    for (int i = 0; i < rad_kernel_count(); ++i)
+        if (strcmp(rad_kernel_at(i)->name, name) == 0) return rad_kernel_at(i)->launch;
+    return NULL;
+}
+
+static void tensor(RadTensor* t, void* d, uint32_t dt, int64_t r, int64_t c) {
+    memset(t, 0, sizeof *t);
+    t->data = d; t->dtype = dt; t->rank = 2;
+    t->shape[0] = r; t->shape[1] = c; t->stride[0] = c; t->stride[1] = 1;
+}
+
+/* Y from the table's launch and from the export must be equal and within the per-element
+ * bound ulp_bf16 + 2K 2^-24 S + 2^-10 S8 of the oracle. */
+static int check(const char* what, int64_t M, int64_t N, int64_t K, const uint16_t* Y1,
+                 const uint16_t* Y2, const uint16_t* Yr, const float* Yf, const float* S,
+                 const float* S8) {
+    double worst = 0.0;
+    int64_t bad = 0, diff = 0;
+    for (int64_t i = 0; i < M * N; ++i) {
+        if (Y1[i] != Y2[i]) ++diff;
+        const double y = bf16f(Y1[i]), r = bf16f(Yr[i]);
+        if (Y1[i] == 0xEEEE || isnan(y) != isnan(r)) { ++bad; continue; }
+        if (isnan(r)) continue;
+        double big = fmax(fabs(y), fabs((double)Yf[i]));
+        if (big < ldexp(1.0, -126)) big = ldexp(1.0, -126);
+        const double ulp = ldexp(1.0, (int)floor(log2(big)) - 7);
+        const double bound = ulp + 2.0 * K * ldexp(1.0, -24) * S[i] + ldexp(1.0, -10) * S8[i];
+        const double v = fabs(y - r) / bound;
+        if (v > worst) worst = v;
+        if (v > 1.0) ++bad;
+    }
+    printf("%s M=%lld N=%lld K=%lld: max_viol %.3f, outside %lld, table-vs-export differ %lld\n",
+           what, (long long)M, (long long)N, (long long)K, worst, (long long)bad, (long long)diff);
+    return bad == 0 && diff == 0;
+}
+
+static int run_decode_mxfp4(void) {
+    const int64_t M = 3, N = 200, K = 512, asc = K / 128, bsc = K / 32;
+    uint8_t* A = malloc(M * K); float* AS = malloc(M * asc * 4);
+    uint8_t* B = malloc(N * K / 2); uint8_t* BS = malloc(N * bsc);
+    for (int64_t i = 0; i < M * K; ++i) A[i] = rnd_e4m3();
+    for (int64_t i = 0; i < M * asc; ++i) AS[i] = 0.001f + 0.01f * (float)(rnd() % 1000) / 1000.f;
+    for (int64_t i = 0; i < N * K / 2; ++i) B[i] = (uint8_t)rnd();
+    for (int64_t i = 0; i < N * bsc; ++i) BS[i] = (uint8_t)(115 + rnd() % 25);
+    void *dA = to_dev(A, M * K), *dAS = to_dev(AS, M * asc * 4), *dB = to_dev(B, N * K / 2),
+         *dBS = to_dev(BS, N * bsc), *dY1 = NULL, *dY2 = NULL;
+    CK(hipMalloc(&dY1, M * N * 2)); CK(hipMalloc(&dY2, M * N * 2));
+    CK(hipMemset(dY1, 0xEE, M * N * 2)); CK(hipMemset(dY2, 0xEE, M * N * 2));
+    RadTensor t[7];
+    tensor(&t[0], dA, RAD_F8E4M3, M, K);
+    tensor(&t[1], dAS, RAD_F32, M, asc);
+    tensor(&t[2], dB, RAD_FP4E2M1, N, K);                 /* FP4: strides in nibbles */
+    tensor(&t[3], dBS, RAD_E8M0, N, bsc);
+    tensor(&t[4], dY1, RAD_BF16, M, N);
+    memset(&t[5], 0, sizeof t[5]); memset(&t[6], 0, sizeof t[6]);     /* a_sum, b_ref absent */
+    const RadParam p[] = { RAD_STR("dtype", "mxfp4a8"), RAD_INT("N", N), RAD_INT("K", K),
+                           RAD_INT("group", 32), RAD_INT("M", M) };
+    RadArgs args = { t, 7, p, (int)(sizeof p / sizeof p[0]), NULL, 0, NULL, 0, 0 };
+    char desc[512];
+    r3d_gfx950_describe("gemm_nt_q_mxfp4_decode", &args, desc, sizeof desc);
+    printf("decode plan: %s\n", desc);
+    RadLaunchFn f = row_launch("gemm_nt_q_mxfp4_decode");
+    const int rc1 = f ? f(&args, NULL) : -1;
+    t[4].data = dY2;
+    const int rc2 = r3d_rad_gemm_nt_q_mxfp4_decode(&args, NULL);
+    CK(hipDeviceSynchronize());
+    uint16_t *Y1 = malloc(M * N * 2), *Y2 = malloc(M * N * 2), *Yr = malloc(M * N * 2);
+    float *Yf = malloc(M * N * 4), *S = malloc(M * N * 4), *S8 = malloc(M * N * 4);
+    CK(hipMemcpy(Y1, dY1, M * N * 2, hipMemcpyDeviceToHost));
+    CK(hipMemcpy(Y2, dY2, M * N * 2, hipMemcpyDeviceToHost));
+    r3d_ref_quant_dot_mxfp4a8(A, K, AS, asc, B, BS, bsc, M, N, K, Yr, N, Yf, S, 1);
+    r3d_ref_group8_mag(0, A, K, AS, asc, B, K / 2, BS, bsc, 1, M, N, K, S8, 1);
+    const int ok = rc1 == RAD_OK && rc2 == RAD_OK &&
+                   check("mxfp4a8 decode", M, N, K, Y1, Y2, Yr, Yf, S, S8);
+    hipFree(dA); hipFree(dAS); hipFree(dB); hipFree(dBS); hipFree(dY1); hipFree(dY2);
+    free(A); free(AS); free(B); free(BS); free(Y1); free(Y2); free(Yr); free(Yf); free(S); free(S8);
+    return ok;
+}
+
+static int run_prefill_fp8(void) {
+    const int64_t M = 130, N = 300, K = 384, asc = K / 128;
+    uint8_t* A = malloc(M * K); float* AS = malloc(M * asc * 4);
+    uint8_t* B = malloc(N * K); uint16_t* BS = malloc(N * asc * 2);
+    for (int64_t i = 0; i < M * K; ++i) A[i] = rnd_e4m3();
+    for (int64_t i = 0; i < M * asc; ++i) AS[i] = 0.001f + 0.01f * (float)(rnd() % 1000) / 1000.f;
+    for (int64_t i = 0; i < N * K; ++i) B[i] = rnd_e4m3();
+    for (int64_t i = 0; i < N * asc; ++i) BS[i] = (uint16_t)(0x3B00 + rnd() % 0x200);  /* bf16 ~0.002..0.008 */
+    void *dA = to_dev(A, M * K), *dAS = to_dev(AS, M * asc * 4), *dB = to_dev(B, N * K),
+         *dBS = to_dev(BS, N * asc * 2), *dY1 = NULL, *dY2 = NULL;
+    CK(hipMalloc(&dY1, M * N * 2)); CK(hipMalloc(&dY2, M * N * 2));
+    CK(hipMemset(dY1, 0xEE, M * N * 2)); CK(hipMemset(dY2, 0xEE, M * N * 2));
+    RadTensor t[7];
+    tensor(&t[0], dA, RAD_F8E4M3, M, K);
+    tensor(&t[1], dAS, RAD_F32, M, asc);
+    tensor(&t[2], dB, RAD_F8E4M3, N, K);
+    tensor(&t[3], dBS, RAD_BF16, N, asc);                 /* per-row weight-scale grid */
+    tensor(&t[4], dY1, RAD_BF16, M, N);
+    memset(&t[5], 0, sizeof t[5]); memset(&t[6], 0, sizeof t[6]);
+    const RadParam p[] = { RAD_STR("dtype", "fp8a8"), RAD_INT("N", N), RAD_INT("K", K),
+                           RAD_INT("group", 128) };
+    RadArgs args = { t, 7, p, (int)(sizeof p / sizeof p[0]), NULL, 0, NULL, 0, 0 };
+    char desc[512];
+    r3d_gfx950_describe("gemm_nt_q_fp8a8", &args, desc, sizeof desc);
+    printf("prefill plan: %s\n", desc);
+    RadLaunchFn f = row_launch("gemm_nt_q_fp8a8");
+    const int rc1 = f ? f(&args, NULL) : -1;
+    t[4].data = dY2;
+    const int rc2 = r3d_rad_gemm_nt_q_fp8(&args, NULL);
+    CK(hipDeviceSynchronize());
+    uint16_t *Y1 = malloc(M * N * 2), *Y2 = malloc(M * N * 2), *Yr = malloc(M * N * 2);
+    float *Yf = malloc(M * N * 4), *S = malloc(M * N * 4), *S8 = malloc(M * N * 4);
+    CK(hipMemcpy(Y1, dY1, M * N * 2, hipMemcpyDeviceToHost));
+    CK(hipMemcpy(Y2, dY2, M * N * 2, hipMemcpyDeviceToHost));
+    r3d_ref_quant_dot_fp8a8(A, K, AS, asc, B, K, BS, asc, 1, M, N, K, Yr, N, Yf, S, 1);
+    r3d_ref_group8_mag(1, A, K, AS, asc, B, K, BS, asc, 1, M, N, K, S8, 1);
+    const int ok = rc1 == RAD_OK && rc2 == RAD_OK &&
+                   check("fp8a8 prefill", M, N, K, Y1, Y2, Yr, Yf, S, S8);
+    hipFree(dA); hipFree(dAS); hipFree(dB); hipFree(dBS); hipFree(dY1); hipFree(dY2);
+    free(A); free(AS); free(B); free(BS); free(Y1); free(Y2); free(Yr); free(Yf); free(S); free(S8);
+    return ok;
+}
+
+int main(int argc, char** argv) {
+    const char* mode = argc > 1 ? argv[1] : "layout";
+    if (strcmp(mode, "layout") == 0) return layout();
+    if (strcmp(mode, "table") == 0) return table();
+    if (strcmp(mode, "run") == 0) {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+            fprintf(stderr, "no GPU\n");
+            return 3;
+        }
+        const int a = run_decode_mxfp4();
+        const int b = run_prefill_fp8();
+        printf("%s\n", a && b ? "PASS" : "FAIL");
+        return a && b ? 0 : 1;
+    }
+    fprintf(stderr, "usage: abi_harness layout|table|run\n");
+    return 2;
+}

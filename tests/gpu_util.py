@@ -53,6 +53,30 @@ def run_row(row, dtype, A, AS, B, BS, M, N, K, dev, y_shape=None, extra=None, tu
     return rc, Y, ok
 
 
+def record(case, row, shape, c, Y=None, Yref_bits=None):
+    """Append one parity record (JSON line) to the file named by R3D_PARITY_LOG, if set:
+    the case, the row, the shape, the comparison figures and, given both outputs, the
+    fraction of elements whose bf16 bits equal the oracle's."""
+    import json
+    import os
+    path = os.environ.get("R3D_PARITY_LOG")
+    if not path:
+        return
+    rec = {"case": case, "row": row, "shape": shape}
+    rec.update({k: c[k] for k in ("rel_l2", "row_rel_l2_max", "max_abs", "max_viol") if k in c})
+    for k in ("row_max_abs", "row_rel_l2"):            # per output row, up to 16 rows listed
+        v = np.asarray(c.get(k, []), np.float64)
+        rec[k] = [float(x) for x in v] if v.size <= 16 else {
+            "rows": int(v.size), "max": float(v.max()), "median": float(np.median(v))}
+    if Y is not None and Yref_bits is not None:
+        y = np.asarray(Y, np.uint16)
+        r = np.asarray(Yref_bits, np.uint16)
+        both_nan = np.isnan(O.bf16_to_f32(y)) & np.isnan(O.bf16_to_f32(r))
+        rec["bits_equal_frac"] = float(np.mean((y == r) | both_nan))
+    with open(path, "a") as f:
+        f.write(json.dumps(rec) + "\n")
+
+
 def compare(Y, Yref_bits, Yf, S, K, S8=None):
     """-> dict with max violation ratio of the per-element bound (oracle.error_bound),
     NaN/inf class mismatches, per-output-row (Y[m, :]) rel_l2 max, whole-tensor rel_l2,
@@ -83,5 +107,8 @@ def compare(Y, Yref_bits, Yf, S, K, S8=None):
         "row_rel_l2_max": float(np.max(rel_row)) if rel_row.size else 0.0,
         "rel_l2": tot,
         "max_abs": float(np.max(np.where(ok, err, 0.0))) if err.size else 0.0,
+        # per output row (Y[m, :]): max-abs error and rel_l2 of each row
+        "row_max_abs": np.max(np.where(ok, err, 0.0), axis=1) if err.size else np.zeros(0),
+        "row_rel_l2": rel_row,
         "sentinel_left": int(np.sum((Y == Y_SENTINEL) & (Yref_bits != Y_SENTINEL))),
     }

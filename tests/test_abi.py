@@ -267,6 +267,17 @@ def test_decode_geometry_policy():
         rc, d = R.describe("gemm_nt_q_mxfp4_decode" if mk is _mx_ops else
                            "gemm_nt_q_fp8a8_decode", ops)
         assert rc == R.RAD_OK and _geom(d)["waves"] == wv, (M, N, K, d)
+    # long K: the policy's seven / eight waves would overflow the 48 KB staging, four fit
+    # (mxfp4a8 N=21504 K=26624..30720 and fp8a8 at 70B-class down shapes)
+    for (mk, M, N, K) in [(_mx_ops, 1, 21504, 26624), (_mx_ops, 1, 21504, 28672),
+                          (_mx_ops, 1, 21504, 30720), (_f8_ops, 1, 8192, 28672),
+                          (_f8_ops, 1, 16384, 24576)]:
+        ops, _ = mk(M=M, N=N, K=K)
+        rc, d = R.describe("gemm_nt_q_mxfp4_decode" if mk is _mx_ops else
+                           "gemm_nt_q_fp8a8_decode", ops)
+        g = _geom(d)
+        assert rc == R.RAD_OK and g["kernel"] == "quad" and g["waves"] == "4", (M, N, K, d)
+        assert int(g["lds"]) <= 48 * 1024, d
     ops, _ = _mx_ops(M=1, N=21504, K=5376, tunables=[("splitk", 2)])
     g = _geom(R.describe("gemm_nt_q_mxfp4_decode", ops)[1])
     assert g["kernel"] == "quad" and g["chunks"] == "2"
@@ -369,6 +380,12 @@ def test_fused_producer_plan(dtype, row):
         assert rc == R.RAD_OK, (M, N, K, d)
         g = _geom(d)
         assert g["kernel"] == "quad" and g["xq"] == "1" and g["waves"] == "8", d
+    # long K (70B-class down projections): eight waves' staging would pass 48 KB, four fit;
+    # the fused producer still runs.  From K = 31744 on even four waves do not fit (refused).
+    for N, K in [(8192, 24576), (8192, 28672)]:
+        rc, d = R.describe(row, _xq_ops(dtype, 1, N, K))
+        g = _geom(d)
+        assert rc == R.RAD_OK and g["kernel"] == "quad" and g["waves"] == "4", (N, K, d)
     if dtype == "fp8a8":
         rc, d = R.describe(row, _xq_ops(dtype, 1, 512, 1024, rblk=128))
         assert rc == R.RAD_OK and _geom(d)["rblk"] == "128", d
@@ -386,6 +403,38 @@ def test_fused_producer_plan(dtype, row):
         assert R.describe(row, ops)[0] == R.RAD_E_UNSUPPORTED
     tile = "gemm_nt_q_mxfp4" if dtype == "mxfp4a8" else "gemm_nt_q_fp8a8"
     assert R.describe(tile, _xq_ops(dtype, 64, 512, 1024))[0] == R.RAD_E_UNSUPPORTED
+
+
+_QWV_SCRIPT = r"""
+import sys
+sys.path.insert(0, %r)
+sys.path.insert(0, %r)
+import test_abi as T
+import libr3d_amd as R
+for mk, row, M, N, K in [(T._mx_ops, "gemm_nt_q_mxfp4_decode", 1, 5376, 21504),
+                         (T._mx_ops, "gemm_nt_q_mxfp4_decode", 1, 21504, 5376),
+                         (T._f8_ops, "gemm_nt_q_fp8a8_decode", 1, 5376, 21504)]:
+    print(R.describe(row, mk(M=M, N=N, K=K)[0])[1])
+for dt, row in (("mxfp4a8", "gemm_nt_q_mxfp4_decode"), ("fp8a8", "gemm_nt_q_fp8a8_decode")):
+    print(R.describe(row, T._xq_ops(dt, 1, 21504, 5376))[1])
+"""
+
+
+def test_seven_wave_lever_only_where_it_launches():
+    """R3D_GFX950_QWV=7 is honoured without a K split and without the fused producer; with
+    either, the policy decides (the seven-wave kernel has no split or fused form, so
+    describe never reports a geometry the launch would refuse)."""
+    e = {k: v for k, v in os.environ.items() if not k.startswith("R3D_")}
+    e["R3D_GFX950_QWV"] = "7"
+    out = subprocess.run([sys.executable, "-c", _QWV_SCRIPT % (ROOT, os.path.join(ROOT, "tests"))],
+                         env=e, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    got = [_geom(l) for l in out.stdout.strip().splitlines()[-5:]]
+    assert (got[0]["chunks"], got[0]["waves"]) == ("2", "4"), got[0]
+    assert (got[1]["chunks"], got[1]["waves"]) == ("1", "7"), got[1]
+    assert (got[2]["chunks"], got[2]["waves"]) == ("2", "4"), got[2]
+    assert got[3]["xq"] == "1" and got[3]["waves"] == "8", got[3]
+    assert got[4]["xq"] == "1" and got[4]["waves"] == "8", got[4]
 
 
 def test_entries_refuse_without_gfx950():

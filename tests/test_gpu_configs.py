@@ -4,7 +4,10 @@
 Bar (besides the per-element bound of tests/test_gpu_gemm.py): per output row
 rel_l2 <= 2^-8 (one bf16 ulp) and whole-tensor rel_l2 <= 2e-3.  C3 (M=2048 prefill) is
 checked on a seeded sample of activation rows: the kernel computes all 2048, the oracle
-the sampled ones.
+the sampled ones; config 3 as written (bf16 activations, the gemm_nt_q_mxfp4a16 row) also
+has its whole quantised activation plane checked byte for byte.  With R3D_PARITY_LOG set,
+every case appends its figures (whole-tensor and per-row rel_l2, per-row max-abs, the
+fraction of outputs bit-equal to the oracle) to that file as JSON lines.
 """
 import numpy as np
 import pytest
@@ -29,7 +32,7 @@ def _run(row, dtype, A, AS, B, BS, M, N, K, gpu):
     return Y
 
 
-def _grade(Y, A, AS, B, BS, K, dtype, rblk=1):
+def _grade(Y, A, AS, B, BS, K, dtype, rblk=1, case=None, row=None):
     from tests import gpu_util as gu
     if dtype == "mxfp4a8":
         Yr, Yf, S = O.quant_dot_mxfp4a8(A, AS, B, BS, nthreads=NT)
@@ -41,6 +44,8 @@ def _grade(Y, A, AS, B, BS, K, dtype, rblk=1):
     assert c["max_viol"] <= 1.0, c
     assert c["row_rel_l2_max"] <= ROW_REL_MAX, c
     assert c["rel_l2"] <= TENSOR_REL_MAX, c
+    if case:
+        gu.record(case, row, [int(Y.shape[0]), int(B.shape[0]), int(K)], c, Y, Yr)
     print("  rel_l2 %.3e  row_rel_l2_max %.3e  max_abs %.3e  max_viol %.3f" % (
         c["rel_l2"], c["row_rel_l2_max"], c["max_abs"], c["max_viol"]))
     return c
@@ -51,7 +56,7 @@ def test_c0_mxfp4_gemv(gpu):
     _, A, AS = synth.activations(M, K, 0x5EED)
     B, BS = synth.mxfp4_weights(N, K, 0x5EED + 1)
     Y = _run("gemm_nt_q_mxfp4_decode", "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
-    _grade(Y, A, AS, B, BS, K, "mxfp4a8")
+    _grade(Y, A, AS, B, BS, K, "mxfp4a8", case="C0", row="gemm_nt_q_mxfp4_decode")
 
 
 def test_c1_fp8_gemv(gpu):
@@ -59,7 +64,7 @@ def test_c1_fp8_gemv(gpu):
     A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 10)
     B, BS = synth.fp8_weights(N, K, 0x5EED + 11)
     Y = _run("gemm_nt_q_fp8a8_decode", "fp8a8", A, AS, B, BS, M, N, K, gpu)
-    _grade(Y, A, AS, B, BS, K, "fp8a8")
+    _grade(Y, A, AS, B, BS, K, "fp8a8", case="C1", row="gemm_nt_q_fp8a8_decode")
 
 
 C2_SHAPES = {"gate_up": (5376, 21504), "down": (21504, 5376), "qkv": (5376, 8192)}
@@ -72,7 +77,23 @@ def test_c2_mxfp4_decode(gpu, shape, M):
     _, A, AS = synth.activations(M, K, 0x5EED + 20 + M)
     B, BS = synth.mxfp4_weights(N, K, 0x5EED + 21 + K)
     Y = _run("gemm_nt_q_mxfp4_decode", "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
-    _grade(Y, A, AS, B, BS, K, "mxfp4a8")
+    _grade(Y, A, AS, B, BS, K, "mxfp4a8", case="C2 %s M=%d" % (shape, M),
+           row="gemm_nt_q_mxfp4_decode")
+
+
+# config 4's other per-layer shapes (q, k / v, o) at its decode batch M = 4; gate/up and
+# down are config 2's shapes, the lm_head test_c4_lm_head_fp8
+C4_SHAPES = {"q": (5376, 4096), "kv": (5376, 2048), "o": (4096, 5376)}
+
+
+@pytest.mark.parametrize("shape", sorted(C4_SHAPES))
+def test_c4_mxfp4_attention_shapes(gpu, shape):
+    M = 4
+    K, N = C4_SHAPES[shape]
+    _, A, AS = synth.activations(M, K, 0x5EED + 50 + K)
+    B, BS = synth.mxfp4_weights(N, K, 0x5EED + 51 + N)
+    Y = _run("gemm_nt_q_mxfp4_decode", "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+    _grade(Y, A, AS, B, BS, K, "mxfp4a8", case="C4 %s M=4" % shape, row="gemm_nt_q_mxfp4_decode")
 
 
 def test_c3_mxfp4_prefill_sampled(gpu):
@@ -81,7 +102,37 @@ def test_c3_mxfp4_prefill_sampled(gpu):
     B, BS = synth.mxfp4_weights(N, K, 0x5EED + 31)
     Y = _run("gemm_nt_q_mxfp4", "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
     rows = np.sort(np.random.default_rng(3).choice(M, size=12, replace=False))
-    _grade(Y[rows], A[rows], AS[rows], B, BS, K, "mxfp4a8")
+    _grade(Y[rows], A[rows], AS[rows], B, BS, K, "mxfp4a8", case="C3 mxfp4a8 (12 sampled rows)",
+           row="gemm_nt_q_mxfp4")
+
+
+def test_c3_mxfp4a16_as_written(gpu):
+    """Config 3 as written: bf16 N(0,1) activations [2048, 5376] quantised by the row itself
+    to mxfp8 (e4m3 + E8M0 per 32), mxfp4 weights [21504, 5376].  The whole quantised plane
+    in the launch scratch must equal oracle.quant_act_mxfp8 byte for byte; Y is held to the
+    bar against oracle.dot_mx8_mxfp4 on 16 sampled rows (all 21504 columns each)."""
+    from tests import gpu_util as gu
+    from tests.test_gpu_prefill import run_a16
+    M, K, N = 2048, 5376, 21504
+    rng = np.random.default_rng(0x5EED + 32)
+    X = synth.bf16_bits(rng.standard_normal((M, K), dtype=np.float32))
+    B, BS = synth.mxfp4_weights(N, K, 0x5EED + 31)
+    rc, Y, Q, SX, ok = run_a16(X, B, BS, M, N, K, gpu)
+    assert rc == R.RAD_OK and ok
+    Qr, SXr = O.quant_act_mxfp8(X)
+    assert np.array_equal(SX, SXr), np.argwhere(SX != SXr)[:8]
+    assert np.array_equal(Q, Qr), np.argwhere(Q != Qr)[:8]
+    rows = np.sort(np.random.default_rng(7).choice(M, size=16, replace=False))
+    Yr, Yf, S = O.dot_mx8_mxfp4(Qr[rows], SXr[rows], B, BS, nthreads=NT)
+    S8 = O.group8_mag("mxfp4a16", Qr[rows], SXr[rows], B, BS, nthreads=NT)
+    c = gu.compare(Y[rows], Yr, Yf, S, K, S8)
+    assert c["sentinel_left"] == 0 and c["nan_mismatch"] == 0 and c["inf_mismatch"] == 0, c
+    assert c["max_viol"] <= 1.0, c
+    assert c["row_rel_l2_max"] <= ROW_REL_MAX, c
+    assert c["rel_l2"] <= TENSOR_REL_MAX, c
+    assert not np.any(Y == gu.Y_SENTINEL)                  # every output element written
+    gu.record("C3 mxfp4a16 as written (16 sampled rows)", "gemm_nt_q_mxfp4a16", [M, N, K], c,
+              Y[rows], Yr)
 
 
 @pytest.mark.parametrize("rblk", [1, 128])
@@ -95,7 +146,8 @@ def test_c3_shape_fp8a8_prefill_sampled(gpu, rblk):
         BS = BS[::128].copy()                 # one scale row per 128 weight rows
     Y = _run("gemm_nt_q_fp8a8", "fp8a8", A, AS, B, BS, M, N, K, gpu)
     rows = np.sort(np.random.default_rng(5).choice(M, size=12, replace=False))
-    _grade(Y[rows], A[rows], AS[rows], B, BS, K, "fp8a8", rblk)
+    _grade(Y[rows], A[rows], AS[rows], B, BS, K, "fp8a8", rblk,
+           case="C3 shape fp8a8 rblk=%d (12 sampled rows)" % rblk, row="gemm_nt_q_fp8a8")
 
 
 def test_c4_lm_head_fp8(gpu):
@@ -103,4 +155,4 @@ def test_c4_lm_head_fp8(gpu):
     A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 40)
     B, BS = synth.fp8_weights(N, K, 0x5EED + 41)
     Y = _run("gemm_nt_q_fp8a8_decode", "fp8a8", A, AS, B, BS, M, N, K, gpu)
-    _grade(Y, A, AS, B, BS, K, "fp8a8")
+    _grade(Y, A, AS, B, BS, K, "fp8a8", case="C4 lm_head M=4", row="gemm_nt_q_fp8a8_decode")

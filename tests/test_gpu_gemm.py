@@ -224,6 +224,64 @@ def test_mxfp4_dequant_bit_exact(gpu, row):
     assert np.array_equal(Y[fin], Yr[fin])
 
 
+# bf16 weight scales for the fp8a8 dequant test: powers of two first (e4m3 x 2^e is exact
+# in bf16, so the output must equal the dequantised weight itself), then scales whose
+# products round, f32-subnormal products, and the two non-finite scales
+F8_DEQ_SCALES = [1.0, 2.0 ** -30, 2.0 ** -9, 0.5, 2.0, 2.0 ** 7, 2.0 ** 40, 2.0 ** 100,
+                 1.5, -0.75, 3.140625, 448.0, 1.0 / 3.0, 2.0 ** -120, float("nan"), float("inf")]
+F8_DEQ_POW2 = 8
+
+
+@pytest.mark.parametrize("row,mt", [(F8_DEC, 1), (F8_DEC, 4), (F8_DEC, 16), (F8_TILE, 16)])
+@pytest.mark.parametrize("rblk", [1, 128])
+def test_fp8_dequant_bit_exact(gpu, row, mt, rblk):
+    """Every e4m3 weight code (+-0, subnormals, the two NaN codes 0x7F / 0xFF) times each
+    bf16 weight scale of F8_DEQ_SCALES through the product path: activation row m is one-hot
+    e4m3 1.0 at k = m with a_scale 1, weight row n carries codes 16 (n % 16) .. 16 (n % 16)
+    + 15 at k = 0..15, and the 128 rows of block b share scale b (per-row grid: every row of
+    the block holds it; 128-row grid: one scale row per block).  So Y[m, n] =
+    bf16(e4m3(16 (n % 16) + m) * scale[n // 128]).  Bit-exact against the oracle's
+    quant_dot for every code and scale (NaN as a class); value-exact against the dequantised
+    weight for the power-of-two scales.  The decode row runs the quad GEMV at M = 1 and 4
+    (16 / mt calls, activation rows shifted along k) and the line GEMV at 16; the tile row
+    the prefill pipeline."""
+    import torch
+    gu = _gu()
+    K, nsc = 128, len(F8_DEQ_SCALES)
+    N = 128 * nsc
+    n = np.arange(N)
+    B = np.zeros((N, K), np.uint8)
+    for k in range(16):
+        B[:, k] = (16 * (n % 16) + k).astype(np.uint8)
+    sc = synth.bf16_bits(np.array(F8_DEQ_SCALES, np.float32))
+    BS = (np.repeat(sc, 128)[:, None] if rblk == 1 else sc[:, None]).astype(np.uint16)
+    Y = np.zeros((16, N), np.uint16)
+    for c0 in range(0, 16, mt):
+        A = np.zeros((mt, K), np.uint8)
+        for m in range(mt):
+            A[m, c0 + m] = 0x38                              # e4m3 1.0
+        AS = np.ones((mt, 1), np.float32)
+        rc, Yc, guards = gu.run_row(row, "fp8a8", A, AS, B, BS, mt, N, K, gpu)
+        assert rc == R.RAD_OK and guards
+        Y[c0:c0 + mt] = Yc
+    A = np.zeros((16, K), np.uint8)
+    A[np.arange(16), np.arange(16)] = 0x38
+    Yr, _, _ = O.quant_dot_fp8a8(A, np.ones((16, 1), np.float32), B, BS, rblk)
+    got, ref = O.bf16_to_f32(Y), O.bf16_to_f32(Yr)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    codes = (16 * (n[None, :] % 16) + np.arange(16)[:, None]).astype(np.uint8)   # [m, n]
+    assert np.isnan(got[(codes & 0x7F) == 0x7F]).all()       # the two NaN codes
+    fin = ~np.isnan(ref)
+    bad = np.argwhere((Y != Yr) & fin & ~((got == 0) & (ref == 0)))
+    assert bad.size == 0, "bits differ at %s: got %s want %s" % (
+        bad[:5].tolist(), [hex(Y[tuple(b)]) for b in bad[:5]], [hex(Yr[tuple(b)]) for b in bad[:5]])
+    # value-exact against the dequantised weight where the scale is a power of two
+    deq = (O.e4m3_to_f32(codes).astype(np.float64) *
+           np.array(F8_DEQ_SCALES, np.float64)[n // 128][None, :])
+    p2 = (n // 128 < F8_DEQ_POW2)[None, :] & np.isfinite(deq)
+    assert np.array_equal(got[p2].astype(np.float64), deq[p2])
+
+
 @pytest.mark.parametrize("row", [MX_DEC, MX_TILE])
 def test_mxfp4_nan_scale_poisons(gpu, row):
     """A 0xFF scale byte poisons its whole output element even when every code in its

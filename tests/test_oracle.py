@@ -453,3 +453,31 @@ def test_group8_mag_bounds():
     _, _, S = O.quant_dot_mxfp4a8(A, AS, B, BS)
     S8 = O.group8_mag("mxfp4a8", A, AS, B, BS)
     assert (S8 <= S * (1 + 1e-5)).all() and (S8 >= S / 8 * (1 - 1e-5)).all()
+
+
+@pytest.mark.parametrize("enc", ["mxfp4a8", "fp8a8"])
+def test_group8_mag_is_sum_of_group_maxima(enc):
+    """S8 is the sum over 8-wide k groups of each group's LARGEST scaled product: products
+    {1, 2, 3} in group 0 and {4} in group 1 give S8 = 3 + 4 = 7 -- a sum inside the groups
+    would give 10, a maximum over all k 4, a missing scale or a wrong group width
+    something else.  The scales (a_scale 2, weight scale 2^-1) multiply every product."""
+    K = 128
+    A = np.zeros((1, K), np.uint8)
+    A[0, [0, 1, 2, 8]] = 0x38                                   # e4m3 1.0
+    AS = np.full((1, 1), 2.0, np.float32)
+    if enc == "mxfp4a8":
+        w = np.zeros(K, np.uint8)
+        w[[0, 1, 2, 8]] = [2, 4, 5, 6]                          # e2m1 1, 2, 3, 4
+        B = (w[0::2] | (w[1::2] << 4)).astype(np.uint8)[None, :]
+        BS = np.full((1, K // 32), 126, np.uint8)               # 2^-1
+    else:
+        B = np.zeros((1, K), np.uint8)
+        B[0, [0, 1, 2, 8]] = [0x38, 0x40, 0x44, 0x48]           # e4m3 1, 2, 3, 4
+        BS = synth.bf16_bits(np.full((1, 1), 0.5, np.float32))
+    S8 = O.group8_mag(enc, A, AS, B, BS)
+    assert S8[0, 0] == np.float32(7.0), S8
+    if enc == "mxfp4a8":
+        _, _, S = O.quant_dot_mxfp4a8(A, AS, B, BS)
+    else:
+        _, _, S = O.quant_dot_fp8a8(A, AS, B, BS, 1)
+    assert S[0, 0] == np.float32(10.0), S
