@@ -236,23 +236,29 @@ F8_DEQ_POW2 = 8
 @pytest.mark.parametrize("rblk", [1, 128])
 def test_fp8_dequant_bit_exact(gpu, row, mt, rblk):
     """Every e4m3 weight code (+-0, subnormals, the two NaN codes 0x7F / 0xFF) times each
-    bf16 weight scale of F8_DEQ_SCALES through the product path: activation row m is one-hot
-    e4m3 1.0 at k = m with a_scale 1, weight row n carries codes 16 (n % 16) .. 16 (n % 16)
-    + 15 at k = 0..15, and the 128 rows of block b share scale b (per-row grid: every row of
-    the block holds it; 128-row grid: one scale row per block).  So Y[m, n] =
-    bf16(e4m3(16 (n % 16) + m) * scale[n // 128]).  Bit-exact against the oracle's
-    quant_dot for every code and scale (NaN as a class); value-exact against the dequantised
-    weight for the power-of-two scales.  The decode row runs the quad GEMV at M = 1 and 4
-    (16 / mt calls, activation rows shifted along k) and the line GEMV at 16; the tile row
-    the prefill pipeline."""
-    import torch
+    bf16 weight scale of F8_DEQ_SCALES through the product path.  Activation row m is
+    one-hot e4m3 1.0 at k = m with a_scale 1.  Weight rows come in groups of 32: row j < 16
+    of a group carries codes 16 j .. 16 j + 15 at k = 0..15 (a NaN code replaced by 0: any
+    NaN code in a row poisons all its outputs, 0 x NaN being NaN), row 16 the code 0x7F
+    alone and row 17 0xFF alone at k = 0, the rest zeros; the 128 rows of block b share
+    scale b (per-row grid: every row of the block holds it; 128-row grid: one scale row per
+    block).  So Y[m, n] = bf16(e4m3(16 j + m) * scale[n // 128]) for j = n % 32 < 16, and
+    NaN in every row m for j = 16, 17.  Bit-exact against the oracle's quant_dot for every
+    code and scale (NaN as a class); value-exact against the dequantised weight for the
+    power-of-two scales.  The decode row runs the quad GEMV at M = 1 and 4 (16 / mt calls,
+    activation rows shifted along k) and the line GEMV at 16; the tile row the prefill
+    pipeline."""
     gu = _gu()
     K, nsc = 128, len(F8_DEQ_SCALES)
     N = 128 * nsc
     n = np.arange(N)
+    j = n % 32
     B = np.zeros((N, K), np.uint8)
     for k in range(16):
-        B[:, k] = (16 * (n % 16) + k).astype(np.uint8)
+        c = (16 * j + k).astype(np.uint8)
+        B[:, k] = np.where((j < 16) & ((c & 0x7F) != 0x7F), c, 0)
+    B[j == 16, 0] = 0x7F
+    B[j == 17, 0] = 0xFF
     sc = synth.bf16_bits(np.array(F8_DEQ_SCALES, np.float32))
     BS = (np.repeat(sc, 128)[:, None] if rblk == 1 else sc[:, None]).astype(np.uint16)
     Y = np.zeros((16, N), np.uint16)
@@ -269,16 +275,18 @@ def test_fp8_dequant_bit_exact(gpu, row, mt, rblk):
     Yr, _, _ = O.quant_dot_fp8a8(A, np.ones((16, 1), np.float32), B, BS, rblk)
     got, ref = O.bf16_to_f32(Y), O.bf16_to_f32(Yr)
     assert np.array_equal(np.isnan(got), np.isnan(ref))
-    codes = (16 * (n[None, :] % 16) + np.arange(16)[:, None]).astype(np.uint8)   # [m, n]
-    assert np.isnan(got[(codes & 0x7F) == 0x7F]).all()       # the two NaN codes
+    assert np.isnan(got[:, (j == 16) | (j == 17)]).all()     # the two NaN codes
     fin = ~np.isnan(ref)
     bad = np.argwhere((Y != Yr) & fin & ~((got == 0) & (ref == 0)))
     assert bad.size == 0, "bits differ at %s: got %s want %s" % (
         bad[:5].tolist(), [hex(Y[tuple(b)]) for b in bad[:5]], [hex(Yr[tuple(b)]) for b in bad[:5]])
-    # value-exact against the dequantised weight where the scale is a power of two
-    deq = (O.e4m3_to_f32(codes).astype(np.float64) *
+    # value-exact against the dequantised weight where the scale is a power of two: all
+    # 254 non-NaN codes at each of the F8_DEQ_POW2 scales
+    codes = (16 * j[None, :] + np.arange(16)[:, None]).astype(np.uint8)            # [m, n]
+    p2 = ((n // 128 < F8_DEQ_POW2) & (j < 16))[None, :] & ((codes & 0x7F) != 0x7F)
+    deq = (O.e4m3_to_f32(np.where(p2, codes, 0).astype(np.uint8)).astype(np.float64) *
            np.array(F8_DEQ_SCALES, np.float64)[n // 128][None, :])
-    p2 = (n // 128 < F8_DEQ_POW2)[None, :] & np.isfinite(deq)
+    assert len(np.unique(codes[p2])) == 254
     assert np.array_equal(got[p2].astype(np.float64), deq[p2])
 
 
