@@ -90,6 +90,17 @@ int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s);
  * src/r3d_gemm_fp8a8.hip:1246-1253 (r3d_rad_gemm_nt_q_gated_fp8_scratch). */
 int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a);
 
+/* gemm_nt_q at dtype "mxfp4a16" that allocates nothing: no counterpart in the reference,
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same operands, parameters, kernels and results as
+ * r3d_rad_gemm_nt_q_mxfp4a16, but RadArgs::scratch is not used: the quantised activations
+ * go to a static device buffer of R3D_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends.  A call needing more (round256(M*K) + M*K/32 bytes) is refused with
+ * RAD_E_SHAPE and a line on stderr.  All calls on one GPU share its buffer: calls that
+ * overlap on one GPU (other streams, other threads) race. */
+#define R3D_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int r3d_rad_gemm_nt_q_mxfp4a16_noalloc(const RadArgs* a, RadStream s);
+
 /* Host-only diagnostic with no counterpart in the reference: runs `row`'s preamble and
  * plan on `a` and writes the chosen arm and launch geometry (or the refusal) into buf.
  * Launches nothing, touches no device memory.  Returns the plan's status code. */

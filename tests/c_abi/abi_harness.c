@@ -76,6 +76,7 @@ static const void* const kExports[] = {
     (const void*)r3d_rad_gemm_nt_q, (const void*)r3d_rad_gemm_nt_q_mxfp4_decode,
     (const void*)r3d_rad_gemm_nt_q_fp8, (const void*)r3d_rad_gemm_nt_q_fp8_decode,
     (const void*)r3d_rad_gemm_nt_q_mxfp4a16, (const void*)r3d_rad_gemm_nt_q_mxfp4a16_scratch,
+    (const void*)r3d_rad_gemm_nt_q_mxfp4a16_noalloc,
     (const void*)r3d_rad_quant_act_fp8, (const void*)r3d_rad_gated_quant_fp8,
     (const void*)r3d_rad_rmsnorm_quant_fp8, (const void*)r3d_rad_gemm_nt_q_gated_fp8,
     (const void*)r3d_rad_gemm_nt_q_gated_fp8_scratch, (const void*)r3d_gfx950_describe,
