@@ -260,6 +260,9 @@ class GemmOperands:
                 t[i].shape[r] = int(s_)
                 t[i].stride[r] = int(st)
 
+        # the launch reads raw pointers: hold the tensors so none is freed (and its memory
+        # reused) while this object can still launch
+        self._tensors = [a, a_scale, b, b_scale, y, a_sum, b_ref]
         fused = a is not None and a_scale is None and a.element_size() == 2
         fill(0, a, "BF16" if dtype == "mxfp4a16" or fused else "F8E4M3")
         fill(1, a_scale, "F32")
@@ -313,11 +316,13 @@ class GemmOperands:
 
     def set_scratch(self, scratch, nbytes=None):
         """Hand `scratch` (a device tensor) to the launch as RadArgs::scratch."""
+        self._scratch = scratch
         self.args.scratch = scratch.data_ptr()
         self.args.scratch_bytes = int(nbytes if nbytes is not None
                                       else scratch.numel() * scratch.element_size())
 
     def set_y(self, y):
+        self._tensors[4] = y
         self._t[4].data = y.data_ptr()
 
 
@@ -333,6 +338,7 @@ class QuantActOperands:
     def __init__(self, x, q, scale, *, n, group, M=None, x_dtype=None, dtype=None,
                  shapes=None, strides=None):
         t = (RadTensor * 3)()
+        self._tensors = [x, q, scale]                 # held while this object can launch
         xdt = x_dtype or ("F32" if str(x.dtype).endswith("float32") else "BF16")
         shapes = shapes or {}
         strides = strides or {}
@@ -380,6 +386,7 @@ class _Args:
 
     def __init__(self, operands, params):
         t = (RadTensor * len(operands))()
+        self._tensors = [op[0] for op in operands]   # held while this object can launch
         for i, (ten, dt, shp, std) in enumerate(operands):
             if ten is None:
                 t[i].data = None
@@ -418,6 +425,7 @@ class _Args:
 
     def set_scratch(self, scratch, nbytes=None):
         """Hand `scratch` (a device tensor) to the launch as RadArgs::scratch."""
+        self._scratch = scratch
         self.args.scratch = scratch.data_ptr()
         self.args.scratch_bytes = int(nbytes if nbytes is not None
                                       else scratch.numel() * scratch.element_size())

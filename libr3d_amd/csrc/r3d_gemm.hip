@@ -12,9 +12,11 @@
 #include <hip/hip_runtime.h>
 
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "r3d_band.h"
+#include "r3d_dump.h"
 #include "r3d_gemm_kernels.h"
 #include "r3d_gemv_lines.h"
 #include "r3d_gemv_quad.h"
@@ -63,7 +65,23 @@ static void debug_once(const char* what, int key) {
     fprintf(stderr, "libr3d_gfx950: %s launched\n", what);
 }
 
+/* A launch that failed: report it on stderr (the caller's next arm takes the launch, as the
+ * reference re-launches a failed arm on the same operands, src/r3d_gemm_mxfp4.hip:1666-1670,
+ * 2118-2122).  R3D_GFX950_FAIL_ARM (a test lever) names arms -- "quad", "lines", "skinny"
+ * -- that report a failure without launching anything, so the fallbacks can be exercised. */
+static bool forced_fail(const char* arm) {
+    static const char* e = getenv("R3D_GFX950_FAIL_ARM");
+    return e && strstr(e, arm) != nullptr;
+}
+
+static int launch_failed(const char* what, hipError_t e) {
+    fprintf(stderr, "libr3d_gfx950: %s launch FAILED (%s)\n", what,
+            e == hipSuccess ? "forced by R3D_GFX950_FAIL_ARM" : hipGetErrorName(e));
+    return RAD_E_DEVICE;
+}
+
 static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream) {
+    if (forced_fail("quad")) return launch_failed("quad decode GEMV", hipSuccess);
     const dim3 grid((unsigned)g.blocks), block((unsigned)(64 * g.wv));
     /* mxfp4 scale rows contiguous (pitch = K/32) in a 16-byte aligned plane: 1 KB staging loads */
     const int sc16 = P.enc == ENC_MXFP4A8 && P.bs_pitch == P.K / 32 &&
@@ -107,10 +125,7 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
 #undef R3D_QUAD1
 #undef R3D_QUADW
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        fprintf(stderr, "libr3d_gfx950: quad decode GEMV launch FAILED (%s)\n", hipGetErrorName(e));
-        return RAD_E_DEVICE;
-    }
+    if (e != hipSuccess) return launch_failed("quad decode GEMV", e);
     debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 quad decode GEMV" : "fp8a8 quad decode GEMV",
                128 + (P.enc << 4) + g.mt + 2 * P.xq);
     return RAD_OK;
@@ -120,6 +135,8 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
  * 16-row call's arithmetic; g is the 16-row geometry */
 static int launch_lines(const GemmPlan& P, const LinesGeom& g, hipStream_t stream,
                         int passes = 1) {
+    if (forced_fail(passes > 1 ? "skinny" : "lines"))
+        return launch_failed(passes > 1 ? "skinny line GEMV" : "line decode GEMV", hipSuccess);
     const dim3 grid((unsigned)g.blocks, (unsigned)passes), block(256);
 #define R3D_LINES(ENC_, MT_, TW_, D_)                                                        \
     hipLaunchKernelGGL((gemv_lines_kernel<ENC_, MT_, TW_, D_>), grid, block, (size_t)g.lds,    \
@@ -151,23 +168,27 @@ static int launch_lines(const GemmPlan& P, const LinesGeom& g, hipStream_t strea
 #undef R3D_LINES_D
 #undef R3D_LINES
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        fprintf(stderr, "libr3d_gfx950: line decode GEMV launch FAILED (%s)\n", hipGetErrorName(e));
-        return RAD_E_DEVICE;
-    }
+    if (e != hipSuccess) return launch_failed("line decode GEMV", e);
     debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 line decode GEMV" : "fp8a8 line decode GEMV",
                192 + (P.enc << 4) + g.mt);
     return RAD_OK;
 }
 
+/* The decode arms in order of preference -- quad GEMV (M <= 4), line GEMV (M = 5..16),
+ * 16-row GEMV (any M <= 16) -- each taking the launch when the one before does not serve
+ * the shape or fails to launch (a failed arm wrote nothing: the next one writes all of Y). */
 static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) {
     QuadGeom qg{};
-    if (quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg, P.xq))
-        return launch_quad(P, qg, stream);
-    if (P.xq) return RAD_E_UNSUPPORTED;     /* fused bf16 activations: the quad GEMV only */
+    if (quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg, P.xq)) {
+        const int rc = launch_quad(P, qg, stream);
+        if (rc == RAD_OK || P.xq) return rc;   /* fused bf16 activations: the quad GEMV only */
+    } else if (P.xq) {
+        return RAD_E_UNSUPPORTED;
+    }
     LinesGeom lg{};
-    if (lines_fits(P) && lines_geom(P.enc, P.M, P.N, P.K, splitk, &lg))
-        return launch_lines(P, lg, stream);
+    if (lines_fits(P) && lines_geom(P.enc, P.M, P.N, P.K, splitk, &lg)) {
+        if (launch_lines(P, lg, stream) == RAD_OK) return RAD_OK;
+    }
     DecodeGeom g{};
     decode_geom(P.M, P.N, P.K, splitk, &g, gemv_wave_lds(P.enc, P.M <= 1 ? 1 : P.M <= 4 ? 4 : 16));
     const dim3 grid((unsigned)g.blocks), block((unsigned)(64 * g.waves));
@@ -187,10 +208,7 @@ static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) 
     }
 #undef R3D_GEMV
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        fprintf(stderr, "libr3d_gfx950: decode GEMV launch FAILED (%s)\n", hipGetErrorName(e));
-        return RAD_E_DEVICE;
-    }
+    if (e != hipSuccess) return launch_failed("decode GEMV", e);
     debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 decode GEMV" : "fp8a8 decode GEMV",
                (P.enc << 4) | (g.mt << 1));
     return RAD_OK;
@@ -207,19 +225,23 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0) 
         GemmPlan S = P;
         S.M = 16;
         LinesGeom lg{};
-        if (lines_fits(S) && lines_geom(P.enc, 16, P.N, P.K, 0, &lg) && lg.mt == 16)
-            return launch_lines(P, lg, stream, passes);      /* all passes in one launch */
-        for (int p = 0; p < passes; ++p) {
-            GemmPlan S = P;
-            const int64_t m0 = 16 * (int64_t)p;
-            S.M = P.M - m0 < 16 ? P.M - m0 : 16;
-            S.A = P.A + m0 * P.a_pitch;
-            S.AS = P.AS + m0 * P.as_pitch;
-            S.Y = P.Y + m0 * P.y_pitch;
-            const int rc = launch_decode(S, 0, stream);
-            if (rc) return rc;
+        int rc = RAD_E_DEVICE;
+        if (lines_fits(S) && lines_geom(P.enc, 16, P.N, P.K, 0, &lg) && lg.mt == 16) {
+            rc = launch_lines(P, lg, stream, passes);       /* all passes in one launch */
+        } else {
+            rc = RAD_OK;
+            for (int p = 0; p < passes && rc == RAD_OK; ++p) {
+                GemmPlan S = P;
+                const int64_t m0 = 16 * (int64_t)p;
+                S.M = P.M - m0 < 16 ? P.M - m0 : 16;
+                S.A = P.A + m0 * P.a_pitch;
+                S.AS = P.AS + m0 * P.as_pitch;
+                S.Y = P.Y + m0 * P.y_pitch;
+                rc = launch_decode(S, 0, stream);
+            }
         }
-        return RAD_OK;
+        if (rc == RAD_OK) return RAD_OK;
+        /* a failed pass: the prefill pipeline below recomputes every row of Y */
     }
     const int mode = P.enc == ENC_MXFP4A16 ? PF_MX8 : P.enc == ENC_FP8A8 ? PF_F8 : PF_A8;
     PrefillGeom g{};
@@ -284,10 +306,7 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0) 
     }
 #undef R3D_PF
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        fprintf(stderr, "libr3d_gfx950: prefill launch FAILED (%s)\n", hipGetErrorName(e));
-        return RAD_E_DEVICE;
-    }
+    if (e != hipSuccess) return launch_failed("prefill", e);
     debug_once(mode == PF_MX8 ? "mxfp4a16 prefill (mxfp8 quantiser + MFMA)"
                : mode == PF_F8 ? "fp8a8 prefill" : "mxfp4a8 prefill",
                160 + 8 * mode + g.wnf);
@@ -502,26 +521,40 @@ static int gemm_gated_entry(const RadArgs* a, RadStream s) {
 
 }  // namespace r3d
 
+/* The row entries (each the launch pointer of the row named in its dump_wrap call, and the
+ * name under which R3D_DUMP captures it). */
 extern "C" {
 
-int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s) { return r3d::quant_entry(a, s); }
-int r3d_rad_gated_quant_fp8(const RadArgs* a, RadStream s) { return r3d::gated_entry(a, s); }
-int r3d_rad_rmsnorm_quant_fp8(const RadArgs* a, RadStream s) { return r3d::rms_entry(a, s); }
+int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s) {
+    return r3d::dump_wrap("quant_act_fp8_act", a, s, r3d::quant_entry);
+}
+int r3d_rad_gated_quant_fp8(const RadArgs* a, RadStream s) {
+    return r3d::dump_wrap("gated_quant_fp8_act", a, s, r3d::gated_entry);
+}
+int r3d_rad_rmsnorm_quant_fp8(const RadArgs* a, RadStream s) {
+    return r3d::dump_wrap("rmsnorm_quant_fp8", a, s, r3d::rms_entry);
+}
 int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s) {
-    return r3d::gemm_gated_entry(a, s);
+    return r3d::dump_wrap("gemm_nt_q_gated_fp8a8", a, s, r3d::gemm_gated_entry);
 }
 int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a) {
     return r3d::gemm_gated_scratch_bytes(a);
 }
 
 int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s) {
-    return r3d::entry(a, s, r3d::ENC_MXFP4A8, false);
+    return r3d::dump_wrap("gemm_nt_q_mxfp4", a, s, [](const RadArgs* x, RadStream t) {
+        return r3d::entry(x, t, r3d::ENC_MXFP4A8, false);
+    });
 }
 int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s) {
-    return r3d::entry(a, s, r3d::ENC_MXFP4A8, true);
+    return r3d::dump_wrap("gemm_nt_q_mxfp4_decode", a, s, [](const RadArgs* x, RadStream t) {
+        return r3d::entry(x, t, r3d::ENC_MXFP4A8, true);
+    });
 }
 int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s) {
-    return r3d::entry(a, s, r3d::ENC_MXFP4A16, false);
+    return r3d::dump_wrap("gemm_nt_q_mxfp4a16", a, s, [](const RadArgs* x, RadStream t) {
+        return r3d::entry(x, t, r3d::ENC_MXFP4A16, false);
+    });
 }
 int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a) {
     long long M = 0, K = 0;
@@ -530,10 +563,14 @@ int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a) {
     return r3d::mxfp4a16_scratch_bytes(M, K);
 }
 int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s) {
-    return r3d::entry(a, s, r3d::ENC_FP8A8, false);
+    return r3d::dump_wrap("gemm_nt_q_fp8a8", a, s, [](const RadArgs* x, RadStream t) {
+        return r3d::entry(x, t, r3d::ENC_FP8A8, false);
+    });
 }
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s) {
-    return r3d::entry(a, s, r3d::ENC_FP8A8, true);
+    return r3d::dump_wrap("gemm_nt_q_fp8a8_decode", a, s, [](const RadArgs* x, RadStream t) {
+        return r3d::entry(x, t, r3d::ENC_FP8A8, true);
+    });
 }
 int r3d_gfx950_describe(const char* row, const RadArgs* a, char* buf, int len) {
     return r3d::describe(row, a, buf, len);

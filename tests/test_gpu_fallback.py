@@ -1,0 +1,66 @@
+"""A failed arm hands its launch to the next one on the same operands, as the reference's
+entries do (src/r3d_gemm_mxfp4.hip:1666-1670 skinny -> tile, :2118-2122 q8x -> legacy
+walk), instead of returning RAD_E_DEVICE at issue time.  The failures are forced from the
+host with the test lever R3D_GFX950_FAIL_ARM, which makes the named arms report a launch
+failure without launching anything; each setting runs in a child process (the lever is
+read once per process), whose calls must still succeed, log the failure, and match the
+oracle within the bar of tests/test_gpu_gemm.py."""
+import json
+import os
+import subprocess
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+_CHILD = r"""
+import json, sys
+sys.path.insert(0, %r)
+import numpy as np
+import torch
+import libr3d_amd as R
+import oracle as O
+from tests import gpu_util as gu
+from tests.test_gpu_gemm import _mx_case, _f8_case
+dev = torch.device("cuda:0")
+out = []
+for row, dtype, M, N, K in %r:
+    if dtype == "mxfp4a8":
+        A, AS, B, BS = _mx_case(M, N, K, M + N)
+        Yr, Yf, S = O.quant_dot_mxfp4a8(A, AS, B, BS, nthreads=8)
+    else:
+        A, AS, B, BS = _f8_case(M, N, K, M + N, 1)
+        Yr, Yf, S = O.quant_dot_fp8a8(A, AS, B, BS, 1, nthreads=8)
+    S8 = O.group8_mag(dtype, A, AS, B, BS, 1, nthreads=8)
+    rc, Y, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, dev)
+    c = gu.compare(Y, Yr, Yf, S, K, S8)
+    out.append([row, M, rc, guards, c["max_viol"], c["sentinel_left"], c["nan_mismatch"]])
+print("RESULT " + json.dumps(out))
+"""
+
+MX_DEC, MX_TILE, F8_DEC = "gemm_nt_q_mxfp4_decode", "gemm_nt_q_mxfp4", "gemm_nt_q_fp8a8_decode"
+
+
+@pytest.mark.parametrize("arms,cases,logged", [
+    # the quad GEMV fails: M <= 4 runs on the 16-row GEMV
+    ("quad", [(MX_DEC, "mxfp4a8", 1, 300, 1024), (F8_DEC, "fp8a8", 3, 300, 1024)],
+     "quad decode GEMV launch FAILED"),
+    # the line GEMV fails: M = 5..16 runs on the 16-row GEMV
+    ("lines", [(MX_DEC, "mxfp4a8", 9, 300, 1024), (F8_DEC, "fp8a8", 16, 300, 1024)],
+     "line decode GEMV launch FAILED"),
+    # the skinny band's passes fail: the prefill pipeline takes M = 17..64
+    ("skinny", [(MX_TILE, "mxfp4a8", 40, 1000, 2048)], "skinny line GEMV launch FAILED"),
+])
+def test_failed_arm_falls_back(gpu, arms, cases, logged):
+    env = dict(os.environ, R3D_GFX950_FAIL_ARM=arms, R3D_DEBUG_GEMM="1")
+    p = subprocess.run([sys.executable, "-c", _CHILD % (ROOT, cases)], env=env,
+                       capture_output=True, text=True, timeout=300)
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    assert logged in p.stderr, p.stderr[-2000:]
+    line = [l for l in p.stdout.splitlines() if l.startswith("RESULT ")][-1]
+    for row, M, rc, guards, viol, unwritten, nan_mm in json.loads(line[7:]):
+        assert rc == 0 and guards, (row, M, rc)
+        assert viol <= 1.0 and unwritten == 0 and nan_mm == 0, (row, M, viol, unwritten)
