@@ -293,7 +293,8 @@ def main():
 CASES = (["c0", "c1", "c3_a16", "c3_a16_quant", "c3_a16_gemm", "c3_a8", "c3_f8", "lm_head_M4"] +
          ["c2_%s_M%d" % (s, m) for s in ("gate_up", "down", "qkv") for m in (1, 4, 16)] +
          ["c4_%s_M4" % s for s in ("q", "kv", "o")] +
-         ["skinny_%s_M%d" % (s, m) for s in ("gate_up", "down", "qkv") for m in (17, 32, 64)])
+         ["skinny_%s_M%d" % (s, m) for s in ("gate_up", "down", "qkv") for m in (17, 32, 64)] +
+         ["lm_head_e4m3_M%d" % m for m in (1, 4, 8, 16)])
 C2_SHAPES = {"gate_up": (5376, 21504), "down": (21504, 5376), "qkv": (5376, 8192)}
 C4_SHAPES = {"q": (5376, 4096), "kv": (5376, 2048), "o": (4096, 5376)}
 
@@ -363,6 +364,8 @@ def run_case(name, dev, stream, steps, warmup):
                     "frac_fp8_peak": round(fl / kern / 1e12 / FP8_PEAK_TFLOPS, 4),
                     "plan": R.describe(row, c.ops[0])[1]})
         return res
+    if name.startswith("lm_head_e4m3_"):
+        return bench_lm_head_e4m3(int(name.rsplit("_M", 1)[1]), dev, stream, steps, warmup, res)
     # bandwidth-bound workloads
     if name == "c1" or name == "lm_head_M4":
         M, K, N = (1, 5376, 21504) if name == "c1" else (4, 5376, 262144)
@@ -394,6 +397,45 @@ def run_case(name, dev, stream, steps, warmup):
                 "frac_hbm": round(nb / kern / 1e9 / HBM_PEAK_GBS, 4),
                 "GBps_wall": round(nb * steps / wall / 1e9, 1),
                 "plan": R.describe(row, c.ops[0])[1]})
+    return res
+
+
+def bench_lm_head_e4m3(M, dev, stream, steps, warmup, res):
+    """The 27B head as logits_gemm_e4m3 reads it: n_vocab 262144 x n_embd 5376 e4m3 codes
+    (uniform over the 254 finite codes) with one bf16 scale per (row, 128 columns), joined
+    in device memory; bf16 N(0,1) x [M, 5376]; f32 logits.  Bytes per launch: codes +
+    scales + x + logits."""
+    import torch
+    import libr3d_amd as R
+    from libr3d_amd import synth
+    N, K = 262144, 5376
+    hdr, c_off, s_off, nb_blob = R.head_header(N, K, "bf16", 1)
+    blob = torch.empty(nb_blob, dtype=torch.uint8, device=dev)
+    blob[:hdr.size].copy_(torch.from_numpy(hdr))
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x5EED + 60)
+    codes = torch.randint(0, 256, (N * K,), dtype=torch.int32, device=dev, generator=g)
+    codes = torch.where((codes & 0x7F) == 0x7F, codes - 1, codes)       # no NaN codes
+    blob[c_off:c_off + N * K].copy_(codes.to(torch.uint8))
+    del codes
+    scols = (K + 127) // 128
+    sv = (torch.rand((N * scols,), device=dev, generator=g) + 0.5) * (0.02 / 448)
+    blob[s_off:s_off + N * scols * 2].copy_(sv.to(torch.bfloat16).view(torch.uint8))
+    del sv
+    X = synth.bf16_bits(np.random.default_rng(0x5EED + 61).standard_normal((M, K)).astype(np.float32))
+    x = torch.from_numpy(X.view(np.int16)).to(dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+
+    class _Case:
+        ops = [R.LogitsOperands(x, blob, y, n_vocab=N, n_embd=K)]
+    row = "logits_gemm_e4m3"
+    wall, kern = time_case(_Case, row, steps, warmup, stream)
+    R.forget_head(blob)
+    nb = N * K + N * scols * 2 + M * K * 2 + M * N * 4
+    res.update({"M": M, "K": K, "N": N, "row": row, "bytes": nb,
+                "kernel": "r3d::logits_e4m3_kernel<2, 0>", "kernel_us": round(kern * 1e6, 3),
+                "GBps": round(nb / kern / 1e9, 1), "frac_hbm": round(nb / kern / 1e9 / HBM_PEAK_GBS, 4),
+                "GBps_wall": round(nb * steps / wall / 1e9, 1)})
     return res
 
 

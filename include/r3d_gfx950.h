@@ -10,6 +10,7 @@
 
 #include <stdint.h>
 #include "rad_abi.h"
+#include "rad_planes.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -89,6 +90,43 @@ int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s);
 /* The gated row's scratch hook: 64 * N * 2 bytes (0 without N).  Replaces
  * src/r3d_gemm_fp8a8.hip:1246-1253 (r3d_rad_gemm_nt_q_gated_fp8_scratch). */
 int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a);
+
+/* logits_gemm over a joined e4m3 + block-scale head: bf16 x [M, n_embd], lm_head a
+ * joined-planes blob (rad_planes.h: "codes" e4m3 [n_vocab, n_embd] dense, "scale" bf16 /
+ * f16 / f32 per (1 or 128 rows, 128 columns)), f32 logits [M, n_vocab], M =
+ * numel(logits) / n_vocab.  Replaces src/r3d_gemm_logits.hip:144-226
+ * (r3d_rad_logits_gemm_e4m3).  The first launch over a blob in device memory reads its
+ * header with one synchronous copy (cached per device and address); see
+ * r3d_gfx950_logits_head_forget. */
+int r3d_rad_logits_gemm_e4m3(const RadArgs* a, RadStream s);
+
+/* The joined head's byte layout, in host memory.  These replace the reference row's
+ * layout hooks (src/r3d_gemm_logits.hip:233-272: r3d_layout_head / r3d_relayout_head /
+ * r3d_unrelayout_head), which join radiance's encoded planes through its rad_planes
+ * helpers; here the two planes are passed directly.
+ *   _bytes: the blob's size for n_vocab x n_embd codes and a scale plane of scale_dtype
+ *           (RAD_BF16 / RAD_F16 / RAD_F32) with scale_block_rows (1 or 128) rows per
+ *           element, or a negative RAD_E_* code;
+ *   _header: the same, and the header itself into *out (the planes go at its entries'
+ *           offsets: a caller can stream them straight into device memory);
+ *   _join:  writes header, codes (rows codes_pitch bytes apart) and scale (rows
+ *           scale_pitch_bytes apart, (n_embd + 127) / 128 elements each) into dst;
+ *   _split: the inverse, into dense planes (either pointer may be null). */
+int64_t r3d_gfx950_logits_head_bytes(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,
+                                     int64_t scale_block_rows);
+int64_t r3d_gfx950_logits_head_header(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,
+                                      int64_t scale_block_rows, RadPlanesHeader* out);
+int r3d_gfx950_logits_head_join(const uint8_t* codes, int64_t codes_pitch, const void* scale,
+                                int64_t scale_pitch_bytes, int64_t n_vocab, int64_t n_embd,
+                                uint32_t scale_dtype, int64_t scale_block_rows, void* dst,
+                                int64_t dst_bytes);
+int r3d_gfx950_logits_head_split(const void* blob, int64_t blob_bytes, uint8_t* codes,
+                                 void* scale);
+
+/* No counterpart in the reference: drops the cached header of the blob at `blob` (every
+ * device).  Call it before a different head is joined at an address a launch has used;
+ * a launch whose cached header no longer matches the device's writes NaN logits. */
+void r3d_gfx950_logits_head_forget(const void* blob);
 
 /* gemm_nt_q at dtype "mxfp4a16" that allocates nothing: no counterpart in the reference,
  * for callers that cannot allocate (code under HIP graph capture, tight serving loops,

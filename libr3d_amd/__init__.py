@@ -20,7 +20,8 @@ __all__ = [
     "RadKernelInfo", "RadOpSchema", "lib", "lib_path", "rows", "schemas", "resolve",
     "launch_row", "gemm_nt_q", "describe", "GemmOperands", "QuantActOperands", "quant_act_fp8",
     "GatedQuantOperands", "GatedGemmOperands", "RmsNormQuantOperands", "build_id",
-    "check_build_id", "mxfp4a16_stage",
+    "check_build_id", "mxfp4a16_stage", "LogitsOperands", "logits_gemm", "head_bytes",
+    "join_head", "split_head", "forget_head", "head_header",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -133,6 +134,21 @@ def lib():
                                                 ctypes.c_int]
         L.r3d_gfx950_build_id.restype = ctypes.c_char_p
         L.r3d_gfx950_build_id.argtypes = []
+        _i64 = ctypes.c_int64
+        L.r3d_gfx950_logits_head_bytes.restype = _i64
+        L.r3d_gfx950_logits_head_bytes.argtypes = [_i64, _i64, ctypes.c_uint32, _i64]
+        L.r3d_gfx950_logits_head_header.restype = _i64
+        L.r3d_gfx950_logits_head_header.argtypes = [_i64, _i64, ctypes.c_uint32, _i64,
+                                                    ctypes.c_void_p]
+        L.r3d_gfx950_logits_head_join.restype = ctypes.c_int
+        L.r3d_gfx950_logits_head_join.argtypes = [
+            ctypes.c_void_p, _i64, ctypes.c_void_p, _i64, _i64, _i64, ctypes.c_uint32, _i64,
+            ctypes.c_void_p, _i64]
+        L.r3d_gfx950_logits_head_split.restype = ctypes.c_int
+        L.r3d_gfx950_logits_head_split.argtypes = [ctypes.c_void_p, _i64, ctypes.c_void_p,
+                                                   ctypes.c_void_p]
+        L.r3d_gfx950_logits_head_forget.restype = None
+        L.r3d_gfx950_logits_head_forget.argtypes = [ctypes.c_void_p]
         _LIB = L
     return _LIB
 
@@ -500,6 +516,98 @@ class GatedGemmOperands(_Args):
                          ([("M", M)] if M is not None else []))
         if scratch is not None:
             self.set_scratch(scratch)
+
+
+class LogitsOperands(_Args):
+    """One logits_gemm call (src/r3d_gemm_logits.hip:144-226).
+
+    x        bf16/int16 [M, n_embd]
+    lm_head  uint8 [bytes]: a joined head (join_head) in device memory
+    logits   float32 [M, n_vocab] out
+    """
+
+    def __init__(self, x, lm_head, logits, *, n_vocab, n_embd, M=None, dtype="bf16",
+                 shapes=None, strides=None):
+        shapes, strides = shapes or {}, strides or {}
+        ops = [(x, "BF16"), (lm_head, "U8"), (logits, "F32")]
+        super().__init__([(t, dt, shapes.get(i), strides.get(i)) for i, (t, dt) in enumerate(ops)],
+                         [("M", M if M is not None else logits.numel() // n_vocab),
+                          ("n_vocab", n_vocab), ("n_embd", n_embd), ("dtype", dtype)])
+
+
+_SCALE_DT = {"bf16": "BF16", "f16": "F16", "f32": "F32"}
+
+
+def head_bytes(n_vocab, n_embd, scale_dtype="bf16", scale_block_rows=1):
+    """Bytes of a joined head (negative: the RAD_E_* refusal)."""
+    return int(lib().r3d_gfx950_logits_head_bytes(n_vocab, n_embd, DT[_SCALE_DT[scale_dtype]],
+                                                  scale_block_rows))
+
+
+HEADER_BYTES = 328                          # sizeof(RadPlanesHeader)
+
+
+def head_header(n_vocab, n_embd, scale_dtype="bf16", scale_block_rows=1):
+    """(header uint8 [HEADER_BYTES], codes offset, scale offset, blob bytes) of a joined
+    head, so its planes can be written straight into device memory at those offsets."""
+    import numpy as np
+    h = np.zeros(HEADER_BYTES, np.uint8)
+    nb = int(lib().r3d_gfx950_logits_head_header(n_vocab, n_embd, DT[_SCALE_DT[scale_dtype]],
+                                                 scale_block_rows, h.ctypes.data))
+    if nb < 0:
+        raise ValueError("head refused (%d)" % nb)
+    e = h[40:].view(np.int64)          # entries from byte 40: 9 int64 each, offset last
+    return h, int(e[8]), int(e[17]), nb
+
+
+def join_head(codes, scale, scale_dtype="bf16", scale_block_rows=1):
+    """The joined-planes blob (numpy uint8, host) of e4m3 codes [n_vocab, n_embd] and a
+    scale grid [ceil(n_vocab / scale_block_rows), ceil(n_embd / 128)] (uint16 bits for
+    bf16 / f16, float32 for f32), through the library's r3d_gfx950_logits_head_join."""
+    import numpy as np
+    codes = np.ascontiguousarray(codes, np.uint8)
+    scale = np.ascontiguousarray(scale, np.float32 if scale_dtype == "f32" else np.uint16)
+    n_vocab, n_embd = codes.shape
+    nb = head_bytes(n_vocab, n_embd, scale_dtype, scale_block_rows)
+    if nb < 0:
+        raise ValueError("head refused (%d)" % nb)
+    blob = np.empty(nb, np.uint8)
+    rc = lib().r3d_gfx950_logits_head_join(
+        codes.ctypes.data, n_embd, scale.ctypes.data, scale.shape[1] * scale.itemsize, n_vocab,
+        n_embd, DT[_SCALE_DT[scale_dtype]], scale_block_rows, blob.ctypes.data, nb)
+    if rc != RAD_OK:
+        raise ValueError("join refused (%d)" % rc)
+    return blob
+
+
+def split_head(blob, n_vocab, n_embd, scale_dtype="bf16", scale_block_rows=1):
+    """The dense planes back out of a host blob: (codes [n_vocab, n_embd], scale grid)."""
+    import numpy as np
+    blob = np.ascontiguousarray(blob, np.uint8)
+    codes = np.empty((n_vocab, n_embd), np.uint8)
+    sdt = np.float32 if scale_dtype == "f32" else np.uint16
+    scale = np.empty(((n_vocab + scale_block_rows - 1) // scale_block_rows, (n_embd + 127) // 128),
+                     sdt)
+    rc = lib().r3d_gfx950_logits_head_split(blob.ctypes.data, blob.size, codes.ctypes.data,
+                                            scale.ctypes.data)
+    if rc != RAD_OK:
+        raise ValueError("split refused (%d)" % rc)
+    return codes, scale
+
+
+def forget_head(lm_head):
+    """Drop the library's cached header for the blob at lm_head (tensor or address)."""
+    ptr = lm_head if isinstance(lm_head, int) else lm_head.data_ptr()
+    lib().r3d_gfx950_logits_head_forget(ctypes.c_void_p(ptr))
+
+
+def logits_gemm(x, lm_head, logits, *, n_vocab, n_embd, stream=None):
+    """Launch the logits_gemm_e4m3 row on `stream` (default the current torch stream)."""
+    import torch
+    ops = LogitsOperands(x, lm_head, logits, n_vocab=n_vocab, n_embd=n_embd)
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    return launch_row("logits_gemm_e4m3", ops, stream)
 
 
 def quant_act_fp8(x, q, scale, *, n, group=128, stream=None):

@@ -75,6 +75,12 @@ __device__ __forceinline__ r3d_i32x4 r3d_ld16_stream(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const r3d_i32x4*>(p));
 }
 
+/* Buffer resource over [base, base + bytes) (raw, stride 0): loads past `bytes` read 0. */
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t r3d_rsrc(const void* base, int64_t bytes) {
+    const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
 /* Non-temporal 16-byte buffer load (buffer_load_dwordx4 ... nt) at byte `off` of the
  * resource; an offset past the resource's num_records returns zeros without touching
  * memory. */

@@ -27,7 +27,7 @@
 namespace r3d {
 
 /* Chip gate, per device, answered once: the rows are gfx950 code objects only. */
-static bool chip_ok() {
+bool chip_ok() {
     static int cache[64];                       /* 0 unknown, 1 yes, 2 no */
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
@@ -42,7 +42,7 @@ static bool chip_ok() {
 }
 
 /* Compute units of the current device, answered once per device. */
-static int cu_count() {
+int cu_count() {
     static int cache[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

@@ -1,0 +1,420 @@
+/* r3d_logits.hip -- the gfx950 logits_gemm_e4m3 row: logits over a joined e4m3 +
+ * block-scale lm_head (the reference's row is src/r3d_gemm_logits.hip:72-226, its layout
+ * hooks :233-272).
+ *
+ *     y[m, n] = sum_k x[m, k] * e4m3(codes[n, k]) * scale[n / br, k / 128]     (f32 out)
+ *
+ * On MFMA.  A decoded e4m3 code has 4 significant bits and an exponent inside bf16's range,
+ * so it is exact in bf16 (v_cvt_scalef32_pk_bf16_fp8 at scale 1 reproduces all 256 codes,
+ * NaN included); x is bf16 already.  v_mfma_f32_16x16x32_bf16 therefore forms every product
+ * x * code exactly -- 8 x 4 significant bits -- and sums 32 of them at f32 accuracy (worst
+ * measured on MI355X: 5.9 * 2^-24 of the sum of magnitudes per instruction, C included).
+ * The scale, which need not be a power of two, is applied once per 128-wide window, in f32:
+ * tot = fma(scale, window_sum, tot).  This differs from the reference's order (one fma per
+ * product, code * scale rounded first) only in where the f32 roundings fall; both stay
+ * within (window count + 4 * 66) * 2^-24 * sum |x * code * scale| of the exact sum.
+ *
+ * Layout of one step (a 128-wide K window, w):
+ *   A = 16 activation rows, staged once per workgroup in LDS as bf16 (rows mb .. mb+mt,
+ *       zero past K up to a multiple of 4 windows), lane (m = l%16, q = l/16) reading its
+ *       row's columns [128w + 16q, +16) and [128w + 64 + 16q, +16);
+ *   B = 16 head rows streamed from HBM: lane (r = l%16, q) loads 16 code bytes of row r at
+ *       each of those two column ranges (buffer loads: a chunk past K or a row past N reads
+ *       zero), and each 8-byte half feeds one of the four MFMAs of the window;
+ *   D = lane (r, q) holds x rows 4q .. 4q+3 for head row r, so its four accumulators share
+ *       one scale: lane (r, q) loads row r's scale for window 4t + q once every four windows
+ *       and the window's value comes from lane r + 16 (w % 4) by one ds_bpermute.
+ * A wave owns G groups of 16 head rows (a chunk), so one A fragment from LDS feeds G x 4
+ * MFMAs; chunks are dealt to waves blocks * 8 apart.  The codes of window w + 1 are in
+ * flight while window w computes.  Bytes per head row: K codes + 2 or 4 per 128 columns
+ * of scale (br = 1) -- the kernel is bound by HBM, the MFMAs run at a few percent.
+ */
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <mutex>
+#include <stdio.h>
+#include <string.h>
+
+#include "r3d_device.h"
+#include "r3d_dump.h"
+#include "r3d_plan.h"
+#include "rad_planes.h"
+#include "rad_plugin.h"
+
+namespace r3d {
+
+typedef __bf16 lg_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 lg_bf16x2 __attribute__((ext_vector_type(2)));
+
+/* Eight e4m3 codes (two dwords, byte 0 first) -> eight bf16, exact. */
+__device__ __forceinline__ lg_bf16x8 lg_codes8(int w0, int w1) {
+    const lg_bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)w0, 1.0f, false);
+    const lg_bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)w0, 1.0f, true);
+    const lg_bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)w1, 1.0f, false);
+    const lg_bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)w1, 1.0f, true);
+    return lg_bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+/* One scale element (bf16, f16 or f32 by SDT 0/1/2) at byte `off` of the plane, widened
+ * exactly; an offset past the plane reads 0. */
+template <int SDT>
+__device__ __forceinline__ float lg_scale(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    if (SDT == 2) return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0));
+    const uint32_t v = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, 0);
+    if (SDT == 0) return __uint_as_float(v << 16);
+    return __half2float(__ushort_as_half((unsigned short)v));
+}
+
+/* The device copy of the header still describes the planes the host planned from. */
+__device__ __forceinline__ bool lg_header_ok(const LogitsGuard& g) {
+    const RadPlanesHeader* h = reinterpret_cast<const RadPlanesHeader*>(g.header);
+    if (h->magic != RAD_PLANES_MAGIC || h->version != RAD_PLANES_VERSION || h->n_planes != 2)
+        return false;
+    const RadPlanesEntry& c = h->entry[g.ic];
+    const RadPlanesEntry& s = h->entry[g.is];
+    return c.dtype == RAD_F8E4M3 && c.offset == g.c_off && c.rows == g.c_rows &&
+           c.cols == g.c_cols && s.dtype == g.s_dtype && s.offset == g.s_off &&
+           s.rows == g.s_rows && s.row_bytes == g.s_row_bytes && s.block[0] == g.s_br;
+}
+
+constexpr uint32_t kLgOob = 0x80000000u;     /* past every buffer's num_records: reads 0 */
+
+template <int G, int SDT>
+__global__ __launch_bounds__(kLogitsWaves * 64) void logits_e4m3_kernel(
+    const uint16_t* __restrict__ X, int64_t x_pitch, const uint8_t* __restrict__ codes,
+    const uint8_t* __restrict__ scale, int64_t s_pitch, int64_t s_bytes, int br,
+    float* __restrict__ Y, int64_t y_pitch, int N, int K, int M, int mt, int nwin,
+    int nwin_pad, int xrow, int64_t chunks, LogitsGuard guard) {
+    constexpr int ESZ = SDT == 2 ? 4 : 2;
+    extern __shared__ __align__(16) uint8_t lg_lds[];
+    const int mb = blockIdx.y * mt;
+    const int live = M - mb < mt ? M - mb : mt;
+
+    /* stage x rows [mb, mb + live) as bf16, zero from K to nwin_pad windows */
+    const int cpr = nwin_pad * 16;                    /* 16-byte chunks per staged row */
+    for (int i = threadIdx.x; i < live * cpr; i += kLogitsWaves * 64) {
+        const int m = i / cpr, c = i - m * cpr;
+        r3d_i32x4 v = {0, 0, 0, 0};
+        if (8 * c < K) v = *reinterpret_cast<const r3d_i32x4*>(X + (int64_t)(mb + m) * x_pitch + 8 * c);
+        *reinterpret_cast<r3d_i32x4*>(lg_lds + m * xrow + 16 * c) = v;
+    }
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, q = l >> 4;
+    const bool ok = lg_header_ok(guard);
+    const __amdgpu_buffer_rsrc_t rs = r3d_rsrc(scale, s_bytes);
+    const uint8_t* xl = lg_lds + r * xrow + 32 * q;   /* this lane's A columns, window 0 */
+
+    for (int64_t ch = (int64_t)blockIdx.x * kLogitsWaves + wave; ch < chunks;
+         ch += (int64_t)gridDim.x * kLogitsWaves) {
+        const int64_t row0 = ch * 16 * G;
+        if (!ok) {                                    /* the head changed under the plan */
+            for (int g = 0; g < G; ++g) {
+                const int64_t row = row0 + 16 * g + r;
+                for (int i = 0; i < 4; ++i)
+                    if (4 * q + i < live && row < N)
+                        Y[(int64_t)(mb + 4 * q + i) * y_pitch + row] = __builtin_nanf("");
+            }
+            continue;
+        }
+        const int64_t rows_here = N - row0 < 16 * G ? N - row0 : 16 * G;
+        const __amdgpu_buffer_rsrc_t rc = r3d_rsrc(codes + row0 * K, rows_here * K);
+        uint32_t coff[G], soff[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int64_t row = row0 + 16 * g + r;
+            coff[g] = (uint32_t)((16 * g + r) * K + 16 * q);
+            soff[g] = row < N ? (uint32_t)((row / br) * s_pitch * ESZ) : kLgOob;
+        }
+        /* window w's two chunk offsets for group g (a chunk at or past K reads zero) */
+        auto code_off = [&](int g, int w, int half) -> uint32_t {
+            const int k = 128 * w + 64 * half + 16 * q;
+            return k < K ? coff[g] + (uint32_t)(128 * w + 64 * half) : kLgOob;
+        };
+        auto scale_off = [&](int g, int w0) -> uint32_t {
+            const int w = w0 + q;
+            return (w < nwin && soff[g] != kLgOob) ? soff[g] + (uint32_t)(w * ESZ) : kLgOob;
+        };
+
+        r3d_i32x4 cc[G][2], cn[G][2];
+        float sc[G], sn[G];
+        r3d_f32x4 tot[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            sc[g] = lg_scale<SDT>(rs, scale_off(g, 0));
+            cc[g][0] = r3d_buf_ld16_stream(rc, code_off(g, 0, 0));
+            cc[g][1] = r3d_buf_ld16_stream(rc, code_off(g, 0, 1));
+            tot[g] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        for (int w0 = 0; w0 < nwin_pad; w0 += 4) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) sn[g] = lg_scale<SDT>(rs, scale_off(g, w0 + 4));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int w = w0 + j;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    cn[g][0] = r3d_buf_ld16_stream(rc, code_off(g, w + 1, 0));
+                    cn[g][1] = r3d_buf_ld16_stream(rc, code_off(g, w + 1, 1));
+                }
+                lg_bf16x8 a0 = {}, a1 = {}, a2 = {}, a3 = {};
+                if (r < live) {
+                    const uint8_t* xp = xl + 256 * w;
+                    a0 = *reinterpret_cast<const lg_bf16x8*>(xp);
+                    a1 = *reinterpret_cast<const lg_bf16x8*>(xp + 16);
+                    a2 = *reinterpret_cast<const lg_bf16x8*>(xp + 128);
+                    a3 = *reinterpret_cast<const lg_bf16x8*>(xp + 144);
+                }
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const r3d_f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    r3d_f32x4 blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        a0, lg_codes8(cc[g][0][0], cc[g][0][1]), z, 0, 0, 0);
+                    blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        a1, lg_codes8(cc[g][0][2], cc[g][0][3]), blk, 0, 0, 0);
+                    blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        a2, lg_codes8(cc[g][1][0], cc[g][1][1]), blk, 0, 0, 0);
+                    blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        a3, lg_codes8(cc[g][1][2], cc[g][1][3]), blk, 0, 0, 0);
+                    const float s = __shfl(sc[g], r + 16 * j, 64);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) tot[g][i] = fmaf(s, blk[i], tot[g][i]);
+                    cc[g][0] = cn[g][0];
+                    cc[g][1] = cn[g][1];
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) sc[g] = sn[g];
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int64_t row = row0 + 16 * g + r;
+            if (row >= N) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * q + i < live) Y[(int64_t)(mb + 4 * q + i) * y_pitch + row] = tot[g][i];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ the blob's header */
+
+/* Host copies of device-resident headers, per (device, blob): the first launch over a
+ * blob in device memory reads its header with one synchronous copy, later launches reuse
+ * it (and the kernel re-checks it against the device copy before reading a plane).  A blob
+ * in pinned or managed memory is read in place every launch. */
+struct HeadCacheEntry {
+    int dev;
+    const void* blob;
+    RadPlanesHeader h;
+};
+static std::mutex g_head_mu;
+static HeadCacheEntry g_head[16];
+static int g_head_n = 0, g_head_next = 0;
+
+static bool head_copy(const void* blob, RadPlanesHeader* out) {
+    if (!blob) return false;
+    hipPointerAttribute_t at;
+    memset(&at, 0, sizeof at);
+    if (hipPointerGetAttributes(&at, blob) != hipSuccess) {
+        (void)hipGetLastError();                      /* unregistered host memory */
+        return false;
+    }
+    if (at.type == hipMemoryTypeHost || at.type == hipMemoryTypeManaged ||
+        at.type == hipMemoryTypeUnified) {
+        memcpy(out, blob, sizeof *out);
+        return rad_planes_header(out) != nullptr;
+    }
+    if (at.type != hipMemoryTypeDevice) return false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    {
+        std::lock_guard<std::mutex> lk(g_head_mu);
+        for (int i = 0; i < g_head_n; ++i)
+            if (g_head[i].dev == dev && g_head[i].blob == blob) {
+                *out = g_head[i].h;
+                return true;
+            }
+    }
+    if (hipMemcpy(out, blob, sizeof *out, hipMemcpyDeviceToHost) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (!rad_planes_header(out)) return false;
+    std::lock_guard<std::mutex> lk(g_head_mu);
+    HeadCacheEntry& e = g_head[g_head_n < 16 ? g_head_n++ : (g_head_next++ & 15)];
+    e.dev = dev;
+    e.blob = blob;
+    e.h = *out;
+    return true;
+}
+
+static void head_forget(const void* blob) {
+    std::lock_guard<std::mutex> lk(g_head_mu);
+    int j = 0;
+    for (int i = 0; i < g_head_n; ++i)
+        if (g_head[i].blob != blob) g_head[j++] = g_head[i];
+    g_head_n = j;
+    g_head_next = 0;
+}
+
+/* ---------------------------------------------------------------------- the row entry */
+
+/* Workgroups of this instantiation one compute unit holds at `lds` bytes of LDS (the
+ * register count answered once by the runtime). */
+template <int G, int SDT>
+static int logits_per_cu(int lds) {
+    static int regs = 0;
+    if (!regs) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&logits_e4m3_kernel<G, SDT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &n, reinterpret_cast<const void*>(&logits_e4m3_kernel<G, SDT>),
+                kLogitsWaves * 64, 0) != hipSuccess || n < 1)
+            n = 1;
+        (void)hipGetLastError();
+        regs = n;
+    }
+    const int by_lds = lds > 0 ? 160 * 1024 / lds : regs;
+    return by_lds < regs ? (by_lds < 1 ? 1 : by_lds) : regs;
+}
+
+template <int G, int SDT>
+static hipError_t launch_logits_t(const LogitsPlan& P, hipStream_t stream) {
+    const LogitsGeom g = logits_geom(P, cu_count(), logits_per_cu<G, SDT>(P.lds));
+    const int esz = SDT == 2 ? 4 : 2;
+    const int64_t s_bytes = P.guard.s_rows * P.s_pitch * esz;
+    hipLaunchKernelGGL((logits_e4m3_kernel<G, SDT>), dim3((unsigned)g.blocks, (unsigned)g.passes),
+                       dim3(kLogitsWaves * 64), (size_t)P.lds, stream, P.X, P.x_pitch, P.codes,
+                       P.scale, P.s_pitch, s_bytes, P.br, P.Y, P.y_pitch, (int)P.N, (int)P.K,
+                       (int)P.M, P.mt, P.nwin, P.nwin_pad, P.xrow, g.chunks, P.guard);
+    return hipGetLastError();
+}
+
+static int logits_entry(const RadArgs* a, RadStream s) {
+    LogitsPlan P{};
+    int rc = plan_logits_e4m3(a, nullptr, &P, true);
+    if (rc) return rc;
+    if (!chip_ok()) return RAD_E_UNSUPPORTED;
+    RadPlanesHeader hc;
+    if (!head_copy(rad_arg_in(a, 1)->data, &hc)) return RAD_E_DTYPE;
+    rc = plan_logits_e4m3(a, &hc, &P, false);
+    if (rc) return rc;
+    hipStream_t stream = (hipStream_t)s;
+    hipError_t e;
+#define R3D_LG(G_)                                                                          \
+    e = P.sdt == 0 ? launch_logits_t<G_, 0>(P, stream)                                      \
+      : P.sdt == 1 ? launch_logits_t<G_, 1>(P, stream)                                      \
+                   : launch_logits_t<G_, 2>(P, stream)
+    if (logits_groups(P) == 2) { R3D_LG(2); } else { R3D_LG(1); }
+#undef R3D_LG
+    if (e != hipSuccess) {
+        fprintf(stderr, "libr3d_gfx950: logits_e4m3 launch FAILED (%s)\n", hipGetErrorName(e));
+        return RAD_E_DEVICE;
+    }
+    return RAD_OK;
+}
+
+/* ------------------------------------------------------------------ joining the planes */
+
+/* The joined head's layout (header, then the codes and the scale plane each at a 256-byte
+ * boundary), written into *h when given; the blob's bytes, or minus a RAD_E_* code. */
+static int64_t head_layout(int64_t N, int64_t K, uint32_t sdt, int64_t br, RadPlanesHeader* h) {
+    if (N <= 0 || K <= 0 || N > 0x7FFFFFFLL || K > 0x7FFFFFFLL) return -RAD_E_SHAPE;
+    if (sdt != RAD_BF16 && sdt != RAD_F16 && sdt != RAD_F32) return -RAD_E_DTYPE;
+    if (br != 1 && br != 128) return -RAD_E_SHAPE;
+    const int64_t esz = sdt == RAD_F32 ? 4 : 2;
+    const int64_t srows = (N + br - 1) / br, scols = (K + 127) / 128;
+    auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
+    const int64_t c_off = up((int64_t)sizeof(RadPlanesHeader));
+    const int64_t s_off = up(c_off + N * K);
+    if (h) {
+        memset(h, 0, sizeof *h);
+        h->magic = RAD_PLANES_MAGIC;
+        h->version = RAD_PLANES_VERSION;
+        h->n_planes = 2;
+        RadPlanesEntry& c = h->entry[0];
+        strncpy(c.role, "codes", RAD_PLANES_ROLE);
+        c.dtype = RAD_F8E4M3;
+        c.block[0] = 1; c.block[1] = 1;
+        c.rows = N; c.cols = K; c.row_bytes = K; c.offset = c_off;
+        RadPlanesEntry& e = h->entry[1];
+        strncpy(e.role, "scale", RAD_PLANES_ROLE);
+        e.dtype = sdt;
+        e.block[0] = br; e.block[1] = 128;
+        e.rows = srows; e.cols = scols; e.row_bytes = scols * esz; e.offset = s_off;
+        h->bytes = s_off + srows * scols * esz;
+    }
+    return s_off + srows * scols * esz;
+}
+
+}  // namespace r3d
+
+extern "C" {
+
+int r3d_rad_logits_gemm_e4m3(const RadArgs* a, RadStream s) {
+    return r3d::dump_wrap("logits_gemm_e4m3", a, s, r3d::logits_entry);
+}
+
+int64_t r3d_gfx950_logits_head_bytes(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,
+                                     int64_t scale_block_rows) {
+    return r3d::head_layout(n_vocab, n_embd, scale_dtype, scale_block_rows, nullptr);
+}
+
+int64_t r3d_gfx950_logits_head_header(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,
+                                      int64_t scale_block_rows, RadPlanesHeader* out) {
+    if (!out) return -RAD_E_INVAL;
+    return r3d::head_layout(n_vocab, n_embd, scale_dtype, scale_block_rows, out);
+}
+
+int r3d_gfx950_logits_head_join(const uint8_t* codes, int64_t codes_pitch, const void* scale,
+                                int64_t scale_pitch_bytes, int64_t n_vocab, int64_t n_embd,
+                                uint32_t scale_dtype, int64_t scale_block_rows, void* dst,
+                                int64_t dst_bytes) {
+    RadPlanesHeader h;
+    const int64_t need = r3d::head_layout(n_vocab, n_embd, scale_dtype, scale_block_rows, &h);
+    if (need < 0) return (int)-need;
+    if (!codes || !scale || !dst || dst_bytes < need) return RAD_E_SHAPE;
+    const RadPlanesEntry& c = h.entry[0];
+    const RadPlanesEntry& e = h.entry[1];
+    if (codes_pitch < n_embd || scale_pitch_bytes < e.row_bytes) return RAD_E_STRIDE;
+    uint8_t* d = (uint8_t*)dst;
+    memset(d, 0, (size_t)need);
+    memcpy(d, &h, sizeof h);
+    for (int64_t i = 0; i < n_vocab; ++i)
+        memcpy(d + c.offset + i * n_embd, codes + i * codes_pitch, (size_t)n_embd);
+    for (int64_t i = 0; i < e.rows; ++i)
+        memcpy(d + e.offset + i * e.row_bytes, (const uint8_t*)scale + i * scale_pitch_bytes,
+               (size_t)e.row_bytes);
+    return RAD_OK;
+}
+
+int r3d_gfx950_logits_head_split(const void* blob, int64_t blob_bytes, uint8_t* codes,
+                                 void* scale) {
+    if (!blob || blob_bytes < (int64_t)sizeof(RadPlanesHeader)) return RAD_E_SHAPE;
+    const RadPlanesHeader* h = rad_planes_header(blob);
+    const RadPlanesEntry* c = nullptr;
+    const RadPlanesEntry* e = nullptr;
+    if (!h || h->n_planes != 2 || !rad_planes_find(blob, "codes", &c) ||
+        !rad_planes_find(blob, "scale", &e))
+        return RAD_E_DTYPE;
+    if (h->bytes > blob_bytes || c->offset + c->rows * c->row_bytes > h->bytes ||
+        e->offset + e->rows * e->row_bytes > h->bytes)
+        return RAD_E_SHAPE;
+    const int64_t esz = e->dtype == RAD_F32 ? 4 : 2;
+    const uint8_t* b = (const uint8_t*)blob;
+    if (codes)
+        for (int64_t i = 0; i < c->rows; ++i)
+            memcpy(codes + i * c->cols, b + c->offset + i * c->row_bytes, (size_t)c->cols);
+    if (scale)
+        for (int64_t i = 0; i < e->rows; ++i)
+            memcpy((uint8_t*)scale + i * e->cols * esz, b + e->offset + i * e->row_bytes,
+                   (size_t)(e->cols * esz));
+    return RAD_OK;
+}
+
+void r3d_gfx950_logits_head_forget(const void* blob) { r3d::head_forget(blob); }
+
+}  /* extern "C" */

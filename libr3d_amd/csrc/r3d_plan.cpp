@@ -5,6 +5,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "rad_planes.h"
 #include "rad_plugin.h"
 #include "r3d_gemv_layout.h"
 #include "r3d_prefill_layout.h"
@@ -738,6 +739,111 @@ int plan_gemm_gated(const RadArgs* a, GemmPlan* G, GatedPlan* E) {
     return RAD_OK;
 }
 
+/* The reference entry's gates, in its order and with its codes (src/r3d_gemm_logits.hip:
+ * 149-186), then this build's: K a multiple of 16 (16-byte code walks; the reference takes a
+ * multiple of 4), 16-byte aligned x rows and codes plane, the codes plane inside the blob's
+ * byte count, and one staged activation row within kLogitsMaxXLds of LDS. */
+int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, bool args_only) {
+    const RadTensor* X = rad_arg_in(a, 0);
+    const RadTensor* W = rad_arg_in(a, 1);
+    const RadTensor* Y = rad_arg_in(a, 2);
+    if (!X || !W || !Y) return RAD_E_UNSUPPORTED;
+    const char* dt = rad_args_gets(a, "dtype");
+    if (!dt || strcmp(dt, "bf16") != 0) return RAD_E_UNSUPPORTED;
+    if (X->dtype != RAD_BF16 || Y->dtype != RAD_F32) return RAD_E_UNSUPPORTED;
+    long long N = 0, K = 0;
+    if (!rad_args_geti(a, "n_vocab", &N) || !rad_args_geti(a, "n_embd", &K)) return RAD_E_SHAPE;
+    if (N <= 0 || K <= 0) return RAD_E_SHAPE;
+    const long long yn = rad_tensor_numel(Y);
+    if (yn <= 0 || yn % N) return RAD_E_SHAPE;
+    const long long M = yn / N;                        /* never the M parameter */
+    if (M > kDimMax || N > kDimMax || K > kDimMax) return RAD_E_SHAPE;
+    if (rad_tensor_numel(X) < M * K) return RAD_E_SHAPE;
+    if (K & 3) return RAD_E_UNSUPPORTED;
+    if (X->rank >= 2 && X->stride[X->rank - 1] != 1) return RAD_E_STRIDE;
+    if (Y->rank >= 2 && Y->stride[Y->rank - 1] != 1) return RAD_E_STRIDE;
+    const int64_t x_pitch = X->rank >= 2 ? X->stride[X->rank - 2] : K;
+    const int64_t y_pitch = Y->rank >= 2 ? Y->stride[Y->rank - 2] : N;
+    if (x_pitch < K || y_pitch < N) return RAD_E_STRIDE;
+    if (args_only) return RAD_OK;
+
+    if (!h || h->n_planes != 2) return RAD_E_DTYPE;
+    if (h->transform[0]) return RAD_E_UNSUPPORTED;
+    const RadPlanesEntry* ec = nullptr;
+    const RadPlanesEntry* es = nullptr;
+    const void* pc = rad_planes_find_at(h, W->data, "codes", &ec);
+    const void* ps = rad_planes_find_at(h, W->data, "scale", &es);
+    if (!pc || !ps || !ec || !es) return RAD_E_DTYPE;
+    if (ec->dtype != RAD_F8E4M3 || ec->block[0] != 1 || ec->block[1] != 1 || ec->rows != N ||
+        ec->cols != K)
+        return RAD_E_SHAPE;
+    if (es->dtype != RAD_BF16 && es->dtype != RAD_F16 && es->dtype != RAD_F32)
+        return RAD_E_UNSUPPORTED;
+    if (es->block[1] != 128 || (es->block[0] != 1 && es->block[0] != 128)) return RAD_E_UNSUPPORTED;
+    const int64_t srows = (N + es->block[0] - 1) / es->block[0], scols = (K + 127) / 128;
+    if (es->rows != srows || es->cols != scols) return RAD_E_SHAPE;
+    if (ec->row_bytes != K) return RAD_E_STRIDE;       /* dense, one byte each */
+    if (h->bytes < es->offset + es->rows * es->row_bytes) return RAD_E_SHAPE;
+
+    /* gfx950 gates */
+    const int64_t ssz = es->dtype == RAD_F32 ? 4 : 2;
+    if (es->row_bytes < scols * ssz || es->row_bytes % ssz || es->offset < 0 || ec->offset < 0)
+        return RAD_E_STRIDE;
+    if (h->bytes < ec->offset + N * K) return RAD_E_SHAPE;
+    if (K % 16) return RAD_E_UNSUPPORTED;
+    if (!aligned16(X->data) || (x_pitch & 7) || !aligned16(pc) || ((uintptr_t)ps % ssz))
+        return RAD_E_UNSUPPORTED;
+    /* buffer offsets are 32-bit: one wave's rows of codes and the whole scale plane */
+    if (64 * K > 0x7FFFFFFFLL || es->rows * es->row_bytes > 0x7FFFFFFFLL) return RAD_E_UNSUPPORTED;
+    const int nwin = (int)scols, nwin_pad = (nwin + 3) / 4 * 4;
+    const int64_t xrow = (int64_t)nwin_pad * 256 + 16;
+    int64_t mt = kLogitsMaxXLds / xrow;
+    if (mt < 1) return RAD_E_UNSUPPORTED;
+    if (mt > 16) mt = 16;
+    if (mt > M) mt = M;
+    if ((M + mt - 1) / mt > 65535) return RAD_E_UNSUPPORTED;      /* passes ride grid.y */
+    P->X = (const uint16_t*)X->data;
+    P->codes = (const uint8_t*)pc;
+    P->scale = (const uint8_t*)ps;
+    P->Y = (float*)Y->data;
+    P->sdt = es->dtype == RAD_BF16 ? 0 : es->dtype == RAD_F16 ? 1 : 2;
+    P->br = (int)es->block[0];
+    P->mt = (int)mt;
+    P->nwin = nwin;
+    P->nwin_pad = nwin_pad;
+    P->xrow = (int)xrow;
+    P->M = M; P->N = N; P->K = K;
+    P->x_pitch = x_pitch;
+    P->s_pitch = es->row_bytes / ssz;
+    P->y_pitch = y_pitch;
+    P->lds = (int)(mt * xrow);
+    LogitsGuard& g = P->guard;
+    g.header = (const uint8_t*)W->data;
+    g.ic = (int32_t)(ec - h->entry);
+    g.is = (int32_t)(es - h->entry);
+    g.c_off = ec->offset; g.c_rows = ec->rows; g.c_cols = ec->cols;
+    g.s_off = es->offset; g.s_rows = es->rows; g.s_row_bytes = es->row_bytes; g.s_br = es->block[0];
+    g.s_dtype = es->dtype; g.pad = 0;
+    return RAD_OK;
+}
+
+/* Two 16-row groups a wave where the head is long enough to give every wave slot of the
+ * chip a few chunks (262144 rows: 8192 chunks), one group below that. */
+int logits_groups(const LogitsPlan& P) { return P.N >= 65536 ? 2 : 1; }
+
+/* The grid: at most per_cu workgroups of 8 waves per compute unit (what one unit holds at
+ * once), walking the chunks. */
+LogitsGeom logits_geom(const LogitsPlan& P, int cus, int per_cu) {
+    LogitsGeom g{};
+    g.groups = logits_groups(P);
+    g.chunks = (P.N + 16 * g.groups - 1) / (16 * g.groups);
+    int64_t blocks = (g.chunks + kLogitsWaves - 1) / kLogitsWaves;
+    if (blocks > (int64_t)cus * per_cu) blocks = (int64_t)cus * per_cu;
+    g.blocks = (int)blocks;
+    g.passes = (P.M + P.mt - 1) / P.mt;
+    return g;
+}
+
 bool env_no_mxfp4()   { static const bool v = getenv("R3D_NO_MXFP4") != nullptr;   return v; }
 bool env_no_fp4_dec() { static const bool v = getenv("R3D_NO_FP4_DEC") != nullptr; return v; }
 bool env_no_fp8a8()   { static const bool v = getenv("R3D_NO_FP8A8") != nullptr;   return v; }
@@ -830,6 +936,23 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
                  Q.x_bf16 ? "bf16" : "f32", (long long)Q.rows, (long long)Q.n, (long long)Q.g,
                  (long long)Q.ngrp, (long long)Q.x_pitch, (long long)Q.q_pitch,
                  (long long)Q.s_pitch);
+        return RAD_OK;
+    }
+    if (strstr(row, "logits_gemm") != nullptr) {
+        /* host-memory operands here (describe launches nothing): the blob's header is read
+         * where it lies */
+        const RadTensor* W = rad_arg_in(a, 1);
+        LogitsPlan L{};
+        int rc = plan_logits_e4m3(a, nullptr, &L, true);
+        if (!rc) rc = plan_logits_e4m3(a, W ? rad_planes_header(W->data) : nullptr, &L, false);
+        if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
+        const LogitsGeom g = logits_geom(L, 256, 1);
+        snprintf(buf, (size_t)len,
+                 "arm=logits M=%lld N=%lld K=%lld mt=%d passes=%lld groups=%d waves=%lld "
+                 "blocks=%d br=%d sdt=%d nwin=%d lds=%d",
+                 (long long)L.M, (long long)L.N, (long long)L.K, L.mt,
+                 (long long)((L.M + L.mt - 1) / L.mt), g.groups, (long long)g.chunks, g.blocks,
+                 L.br, L.sdt, L.nwin, L.lds);
         return RAD_OK;
     }
     if (strstr(row, "rmsnorm_quant_fp8") != nullptr) {

@@ -8,6 +8,7 @@
 
 #include <stdint.h>
 #include "rad_abi.h"
+#include "rad_planes.h"
 
 namespace r3d {
 
@@ -217,6 +218,53 @@ int plan_rmsnorm_quant_fp8(const RadArgs* a, RmsPlan* P);
  * plan over it.  Returns RAD_OK or the reference's refusal code. */
 int plan_gemm_gated(const RadArgs* a, GemmPlan* G, GatedPlan* E);
 int64_t gemm_gated_scratch_bytes(const RadArgs* a);   /* 64 * N * 2, or 0 without N */
+
+/* logits_gemm over a joined e4m3 + block-scale head (src/r3d_gemm_logits.hip:149-186):
+ * x bf16 [M, K] (K = n_embd), lm_head a joined-planes blob (rad_planes.h) holding "codes"
+ * (e4m3 [N, K] dense) and "scale" (bf16 / f16 / f32, one per (1 or 128 rows, 128 cols)),
+ * logits f32 [M, N] (N = n_vocab); M = numel(logits) / N.  The plane addresses are the
+ * blob's (W->data) plus the header's offsets; `guard` carries what the kernel re-checks
+ * against the device copy of the header before it reads a plane. */
+struct LogitsGuard {
+    const uint8_t* header;   /* the blob's first byte (its header) */
+    int32_t ic, is;          /* entry indices of "codes" and "scale" */
+    int64_t c_off, c_rows, c_cols;
+    int64_t s_off, s_rows, s_row_bytes, s_br;
+    uint32_t s_dtype, pad;
+};
+struct LogitsPlan {
+    const uint16_t* X;
+    const uint8_t* codes;
+    const uint8_t* scale;
+    float* Y;
+    int sdt;                 /* scale element: 0 bf16, 1 f16, 2 f32 */
+    int br;                  /* weight rows per scale row: 1 or 128 */
+    int mt;                  /* activation rows per pass (1..16); passes = ceil(M / mt) */
+    int nwin, nwin_pad;      /* 128-wide K windows; padded to the 4-window unroll */
+    int xrow;                /* LDS pitch of one staged activation row, bytes */
+    int64_t M, N, K;
+    int64_t x_pitch, s_pitch, y_pitch;   /* elements */
+    int lds;                 /* dynamic LDS bytes per workgroup */
+    LogitsGuard guard;
+};
+/* `h` null: the gates that need no header (args_only); else a host copy of the header. */
+int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, bool args_only);
+constexpr int kLogitsWaves = 8;                /* waves per workgroup */
+constexpr int kLogitsMaxXLds = 144 * 1024;     /* LDS for the staged activation rows */
+/* Launch geometry: each wave owns `groups` x 16 head rows at a time (a chunk) and walks
+ * chunks blocks * 8 apart; blocks.y = passes over the activation rows. */
+struct LogitsGeom {
+    int groups;
+    int64_t chunks;
+    int blocks;
+    int64_t passes;
+};
+int logits_groups(const LogitsPlan& P);
+LogitsGeom logits_geom(const LogitsPlan& P, int cus, int per_cu);
+
+/* The current device: gfx950 or not (answered once per device), and its compute units. */
+bool chip_ok();
+int cu_count();
 
 /* Environment levers, read once per process (function-local statics). */
 bool env_no_mxfp4();        /* R3D_NO_MXFP4: all mxfp4a8 rows */

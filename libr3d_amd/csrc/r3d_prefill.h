@@ -57,12 +57,6 @@ __device__ __forceinline__ void r3d_mfma_mx_inplace(r3d_f32x4& acc, r3d_i32x4 a,
         : "v"(a), "v"(b), "v"(sa), "v"(sb));
 }
 
-/* Buffer resource over [base, base + bytes) (raw, stride 0): loads past `bytes` read 0. */
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t r3d_rsrc(const void* base, int64_t bytes) {
-    const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
-
 /* Buffer load of `bytes` (16, 4 or 2) per lane straight into LDS at lds + lane *
  * max(bytes, 4). */
 template <int BYTES>

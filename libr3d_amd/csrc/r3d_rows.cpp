@@ -14,6 +14,8 @@
  *   rmsnorm_quant_fp8        prio 1000  n DIV 4, group EQ 128, dtype IN bf16  norm producer
  *   gemm_nt_q_gated_fp8a8    prio 1000  dtype IN fp8a8, M LE 64, K DIV 128, group EQ 128,
  *                                       act IN silu sigmoid              GEMM + gated producer
+ *   logits_gemm_e4m3         prio 1000  n_vocab GE 1, n_embd GE 128, dtype IN bf16
+ *                                                                         joined e4m3 lm_head
  * gemm_nt_q_mxfp4a16 has no counterpart in the reference: it takes bf16 activations (no
  * a_scale), quantises them to mxfp8 (e4m3 + E8M0 per 32 of K) in the launch scratch its
  * hook sizes, and runs the prefill GEMM with both block scales inside the MFMA.
@@ -48,6 +50,7 @@ int r3d_rad_gated_quant_fp8(const RadArgs* a, RadStream s);
 int r3d_rad_rmsnorm_quant_fp8(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s);
 int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a);
+int r3d_rad_logits_gemm_e4m3(const RadArgs* a, RadStream s);
 }
 
 namespace {
@@ -141,6 +144,20 @@ const RadOperandSpec kRmsOperands[] = {
     {"out_bf16", RAD_OPD_OUT, 1},
 };
 
+/* logits_gemm's schema (src/r3d_rows.cpp:233-245 of the reference): gemm_nt's three
+ * operands in its order, the extents spelled n_vocab / n_embd. */
+const RadParamSpec kLogitsParams[] = {
+    {"M", RAD_P_INT, RAD_REQUIRED, 0},
+    {"n_vocab", RAD_P_INT, RAD_REQUIRED, 0},
+    {"n_embd", RAD_P_INT, RAD_REQUIRED, 0},
+    {"dtype", RAD_P_STR, RAD_REQUIRED, 0},
+};
+const RadOperandSpec kLogitsOperands[] = {
+    {"x", RAD_OPD_IN, 0},
+    {"lm_head", RAD_OPD_WEIGHT, 0},
+    {"logits", RAD_OPD_OUT, 0},
+};
+
 const RadOpSchema kSchemas[] = {
     {"gemm_nt_q", kGemmNtQParams, 8, kGemmNtQOperands, 7,
      "Y[M,N] = A[M,K] . dequant(B)[N,K]^T with block-scaled operands; `dtype` names the "
@@ -161,6 +178,9 @@ const RadOpSchema kSchemas[] = {
      "RMS norm (optionally after a residual add that is written back) and the fp8 group "
      "quantiser in one pass over the row; the bf16 normed values are what the codes are "
      "taken over, and out_bf16 carries them when present."},
+    {"logits_gemm", kLogitsParams, 4, kLogitsOperands, 3,
+     "logits[M, n_vocab] = x[M, n_embd] . dequant(lm_head)[n_vocab, n_embd]^T in f32; M "
+     "derives from numel(logits) / n_vocab."},
 };
 
 /* the band rows' constraint (src/r3d_rows.cpp:1262-1265) */
@@ -208,6 +228,13 @@ const RadConstraint cFp8Gated[] = {
 const RadConstraint cRmsQuant[] = {
     {"n", RAD_C_DIV, 4, nullptr},
     {"group", RAD_C_EQ, 128, nullptr},
+    {"dtype", RAD_C_IN, 0, "bf16"},
+};
+
+/* the e4m3 lm_head row (src/r3d_rows.cpp:1042-1046) */
+const RadConstraint cLogitsRow[] = {
+    {"n_vocab", RAD_C_GE, 1, nullptr},
+    {"n_embd", RAD_C_GE, 128, nullptr},
     {"dtype", RAD_C_IN, 0, "bf16"},
 };
 
@@ -325,6 +352,21 @@ const RadKernelInfo kRows[] = {
      RAD_DOMAIN_DEVICE, kPrioTile, cFp8Gated, 5, nullptr, 0, nullptr,
      nullptr, nullptr, r3d_rad_gemm_nt_q_gated_fp8, r3d_rad_gemm_nt_q_gated_fp8_scratch,
      nullptr, nullptr, nullptr, nullptr},
+
+    /* The layout hooks stay null: radiance's encoding and layout structures are not part of
+     * this build's ABI headers, so the head is joined by r3d_gfx950_logits_head_join (the
+     * same blob the reference's relayout hook writes, src/r3d_gemm_logits.hip:233-272). */
+    {"logits_gemm_e4m3", "logits_gemm", "vocab",
+     "lm_head GEMV on gfx950 bf16 MFMA: e4m3 codes widened exactly to bf16 in registers "
+     "(v_cvt_scalef32_pk_bf16_fp8), 16 activation rows staged once per workgroup in LDS, "
+     "16 head rows per MFMA streamed from HBM with 16-byte buffer loads, the block scale "
+     "applied once per 128-column window in f32",
+     "codes [n_vocab, n_embd] e4m3 dense, scale per (1 or 128 rows, 128 cols); n_embd a "
+     "multiple of 16; M derives from numel(logits)/n_vocab, up to 16 rows a pass (fewer "
+     "where LDS holds fewer rows of n_embd), passes ride grid.y",
+     "bf16 x, joined e4m3 + bf16/f16/f32 head, f32 logits",
+     RAD_DOMAIN_DEVICE, kPrioTile, cLogitsRow, 3, nullptr, 0, nullptr,
+     nullptr, nullptr, r3d_rad_logits_gemm_e4m3, nullptr, nullptr, nullptr, nullptr, nullptr},
 };
 
 bool row_hidden(const RadKernelInfo& k) {
@@ -348,8 +390,9 @@ uint32_t rad_plugin_abi_version(void) { return RAD_ABI_VERSION; }
 const RadPluginInfo* rad_plugin_info(void) {
     static const RadPluginInfo info = {
         RAD_PLUGIN_KERNEL, "libr3d_gfx950", "0.1.0",
-        "radiance gemm_nt_q rows (mxfp4a8, fp8a8, mxfp4a16), gemm_nt_q_gated (fp8a8) and the "
-        "quant_act_fp8 / gated_quant_fp8 / rmsnorm_quant_fp8 producers for "
+        "radiance gemm_nt_q rows (mxfp4a8, fp8a8, mxfp4a16), gemm_nt_q_gated (fp8a8), the "
+        "e4m3 logits_gemm lm_head and the quant_act_fp8 / gated_quant_fp8 / "
+        "rmsnorm_quant_fp8 producers for "
         "AMD Instinct MI355X (CDNA4)",
         "gfx950",
     };

@@ -39,6 +39,8 @@ def _lib():
         L.r3d_ref_grid_block.restype = ctypes.c_int64
         L.r3d_ref_grid_block.argtypes = [_i64, _i64]
         L.r3d_ref_max_threads.restype = ctypes.c_int
+        L.r3d_ref_f16_to_f32.restype = ctypes.c_float
+        L.r3d_ref_f16_to_f32.argtypes = [ctypes.c_uint16]
         _L = L
     return _L
 
@@ -241,6 +243,34 @@ def group8_mag(enc, A, AS, B, BS, rblk=1, nthreads=1):
                               ctypes.c_int(rblk), _i64(M), _i64(N), _i64(K), _p(S8, _f32p),
                               ctypes.c_int(nthreads))
     return S8
+
+
+def f16_to_f32(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    L = _lib()
+    return np.array([L.r3d_ref_f16_to_f32(int(v)) for v in h.reshape(-1)],
+                    np.float32).reshape(h.shape)
+
+
+SCALE_DTYPES = {"bf16": 0, "f16": 1, "f32": 2}
+
+
+def logits_e4m3(x, codes, scale, sdt, br, nthreads=1):
+    """x bf16 bits [M, K]; codes e4m3 [N, K]; scale [ceil(N/br), ceil(K/128)] as uint16
+    bits ("bf16" / "f16") or float32 ("f32").  Returns (Y f32 [M, N], S f32 [M, N])."""
+    x = np.ascontiguousarray(x, np.uint16)
+    codes = np.ascontiguousarray(codes, np.uint8)
+    scale = np.ascontiguousarray(scale, np.float32 if sdt == "f32" else np.uint16)
+    M, K = x.shape
+    N = codes.shape[0]
+    assert codes.shape[1] == K and scale.shape == ((N + br - 1) // br, (K + 127) // 128)
+    Y = np.empty((M, N), np.float32)
+    S = np.empty((M, N), np.float32)
+    _lib().r3d_ref_logits_e4m3(_p(x, _u16p), _i64(K), _p(codes, _u8p),
+                               scale.ctypes.data_as(ctypes.c_void_p), ctypes.c_int(SCALE_DTYPES[sdt]),
+                               _i64(scale.shape[1]), ctypes.c_int(br), _i64(M), _i64(N), _i64(K),
+                               _p(Y, _f32p), _i64(N), _p(S, _f32p), ctypes.c_int(nthreads))
+    return Y, S
 
 
 def bf16_ulp(y):

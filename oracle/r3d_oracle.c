@@ -37,6 +37,12 @@
  *                   poisons the element even when every code is zero; row / column
  *                   permutation equivariance (catches transposed operands).
  *   mxfp8 quantiser and mx8 x mxfp4 dot: same invariants, plus float64 brute force.
+ *   f16 decode      all 65536 bit patterns vs numpy's float16 -> float32 (NaN as a class).
+ *   logits_e4m3     float64 brute force within K*2^-24*S; every one of the 256 codes
+ *                   through a one-hot x at unit scale (vs torch.float8_e4m3fn); a single
+ *                   nonzero term is exact; power-of-two scales per 128-column block and per
+ *                   row block (br = 128 against the same grid expanded to br = 1, bit for
+ *                   bit); head-row permutation equivariance; a NaN code poisons its row.
  *   "parity unpinned" beyond these: no reference-held vectors exist for this path (the
  *   kbench packs are off-repo, tools/gate.sh:18-20), so bit-parity with libref itself on
  *   non-trivial inputs rests on the restatement below.
@@ -473,6 +479,50 @@ void r3d_ref_group8_mag(int enc, const uint8_t* A, int64_t a_pitch, const float*
                 tot += mx;
             }
             S8[m * N + n] = (float)tot;
+        }
+    }
+}
+
+float r3d_ref_f16_to_f32(uint16_t h) {
+    const uint32_t sgn = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31u, m = h & 1023u;
+    if (e == 31) return u2f(sgn | 0x7F800000u | (m << 13));          /* inf, NaN */
+    if (e == 0) {
+        const float v = (float)m * 0x1p-24f;                          /* m * 2^-24, exact */
+        return sgn ? -v : v;
+    }
+    return u2f(sgn | ((e - 15u + 127u) << 23) | (m << 13));
+}
+
+static inline float ld_scale(const void* s, int sdt, int64_t i) {
+    if (sdt == 2) return ((const float*)s)[i];
+    const uint16_t v = ((const uint16_t*)s)[i];
+    return sdt == 1 ? r3d_ref_f16_to_f32(v) : r3d_ref_bf16_to_f32(v);
+}
+
+/* logits_gemm over the joined e4m3 head (src/r3d_gemm_logits.hip:1-11 states the
+ * reference's order; its kernel, :100-124, takes the same two steps per column): the
+ * decoded code times the block scale, one f32 rounding, then one fused multiply-add into
+ * the output's single f32 accumulator, over ascending k. */
+void r3d_ref_logits_e4m3(const uint16_t* x, int64_t x_pitch, const uint8_t* codes,
+                         const void* scale, int sdt, int64_t s_pitch, int br, int64_t M,
+                         int64_t N, int64_t K, float* Y, int64_t y_pitch, float* S,
+                         int nthreads) {
+    R3D_SET_THREADS(nthreads);
+    R3D_PARALLEL_FOR
+    for (int64_t n = 0; n < N; ++n) {
+        const uint8_t* crow = codes + n * K;
+        const int64_t sbase = (n / br) * s_pitch;
+        for (int64_t m = 0; m < M; ++m) {
+            const uint16_t* xr = x + m * x_pitch;
+            float acc = 0.0f, mag = 0.0f;
+            for (int64_t k = 0; k < K; ++k) {
+                const float cv = r3d_ref_e4m3_to_f32(crow[k]) * ld_scale(scale, sdt, sbase + k / 128);
+                const float xv = r3d_ref_bf16_to_f32(xr[k]);
+                acc = fmaf(xv, cv, acc);
+                mag = mag + fabsf(xv * cv);
+            }
+            Y[m * y_pitch + n] = acc;
+            if (S) S[m * N + n] = mag;
         }
     }
 }

@@ -122,6 +122,21 @@ void r3d_ref_group8_mag(int enc, const uint8_t* A, int64_t a_pitch, const float*
 /* Wall-clock helper for the CPU baseline: number of OpenMP threads available. */
 int r3d_ref_max_threads(void);
 
+/* IEEE binary16 bits -> f32, exact (subnormals, infinities and NaN kept). */
+float r3d_ref_f16_to_f32(uint16_t h);
+
+/* logits_gemm over a joined e4m3 head.
+ *   x      [M, K] bf16 bits, row pitch x_pitch (elements)
+ *   codes  [N, K] e4m3, dense
+ *   scale  [ceil(N/br), ceil(K/128)] of sdt (0 bf16 bits, 1 f16 bits, 2 f32), row pitch
+ *          s_pitch (elements); br 1 or 128
+ *   Y      [M, N] f32 (pitch y_pitch); S (optional) [M, N] the magnitude sum
+ *          sum_k |x * (code * s)| accumulated in f32, for error bounds. */
+void r3d_ref_logits_e4m3(const uint16_t* x, int64_t x_pitch, const uint8_t* codes,
+                         const void* scale, int sdt, int64_t s_pitch, int br, int64_t M,
+                         int64_t N, int64_t K, float* Y, int64_t y_pitch, float* S,
+                         int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

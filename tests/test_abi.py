@@ -35,7 +35,12 @@ def test_plugin_identity_and_schema():
     assert info.targets == b"gfx950" and info.kind == 1
     sch = R.schemas()
     assert [s["op"] for s in sch] == ["gemm_nt_q", "quant_act_fp8", "gemm_nt_q_gated",
-                                      "gated_quant_fp8", "rmsnorm_quant_fp8"]
+                                      "gated_quant_fp8", "rmsnorm_quant_fp8", "logits_gemm"]
+    lg = sch[5]                             # src/r3d_rows.cpp:235-245, verbatim
+    assert [(p[0], p[1], p[2]) for p in lg["params"]] == [
+        ("M", 0, 0), ("n_vocab", 0, 0), ("n_embd", 0, 0), ("dtype", 1, 0)]
+    assert [(o[0], o[1], o[2]) for o in lg["operands"]] == [
+        ("x", 0, 0), ("lm_head", 3, 0), ("logits", 1, 0)]
     rq = sch[4]                             # src/r3d_rows.cpp:701-716, verbatim
     assert [(p[0], p[1], p[2]) for p in rq["params"]] == [
         ("M", 0, 0), ("n", 0, 0), ("eps", 2, 0), ("group", 0, 0), ("dtype", 1, 0), ("wadd", 2, 1)]
@@ -67,7 +72,14 @@ def test_rows_and_resolver():
     rows = {r["name"]: r for r in R.rows()}
     assert set(rows) == {"gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", "gemm_nt_q_fp8a8",
                          "gemm_nt_q_fp8a8_decode", "gemm_nt_q_mxfp4a16", "quant_act_fp8_act",
-                         "gated_quant_fp8_act", "gemm_nt_q_gated_fp8a8", "rmsnorm_quant_fp8"}
+                         "gated_quant_fp8_act", "gemm_nt_q_gated_fp8a8", "rmsnorm_quant_fp8",
+                         "logits_gemm_e4m3"}
+    lg = lambda **kw: (R.resolve("logits_gemm", kw) or {}).get("name")
+    assert lg(M=4, n_vocab=262144, n_embd=5376, dtype="bf16") == "logits_gemm_e4m3"
+    assert lg(M=4, n_vocab=262144, n_embd=64, dtype="bf16") is None          # n_embd GE 128
+    assert lg(M=4, n_vocab=262144, n_embd=5376, dtype="f16") is None
+    assert lg(M=4, n_vocab=0, n_embd=5376, dtype="bf16") is None
+    assert rows["logits_gemm_e4m3"]["priority"] == 1000 and not rows["logits_gemm_e4m3"]["scratch"]
     rq = lambda **kw: (R.resolve("rmsnorm_quant_fp8", kw) or {}).get("name")
     assert rq(M=4, n=5376, eps=1e-6, group=128, dtype="bf16") == "rmsnorm_quant_fp8"
     assert rq(M=4, n=5378, eps=1e-6, group=128, dtype="bf16") is None      # n DIV 4
@@ -118,22 +130,23 @@ QA = "quant_act_fp8_act"
 GQ = "gated_quant_fp8_act"
 GG = "gemm_nt_q_gated_fp8a8"
 RQ = "rmsnorm_quant_fp8"
+LG = "logits_gemm_e4m3"
 
 
 @pytest.mark.parametrize("env,expect", [
     ({}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG, "gemm_nt_q_mxfp4",
-          "gemm_nt_q_mxfp4_decode", A16, QA, RQ]),
-    ({"R3D_NO_MXFP4": "1"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG, QA, RQ]),
+          "gemm_nt_q_mxfp4_decode", A16, LG, QA, RQ]),
+    ({"R3D_NO_MXFP4": "1"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG, LG, QA, RQ]),
     ({"R3D_NO_FP4_DEC": "1"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG,
-                               "gemm_nt_q_mxfp4", A16, QA, RQ]),
-    ({"R3D_NO_FP8A8": "1"}, [GQ, "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA, RQ]),
+                               "gemm_nt_q_mxfp4", A16, LG, QA, RQ]),
+    ({"R3D_NO_FP8A8": "1"}, [GQ, "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, LG, QA, RQ]),
     ({"R3D_NO_FP8_DEC": "1"}, [GQ, "gemm_nt_q_fp8a8", GG, "gemm_nt_q_mxfp4",
-                               "gemm_nt_q_mxfp4_decode", A16, QA, RQ]),
+                               "gemm_nt_q_mxfp4_decode", A16, LG, QA, RQ]),
     ({"R3D_NO_FP8_DEC": "", "R3D_NO_FP4_DEC": "0"}, [GQ, "gemm_nt_q_fp8a8", GG,
-                                                     "gemm_nt_q_mxfp4", A16, QA, RQ]),
+                                                     "gemm_nt_q_mxfp4", A16, LG, QA, RQ]),
     ({"R3D_MXFP4_Q8X": "0"}, [GQ, "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode", GG,
-                              "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, QA, RQ]),
-    ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, [GQ, QA, RQ]),
+                              "gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", A16, LG, QA, RQ]),
+    ({"R3D_NO_MXFP4": "1", "R3D_NO_FP8A8": "1"}, [GQ, LG, QA, RQ]),
 ])
 def test_kill_switch_matrix(env, expect):
     """Presence-tested levers hide rows at registration (the value does not matter: an

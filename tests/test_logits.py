@@ -1,0 +1,260 @@
+"""logits_gemm_e4m3 on the CPU: the joined-planes blob (the library's join / split against
+the layout rad_planes.h states, written out independently in tests/logits_util.py), every
+gate of the row's plan (through r3d_gfx950_describe, which reads a host header and launches
+nothing), and the oracle's logits restatement pinned against float64 sums, all 256 codes,
+closed forms and invariants."""
+import numpy as np
+import pytest
+
+import libr3d_amd as R
+import oracle as O
+from libr3d_amd import synth
+from tests import logits_util as LU
+
+ROW = "logits_gemm_e4m3"
+
+
+# ------------------------------------------------------------------ the joined blob
+@pytest.mark.parametrize("N,K,sdt,br", [(300, 208, "bf16", 1), (257, 128, "f16", 128),
+                                        (5, 1040, "f32", 1), (1, 16, "bf16", 128)])
+def test_join_layout_and_round_trip(N, K, sdt, br):
+    rng = np.random.default_rng(N + K)
+    codes = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    sshape = ((N + br - 1) // br, (K + 127) // 128)
+    scale = (rng.standard_normal(sshape).astype(np.float32) if sdt == "f32"
+             else rng.integers(0, 65536, sshape, dtype=np.uint16))
+    blob = R.join_head(codes, scale, sdt, br)
+    h = LU.header(N, K, sdt, br)
+    assert blob.size == R.head_bytes(N, K, sdt, br) == h[32:40].view(np.int64)[0]
+    assert np.array_equal(blob[:LU.HEADER_BYTES], h)           # the header, byte for byte
+    c_off, s_off = LU.up256(LU.HEADER_BYTES), LU.up256(LU.up256(LU.HEADER_BYTES) + N * K)
+    assert np.array_equal(blob[c_off:c_off + N * K].reshape(N, K), codes)
+    assert np.array_equal(blob[s_off:].view(scale.dtype).reshape(sshape), scale)
+    c2, s2 = R.split_head(blob, N, K, sdt, br)
+    assert np.array_equal(c2, codes) and np.array_equal(s2, scale)
+
+
+def test_join_refusals():
+    L = R.lib()
+    assert R.head_bytes(10, 128, "bf16", 2) == -R.RAD_E_SHAPE            # br 1 or 128
+    assert R.head_bytes(0, 128) == -R.RAD_E_SHAPE
+    assert L.r3d_gfx950_logits_head_bytes(10, 128, R.DT["U8"], 1) == -R.RAD_E_DTYPE
+    codes = np.zeros((4, 128), np.uint8)
+    scale = np.zeros((4, 1), np.uint16)
+    dst = np.zeros(R.head_bytes(4, 128) - 1, np.uint8)
+    assert L.r3d_gfx950_logits_head_join(codes.ctypes.data, 128, scale.ctypes.data, 2, 4, 128,
+                                         R.DT["BF16"], 1, dst.ctypes.data,
+                                         dst.size) == R.RAD_E_SHAPE        # dst too small
+    bad = R.join_head(codes, scale)
+    bad[0] ^= 1                                                           # magic
+    assert L.r3d_gfx950_logits_head_split(bad.ctypes.data, bad.size, None, None) == R.RAD_E_DTYPE
+
+
+# ------------------------------------------------------------------ the plan's gates
+class HostT:
+    """A host buffer standing in for a device tensor (describe never launches)."""
+
+    def __init__(self, arr, offset=0):
+        self.arr, self.offset = arr, offset
+        self.shape, self.dtype = arr.shape, arr.dtype
+
+    def data_ptr(self):
+        return self.arr.ctypes.data + self.offset
+
+    def numel(self):
+        return int(np.prod(self.shape))
+
+    def stride(self):
+        return tuple(s // self.arr.itemsize for s in self.arr.strides)
+
+
+def _aligned(shape, dtype):
+    n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+    raw = np.zeros(n + 256, np.uint8)
+    off = (-raw.ctypes.data) % 256
+    return raw[off:off + n].view(dtype).reshape(shape)
+
+
+def _ops(M=4, N=1000, K=5376, sdt="bf16", br=1, h=None, xdt="BF16", ydt="F32", shapes=None,
+         strides=None):
+    x = HostT(_aligned((M, K), np.uint16))
+    blob = h if h is not None else LU.header(N, K, sdt, br)
+    w = HostT(_aligned(blob.shape, np.uint8))
+    w.arr[:] = blob
+    y = HostT(_aligned((M, N), np.float32))
+    ops = R.LogitsOperands(x, w, y, n_vocab=N, n_embd=K, shapes=shapes, strides=strides)
+    ops._t[0].dtype, ops._t[2].dtype = R.DT[xdt], R.DT[ydt]
+    return ops, (x, w, y)
+
+
+def _desc(ops):
+    rc, d = R.describe(ROW, ops)
+    return rc, dict(kv.split("=") for kv in d.split() if "=" in kv) if rc == 0 else d
+
+
+def test_plan_geometry():
+    ops, keep = _ops(M=4, N=262144, K=5376)
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK, g
+    # 5376 = 42 windows of 128, padded to 44; one staged row 44 * 256 + 16 bytes
+    assert g["nwin"] == "42" and g["lds"] == str(4 * (44 * 256 + 16)) and g["mt"] == "4"
+    assert g["groups"] == "2" and g["waves"] == str(262144 // 32) and g["passes"] == "1"
+    ops, keep = _ops(M=16, N=1000, K=5376)
+    rc, g = _desc(ops)                    # 147456 // 11280 = 13 rows a pass
+    assert rc == R.RAD_OK and g["mt"] == "13" and g["passes"] == "2" and g["groups"] == "1"
+    ops, keep = _ops(M=40, N=1000, K=256)
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK and g["mt"] == "16" and g["passes"] == "3"
+    ops, keep = _ops(M=3, N=50, K=144, sdt="f32", br=128)
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK and g["nwin"] == "2" and g["sdt"] == "2" and g["br"] == "128"
+    ops, keep = _ops(M=1, N=50, K=16)                 # below the row's n_embd GE 128: the
+    assert _desc(ops)[0] == R.RAD_OK                  # constraint is the resolver's, not a gate
+
+
+def _hdr(N=1000, K=5376, sdt="bf16", br=1, **fields):
+    h = LU.header(N, K, sdt, br)
+    for key, v in fields.items():
+        name, _, ent = key.partition("__")
+        LU.set_field(h, name, v, None if not ent else int(ent))
+    return h
+
+
+@pytest.mark.parametrize("case,rc", [
+    (dict(ydt="BF16"), R.RAD_E_UNSUPPORTED),                    # logits are f32
+    (dict(xdt="F32"), R.RAD_E_UNSUPPORTED),                     # x is bf16
+    (dict(K=130, h=LU.header(1000, 130)), R.RAD_E_UNSUPPORTED),  # K % 4 (reference gate)
+    (dict(K=132, h=LU.header(1000, 132)), R.RAD_E_UNSUPPORTED),  # K % 16 (16-byte walks)
+    (dict(h=_hdr(magic=0)), R.RAD_E_DTYPE),                      # no header
+    (dict(h=_hdr(n_planes=3)), R.RAD_E_DTYPE),
+    (dict(h=_hdr(transform0=1)), R.RAD_E_UNSUPPORTED),
+    (dict(h=_hdr(role__1="zero")), R.RAD_E_DTYPE),
+    (dict(h=_hdr(dtype__0=4)), R.RAD_E_SHAPE),                   # e5m2 codes
+    (dict(h=_hdr(rows__0=999)), R.RAD_E_SHAPE),
+    (dict(h=_hdr(block1__0=2)), R.RAD_E_SHAPE),
+    (dict(h=_hdr(dtype__1=7)), R.RAD_E_UNSUPPORTED),             # u8 scales
+    (dict(h=_hdr(block1__1=64)), R.RAD_E_UNSUPPORTED),
+    (dict(h=_hdr(block0__1=2)), R.RAD_E_UNSUPPORTED),
+    (dict(h=_hdr(rows__1=999)), R.RAD_E_SHAPE),
+    (dict(h=_hdr(cols__1=41)), R.RAD_E_SHAPE),
+    (dict(h=_hdr(row_bytes__0=5392)), R.RAD_E_STRIDE),           # codes dense
+    (dict(h=_hdr(bytes=1024)), R.RAD_E_SHAPE),                   # scale past the blob
+    (dict(h=_hdr(row_bytes__1=82)), R.RAD_E_STRIDE),             # scale rows shorter than 42
+    (dict(h=_hdr(offset__0=200000)), R.RAD_E_SHAPE),             # codes past the blob
+    (dict(h=_hdr(offset__0=520)), R.RAD_E_UNSUPPORTED),          # codes not 16-byte aligned
+    (dict(M=1, N=4, K=80000, h=LU.header(4, 80000)), R.RAD_E_UNSUPPORTED),  # a row past LDS
+])
+def test_plan_refusals(case, rc):
+    ops, keep = _ops(**case)
+    assert _desc(ops)[0] == rc, (case, _desc(ops))
+
+
+def test_plan_shape_and_stride_refusals():
+    # numel(logits) not a multiple of n_vocab
+    ops, keep = _ops(N=1000, shapes={2: [4, 999]}, strides={2: [999, 1]})
+    assert _desc(ops)[0] == R.RAD_E_SHAPE
+    # x smaller than M x K
+    ops, keep = _ops(shapes={0: [3, 5376]}, strides={0: [5376, 1]})
+    assert _desc(ops)[0] == R.RAD_E_SHAPE
+    # a last-dimension stride other than 1; a row pitch shorter than the row
+    ops, keep = _ops(strides={2: [1000, 2]})
+    assert _desc(ops)[0] == R.RAD_E_STRIDE
+    ops, keep = _ops(strides={0: [5000, 1]})
+    assert _desc(ops)[0] == R.RAD_E_STRIDE
+    # x rows 8-element aligned with a longer pitch are taken; a 16-byte misaligned x is not
+    ops, keep = _ops(M=2, K=256, N=10, h=LU.header(10, 256), shapes={0: [2, 256]},
+                     strides={0: [264, 1]})
+    assert _desc(ops)[0] == R.RAD_OK
+    ops, keep = _ops(M=2, K=256, N=10, h=LU.header(10, 256), shapes={0: [2, 256]},
+                     strides={0: [260, 1]})
+    assert _desc(ops)[0] == R.RAD_E_UNSUPPORTED
+    # M comes from numel(logits) / n_vocab, not the M parameter
+    x = HostT(_aligned((6, 256), np.uint16))
+    w = HostT(_aligned((LU.HEADER_BYTES,), np.uint8))
+    w.arr[:] = LU.header(10, 256)
+    y = HostT(_aligned((6, 10), np.float32))
+    ops = R.LogitsOperands(x, w, y, n_vocab=10, n_embd=256, M=1)
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK and g["M"] == "6"
+
+
+def test_launch_refuses_without_gfx950():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    ops, keep = _ops(M=1, N=10, K=256, h=LU.header(10, 256))
+    assert R.launch_row(ROW, ops, 0) == R.RAD_E_UNSUPPORTED
+
+
+# ------------------------------------------------------------------ the oracle, pinned
+def test_f16_decode_exhaustive():
+    h = np.arange(65536, dtype=np.uint16)
+    got = O.f16_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("sdt,br", [("bf16", 1), ("f16", 128), ("f32", 1), ("bf16", 128)])
+def test_oracle_against_float64(sdt, br):
+    """Bound: the oracle's f32 chain is within K * 2^-24 of the magnitude sum of the exact
+    float64 value; the scales swing over 2^-8 .. 2^8 across blocks and rows, so a scale
+    taken from the wrong block or row misses by far more."""
+    rng = np.random.default_rng(7)
+    M, N, K = 3, 260, 400
+    codes, _ = LU.head(N, K, 3, sdt, br)
+    sshape = ((N + br - 1) // br, (K + 127) // 128)
+    sv = np.ldexp(1.0, rng.integers(-8, 9, sshape)) * rng.uniform(1, 2, sshape)
+    sbits = (synth.bf16_bits(sv.astype(np.float32)) if sdt == "bf16" else
+             sv.astype(np.float16).view(np.uint16) if sdt == "f16" else sv.astype(np.float32))
+    x = synth.bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    Y, S = O.logits_e4m3(x, codes, sbits, sdt, br)
+    ye, se = LU.exact(x, codes, sbits, sdt, br)
+    assert np.all(np.abs(Y - ye) <= (K + 1) * 2.0 ** -24 * se + 1e-30)
+    assert np.allclose(S, se, rtol=K * 2.0 ** -23)
+    # the same scales transposed within each row block would not pass
+    if sshape[0] >= 3 and sshape[1] >= 3:
+        bad = sbits.copy()
+        bad[:, [0, 1]] = bad[:, [1, 0]]
+        yb, _ = LU.exact(x, codes, bad, sdt, br)
+        assert np.any(np.abs(Y - yb) > (K + 1) * 2.0 ** -24 * se)
+
+
+@pytest.mark.parametrize("sdt", ["bf16", "f16", "f32"])
+def test_oracle_every_code_one_hot(sdt):
+    """Row n carries code n at column 5 and zeros elsewhere, x is one-hot at column 5: the
+    single product is exact, so y[n] = f32(e4m3(n) * s) -- against torch's float8_e4m3fn
+    decode (a library, not this oracle), NaN codes poisoning their row."""
+    N, K = 256, 256
+    codes = np.zeros((N, K), np.uint8)
+    codes[:, 5] = np.arange(256)
+    s = np.float32(1.3125)
+    sbits = {"bf16": synth.bf16_bits(np.full((N, 2), s, np.float32)),
+             "f16": np.full((N, 2), s, np.float16).view(np.uint16),
+             "f32": np.full((N, 2), s, np.float32)}[sdt]
+    x = np.zeros((2, K), np.uint16)
+    x[0, 5] = synth.bf16_bits(np.array([1.0], np.float32))[0]
+    x[1, 5] = synth.bf16_bits(np.array([-0.25], np.float32))[0]
+    Y, _ = O.logits_e4m3(x, codes, sbits, sdt, 1)
+    dec = LU.e4m3_values(np.arange(256, dtype=np.uint8))
+    ref = np.stack([(dec * s).astype(np.float32), (dec * s * np.float32(-0.25)).astype(np.float32)])
+    ref = ref + np.float32(0.0)           # the accumulator starts at +0: -0 + +0 = +0
+    nan = np.isnan(ref)
+    assert nan.sum() == 4 and np.array_equal(np.isnan(Y), nan)
+    assert np.array_equal(Y[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_oracle_row_block_scale_equals_expanded_grid():
+    """br = 128 is the per-row grid with each scale repeated over its 128 rows, bit for bit;
+    permuting head rows (with their per-row scales) permutes the logits, bit for bit."""
+    rng = np.random.default_rng(11)
+    M, N, K = 2, 300, 256
+    codes, sb = LU.head(N, K, 5, "bf16", 128)
+    x = synth.bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    Y128, _ = O.logits_e4m3(x, codes, sb, "bf16", 128)
+    Y1, _ = O.logits_e4m3(x, codes, np.repeat(sb, 128, axis=0)[:N], "bf16", 1)
+    assert np.array_equal(Y128.view(np.uint32), Y1.view(np.uint32))
+    perm = rng.permutation(N)
+    Yp, _ = O.logits_e4m3(x, codes[perm], np.repeat(sb, 128, axis=0)[:N][perm], "bf16", 1)
+    assert np.array_equal(Yp.view(np.uint32), Y1[:, perm].view(np.uint32))
