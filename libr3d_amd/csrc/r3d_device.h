@@ -81,6 +81,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t r3d_rsrc(const void* base, int
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
 }
 
+/* Buffer load of `bytes` (16, 4 or 2) per lane straight into LDS at lds + lane *
+ * max(bytes, 4). */
+template <int BYTES>
+__device__ __forceinline__ void r3d_buf_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff,
+                                            uint32_t soff) {
+    static_assert(BYTES == 16 || BYTES == 4 || BYTES == 2, "dwordx4, dword or ushort loads");
+    if constexpr (BYTES == 16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                                 voff, soff, 0, 0);
+    else if constexpr (BYTES == 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
+                                                 voff, soff, 0, 0);
+    else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 2,
+                                                 voff, soff, 0, 0);
+}
+
 /* Non-temporal 16-byte buffer load (buffer_load_dwordx4 ... nt) at byte `off` of the
  * resource; an offset past the resource's num_records returns zeros without touching
  * memory. */

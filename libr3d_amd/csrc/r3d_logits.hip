@@ -80,20 +80,47 @@ __device__ __forceinline__ bool lg_header_ok(const LogitsGuard& g) {
 
 constexpr uint32_t kLgOob = 0x80000000u;     /* past every buffer's num_records: reads 0 */
 
-template <int G, int SDT>
-__global__ __launch_bounds__(kLogitsWaves * 64) void logits_e4m3_kernel(
+/* A chunk is 16 head rows (four groups of 4) over the whole of K, walked in 256-wide
+ * windows.  v_mfma_f32_16x16x32_bf16 sees 16 "rows" in source A; here A row i is (head row
+ * i % 4 of the group, K slot i / 4) and source B column j is (K slot j / 4, activation row
+ * j % 4): lane l = 16 kq + 4 slot + lr holds, for head row lr and activation row lr, the
+ * 16 bytes [64 slot + 16 kq, +16) of the window -- one buffer_load_dwordx4 per group and
+ * window reads the group's 4 rows x 256 contiguous bytes.  Each 8-byte half feeds one MFMA;
+ * D[i][j] is a slot-partial dot product whenever the two slots agree, which in the result
+ * layout (lane l holds D[4 (l/16) + v][l % 16]) are the lanes l = 20 s + t: slot s,
+ * activation row t, head rows v = 0..3 in the four elements (the other 12 of each 16 are
+ * never read).  Slots 0-1 lie in the window's first 128-wide scale block, 2-3 in its
+ * second, so the chunk's scale table in LDS ([block][16 rows] f32) gives each used lane its
+ * four rows' scales with one ds_read_b128.  After the K walk the four slot lanes of each
+ * (activation row, head row) are summed in slot order.  Activation rows beyond 4 take
+ * further MFMAs on the same A operand (XG groups of 4).
+ *
+ * Persistent: a workgroup stages its activation rows once, and each wave walks the chunks
+ * blocks * waves apart as one stream of windows -- the register ring (D windows in flight)
+ * runs straight across chunk boundaries.  The next chunk's scale table is loaded into
+ * registers (its first kLgTB values a lane) when a chunk starts and written over the
+ * wave's table when the chunk ends. */
+constexpr int kLgTB = 12;                             /* table values a lane prefetches */
+
+template <int D, int XG, int SDT>
+__global__ __launch_bounds__(512) void logits_e4m3_kernel(
     const uint16_t* __restrict__ X, int64_t x_pitch, const uint8_t* __restrict__ codes,
     const uint8_t* __restrict__ scale, int64_t s_pitch, int64_t s_bytes, int br,
     float* __restrict__ Y, int64_t y_pitch, int N, int K, int M, int mt, int nwin,
-    int nwin_pad, int xrow, int64_t chunks, LogitsGuard guard) {
+    int nw_pad, int xrow, int xbytes, int64_t chunks, LogitsGuard guard) {
+    static_assert(D >= 1 && D <= 3, "one to three windows in flight");
     constexpr int ESZ = SDT == 2 ? 4 : 2;
+    constexpr int RS = D + 1;                         /* register ring: one window read, D in flight */
     extern __shared__ __align__(16) uint8_t lg_lds[];
+    const int nwaves = blockDim.x >> 6;
     const int mb = blockIdx.y * mt;
     const int live = M - mb < mt ? M - mb : mt;
 
-    /* stage x rows [mb, mb + live) as bf16, zero from K to nwin_pad windows */
-    const int cpr = nwin_pad * 16;                    /* 16-byte chunks per staged row */
-    for (int i = threadIdx.x; i < live * cpr; i += kLogitsWaves * 64) {
+    /* stage x rows [mb, mb + live) as bf16, zero from K to nw_pad windows of 256; a row is
+     * xrow bytes apart (nw_pad * 512 + 16: the 16 keeps the four rows a B-operand read
+     * touches on different banks) */
+    const int cpr = nw_pad * 32;                      /* 16-byte chunks per staged row */
+    for (int i = threadIdx.x; i < live * cpr; i += blockDim.x) {
         const int m = i / cpr, c = i - m * cpr;
         r3d_i32x4 v = {0, 0, 0, 0};
         if (8 * c < K) v = *reinterpret_cast<const r3d_i32x4*>(X + (int64_t)(mb + m) * x_pitch + 8 * c);
@@ -101,101 +128,128 @@ __global__ __launch_bounds__(kLogitsWaves * 64) void logits_e4m3_kernel(
     }
     __syncthreads();
 
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, q = l >> 4;
-    const bool ok = lg_header_ok(guard);
-    const __amdgpu_buffer_rsrc_t rs = r3d_rsrc(scale, s_bytes);
-    const uint8_t* xl = lg_lds + r * xrow + 32 * q;   /* this lane's A columns, window 0 */
-
-    for (int64_t ch = (int64_t)blockIdx.x * kLogitsWaves + wave; ch < chunks;
-         ch += (int64_t)gridDim.x * kLogitsWaves) {
-        const int64_t row0 = ch * 16 * G;
-        if (!ok) {                                    /* the head changed under the plan */
-            for (int g = 0; g < G; ++g) {
-                const int64_t row = row0 + 16 * g + r;
-                for (int i = 0; i < 4; ++i)
-                    if (4 * q + i < live && row < N)
-                        Y[(int64_t)(mb + 4 * q + i) * y_pitch + row] = __builtin_nanf("");
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, kq = l >> 4, slot = (l >> 2) & 3, lr = l & 3;
+    const int64_t ch0 = (int64_t)blockIdx.x * nwaves + wave, stride = (int64_t)gridDim.x * nwaves;
+    if (ch0 >= chunks) return;
+    const int nch = (int)((chunks - ch0 + stride - 1) / stride);
+    if (!lg_header_ok(guard)) {                       /* the head changed under the plan */
+        for (int k = 0; k < nch; ++k)
+            for (int i = l; i < 16 * live; i += 64) {
+                const int64_t row = (ch0 + k * stride) * 16 + (i & 15);
+                if (row < N) Y[(int64_t)(mb + (i >> 4)) * y_pitch + row] = __builtin_nanf("");
             }
-            continue;
-        }
-        const int64_t rows_here = N - row0 < 16 * G ? N - row0 : 16 * G;
-        const __amdgpu_buffer_rsrc_t rc = r3d_rsrc(codes + row0 * K, rows_here * K);
-        uint32_t coff[G], soff[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const int64_t row = row0 + 16 * g + r;
-            coff[g] = (uint32_t)((16 * g + r) * K + 16 * q);
-            soff[g] = row < N ? (uint32_t)((row / br) * s_pitch * ESZ) : kLgOob;
-        }
-        /* window w's two chunk offsets for group g (a chunk at or past K reads zero) */
-        auto code_off = [&](int g, int w, int half) -> uint32_t {
-            const int k = 128 * w + 64 * half + 16 * q;
-            return k < K ? coff[g] + (uint32_t)(128 * w + 64 * half) : kLgOob;
-        };
-        auto scale_off = [&](int g, int w0) -> uint32_t {
-            const int w = w0 + q;
-            return (w < nwin && soff[g] != kLgOob) ? soff[g] + (uint32_t)(w * ESZ) : kLgOob;
-        };
-
-        r3d_i32x4 cc[G][2], cn[G][2];
-        float sc[G], sn[G];
-        r3d_f32x4 tot[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            sc[g] = lg_scale<SDT>(rs, scale_off(g, 0));
-            cc[g][0] = r3d_buf_ld16_stream(rc, code_off(g, 0, 0));
-            cc[g][1] = r3d_buf_ld16_stream(rc, code_off(g, 0, 1));
-            tot[g] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-        for (int w0 = 0; w0 < nwin_pad; w0 += 4) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) sn[g] = lg_scale<SDT>(rs, scale_off(g, w0 + 4));
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int w = w0 + j;
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    cn[g][0] = r3d_buf_ld16_stream(rc, code_off(g, w + 1, 0));
-                    cn[g][1] = r3d_buf_ld16_stream(rc, code_off(g, w + 1, 1));
-                }
-                lg_bf16x8 a0 = {}, a1 = {}, a2 = {}, a3 = {};
-                if (r < live) {
-                    const uint8_t* xp = xl + 256 * w;
-                    a0 = *reinterpret_cast<const lg_bf16x8*>(xp);
-                    a1 = *reinterpret_cast<const lg_bf16x8*>(xp + 16);
-                    a2 = *reinterpret_cast<const lg_bf16x8*>(xp + 128);
-                    a3 = *reinterpret_cast<const lg_bf16x8*>(xp + 144);
-                }
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const r3d_f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                    r3d_f32x4 blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        a0, lg_codes8(cc[g][0][0], cc[g][0][1]), z, 0, 0, 0);
-                    blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        a1, lg_codes8(cc[g][0][2], cc[g][0][3]), blk, 0, 0, 0);
-                    blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        a2, lg_codes8(cc[g][1][0], cc[g][1][1]), blk, 0, 0, 0);
-                    blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        a3, lg_codes8(cc[g][1][2], cc[g][1][3]), blk, 0, 0, 0);
-                    const float s = __shfl(sc[g], r + 16 * j, 64);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) tot[g][i] = fmaf(s, blk[i], tot[g][i]);
-                    cc[g][0] = cn[g][0];
-                    cc[g][1] = cn[g][1];
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < G; ++g) sc[g] = sn[g];
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const int64_t row = row0 + 16 * g + r;
-            if (row >= N) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (4 * q + i < live) Y[(int64_t)(mb + 4 * q + i) * y_pitch + row] = tot[g][i];
-        }
+        return;
     }
+    const int nb_pad = 2 * nw_pad;                    /* scale blocks in a table */
+    float* tab = reinterpret_cast<float*>(lg_lds + xbytes) + (size_t)wave * 16 * nb_pad;
+    const __amdgpu_buffer_rsrc_t rs = r3d_rsrc(scale, s_bytes);
+    /* table value i of chunk k: row 16 chunk + i % 16, block i / 16 (zero past N and K) */
+    auto tab_off = [&](int k, int i) -> uint32_t {
+        const int64_t row = (ch0 + (int64_t)k * stride) * 16 + (i & 15);
+        const int b = i >> 4;
+        return k < nch && row < N && b < nwin ? (uint32_t)(((row / br) * s_pitch + b) * ESZ)
+                                              : kLgOob;
+    };
+    auto tab_sync = [&](int k, float* tab, int from) {   /* values from..end, loaded and written */
+        for (int i = from + l; i < 16 * nb_pad; i += 64) tab[i] = lg_scale<SDT>(rs, tab_off(k, i));
+    };
+
+    /* the load cursor: chunk lk, window lw */
+    const int kl = 64 * slot + 16 * kq;
+    int lk = 0, lw = 0;
+    r3d_i32x4 cb[RS][4];                              /* stream window t sits in slot t % RS */
+    auto issue = [&](r3d_i32x4* dst) __attribute__((always_inline)) {
+        const int64_t row0 = (ch0 + (int64_t)lk * stride) * 16;
+        const int64_t rows_here = lk >= nch ? 0 : (N - row0 < 16 ? N - row0 : 16);
+        const __amdgpu_buffer_rsrc_t rc = r3d_rsrc(codes + (lk >= nch ? 0 : row0 * K), rows_here * K);
+        const int k = 256 * lw + kl;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            dst[g] = r3d_buf_ld16_stream(rc, k < K ? (uint32_t)((4 * g + lr) * K + k) : kLgOob);
+        if (++lw == nw_pad) { lw = 0; ++lk; }
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(cb[d]);
+    tab_sync(0, tab, 0);
+
+    const uint8_t* xl = lg_lds + 2 * kl;              /* + x row * xrow + 512 w + 16 h */
+    for (int k = 0; k < nch; ++k) {
+        float tv[kLgTB];                              /* the next chunk's table, first values */
+#pragma unroll
+        for (int i = 0; i < kLgTB; ++i)
+            tv[i] = 64 * i + l < 16 * nb_pad ? lg_scale<SDT>(rs, tab_off(k + 1, 64 * i + l)) : 0.0f;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   /* this chunk's table is written */
+        r3d_f32x4 tot[XG][4];
+#pragma unroll
+        for (int xg = 0; xg < XG; ++xg)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) tot[xg][g] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int w0 = 0; w0 < nw_pad; w0 += RS) {
+#pragma unroll
+            for (int j = 0; j < RS; ++j) {
+                const int w = w0 + j;
+                issue(cb[(j + D) % RS]);
+                lg_bf16x8 xa[XG][2];
+#pragma unroll
+                for (int xg = 0; xg < XG; ++xg) {
+                    xa[xg][0] = lg_bf16x8{};
+                    xa[xg][1] = lg_bf16x8{};
+                    if (4 * xg + lr < live) {
+                        const uint8_t* xp = xl + (4 * xg + lr) * xrow + 512 * w;
+                        xa[xg][0] = *reinterpret_cast<const lg_bf16x8*>(xp);
+                        xa[xg][1] = *reinterpret_cast<const lg_bf16x8*>(xp + 16);
+                    }
+                }
+                const float* st = tab + 16 * (2 * w + (kq >> 1));   /* used lanes: kq == slot */
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const r3d_i32x4 c = cb[j][g];
+                    const lg_bf16x8 c0 = lg_codes8(c[0], c[1]), c1 = lg_codes8(c[2], c[3]);
+                    const r3d_f32x4 sv = *reinterpret_cast<const r3d_f32x4*>(st + 4 * g);
+#pragma unroll
+                    for (int xg = 0; xg < XG; ++xg) {
+                        const r3d_f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                        r3d_f32x4 blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c0, xa[xg][0], z, 0, 0, 0);
+                        blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c1, xa[xg][1], blk, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) tot[xg][g][v] = fmaf(sv[v], blk[v], tot[xg][g][v]);
+                    }
+                }
+            }
+        }
+        /* lanes t = 0..3 sum the slot lanes 20 s + t in slot order and store head rows
+         * 16 chunk + 4 g + v */
+        const int64_t row0 = (ch0 + (int64_t)k * stride) * 16;
+#pragma unroll
+        for (int xg = 0; xg < XG; ++xg)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                r3d_f32x4 o;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float t0 = tot[xg][g][v];
+                    const float t1 = __shfl(t0, (l + 20) & 63, 64);
+                    const float t2 = __shfl(t0, (l + 40) & 63, 64);
+                    const float t3 = __shfl(t0, (l + 60) & 63, 64);
+                    o[v] = ((t0 + t1) + t2) + t3;
+                }
+                const int m = 4 * xg + l;
+                if (l < 4 && m < live) {
+                    float* yp = Y + (int64_t)(mb + m) * y_pitch + row0 + 4 * g;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        if (row0 + 4 * g + v < N) yp[v] = o[v];
+                }
+            }
+        /* every read of this chunk's table has been consumed: the next chunk's goes in its
+         * place, the prefetched values, then any beyond them */
+#pragma unroll
+        for (int i = 0; i < kLgTB; ++i)
+            if (64 * i + l < 16 * nb_pad) tab[64 * i + l] = tv[i];
+        if (16 * nb_pad > 64 * kLgTB) tab_sync(k + 1, tab, 64 * kLgTB);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* the loads past the last chunk */
 }
 
 /* ------------------------------------------------------------------ the blob's header */
@@ -261,37 +315,47 @@ static void head_forget(const void* blob) {
 
 /* ---------------------------------------------------------------------- the row entry */
 
-/* Workgroups of this instantiation one compute unit holds at `lds` bytes of LDS (the
- * register count answered once by the runtime). */
-template <int G, int SDT>
-static int logits_per_cu(int lds) {
-    static int regs = 0;
-    if (!regs) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&logits_e4m3_kernel<G, SDT>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+/* Workgroups of `waves` waves of this instantiation one compute unit holds at `lds` bytes
+ * of LDS (the register count answered once by the runtime). */
+template <int D, int XG, int SDT>
+static int logits_per_cu(int waves, int lds) {
+    static int regs[9];
+    if (!regs[waves]) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&logits_e4m3_kernel<D, XG, SDT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLogitsLds);
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &n, reinterpret_cast<const void*>(&logits_e4m3_kernel<G, SDT>),
-                kLogitsWaves * 64, 0) != hipSuccess || n < 1)
+                &n, reinterpret_cast<const void*>(&logits_e4m3_kernel<D, XG, SDT>), waves * 64,
+                0) != hipSuccess || n < 1)
             n = 1;
         (void)hipGetLastError();
-        regs = n;
+        regs[waves] = n;
     }
-    const int by_lds = lds > 0 ? 160 * 1024 / lds : regs;
-    return by_lds < regs ? (by_lds < 1 ? 1 : by_lds) : regs;
+    const int by_lds = lds > 0 ? kLogitsLds / lds : regs[waves];
+    const int n = by_lds < regs[waves] ? by_lds : regs[waves];
+    return n < 1 ? 1 : n;
 }
 
-template <int G, int SDT>
+template <int D, int XG, int SDT>
 static hipError_t launch_logits_t(const LogitsPlan& P, hipStream_t stream) {
-    const LogitsGeom g = logits_geom(P, cu_count(), logits_per_cu<G, SDT>(P.lds));
+    const LogitsGeom g = logits_geom(P, cu_count(), logits_per_cu<D, XG, SDT>(P.waves, P.lds));
     const int esz = SDT == 2 ? 4 : 2;
     const int64_t s_bytes = P.guard.s_rows * P.s_pitch * esz;
-    hipLaunchKernelGGL((logits_e4m3_kernel<G, SDT>), dim3((unsigned)g.blocks, (unsigned)g.passes),
-                       dim3(kLogitsWaves * 64), (size_t)P.lds, stream, P.X, P.x_pitch, P.codes,
-                       P.scale, P.s_pitch, s_bytes, P.br, P.Y, P.y_pitch, (int)P.N, (int)P.K,
-                       (int)P.M, P.mt, P.nwin, P.nwin_pad, P.xrow, g.chunks, P.guard);
+    hipLaunchKernelGGL((logits_e4m3_kernel<D, XG, SDT>),
+                       dim3((unsigned)g.blocks, (unsigned)g.passes), dim3(P.waves * 64),
+                       (size_t)P.lds, stream, P.X, P.x_pitch, P.codes, P.scale, P.s_pitch,
+                       s_bytes, P.br, P.Y, P.y_pitch, (int)P.N, (int)P.K, (int)P.M, P.mt,
+                       P.nwin, P.nw_pad, P.xrow, P.mt * P.xrow, g.chunks, P.guard);
     return hipGetLastError();
 }
+
+template <int D, int XG>
+static hipError_t launch_logits_dx(const LogitsPlan& P, hipStream_t s) {
+    return P.sdt == 0 ? launch_logits_t<D, XG, 0>(P, s)
+         : P.sdt == 1 ? launch_logits_t<D, XG, 1>(P, s)
+                      : launch_logits_t<D, XG, 2>(P, s);
+}
+
 
 static int logits_entry(const RadArgs* a, RadStream s) {
     LogitsPlan P{};
@@ -303,13 +367,11 @@ static int logits_entry(const RadArgs* a, RadStream s) {
     rc = plan_logits_e4m3(a, &hc, &P, false);
     if (rc) return rc;
     hipStream_t stream = (hipStream_t)s;
-    hipError_t e;
-#define R3D_LG(G_)                                                                          \
-    e = P.sdt == 0 ? launch_logits_t<G_, 0>(P, stream)                                      \
-      : P.sdt == 1 ? launch_logits_t<G_, 1>(P, stream)                                      \
-                   : launch_logits_t<G_, 2>(P, stream)
-    if (logits_groups(P) == 2) { R3D_LG(2); } else { R3D_LG(1); }
-#undef R3D_LG
+    /* 5..8 activation rows a pass: two groups of 4, one window in flight (the plan's rule) */
+    const hipError_t e = P.mt > 4        ? launch_logits_dx<1, 2>(P, stream)
+                       : P.depth == 3    ? launch_logits_dx<3, 1>(P, stream)
+                       : P.depth == 2    ? launch_logits_dx<2, 1>(P, stream)
+                                         : launch_logits_dx<1, 1>(P, stream);
     if (e != hipSuccess) {
         fprintf(stderr, "libr3d_gfx950: logits_e4m3 launch FAILED (%s)\n", hipGetErrorName(e));
         return RAD_E_DEVICE;

@@ -795,12 +795,43 @@ int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, 
         return RAD_E_UNSUPPORTED;
     /* buffer offsets are 32-bit: one wave's rows of codes and the whole scale plane */
     if (64 * K > 0x7FFFFFFFLL || es->rows * es->row_bytes > 0x7FFFFFFFLL) return RAD_E_UNSUPPORTED;
-    const int nwin = (int)scols, nwin_pad = (nwin + 3) / 4 * 4;
-    const int64_t xrow = (int64_t)nwin_pad * 256 + 16;
-    int64_t mt = kLogitsMaxXLds / xrow;
-    if (mt < 1) return RAD_E_UNSUPPORTED;
-    if (mt > 16) mt = 16;
-    if (mt > M) mt = M;
+    const int nwin = (int)scols;
+    const int64_t nw = (K + 255) / 256;
+    /* Shape: waves a workgroup and windows in flight.  Activation rows are staged
+     * nw_pad * 512 + 16 bytes apart, at most 8 rows a pass, and 5..8 rows keep one window
+     * in flight (registers); the first shape with LDS for min(M, 8) rows beside the waves'
+     * scale tables wins, else the first with room for one row.  R3D_LOGITS_SHAPE="W,D"
+     * (W 4|8 waves, D 1..3 windows) is tried first (a tuning lever, read once). */
+    const int64_t want = M < 8 ? M : 8;
+    static const char* lever = getenv("R3D_LOGITS_SHAPE");
+    int shapes[5][2] = {{0, 0}, {8, 2}, {8, 1}, {4, 2}, {4, 1}};
+    int lw = 0, ld = 0;
+    if (lever && sscanf(lever, "%d,%d", &lw, &ld) == 2 && (lw == 4 || lw == 8) && ld >= 1 && ld <= 3) {
+        shapes[0][0] = lw;
+        shapes[0][1] = ld;
+    }
+    int wv = 0, dp = 0, nw_pad = 0;
+    int64_t xrow = 0, stab = 0, mt = 0;
+    for (int pass = 0; pass < 2 && !wv; ++pass)
+        for (const auto& sh : shapes) {
+            if (!sh[0]) continue;
+            const int np = (int)((nw + sh[1]) / (sh[1] + 1) * (sh[1] + 1));
+            const int64_t xr = (int64_t)np * 512 + 16, st = (int64_t)sh[0] * 16 * 2 * np * 4;
+            int64_t rows = (kLogitsLds - st) / xr;
+            if (rows < 1) continue;
+            if (rows > want) rows = want;
+            if (rows > 4 && sh[1] > 1) rows = 4;
+            /* first pass: a shape that holds the wanted rows (the lever: any that fits) */
+            if (pass == 0 && rows < want && &sh != &shapes[0]) continue;
+            wv = sh[0];
+            dp = sh[1];
+            nw_pad = np;
+            xrow = xr;
+            stab = st;
+            mt = rows;
+            break;
+        }
+    if (!wv) return RAD_E_UNSUPPORTED;
     if ((M + mt - 1) / mt > 65535) return RAD_E_UNSUPPORTED;      /* passes ride grid.y */
     P->X = (const uint16_t*)X->data;
     P->codes = (const uint8_t*)pc;
@@ -810,13 +841,15 @@ int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, 
     P->br = (int)es->block[0];
     P->mt = (int)mt;
     P->nwin = nwin;
-    P->nwin_pad = nwin_pad;
+    P->nw_pad = nw_pad;
     P->xrow = (int)xrow;
+    P->waves = wv;
+    P->depth = dp;
     P->M = M; P->N = N; P->K = K;
     P->x_pitch = x_pitch;
     P->s_pitch = es->row_bytes / ssz;
     P->y_pitch = y_pitch;
-    P->lds = (int)(mt * xrow);
+    P->lds = (int)(mt * xrow + stab);
     LogitsGuard& g = P->guard;
     g.header = (const uint8_t*)W->data;
     g.ic = (int32_t)(ec - h->entry);
@@ -827,17 +860,10 @@ int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, 
     return RAD_OK;
 }
 
-/* Two 16-row groups a wave where the head is long enough to give every wave slot of the
- * chip a few chunks (262144 rows: 8192 chunks), one group below that. */
-int logits_groups(const LogitsPlan& P) { return P.N >= 65536 ? 2 : 1; }
-
-/* The grid: at most per_cu workgroups of 8 waves per compute unit (what one unit holds at
- * once), walking the chunks. */
 LogitsGeom logits_geom(const LogitsPlan& P, int cus, int per_cu) {
     LogitsGeom g{};
-    g.groups = logits_groups(P);
-    g.chunks = (P.N + 16 * g.groups - 1) / (16 * g.groups);
-    int64_t blocks = (g.chunks + kLogitsWaves - 1) / kLogitsWaves;
+    g.chunks = (P.N + 15) / 16;
+    int64_t blocks = (g.chunks + P.waves - 1) / P.waves;
     if (blocks > (int64_t)cus * per_cu) blocks = (int64_t)cus * per_cu;
     g.blocks = (int)blocks;
     g.passes = (P.M + P.mt - 1) / P.mt;
@@ -948,11 +974,10 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
         if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
         const LogitsGeom g = logits_geom(L, 256, 1);
         snprintf(buf, (size_t)len,
-                 "arm=logits M=%lld N=%lld K=%lld mt=%d passes=%lld groups=%d waves=%lld "
-                 "blocks=%d br=%d sdt=%d nwin=%d lds=%d",
-                 (long long)L.M, (long long)L.N, (long long)L.K, L.mt,
-                 (long long)((L.M + L.mt - 1) / L.mt), g.groups, (long long)g.chunks, g.blocks,
-                 L.br, L.sdt, L.nwin, L.lds);
+                 "arm=logits M=%lld N=%lld K=%lld mt=%d passes=%lld depth=%d wg_waves=%d "
+                 "chunks=%lld blocks=%d br=%d sdt=%d nwin=%d lds=%d",
+                 (long long)L.M, (long long)L.N, (long long)L.K, L.mt, (long long)g.passes,
+                 L.depth, L.waves, (long long)g.chunks, g.blocks, L.br, L.sdt, L.nwin, L.lds);
         return RAD_OK;
     }
     if (strstr(row, "rmsnorm_quant_fp8") != nullptr) {

@@ -240,26 +240,26 @@ struct LogitsPlan {
     int sdt;                 /* scale element: 0 bf16, 1 f16, 2 f32 */
     int br;                  /* weight rows per scale row: 1 or 128 */
     int mt;                  /* activation rows per pass (1..16); passes = ceil(M / mt) */
-    int nwin, nwin_pad;      /* 128-wide K windows; padded to the 4-window unroll */
+    int nwin;                /* 128-wide scale blocks along K */
+    int nw_pad;              /* 256-wide code windows, padded to the ring's unroll */
     int xrow;                /* LDS pitch of one staged activation row, bytes */
+    int waves, depth;        /* waves a workgroup; windows in flight per wave (1..3) */
     int64_t M, N, K;
     int64_t x_pitch, s_pitch, y_pitch;   /* elements */
-    int lds;                 /* dynamic LDS bytes per workgroup */
+    int lds;                 /* dynamic LDS bytes per workgroup: x rows, then scale tables */
     LogitsGuard guard;
 };
 /* `h` null: the gates that need no header (args_only); else a host copy of the header. */
 int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, bool args_only);
-constexpr int kLogitsWaves = 8;                /* waves per workgroup */
-constexpr int kLogitsMaxXLds = 144 * 1024;     /* LDS for the staged activation rows */
-/* Launch geometry: each wave owns `groups` x 16 head rows at a time (a chunk) and walks
- * chunks blocks * 8 apart; blocks.y = passes over the activation rows. */
+constexpr int kLogitsLds = 160 * 1024;         /* LDS of one compute unit */
+/* The grid: 16-row chunks dealt to waves blocks * waves apart, at most per_cu workgroups
+ * per compute unit (what one unit holds at once); blocks.y = passes over the activation
+ * rows. */
 struct LogitsGeom {
-    int groups;
     int64_t chunks;
     int blocks;
     int64_t passes;
 };
-int logits_groups(const LogitsPlan& P);
 LogitsGeom logits_geom(const LogitsPlan& P, int cus, int per_cu);
 
 /* The current device: gfx950 or not (answered once per device), and its compute units. */

@@ -57,23 +57,6 @@ __device__ __forceinline__ void r3d_mfma_mx_inplace(r3d_f32x4& acc, r3d_i32x4 a,
         : "v"(a), "v"(b), "v"(sa), "v"(sb));
 }
 
-/* Buffer load of `bytes` (16, 4 or 2) per lane straight into LDS at lds + lane *
- * max(bytes, 4). */
-template <int BYTES>
-__device__ __forceinline__ void r3d_buf_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff,
-                                            uint32_t soff) {
-    static_assert(BYTES == 16 || BYTES == 4 || BYTES == 2, "dwordx4, dword or ushort loads");
-    if constexpr (BYTES == 16)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
-                                                 voff, soff, 0, 0);
-    else if constexpr (BYTES == 4)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
-                                                 voff, soff, 0, 0);
-    else
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 2,
-                                                 voff, soff, 0, 0);
-}
-
 template <int MODE, int WNF, int WMW>
 __global__ __launch_bounds__(512) void prefill_kernel(
     const uint8_t* __restrict__ A, const void* __restrict__ ASv,

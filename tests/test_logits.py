@@ -96,15 +96,25 @@ def test_plan_geometry():
     ops, keep = _ops(M=4, N=262144, K=5376)
     rc, g = _desc(ops)
     assert rc == R.RAD_OK, g
-    # 5376 = 42 windows of 128, padded to 44; one staged row 44 * 256 + 16 bytes
-    assert g["nwin"] == "42" and g["lds"] == str(4 * (44 * 256 + 16)) and g["mt"] == "4"
-    assert g["groups"] == "2" and g["waves"] == str(262144 // 32) and g["passes"] == "1"
+    # 5376 = 42 scale blocks = 21 windows of 256 (a multiple of the 3-window ring); one
+    # staged row 21 * 512 + 16 bytes; 8 waves' scale tables of 16 rows x 42 blocks in f32
+    xrow = 21 * 512 + 16
+    assert g["nwin"] == "42" and g["mt"] == "4" and g["wg_waves"] == "8" and g["depth"] == "2"
+    assert g["lds"] == str(4 * xrow + 8 * 16 * 42 * 4) and g["chunks"] == str(262144 // 16)
+    assert g["passes"] == "1" and g["blocks"] == "256"          # describe assumes 1 per CU
+    ops, keep = _ops(M=1, N=1000, K=5376)
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK and g["wg_waves"] == "8" and g["depth"] == "2" and g["mt"] == "1"
+    assert g["lds"] == str(xrow + 8 * 16 * 42 * 4)
     ops, keep = _ops(M=16, N=1000, K=5376)
-    rc, g = _desc(ops)                    # 147456 // 11280 = 13 rows a pass
-    assert rc == R.RAD_OK and g["mt"] == "13" and g["passes"] == "2" and g["groups"] == "1"
+    rc, g = _desc(ops)          # at most 8 rows a pass; 5..8 rows keep one window in flight
+    assert rc == R.RAD_OK and g["mt"] == "8" and g["passes"] == "2" and g["depth"] == "1"
+    ops, keep = _ops(M=6, N=1000, K=5376)
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK and g["mt"] == "6" and g["passes"] == "1" and g["depth"] == "1"
     ops, keep = _ops(M=40, N=1000, K=256)
     rc, g = _desc(ops)
-    assert rc == R.RAD_OK and g["mt"] == "16" and g["passes"] == "3"
+    assert rc == R.RAD_OK and g["mt"] == "8" and g["passes"] == "5" and g["depth"] == "1"
     ops, keep = _ops(M=3, N=50, K=144, sdt="f32", br=128)
     rc, g = _desc(ops)
     assert rc == R.RAD_OK and g["nwin"] == "2" and g["sdt"] == "2" and g["br"] == "128"
