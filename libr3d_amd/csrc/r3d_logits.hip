@@ -97,10 +97,22 @@ constexpr uint32_t kLgOob = 0x80000000u;     /* past every buffer's num_records:
  *
  * Persistent: a workgroup stages its activation rows once, and each wave walks the chunks
  * blocks * waves apart as one stream of windows -- the register ring (D windows in flight)
- * runs straight across chunk boundaries.  The next chunk's scale table is loaded into
- * registers (its first kLgTB values a lane) when a chunk starts and written over the
- * wave's table when the chunk ends. */
-constexpr int kLgTB = 12;                             /* table values a lane prefetches */
+ * runs straight across chunk boundaries.  The next chunk's scales are loaded into registers
+ * when a chunk starts and written over the wave's table when it ends: a full chunk of a
+ * per-row scale grid whose 16 rows form one 16-byte aligned span of whole 16-byte units is
+ * fetched by the unit (at most kLgTU a lane); a per-128-rows grid's one scale row by the
+ * element; anything else by the table value (the first 4 kLgTU a lane ahead, the rest when
+ * the chunk ends). */
+constexpr int kLgTU = 2;                              /* 16-byte units a lane prefetches */
+
+/* Element i (0..15 / ESZ) of a 16-byte unit of scale elements, widened exactly. */
+template <int SDT>
+__device__ __forceinline__ float lg_unit_elem(const r3d_i32x4& u, int i) {
+    if (SDT == 2) return __int_as_float(u[i]);
+    const uint32_t h = (uint32_t)u[i >> 1] >> (16 * (i & 1)) & 0xFFFFu;
+    if (SDT == 0) return __uint_as_float(h << 16);
+    return __half2float(__ushort_as_half((unsigned short)h));
+}
 
 template <int D, int XG, int SDT>
 __global__ __launch_bounds__(512) void logits_e4m3_kernel(
@@ -154,6 +166,89 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
     auto tab_sync = [&](int k, float* tab, int from) {   /* values from..end, loaded and written */
         for (int i = from + l; i < 16 * nb_pad; i += 64) tab[i] = lg_scale<SDT>(rs, tab_off(k, i));
     };
+    /* how chunk k's scales are fetched: 1 by 16-byte unit, 2 one scale row by element, 0 by
+     * table value (wave-uniform) */
+    const int64_t span = 16 * s_pitch * ESZ;          /* a full chunk's rows, per-row grid */
+    const int nunits = (int)(span / 16);
+    auto tab_kind = [&](int k) -> int {
+        if (k >= nch) return 0;
+        if (br != 1) return 2;
+        const int64_t row0 = (ch0 + (int64_t)k * stride) * 16;
+        if (N - row0 < 16 || (span & 15) || nunits > 64 * kLgTU ||
+            ((reinterpret_cast<uintptr_t>(scale) + row0 * s_pitch * ESZ) & 15))
+            return 0;
+        return 1;
+    };
+    auto tab_fetch = [&](int k, r3d_i32x4* tu) __attribute__((always_inline)) {
+        const int kind = tab_kind(k);
+        const int64_t row0 = (ch0 + (int64_t)k * stride) * 16;
+#pragma unroll
+        for (int j = 0; j < kLgTU; ++j) tu[j] = r3d_i32x4{0, 0, 0, 0};
+        if (kind == 1) {
+#pragma unroll
+            for (int j = 0; j < kLgTU; ++j) {
+                const int u = l + 64 * j;
+                tu[j] = r3d_buf_ld16_stream(rs, u < nunits ? (uint32_t)(row0 * s_pitch * ESZ + 16 * u)
+                                                           : kLgOob);
+            }
+        } else if (kind == 2) {
+            const int64_t srow = row0 / br;
+#pragma unroll
+            for (int j = 0; j < 4 * kLgTU; ++j) {
+                const int b = l + 64 * j;
+                if (64 * j < nwin)
+                    tu[j >> 2][j & 3] = __float_as_int(lg_scale<SDT>(
+                        rs, b < nwin ? (uint32_t)((srow * s_pitch + b) * ESZ) : kLgOob));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4 * kLgTU; ++j)
+                if (64 * j < 16 * nb_pad)
+                    tu[j >> 2][j & 3] = __float_as_int(lg_scale<SDT>(rs, tab_off(k, l + 64 * j)));
+        }
+    };
+    auto tab_write = [&](int k, const r3d_i32x4* tu) __attribute__((always_inline)) {
+        const int kind = tab_kind(k);
+        if (kind == 1) {
+            constexpr int EPU = 16 / ESZ;             /* elements a unit */
+            const int sp = (int)s_pitch;
+#pragma unroll
+            for (int j = 0; j < kLgTU; ++j) {
+                const int u = l + 64 * j;
+                if (u >= nunits) continue;
+                int e = EPU * u, row = e / sp, b = e - row * sp;
+#pragma unroll
+                for (int i = 0; i < EPU; ++i) {
+                    if (b < nwin) tab[16 * b + row] = lg_unit_elem<SDT>(tu[j], i);
+                    if (++b == sp) { b = 0; ++row; }
+                }
+            }
+        } else if (kind == 2) {
+#pragma unroll
+            for (int j = 0; j < 4 * kLgTU; ++j) {
+                const int b = l + 64 * j;
+                if (64 * j < nb_pad && b < nb_pad) {
+                    const float v = __int_as_float(tu[j >> 2][j & 3]);
+                    r3d_f32x4* t = reinterpret_cast<r3d_f32x4*>(tab + 16 * b);
+                    t[0] = t[1] = t[2] = t[3] = r3d_f32x4{v, v, v, v};
+                }
+            }
+            if (nb_pad > 64 * 4 * kLgTU) {            /* per-128-rows grids of very long K */
+                const int64_t srow = ((ch0 + (int64_t)k * stride) * 16) / br;
+                for (int b = 64 * 4 * kLgTU + l; b < nb_pad; b += 64) {
+                    const float v = lg_scale<SDT>(rs, b < nwin ? (uint32_t)((srow * s_pitch + b) * ESZ)
+                                                               : kLgOob);
+                    r3d_f32x4* t = reinterpret_cast<r3d_f32x4*>(tab + 16 * b);
+                    t[0] = t[1] = t[2] = t[3] = r3d_f32x4{v, v, v, v};
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4 * kLgTU; ++j)
+                if (64 * j + l < 16 * nb_pad) tab[64 * j + l] = __int_as_float(tu[j >> 2][j & 3]);
+            if (16 * nb_pad > 64 * 4 * kLgTU) tab_sync(k, tab, 64 * 4 * kLgTU);
+        }
+    };
 
     /* the load cursor: chunk lk, window lw */
     const int kl = 64 * slot + 16 * kq;
@@ -172,13 +267,13 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(cb[d]);
     tab_sync(0, tab, 0);
+    if (tab_kind(0) == 1)                             /* keep the never-written blocks zero */
+        for (int i = l; i < 16 * nb_pad; i += 64) tab[i] = (i >> 4) < nwin ? tab[i] : 0.0f;
 
     const uint8_t* xl = lg_lds + 2 * kl;              /* + x row * xrow + 512 w + 16 h */
     for (int k = 0; k < nch; ++k) {
-        float tv[kLgTB];                              /* the next chunk's table, first values */
-#pragma unroll
-        for (int i = 0; i < kLgTB; ++i)
-            tv[i] = 64 * i + l < 16 * nb_pad ? lg_scale<SDT>(rs, tab_off(k + 1, 64 * i + l)) : 0.0f;
+        r3d_i32x4 tu[kLgTU];                          /* the next chunk's scales */
+        tab_fetch(k + 1, tu);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   /* this chunk's table is written */
         r3d_f32x4 tot[XG][4];
 #pragma unroll
@@ -243,11 +338,8 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
                 }
             }
         /* every read of this chunk's table has been consumed: the next chunk's goes in its
-         * place, the prefetched values, then any beyond them */
-#pragma unroll
-        for (int i = 0; i < kLgTB; ++i)
-            if (64 * i + l < 16 * nb_pad) tab[64 * i + l] = tv[i];
-        if (16 * nb_pad > 64 * kLgTB) tab_sync(k + 1, tab, 64 * kLgTB);
+         * place */
+        if (k + 1 < nch) tab_write(k + 1, tu);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* the loads past the last chunk */
 }

@@ -1,8 +1,8 @@
 """logits_gemm_e4m3 on the GPU, through the row's launch pointer: parity with the oracle
-and with the exact float64 sum over ragged and strided shapes, every scale dtype and both
-scale row blocks, passes over many activation rows, the two-group launch; all 256 codes
-bit-exact through one-hot activations; red zones round every operand; the cached header's
-guard; refusals that need the device header."""
+and with the exact float64 sum over ragged and strided shapes, every scale dtype, both
+scale row blocks and hand-built scale-plane layouts, passes over many activation rows, the
+persistent chunk walk; all 256 codes bit-exact through one-hot activations; red zones round
+every operand; the cached header's guard; refusals that need the device header."""
 import numpy as np
 import pytest
 import torch
@@ -19,14 +19,42 @@ Y_FILL = np.float32(-7.75e33)            # no output equals it
 
 
 def kernel_bound(K, S):
-    """|y - exact| for the kernel: 4 chained 32-deep MFMAs per 128-wide window, each within
-    66 * 2^-24 of the magnitudes it sums (33 terms, each truncated below 2^-23 of the
-    largest), then one fma into the f32 accumulator per window."""
-    nwin = (K + 127) // 128
-    return (4 * 66 + 2 * nwin + 2) * 2.0 ** -24 * np.asarray(S, np.float64) + 2.0 ** -126
+    """|y - exact| for the kernel.  Per 256-wide window each of four K slots is two chained
+    32-deep MFMAs, each within 66 * 2^-24 of the magnitudes it sums (33 terms, each
+    truncated below 2^-23 of the largest; the second's C is the first's result), so within
+    132 * 2^-24 of the slot's magnitudes; then one fma per window into the slot's f32
+    accumulator, and three adds over the slots.  The product code * x is exact (4 x 8
+    significant bits), and code * scale needs none (the scale multiplies the window sum)."""
+    nw = (K + 255) // 256
+    return (132 + 2 * nw + 4) * 2.0 ** -24 * np.asarray(S, np.float64) + 2.0 ** -126
 
 
-def run(x, codes, sbits, sdt, br, dev, x_pitch=None, y_pitch=None, forget=True):
+def custom_blob(codes, sbits, sdt, br, s_pad=0, s_shift=0):
+    """A joined head written by hand: the scale plane's rows s_pad elements longer than
+    ceil(K / 128), and the plane s_shift bytes past its 256-byte boundary -- layouts the
+    library's own join never writes but rad_planes.h admits."""
+    N, K = codes.shape
+    h = LU.header(N, K, sdt, br)
+    esz = 4 if sdt == "f32" else 2
+    srows, scols = sbits.shape
+    rb = (scols + s_pad) * esz
+    c_off = LU.up256(LU.HEADER_BYTES)
+    s_off = LU.up256(c_off + N * K) + s_shift
+    LU.set_field(h, "row_bytes", rb, 1)
+    LU.set_field(h, "offset", s_off, 1)
+    LU.set_field(h, "bytes", s_off + srows * rb)
+    blob = np.zeros(s_off + srows * rb, np.uint8)
+    blob[:LU.HEADER_BYTES] = h
+    blob[c_off:c_off + N * K] = codes.reshape(-1)
+    plane = np.zeros((srows, scols + s_pad), sbits.dtype)
+    plane[:, :scols] = sbits
+    if s_pad:                            # NaN in every padding element
+        plane[:, scols:] = np.float32(np.nan) if sdt == "f32" else 0x7FC0 if sdt == "bf16" else 0x7E00
+    blob[s_off:] = plane.view(np.uint8).reshape(-1)
+    return blob
+
+
+def run(x, codes, sbits, sdt, br, dev, x_pitch=None, y_pitch=None, forget=True, blob=None):
     """Launch the row on guarded device copies; returns (rc, Y [M, N] f32, guards ok)."""
     M, K = x.shape
     N = codes.shape[0]
@@ -35,7 +63,7 @@ def run(x, codes, sbits, sdt, br, dev, x_pitch=None, y_pitch=None, forget=True):
     xh[:, :K] = x
     yp = y_pitch or N
     gx = gu.Guarded(xh, dev)
-    gw = gu.Guarded(R.join_head(codes, sbits, sdt, br), dev)
+    gw = gu.Guarded(R.join_head(codes, sbits, sdt, br) if blob is None else blob, dev)
     gy = gu.Guarded(np.full((M, yp), Y_FILL, np.float32), dev)
     ops = R.LogitsOperands(gx.t, gw.t, gy.t, n_vocab=N, n_embd=K,
                            shapes={0: [M, K], 2: [M, N]}, strides={0: [xp, 1], 2: [yp, 1]})
@@ -81,9 +109,9 @@ CASES = [  # M, N, K, sdt, br, x_pitch, y_pitch
     (8, 2000, 1024, "f32", 1, None, None),
     (16, 1000, 640, "bf16", 128, 648, 1003),     # strided x and logits
     (20, 700, 256, "bf16", 1, None, None),       # two passes over x
-    (6, 200, 16384, "bf16", 1, None, None),      # four rows of x fit LDS: two passes
+    (6, 200, 16384, "bf16", 1, None, None),      # 32 KB rows of x: 4 a pass, two passes
     (2, 96, 144, "bf16", 1, None, None),         # two windows, the second 16 wide
-    (5, 70000, 256, "bf16", 1, None, None),      # two 16-row groups a wave
+    (5, 70000, 256, "bf16", 1, None, None),      # many chunks a wave, 5 rows of x
 ]
 
 
@@ -95,6 +123,20 @@ def test_logits_parity(gpu, M, N, K, sdt, br, xp, yp):
     rc, Y, ok = run(x, codes, sbits, sdt, br, gpu, xp, yp)
     assert rc == R.RAD_OK and ok
     check(Y, x, codes, sbits, sdt, br, "logits_M%d_N%d_K%d_%s_br%d" % (M, N, K, sdt, br))
+
+
+@pytest.mark.parametrize("sdt,br,pad,shift", [("bf16", 1, 3, 0), ("f16", 1, 0, 2),
+                                              ("f32", 1, 1, 4), ("bf16", 128, 5, 6)])
+def test_scale_plane_layouts(gpu, sdt, br, pad, shift):
+    """Scale rows padded past ceil(K / 128) (the padding holds NaN: read, it would poison the
+    logits) and scale planes off 16-byte alignment: the per-chunk scale fetch falls back from
+    whole 16-byte units to single elements and must read only the grid."""
+    M, N, K = 3, 300, 640
+    codes, sbits = LU.head(N, K, 17, sdt, br)
+    x = synth.bf16_bits(np.random.default_rng(18).standard_normal((M, K)).astype(np.float32))
+    rc, Y, ok = run(x, codes, sbits, sdt, br, gpu, blob=custom_blob(codes, sbits, sdt, br, pad, shift))
+    assert rc == R.RAD_OK and ok
+    check(Y, x, codes, sbits, sdt, br, "logits_layout_%s_br%d_pad%d_shift%d" % (sdt, br, pad, shift))
 
 
 @pytest.mark.parametrize("sdt", ["bf16", "f16", "f32"])
