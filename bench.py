@@ -281,6 +281,14 @@ def main():
         extra.update(bench_gated(dev, stream, ksteps))
         extra.update(bench_skinny(dev, stream, ksteps))
         extra.update(bench_c4(dev, stream, steps=5))
+        torch.cuda.empty_cache()
+        for m in (1, 4):                 # the reference's lm_head row on the 27B head
+            r = run_case("lm_head_e4m3_M%d" % m, dev, stream, max(100, ksteps), 10)
+            extra["lm_head_e4m3_M%d" % m] = {k: r[k] for k in ("M", "K", "N", "bytes", "kernel",
+                                                                "kernel_us", "GBps", "frac_hbm")}
+            log("[bench] lm_head logits_gemm_e4m3 M=%d: %.1f us, %.1f GB/s (%.1f%%)" % (
+                m, r["kernel_us"], r["GBps"], 100 * r["frac_hbm"]))
+            torch.cuda.empty_cache()
     if extra:
         out["extra"] = extra
 
@@ -433,7 +441,8 @@ def bench_lm_head_e4m3(M, dev, stream, steps, warmup, res):
     R.forget_head(blob)
     nb = N * K + N * scols * 2 + M * K * 2 + M * N * 4
     res.update({"M": M, "K": K, "N": N, "row": row, "bytes": nb,
-                "kernel": "r3d::logits_e4m3_kernel<2, 0>", "kernel_us": round(kern * 1e6, 3),
+                "kernel": "r3d::logits_e4m3_kernel<%d, %d, 0>" % (2 if M <= 4 else 1, 1 if M <= 4 else 2),
+                "kernel_us": round(kern * 1e6, 3),
                 "GBps": round(nb / kern / 1e9, 1), "frac_hbm": round(nb / kern / 1e9 / HBM_PEAK_GBS, 4),
                 "GBps_wall": round(nb * steps / wall / 1e9, 1)})
     return res
@@ -694,7 +703,8 @@ def bench_c4(dev, stream, steps=5):
     """Config 4: one decode step of a 27B-class model at M=4 -- 62 layers of q/k/v/o and
     gate/up/down in mxfp4a8 plus an fp8a8 lm_head (K=5376, N=262144).  Weights are random
     codes generated on the device (bandwidth does not depend on values; NaN-free); the
-    435 launches run eagerly and as one captured HIP graph."""
+    435 launches run eagerly and as one captured HIP graph; then eagerly again with the
+    reference's own lm_head row, logits_gemm_e4m3 over the joined e4m3 head."""
     import torch
     import libr3d_amd as R
     M, H, I, L, V = 4, 5376, 21504, 62, 262144
@@ -781,7 +791,34 @@ def bench_c4(dev, stream, steps=5):
     except Exception as e:          # graph capture unavailable: report eager only
         res["c4_decode_step_graph"] = {"error": repr(e)[:200]}
         log("[bench] C4 graph capture failed: %r" % (e,))
-    del keep, launches
+    # the same step with the reference's own lm_head row: bf16 x through logits_gemm_e4m3
+    # over the joined e4m3 head (codes + one bf16 scale per row and 128 columns), f32 logits
+    hdr, c_off, s_off, nb_blob = R.head_header(V, H, "bf16", 1)
+    blob = torch.empty(nb_blob, dtype=torch.uint8, device=dev)
+    blob[:hdr.size].copy_(torch.from_numpy(hdr))
+    blob[c_off:c_off + V * H].copy_(codes(V * H, True))
+    scols = (H + 127) // 128
+    blob[s_off:s_off + V * scols * 2].view(torch.int16).fill_(0x3C00)     # bf16 0.0078125
+    xh = torch.randn((M, H), device=dev, generator=g).to(torch.bfloat16).view(torch.int16)
+    yl = torch.empty((M, V), dtype=torch.float32, device=dev)
+    lops = R.LogitsOperands(xh, blob, yl, n_vocab=V, n_embd=H)
+    launches[-1] = (R.row_launcher("logits_gemm_e4m3"), lops)
+    total_e4 = total - f8_bytes(M, V, H) + V * H + V * scols * 2 + M * H * 2 + M * V * 4
+    step(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(stream)
+    torch.cuda.synchronize()
+    e4 = (time.perf_counter() - t0) / steps
+    R.forget_head(blob)
+    res["c4_decode_step_eager_e4m3_head"] = {
+        "bytes": total_e4, "ms": round(e4 * 1e3, 3), "GBps": round(total_e4 / e4 / 1e9, 1),
+        "frac_hbm": round(total_e4 / e4 / 1e9 / HBM_PEAK_GBS, 4),
+        "lm_head": "logits_gemm_e4m3 (bf16 x, joined e4m3 + bf16 scale head, f32 logits)"}
+    log("[bench] C4 decode step with the e4m3 logits head: eager %.3f ms (%.1f GB/s)" % (
+        e4 * 1e3, total_e4 / e4 / 1e9))
+    del keep, launches, blob
     return res
 
 

@@ -56,7 +56,8 @@ const DumpConfig& config() {
         x.on = true;
         x.dir = d;
         const char* o = getenv("R3D_DUMP_OPS");
-        std::string ops = o && *o ? o : "gemm_nt_q,quant_act_fp8,gated_quant_fp8,rmsnorm_quant_fp8";
+        std::string ops =
+            o && *o ? o : "gemm_nt_q,quant_act_fp8,gated_quant_fp8,rmsnorm_quant_fp8,logits_gemm";
         size_t p = 0;
         while (p <= ops.size()) {
             const size_t e = ops.find(',', p);

@@ -12,6 +12,9 @@ PRE state, and those are compared with the POST state the GPU wrote:
       mxfp4a16 row's quantised activations in the scratch bit for bit
   gemm_nt_q_gated (fp8a8)                                the gate_up plane in the scratch
       within the GEMM bound, the codes, scales and gated output bit for bit from it
+  logits_gemm_e4m3                                       the planes out of the captured
+      joined head, the logits within the row's bound (its MFMA sums and the oracle's
+      f32 chain: (140 + 2 ceil(K/256) + K) 2^-24 S), NaN classes equal
 --device re-launches each capture through libr3d_gfx950.so on a GPU instead (operands
 rebuilt from PRE at the same offsets, the same parameters, tunables and scratch size) and
 requires the outputs to equal POST byte for byte: the kernels are deterministic.
@@ -313,6 +316,47 @@ def check_gemm_gated(c, O, gu):
         M, N, K, cmp["max_viol"], "bit-exact" if ok2 else "DIFFER")
 
 
+def head_planes(blob):
+    """(codes [N, K] uint8, scale grid (uint16 bits or float32), scale dtype name, rows per
+    scale row) out of a joined head (include/rad_planes.h's layout)."""
+    b = np.asarray(blob, np.uint8)
+    u32 = b[:40].view(np.uint32)
+    if u32[0] != 0x534E4C50 or u32[1] != 1:
+        raise ValueError("no joined-planes header")
+    ents = {}
+    for i in range(int(u32[2])):
+        e = b[40 + 72 * i: 40 + 72 * (i + 1)]
+        role = bytes(e[:16]).split(b"\0")[0].decode()
+        dt = int(e[16:20].view(np.uint32)[0])
+        blk0, blk1, rows, cols, rb, off = (int(v) for v in e[24:72].view(np.int64))
+        ents[role] = (dt, blk0, rows, cols, rb, off)
+    dt, _, rows, cols, rb, off = ents["codes"]
+    codes = b[off:off + rows * rb].reshape(rows, rb)[:, :cols].copy()
+    dt, br, srows, scols, rb, off = ents["scale"]
+    sdt = {DT["BF16"]: "bf16", DT["F16"]: "f16", DT["F32"]: "f32"}[dt]
+    e = 4 if sdt == "f32" else 2
+    grid = b[off:off + srows * rb].view(np.float32 if e == 4 else np.uint16).reshape(srows, rb // e)
+    return codes, grid[:, :scols].copy(), sdt, br
+
+
+def check_logits(c, O):
+    N, K = c.geti("n_vocab"), c.geti("n_embd")
+    tx, ty = c.tensors[0], c.tensors[2]
+    M = numel(ty) // N
+    X = rows_of(c.pre[0], tx, M, K, row_stride(tx, K), 2)
+    codes, grid, sdt, br = head_planes(c.pre[1])
+    Y = f32(rows_of(c.post[2], ty, M, N, row_stride(ty, N), 4)).astype(np.float64)
+    Yo, S = O.logits_e4m3(X, codes, grid, sdt, br, nthreads=8)
+    nan = np.isnan(Yo)
+    if not np.array_equal(np.isnan(Y), nan):
+        return False, "NaN pattern differs"
+    bound = (140 + 2 * ((K + 255) // 256) + K) * 2.0 ** -24 * S.astype(np.float64) + 2.0 ** -126
+    viol = (np.abs(Y - Yo) / bound)[~nan]
+    use = float(viol.max()) if viol.size else 0.0
+    return use <= 1.0, "M=%d N=%d K=%d %s scales, %d rows a scale row; bound use %.3f" % (
+        M, N, K, sdt, br, use)
+
+
 def replay_oracle(c):
     import oracle as O
     from tests import gpu_util as gu       # the comparison helpers (numpy only here)
@@ -326,6 +370,8 @@ def replay_oracle(c):
         return check_gated(c, O)
     if c.row.startswith("rmsnorm_quant_fp8"):
         return check_rms(c, O)
+    if c.row.startswith("logits_gemm"):
+        return check_logits(c, O)
     return False, "no oracle for row %s" % c.row
 
 
@@ -377,6 +423,8 @@ def replay_device(c):
     ops.args = args
     rc = fn(ops, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
+    if c.row.startswith("logits_gemm") and bufs[1] is not None:
+        R.forget_head(bufs[1])          # the next capture's head may land at this address
     if rc != c.rc:
         return False, "status %d, the capture recorded %d" % (rc, c.rc)
     if c.post is None:

@@ -113,3 +113,29 @@ def test_rmsnorm_capture_with_residual_replays_exact(tmp_path):
                   [b(x), b(r2), b(w), b(q), b(sc), b(out)])
     ok, msg = RD.replay_oracle(RD.Capture(str(tmp_path / "0000_rmsnorm_quant_fp8")))
     assert ok, msg
+
+
+@pytest.mark.parametrize("sdt,br", [("bf16", 1), ("f32", 128)])
+def test_logits_capture_replays_within_bound(tmp_path, sdt, br):
+    """The joined head travels as one U8 operand: the checker takes its planes out of the
+    captured blob (tests/logits_util.py's layout), and a logit moved far outside the bound
+    replays DIVERGENT."""
+    from tests import logits_util as LU
+    import libr3d_amd as R
+    rng = np.random.default_rng(9)
+    M, N, K = 2, 40, 384
+    codes, sb = LU.head(N, K, 10, sdt, br)
+    blob = R.join_head(codes, sb, sdt, br)
+    x = synth.bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    Y, _ = O.logits_e4m3(x, codes, sb, sdt, br)
+    ten = [("BF16", [M, K], [K, 1]), ("U8", [blob.size], [1]), ("F32", [M, N], [N, 1])]
+    pre = [b(x), blob, np.zeros(M * N * 4, np.uint8)]
+    params = [("M", M), ("n_vocab", N), ("n_embd", K), ("dtype", "bf16")]
+    write_capture(tmp_path / "0000_logits_gemm_e4m3", "logits_gemm_e4m3", params, ten, pre,
+                  [b(x), blob, b(Y)])
+    bad = Y.copy()
+    bad[1, 3] = bad[1, 3] * 1.01 + 1.0
+    write_capture(tmp_path / "0001_logits_gemm_e4m3", "logits_gemm_e4m3", params, ten, pre,
+                  [b(x), blob, b(bad)])
+    res = [RD.replay_oracle(RD.Capture(c)) for c in RD.captures([str(tmp_path)])]
+    assert res[0][0] and not res[1][0], res

@@ -1,6 +1,6 @@
 """R3D_DUMP end to end on the GPU: a child process with R3D_DUMP set launches every kind of
 row this library registers (decode, prefill, bf16-in decode, mxfp4a16 with its scratch, the
-three producers, the gated GEMM), each through its row's launch pointer; the library writes
+three producers, the gated GEMM, the e4m3 lm_head), each through its row's launch pointer; the library writes
 one capture per launch; tests/replay_dump.py then rebuilds each launch from its capture and
 (1) checks what the GPU wrote against the oracle, (2) re-launches it on the GPU and requires
 byte-identical outputs.  Also: R3D_DUMP_MAX bounds the captures per row, and R3D_DUMP_OPS
@@ -74,13 +74,21 @@ gg = R.GatedGemmOperands(*t, qg, sg, None, N=512, K=256, act="sigmoid", M=3)
 live.append(torch.empty(R.row_scratch_bytes("gemm_nt_q_gated_fp8a8", gg), dtype=torch.uint8, device=dev))
 gg.set_scratch(live[-1])
 assert R.launch_row("gemm_nt_q_gated_fp8a8", gg, st) == 0
+from tests import logits_util as LU
+codes, sb = LU.head(300, 640, 14, "bf16", 1)
+hb = torch.from_numpy(R.join_head(codes, sb)).to(dev)
+xl = T(synth.bf16_bits(np.random.default_rng(15).standard_normal((3, 640)).astype(np.float32)))
+yl = torch.empty((3, 300), dtype=torch.float32, device=dev)
+live.extend([hb, xl, yl])
+assert R.launch_row("logits_gemm_e4m3", R.LogitsOperands(xl, hb, yl, n_vocab=300, n_embd=640), st) == 0
 torch.cuda.synchronize()
 print("LAUNCHED")
 """
 
 ROWS = {"gemm_nt_q_mxfp4_decode": 2, "gemm_nt_q_mxfp4": 1, "gemm_nt_q_fp8a8": 1,
         "gemm_nt_q_fp8a8_decode": 1, "gemm_nt_q_mxfp4a16": 1, "quant_act_fp8_act": 1,
-        "gated_quant_fp8_act": 1, "rmsnorm_quant_fp8": 1, "gemm_nt_q_gated_fp8a8": 1}
+        "gated_quant_fp8_act": 1, "rmsnorm_quant_fp8": 1, "gemm_nt_q_gated_fp8a8": 1,
+        "logits_gemm_e4m3": 1}
 
 
 def _capture(tmp_path, **env_extra):
