@@ -64,6 +64,19 @@ class Case:
         self.y = torch.empty((M, N), dtype=torch.int16, device=dev)
         self.ops = [R.GemmOperands(self.a, self.as_, b, bs, self.y, dtype=dtype, N=N, K=K)
                     for b, bs in zip(self.b, self.bs)]
+        self.scratch = None
+
+    def hook_scratch(self, row):
+        """Hand every call the launch scratch `row`'s hook asks for (one buffer: the calls
+        run in order on one stream), as an engine's arena would; returns its bytes."""
+        import torch
+        import libr3d_amd as R
+        need = R.row_scratch_bytes(row, self.ops[0])
+        if need > 0:
+            self.scratch = torch.empty(need, dtype=torch.uint8, device=self.y.device)
+            for o in self.ops:
+                o.set_scratch(self.scratch, need)
+        return need
 
 
 def copies_for(nbytes):
@@ -399,6 +412,8 @@ def run_case(name, dev, stream, steps, warmup):
         row = "gemm_nt_q_mxfp4" if name.startswith("skinny_") else "gemm_nt_q_mxfp4_decode"
     copies = 1 if name == "c0" else copies_for(B.nbytes + BS.nbytes)
     c = Case(dtype, A, AS, B, BS, M, N, K, copies, dev)
+    if name.startswith("skinny_"):
+        res["scratch_bytes"] = c.hook_scratch(row)          # split K where it applies
     wall, kern = time_case(c, row, steps, warmup, stream)
     res.update({"M": M, "K": K, "N": N, "row": row, "bytes": nb, "copies": copies,
                 "kernel_us": round(kern * 1e6, 3), "GBps": round(nb / kern / 1e9, 1),
@@ -674,28 +689,41 @@ def bench_gated(dev, stream, steps=50):
 
 
 def bench_skinny(dev, stream, steps=50):
-    """The skinny band (M = 17..64) on the mxfp4a8 tile row at config 2's shapes, cold: the
-    row's own dispatch (16-row decode passes on a narrow N, else the prefill pipeline)."""
+    """The skinny band (M = 17..64) on the tile rows at config 2's shapes, cold: the row's
+    own dispatch with the launch scratch its hook asks for (split K where it applies), and
+    without scratch (16-row decode passes on a narrow N, else the prefill pipeline)."""
     import torch
     import libr3d_amd as R
     from libr3d_amd import synth
     res = {}
-    for name, (K, N) in (("gate_up", (5376, 21504)), ("down", (21504, 5376)),
-                         ("qkv", (5376, 8192))):
-        B, BS = synth.mxfp4_weights(N, K, 0x5EED + 21 + K)
-        for M in (17, 32, 64):
-            _, A, AS = synth.activations(M, K, 0x5EED + 50 + M)
-            c = Case("mxfp4a8", A, AS, B, BS, M, N, K, copies_for(B.nbytes + BS.nbytes), dev)
-            wall, kern = time_case(c, "gemm_nt_q_mxfp4", steps, 10, stream)
-            nb = mx_bytes(M, N, K)
-            arm = R.describe("gemm_nt_q_mxfp4", c.ops[0])[1].split()[0]
-            res["skinny_mxfp4_%s_M%d" % (name, M)] = {
-                "K": K, "N": N, "us": round(kern * 1e6, 2), "GBps": round(nb / kern / 1e9, 1),
-                "frac_hbm": round(nb / kern / 1e9 / HBM_PEAK_GBS, 4), "arm": arm}
-            log("[bench] skinny %s M=%d: %.2f us, %.1f GB/s (%s)" % (name, M, kern * 1e6,
-                                                                  nb / kern / 1e9, arm))
-            del c
-    torch.cuda.empty_cache()
+    for dtype, row in (("mxfp4a8", "gemm_nt_q_mxfp4"), ("fp8a8", "gemm_nt_q_fp8a8")):
+        for name, (K, N) in (("gate_up", (5376, 21504)), ("down", (21504, 5376)),
+                             ("qkv", (5376, 8192))):
+            if dtype == "mxfp4a8":
+                B, BS = synth.mxfp4_weights(N, K, 0x5EED + 21 + K)
+            else:
+                B, BS = synth.fp8_weights(N, K, 0x5EED + 21 + K)
+            for M in (17, 32, 64):
+                _, A, AS = synth.activations(M, K, 0x5EED + 50 + M)
+                c = Case(dtype, A, AS, B, BS, M, N, K, copies_for(B.nbytes + BS.nbytes), dev)
+                nb = mx_bytes(M, N, K) if dtype == "mxfp4a8" else f8_bytes(M, N, K)
+                out = {"K": K, "N": N}
+                for tag in ("noscratch", "hook"):
+                    if tag == "hook" and not c.hook_scratch(row):
+                        break
+                    wall, kern = time_case(c, row, steps, 10, stream)
+                    arm = R.describe(row, c.ops[0])[1].split()[0]
+                    out.update({"us_" + tag: round(kern * 1e6, 2), "arm_" + tag: arm})
+                    log("[bench] skinny %s %s M=%d %s: %.2f us, %.1f GB/s (%s)" % (
+                        dtype, name, M, tag, kern * 1e6, nb / kern / 1e9, arm))
+                us = out.get("us_hook", out["us_noscratch"])
+                out.update({"us": us, "GBps": round(nb / (us * 1e-6) / 1e9, 1),
+                            "frac_hbm": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                            "arm": out.get("arm_hook", out["arm_noscratch"])})
+                res["skinny_%s_%s_M%d" % ("mxfp4" if dtype == "mxfp4a8" else "fp8",
+                                          name, M)] = out
+                del c
+        torch.cuda.empty_cache()
     return res
 
 

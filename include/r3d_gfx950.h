@@ -48,6 +48,17 @@ int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s);
 /* gemm_nt_q at fp8a8, prefill row.  Replaces src/r3d_gemm_fp8a8.hip:1054-1099. */
 int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s);
 
+/* Scratch hooks (RadKernelInfo::scratch) of the two tile rows, r3d_rad_gemm_nt_q (mxfp4a8)
+ * and r3d_rad_gemm_nt_q_fp8.  No counterpart in the reference, whose tile rows take no
+ * scratch: up to M = 128 on an N too narrow to fill the chip with 128-row tiles, these rows
+ * split K across workgroups into f32 partial planes in RadArgs::scratch and sum them in
+ * order on the same stream.  The hook returns the bytes of those planes (kc * M * N * 4 at
+ * the N and K parameters and M = numel(y) / N -- without y the M parameter, else 128), 0 when no split applies.
+ * The scratch is optional: a launch without it, or with less, or at an address that is not
+ * 16-byte aligned, runs the unsplit arms (never a refusal). */
+int64_t r3d_rad_gemm_nt_q_scratch(const RadArgs* a);
+int64_t r3d_rad_gemm_nt_q_fp8_scratch(const RadArgs* a);
+
 /* gemm_nt_q at fp8a8, decode band M <= 16.  Replaces src/r3d_gemm_fp8a8.hip:1101-1130.
  * Takes a bf16 activation row at M = 1 as the mxfp4a8 decode entry does. */
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);

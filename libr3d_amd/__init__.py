@@ -655,7 +655,8 @@ def describe(row_name, ops):
 
 def gemm_nt_q(a, a_scale, b, b_scale, y, *, dtype, N, K, group=None, stream=None, row=None):
     """Resolve and launch gemm_nt_q on `stream` (a raw hipStream_t int, default the
-    current torch stream).  Returns (status, row name)."""
+    current torch stream), with launch scratch of the size the row's hook asks for.
+    Returns (status, row name)."""
     import torch
     ops = GemmOperands(a, a_scale, b, b_scale, y, dtype=dtype, N=N, K=K, group=group)
     M = y.numel() // N
@@ -665,6 +666,9 @@ def gemm_nt_q(a, a_scale, b, b_scale, y, *, dtype, N, K, group=None, stream=None
         if r is None:
             return RAD_E_UNSUPPORTED, None
         row = r["name"]
+    need = row_scratch_bytes(row, ops)
+    if need > 0:                        # the row's hook sized it, as an engine's arena would
+        ops.set_scratch(torch.empty(need, dtype=torch.uint8, device=y.device), need)
     if stream is None:
         stream = torch.cuda.current_stream().cuda_stream
     return launch_row(row, ops, stream), row

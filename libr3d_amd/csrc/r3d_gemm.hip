@@ -67,8 +67,9 @@ static void debug_once(const char* what, int key) {
 
 /* A launch that failed: report it on stderr (the caller's next arm takes the launch, as the
  * reference re-launches a failed arm on the same operands, src/r3d_gemm_mxfp4.hip:1666-1670,
- * 2118-2122).  R3D_GFX950_FAIL_ARM (a test lever) names arms -- "quad", "lines", "skinny"
- * -- that report a failure without launching anything, so the fallbacks can be exercised. */
+ * 2118-2122).  R3D_GFX950_FAIL_ARM (a test lever) names arms -- "quad", "lines", "skinny",
+ * "splitk" -- that report a failure without launching anything, so the fallbacks can be
+ * exercised. */
 static bool forced_fail(const char* arm) {
     static const char* e = getenv("R3D_GFX950_FAIL_ARM");
     return e && strstr(e, arm) != nullptr;
@@ -217,11 +218,25 @@ static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) 
 /* The prefill GEMM: mode PF_A8 reads A/AS as given (e4m3 + f32 per 128) against e2m1
  * weights, PF_F8 the same activations against e4m3 weights with bf16 row scales, PF_MX8 the
  * mxfp8 planes the quantiser left in P.scratch.  stage (mxfp4a16 only): 0 both launches, 1
- * the quantiser alone, 2 the GEMM alone on the planes already in the scratch. */
-static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0) {
+ * the quantiser alone, 2 the GEMM alone on the planes already in the scratch.  part /
+ * part_bytes: launch scratch for split K's partial planes (tile_splitk); the split runs
+ * when it applies and they hold tile_splitk_bytes at a 16-byte aligned address, else (and
+ * when a split launch fails) the unsplit arms below take the launch. */
+static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
+                          uint8_t* part = nullptr, int64_t part_bytes = 0) {
+    const int mode = P.enc == ENC_MXFP4A16 ? PF_MX8 : P.enc == ENC_FP8A8 ? PF_F8 : PF_A8;
+    PrefillGeom g{};
+    prefill_geom(P.M, P.N, P.K, mode, cu_count(), &g);
+    if (g.tiles > 0x7FFFFFFF || g.grid_m > 0x7FFFFFFF) return RAD_E_SHAPE;
+    int cst = 0;
+    PrefillGeom gs{};                                    /* the split's tile */
+    const int kc = part && ((uintptr_t)part & 15) == 0
+                       ? tile_splitk(P.enc, P.M, P.N, P.K, cu_count(), &cst, &gs) : 0;
+    const bool split = kc > 0 && part_bytes >= (int64_t)kc * P.M * P.N * 4 &&
+                       gs.grid_m == 1 && gs.tiles * kc <= 0x7FFFFFFF;
     /* the skinny band on a narrow N: 16-row passes of the decode GEMVs (each output row is
      * the same arithmetic either way) */
-    if (const int passes = skinny_passes(P.enc, P.M, P.N, cu_count())) {
+    if (const int passes = split ? 0 : skinny_passes(P.enc, P.M, P.N, cu_count())) {
         GemmPlan S = P;
         S.M = 16;
         LinesGeom lg{};
@@ -243,10 +258,6 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0) 
         if (rc == RAD_OK) return RAD_OK;
         /* a failed pass: the prefill pipeline below recomputes every row of Y */
     }
-    const int mode = P.enc == ENC_MXFP4A16 ? PF_MX8 : P.enc == ENC_FP8A8 ? PF_F8 : PF_A8;
-    PrefillGeom g{};
-    prefill_geom(P.M, P.N, P.K, mode, cu_count(), &g);
-    if (g.tiles > 0x7FFFFFFF || g.grid_m > 0x7FFFFFFF) return RAD_E_SHAPE;
     const uint8_t* A = P.A;
     const void* AS = P.AS;
     int64_t a_pitch = P.a_pitch, as_pitch = P.as_pitch;
@@ -275,37 +286,73 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0) 
         256 * (mode == PF_F8 ? 2 * P.bs_pitch : P.bs_pitch) >= lim ||
         256 * (mode == PF_MX8 ? as_pitch : 4 * as_pitch) >= lim)
         return RAD_E_UNSUPPORTED;
-    const dim3 grid((unsigned)g.tiles), block(512);
+    /* one launch of the tile kernel of geometry g over g.tiles x ukc units (ukc = 1: the
+     * whole K walk into bf16 Y; else chunks of ucst steps into the f32 planes at pp) */
+    auto tiles_launch = [&](const PrefillGeom& g, int ukc, int ucst, float* pp) -> hipError_t {
+        const dim3 grid((unsigned)(g.tiles * ukc)), block(512);
+#define R3D_PF_L(MODE_, WNF_, WMF_) PrefillLayout<WNF_, WMF_, 3, MODE_ == PF_F8 ? 2 : 1>
 #define R3D_PF(MODE_, WNF_, WMF_)                                                          \
-    static_assert(PrefillLayout<WNF_, WMF_, 3, MODE_ == PF_F8 ? 2 : 1>::LDS ==              \
+    static_assert(R3D_PF_L(MODE_, WNF_, WMF_)::LDS ==                                      \
                       3 * prefill_stage_bytes(WNF_, WMF_, MODE_ == PF_F8 ? 2 : 1),          \
                   "host and kernel ring sizes differ");                                    \
+    if ((int)R3D_PF_L(MODE_, WNF_, WMF_)::LDS != g.lds) return hipErrorInvalidValue;        \
     hipLaunchKernelGGL((prefill_kernel<MODE_, WNF_, WMF_>), grid, block,                    \
-                       (size_t)(PrefillLayout<WNF_, WMF_, 3, MODE_ == PF_F8 ? 2 : 1>::LDS),  \
+                       (size_t)(R3D_PF_L(MODE_, WNF_, WMF_)::LDS),                          \
                        stream, A, AS, P.B, (const uint8_t*)P.BS, P.Y, (int)P.M, (int)P.N,  \
                        g.steps, (int)g.grid_m, (int)g.tiles, P.rblk, a_pitch, as_pitch,     \
-                       P.b_pitch, P.bs_pitch, P.y_pitch)
-    if (mode == PF_MX8) {
-        switch (g.wnf) {
-            case 8: R3D_PF(PF_MX8, 8, 4); break;
-            case 7: R3D_PF(PF_MX8, 7, 4); break;
-            case 6: R3D_PF(PF_MX8, 6, 4); break;
-            default: R3D_PF(PF_MX8, 4, 4); break;
+                       P.b_pitch, P.bs_pitch, P.y_pitch, ukc, ucst, pp)
+        if (mode == PF_MX8) {
+            switch (g.wnf) {
+                case 8: R3D_PF(PF_MX8, 8, 4); break;
+                case 7: R3D_PF(PF_MX8, 7, 4); break;
+                case 6: R3D_PF(PF_MX8, 6, 4); break;
+                default: R3D_PF(PF_MX8, 4, 4); break;
+            }
+        } else if (mode == PF_F8) {
+            if (g.wmf == 1) {
+                R3D_PF(PF_F8, 4, 1);                    /* split K up to 64 tokens */
+            } else {
+                R3D_PF(PF_F8, 4, 2);
+            }
+        } else if (g.wmf == 1) {
+            R3D_PF(PF_A8, 8, 1);                        /* split K up to 64 tokens */
+        } else if (g.wmf == 2) {
+            R3D_PF(PF_A8, 4, 2);                        /* up to 128 tokens */
+        } else {
+            switch (g.wnf) {
+                case 8: R3D_PF(PF_A8, 8, 4); break;
+                case 7: R3D_PF(PF_A8, 7, 4); break;
+                case 6: R3D_PF(PF_A8, 6, 4); break;
+                default: R3D_PF(PF_A8, 4, 4); break;
+            }
         }
-    } else if (mode == PF_F8) {
-        R3D_PF(PF_F8, 4, 2);
-    } else if (g.wmf == 2) {
-        R3D_PF(PF_A8, 4, 2);                            /* up to 128 tokens */
-    } else {
-        switch (g.wnf) {
-            case 8: R3D_PF(PF_A8, 8, 4); break;
-            case 7: R3D_PF(PF_A8, 7, 4); break;
-            case 6: R3D_PF(PF_A8, 6, 4); break;
-            default: R3D_PF(PF_A8, 4, 4); break;
-        }
-    }
 #undef R3D_PF
-    const hipError_t e = hipGetLastError();
+#undef R3D_PF_L
+        return hipGetLastError();
+    };
+    if (split) {
+        /* partial planes, then their in-order sum into Y */
+        hipError_t e = hipSuccess;
+        if (forced_fail("splitk")) {
+            launch_failed("split-K prefill", hipSuccess);
+        } else if ((e = tiles_launch(gs, kc, cst, reinterpret_cast<float*>(part))) != hipSuccess) {
+            launch_failed("split-K prefill", e);
+        } else {
+            const int64_t lanes = P.M * ((P.N + 3) / 4);
+            hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((lanes + 255) / 256)),
+                               dim3(256), 0, stream, reinterpret_cast<const float*>(part), kc,
+                               (int)P.M, (int)P.N, P.Y, P.y_pitch);
+            e = hipGetLastError();
+            if (e == hipSuccess) {
+                debug_once(mode == PF_F8 ? "fp8a8 split-K prefill" : "mxfp4a8 split-K prefill",
+                           200 + 8 * mode);
+                return RAD_OK;
+            }
+            launch_failed("split-K reduce", e);
+        }
+        /* a failed split: the whole K walk below recomputes every element of Y */
+    }
+    const hipError_t e = tiles_launch(g, 1, g.steps, nullptr);
     if (e != hipSuccess) return launch_failed("prefill", e);
     debug_once(mode == PF_MX8 ? "mxfp4a16 prefill (mxfp8 quantiser + MFMA)"
                : mode == PF_F8 ? "fp8a8 prefill" : "mxfp4a8 prefill",
@@ -329,7 +376,8 @@ static int entry(const RadArgs* a, RadStream s, int enc, bool decode) {
     if (!chip_ok()) return RAD_E_UNSUPPORTED;
     hipStream_t stream = (hipStream_t)s;
     if (decode) return launch_decode(P, decode_splitk(a), stream);
-    return launch_prefill(P, stream);
+    if (enc == ENC_MXFP4A16) return launch_prefill(P, stream);
+    return launch_prefill(P, stream, 0, (uint8_t*)a->scratch, a->scratch ? a->scratch_bytes : 0);
 }
 
 /* quant_act_fp8 (src/r3d_band.hip:460-487): the reference's gates, then one wave per
@@ -546,6 +594,9 @@ int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s) {
         return r3d::entry(x, t, r3d::ENC_MXFP4A8, false);
     });
 }
+int64_t r3d_rad_gemm_nt_q_scratch(const RadArgs* a) {
+    return r3d::tile_scratch_bytes(a, r3d::ENC_MXFP4A8, r3d::cu_count());
+}
 int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s) {
     return r3d::dump_wrap("gemm_nt_q_mxfp4_decode", a, s, [](const RadArgs* x, RadStream t) {
         return r3d::entry(x, t, r3d::ENC_MXFP4A8, true);
@@ -566,6 +617,9 @@ int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s) {
     return r3d::dump_wrap("gemm_nt_q_fp8a8", a, s, [](const RadArgs* x, RadStream t) {
         return r3d::entry(x, t, r3d::ENC_FP8A8, false);
     });
+}
+int64_t r3d_rad_gemm_nt_q_fp8_scratch(const RadArgs* a) {
+    return r3d::tile_scratch_bytes(a, r3d::ENC_FP8A8, r3d::cu_count());
 }
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s) {
     return r3d::dump_wrap("gemm_nt_q_fp8a8_decode", a, s, [](const RadArgs* x, RadStream t) {

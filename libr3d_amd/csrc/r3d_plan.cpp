@@ -501,6 +501,67 @@ int skinny_passes(int enc, int64_t M, int64_t N, int ncu) {
     return passes * act < 300 ? passes : 0;
 }
 
+int tile_splitk(int enc, int64_t M, int64_t N, int64_t K, int ncu, int* cst, PrefillGeom* g) {
+    if ((enc != ENC_MXFP4A8 && enc != ENC_FP8A8) || M < 1 || M > 128 || N < 1 || K < 128)
+        return 0;
+    static const long long lever = [] {
+        const char* e = getenv("R3D_GFX950_SPLITK_UNITS");
+        return e ? atoll(e) : -1LL;
+    }();
+    if (ncu <= 0) ncu = 256;
+    const int64_t target = lever >= 0 ? lever : ncu;
+    /* e2m1 weights, short K, two 16-row passes: the passes measured faster (config 2 qkv,
+     * M = 17 / 32: 14.3 / 15.8 us against 16.4 / 17.5 split) */
+    if (enc == ENC_MXFP4A8 && M <= 32 && K <= 8192 && skinny_passes(enc, M, N, ncu)) return 0;
+    /* the split's tile: 64 tokens up to M = 64 (256 e2m1 / 128 e4m3 weight rows), else
+     * 128 x 128 */
+    const int wmf = M <= 64 ? 1 : 2;
+    const int wnf = enc == ENC_MXFP4A8 && wmf == 1 ? 8 : 4;
+    const int64_t bn = 32 * wnf;
+    const int64_t tiles = (N + bn - 1) / bn;
+    const int64_t steps = K / 128;
+    int64_t kc = target / tiles;
+    if (kc > steps / kSplitMinSteps) kc = steps / kSplitMinSteps;
+    if (kc < 2 || tiles * kc > 0x7FFFFFFF) return 0;
+    const int64_t c = (steps + kc - 1) / kc;
+    kc = (steps + c - 1) / c;                           /* no empty chunk */
+    if (kc < 2) return 0;
+    if (cst) *cst = (int)c;
+    if (g) {
+        g->wnf = wnf;
+        g->wmf = wmf;
+        g->nst = 3;
+        g->bn = (int)bn;
+        g->bm = 64 * wmf;
+        g->grid_m = 1;
+        g->grid_n = tiles;
+        g->tiles = tiles;
+        g->steps = (int)steps;
+        g->lds = g->nst * prefill_stage_bytes(wnf, wmf, enc == ENC_FP8A8 ? 2 : 1);
+    }
+    return (int)kc;
+}
+
+int64_t tile_splitk_bytes(int enc, int64_t M, int64_t N, int64_t K, int ncu) {
+    const int kc = tile_splitk(enc, M, N, K, ncu, nullptr, nullptr);
+    return kc ? (int64_t)kc * M * N * 4 : 0;
+}
+
+int64_t tile_scratch_bytes(const RadArgs* a, int enc, int ncu) {
+    long long N = 0, K = 0, M = 0;
+    if (!rad_args_geti(a, "N", &N) || !rad_args_geti(a, "K", &K)) return 0;
+    if (N <= 0 || K <= 0 || N > (1LL << 34) || K > (1LL << 27)) return 0;
+    /* the launch's own M (numel(y) / N) when y is there, else the M parameter, else the
+     * largest M the split takes */
+    const RadTensor* Y = rad_arg_in(a, 4);
+    const long long yn = Y ? rad_tensor_numel(Y) : 0;
+    if (yn > 0 && yn % N == 0)
+        M = yn / N;
+    else if (!rad_args_geti(a, "M", &M) || M <= 0)
+        M = 128;
+    return tile_splitk_bytes(enc, M, N, K, ncu);
+}
+
 int band_row_pitch(const RadTensor* t, int64_t cols, int64_t* pitch) {
     if (!t || !t->data) return -1;
     if (t->rank == 1) {
@@ -1060,6 +1121,17 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
                  ename, (long long)P.M, (long long)P.N, (long long)P.K,
                  g.mt, g.chunks, g.waves, (long long)g.tiles, (long long)g.blocks, g.steps,
                  P.rblk);
+    } else if (int cst = 0, kc = a->scratch && ((uintptr_t)a->scratch & 15) == 0
+                                  ? tile_splitk(P.enc, P.M, P.N, P.K, 256, &cst, nullptr) : 0;
+               kc && a->scratch_bytes >= (int64_t)kc * P.M * P.N * 4) {
+        PrefillGeom g{};
+        tile_splitk(P.enc, P.M, P.N, P.K, 256, nullptr, &g);
+        snprintf(buf, (size_t)len,
+                 "arm=splitk enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d tiles=%lld kc=%d cst=%d "
+                 "steps=%d lds=%d partials=%lld (f32 partial planes in scratch, summed in "
+                 "chunk order)",
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K, g.bn, g.bm,
+                 (long long)g.tiles, kc, cst, g.steps, g.lds, (long long)kc * P.M * P.N * 4);
     } else if (const int passes = skinny_passes(P.enc, P.M, P.N, 256)) {
         snprintf(buf, (size_t)len,
                  "arm=skinny enc=%s M=%lld N=%lld K=%lld passes=%d (16-row decode GEMV passes)",

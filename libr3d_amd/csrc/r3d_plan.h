@@ -152,6 +152,23 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
  * R3D_GFX950_SKINNY=0 / 1 turns the passes off / on for every skinny shape. */
 int skinny_passes(int enc, int64_t M, int64_t N, int ncu);
 
+/* Split K on the tile rows (mxfp4a8, fp8a8) up to M = 128, where a narrow N leaves most
+ * CUs idle under the prefill pipeline's one tile per 128 weight rows: the K steps are cut
+ * into kc chunks of *cst steps (every chunk non-empty), the tile x chunk units write f32
+ * partial tiles into the launch scratch and a second kernel sums the chunks in order into
+ * bf16 Y.  The split's tile (*g): up to M = 64 one 64-token group a wave (e2m1 weights: 256
+ * rows, e4m3: 128), else the 128 x 128 tile.  Returns kc (0: no split).  Units aim at one
+ * per CU (R3D_GFX950_SPLITK_UNITS overrides the target, 0 turns the split off) with at
+ * least kSplitMinSteps steps a chunk.  e2m1 weights at M <= 32 with K <= 8192 keep the
+ * skinny passes where those apply (measured faster there). */
+constexpr int kSplitMinSteps = 4;
+int tile_splitk(int enc, int64_t M, int64_t N, int64_t K, int ncu, int* cst, PrefillGeom* g);
+/* Launch scratch the split needs: kc f32 planes of M x N (0 without a split). */
+int64_t tile_splitk_bytes(int enc, int64_t M, int64_t N, int64_t K, int ncu);
+/* The tile rows' scratch hook: tile_splitk_bytes at the args' N and K and M (numel(y) / N,
+ * else the "M" param, else 128 -- the largest M the split takes); 0 without N or K. */
+int64_t tile_scratch_bytes(const RadArgs* a, int enc, int ncu);
+
 /* The band rows' operand walk (src/r3d_band.hip:419-449 of the reference): a rank-1 tensor
  * of exactly `cols` unit-stride elements is one row read by every row (pitch 0); rank 2
  * needs a unit inner stride and pitches by stride[0] when shape[1] == cols, else reads flat

@@ -62,8 +62,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     const uint8_t* __restrict__ A, const void* __restrict__ ASv,
     const uint8_t* __restrict__ B, const uint8_t* __restrict__ BS,
     uint16_t* __restrict__ Y,
-    int M, int N, int steps, int grid_m, int tiles, int rblk,
-    int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch) {
+    int M, int N, int ksteps, int grid_m, int tiles, int rblk,
+    int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch,
+    int kc, int cst, float* __restrict__ part) {
     constexpr bool F8 = MODE == PF_F8;                   /* e4m3 weights, bf16 row scales */
     constexpr int WH = F8 ? 2 : 1;                        /* 1 KB images per weight fragment */
     constexpr int WB = 64 * WH;                           /* weight bytes per row per step */
@@ -74,12 +75,21 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     /* 0 .. 7 */
     const int li = lane & 15, q = lane >> 4;
 
-    /* Workgroups go round-robin over the 8 XCDs; give each XCD a contiguous run of tiles,
+    /* The grid is tiles x kc units: unit u is K chunk u / tiles (steps [cst c, cst c + cst)
+     * of the K walk, clipped to ksteps) of tile u % tiles.  kc = 1 is the whole K walk.
+     * Workgroups go round-robin over the 8 XCDs; give each XCD a contiguous run of units,
      * token tiles fastest, so the workgroups sharing an L2 share weight and activation
-     * tiles. */
+     * tiles (and, split, one chunk's activation columns). */
+    /* the split runs on the tiles of up to 128 tokens of the flushed modes only; the other
+     * instantiations compile it out (it costs them registers) and take kc = 1 */
+    constexpr bool KS = MODE != PF_MX8 && WMW <= 2;
     const int bid = blockIdx.x;
-    const int per = tiles >> 3, rem = tiles & 7, x = bid & 7;
-    const int t = x * per + (x < rem ? x : rem) + (bid >> 3);
+    const int units = KS ? tiles * kc : tiles;
+    const int per = units >> 3, rem = units & 7, x = bid & 7;
+    const int u = x * per + (x < rem ? x : rem) + (bid >> 3);
+    const int kci = KS ? u / tiles : 0, t = u - kci * tiles;
+    const int64_t s0 = (int64_t)kci * cst;             /* first K step of the chunk */
+    const int steps = !KS ? ksteps : ksteps - (int)s0 < cst ? ksteps - (int)s0 : cst;
     const int tm = t % grid_m, tn = t / grid_m;
     const int64_t n0 = (int64_t)tn * L::BN, m0 = (int64_t)tm * L::BM;
 
@@ -88,8 +98,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(
      * rides in the scalar offset.  The host keeps 256 rows of any operand under 2^31
      * bytes. */
     const int64_t xs_pitch = MODE == PF_MX8 ? as_pitch : 4 * as_pitch;     /* bytes */
-    const __amdgpu_buffer_rsrc_t rB = r3d_rsrc(B + n0 * b_pitch, (N - n0) * b_pitch);
-    const __amdgpu_buffer_rsrc_t rA = r3d_rsrc(A + m0 * a_pitch, (M - m0) * a_pitch);
+    /* a chunk starts s0 steps into every row: WB weight bytes, 128 activation bytes, one
+     * weight scale dword (e4m3 weights: one bf16) and one activation scale dword a step */
+    const int64_t wk = WB * s0, ak = 128 * s0, wsk = (F8 ? 2 : 4) * s0, ask = 4 * s0;
+    const __amdgpu_buffer_rsrc_t rB = r3d_rsrc(B + n0 * b_pitch + wk, (N - n0) * b_pitch - wk);
+    const __amdgpu_buffer_rsrc_t rA = r3d_rsrc(A + m0 * a_pitch + ak, (M - m0) * a_pitch - ak);
     /* scales: waves 0-3 fetch the weight rows' scales (E8M0 dwords; e4m3 weights: the bf16
      * of the row's scale row n / rblk), waves 4-7 the tokens' */
     const bool wsc = wave < 4;
@@ -97,8 +110,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     const int64_t srn = F8 ? (N - 1) / rblk + 1 : N;     /* scale rows */
     const int64_t ws_pitch = F8 ? 2 * bs_pitch : bs_pitch;    /* bytes */
     const __amdgpu_buffer_rsrc_t rSX =
-        wsc ? r3d_rsrc(BS + sr0 * ws_pitch, (srn - sr0) * ws_pitch)
-            : r3d_rsrc(reinterpret_cast<const uint8_t*>(ASv) + m0 * xs_pitch, (M - m0) * xs_pitch);
+        wsc ? r3d_rsrc(BS + sr0 * ws_pitch + wsk, (srn - sr0) * ws_pitch - wsk)
+            : r3d_rsrc(reinterpret_cast<const uint8_t*>(ASv) + m0 * xs_pitch + ask,
+                       (M - m0) * xs_pitch - ask);
     /* A plane load covers 16 rows x 64 bytes with four consecutive lanes on each row
      * (lane l: row l / 4), so every row is one 64-byte run; chunk l % 4 of the run is
      * fetched XOR-swizzled by (row / 2) % 4.  An MFMA operand read (row li, chunk q) then
@@ -221,12 +235,23 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         else
             af[slot] = *reinterpret_cast<const float*>(st + L::AS + 4 * (16 * g + li));
     };
+    /* one token group a wave (the split tiles): a wave whose 16 tokens all lie past M
+     * (clamped padding rows, never stored) skips its MFMAs; its flushes still run, on stale
+     * results into accumulators that are never stored.  (Wider tiles issue every MFMA: the
+     * branch costs them registers.) */
+    const int mlive = WMW == 1 && 16 * (int64_t)wm >= M - m0 ? 0 : WMW;
+    /* the result pair dq[2] alternates by group, or by step (the weight set) at one group a
+     * step */
     auto group = [&](int mi, int set) __attribute__((always_inline)) {
         const int slot = mi & 3;
+        const bool live = mi < mlive;
+        const int dc = WMW == 1 ? set : (mi & 1), dp = dc ^ 1;
         if (MODE == PF_MX8) {
+            if (live) {
 #pragma unroll
-            for (int ni = 0; ni < WNF; ++ni)
-                r3d_mfma_mx_inplace(acc[ni][mi], wS[set][ni], xS[set][ni], ar[slot], ax[slot]);
+                for (int ni = 0; ni < WNF; ++ni)
+                    r3d_mfma_mx_inplace(acc[ni][mi], wS[set][ni], xS[set][ni], ar[slot], ax[slot]);
+            }
         } else if (F8) {
             /* libref's (sub * sa) * sb flush (src/r3d_gemm_fp8a8.hip:9-15), deferred one
              * group; the flushed group of group 0 is the previous step's last, whose weight
@@ -235,11 +260,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(
             const int ps = mi == 0 ? set ^ 1 : set;
 #pragma unroll
             for (int ni = 0; ni < WNF; ++ni) {
-                dq[mi & 1][ni] = r3d_mfma_fp8_fp8(wF[set][ni], ar[slot]);
+                if (live) dq[dc][ni] = r3d_mfma_fp8_fp8(wF[set][ni], ar[slot]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float sb = __uint_as_float((uint32_t)sbF[ps][ni][i] << 16);
-                    acc[ni][pm][i] = acc[ni][pm][i] + (dq[(mi + 1) & 1][ni][i] * sprev) * sb;
+                    acc[ni][pm][i] = acc[ni][pm][i] + (dq[dp][ni][i] * sprev) * sb;
                 }
             }
             sprev = af[slot];
@@ -247,10 +272,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(
             const int pm = mi == 0 ? WMW - 1 : mi - 1;         /* the group flushed now */
 #pragma unroll
             for (int ni = 0; ni < WNF; ++ni) {
-                dq[mi & 1][ni] = r3d_mfma_fp4_fp8(wS[set][ni], xS[set][ni], ar[slot], R3D_E8M0_ONE);
+                if (live)
+                    dq[dc][ni] = r3d_mfma_fp4_fp8(wS[set][ni], xS[set][ni], ar[slot], R3D_E8M0_ONE);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[ni][pm][i] = acc[ni][pm][i] + dq[(mi + 1) & 1][ni][i] * sprev;
+                    acc[ni][pm][i] = acc[ni][pm][i] + dq[dp][ni][i] * sprev;
             }
             sprev = af[slot];        /* this group's scale, kept past the slot's refill */
         }
@@ -342,6 +368,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(
      * one stage (LOADS loads) is younger than the one it waits for. */
     auto step = [&](int s, int set, uint8_t* cur, const uint8_t* nxt, uint8_t* prv) __attribute__((always_inline)) {
         if (SS) { step_ss(s, set, cur, nxt, prv); return; }
+        if (WMW == 1) {
+            /* one token group: its MFMAs, then the barrier, stage s + 3 whole into the slot
+             * just released, and stage s + 1's fragments (stage s + 2 went out a step ago,
+             * so the wait leaves exactly one stage in flight, as below) */
+            group(0, set);
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(L::LOADS) : "memory");
+            issue_part(0, s + 3, cur);
+            read_w(nxt, set ^ 1);
+            read_a(nxt, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            return;
+        }
 #pragma unroll
         for (int mi = 0; mi < WMW; ++mi) {
             group(mi, set);
@@ -372,7 +410,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     issue_part(1, 2, smem + 2 * L::STAGE);
     read_w(smem, 0);
     read_a(smem, 0);
-    read_a(smem, 1);
+    if (WMW > 1) read_a(smem, 1);
     int sl = 0;                                         /* ring slot of stage s */
     int s = 0;
     for (; s + 2 <= steps; s += 2) {
@@ -401,21 +439,48 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         for (int t = WMW * WNF - LAG; t < WMW * WNF; ++t) flush1(t, WMW - 1, sprev, ls);
     } else {
         /* the last group's results (at e4m3 weights with the last step's weight set's
-         * scales: steps alternate sets starting from set 0) */
+         * scales: steps alternate sets starting from set 0; at one group a step its result
+         * pair alternates the same way) */
         const int ls = (steps - 1) & 1;
 #pragma unroll
         for (int ni = 0; ni < WNF; ++ni)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                const float d = WMW == 1 ? (ls ? dq[1][ni][i] : dq[0][ni][i])
+                                         : dq[(WMW - 1) & 1][ni][i];
                 if (F8) {
                     const uint32_t sbb = (uint32_t)(ls ? sbF[1][ni][i] : sbF[0][ni][i]);
                     const float sb = __uint_as_float(sbb << 16);
-                    acc[ni][WMW - 1][i] =
-                        acc[ni][WMW - 1][i] + (dq[(WMW - 1) & 1][ni][i] * sprev) * sb;
+                    acc[ni][WMW - 1][i] = acc[ni][WMW - 1][i] + (d * sprev) * sb;
                 } else {
-                    acc[ni][WMW - 1][i] = acc[ni][WMW - 1][i] + dq[(WMW - 1) & 1][ni][i] * sprev;
+                    acc[ni][WMW - 1][i] = acc[ni][WMW - 1][i] + d * sprev;
                 }
             }
+    }
+
+    /* ---- split K: the f32 partial tile goes to plane kci of part ([kc][M][N], 16-byte
+     * aligned), four consecutive columns a lane */
+    if (KS && part) {
+        float* pp = part + (int64_t)kci * M * N;
+        const bool v4 = (N & 3) == 0;
+#pragma unroll
+        for (int ni = 0; ni < WNF; ++ni)
+#pragma unroll
+            for (int mi = 0; mi < WMW; ++mi) {
+                const int64_t m = m0 + 16 * (wm * WMW + mi) + li;
+                const int64_t n = n0 + 16 * (wn * WNF + ni) + 4 * q;
+                if (m >= M || n >= N) continue;
+                const r3d_f32x4 v = acc[ni][mi];
+                float* d = pp + m * N + n;
+                if (v4) {
+                    *reinterpret_cast<r3d_f32x4*>(d) = v;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (n + i < N) d[i] = v[i];
+                }
+            }
+        return;
     }
 
     /* ---- epilogue: lane holds Y[m0 + 16 g + li][n0 + 16 f + 4 q + i], i = 0..3.  The bf16
@@ -452,6 +517,46 @@ __global__ __launch_bounds__(512) void prefill_kernel(
             for (int i = 0; i < 8; ++i)
                 if (n + i < N) yp[i] = h[i];
         }
+    }
+}
+
+/* Split K's second kernel: Y[m, n] = bf16(sum over c = 0 .. kc-1 of part[c][m][n]), the
+ * chunks added in order from +0 (so every call sums the same way), four columns a lane;
+ * the chunk loads go out four at a time ahead of their adds. */
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+    const float* __restrict__ part, int kc, int M, int N, uint16_t* __restrict__ Y,
+    int64_t y_pitch) {
+    const int cpr = (N + 3) >> 2;
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (int64_t)M * cpr) return;
+    const int m = (int)(e / cpr), n = 4 * (int)(e - (int64_t)m * cpr);
+    const int64_t plane = (int64_t)M * N;
+    const float* p = part + (int64_t)m * N + n;
+    r3d_f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+    if ((N & 3) == 0) {
+        int c = 0;
+        for (; c + 4 <= kc; c += 4) {
+            r3d_f32x4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = *reinterpret_cast<const r3d_f32x4*>(p + (c + j) * plane);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s += v[j];
+        }
+        for (; c < kc; ++c) s += *reinterpret_cast<const r3d_f32x4*>(p + c * plane);
+    } else {
+        for (int c = 0; c < kc; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (n + i < N) s[i] += p[c * plane + i];
+    }
+    uint16_t* yp = Y + m * y_pitch + n;
+    const uint32_t lo = r3d_pack_bf16x2(s[0], s[1]), hi = r3d_pack_bf16x2(s[2], s[3]);
+    if (((uintptr_t)yp & 7) == 0 && n + 4 <= N) {
+        *reinterpret_cast<uint2*>(yp) = make_uint2(lo, hi);
+    } else {
+        const uint16_t h[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
+        for (int i = 0; i < 4; ++i)
+            if (n + i < N) yp[i] = h[i];
     }
 }
 

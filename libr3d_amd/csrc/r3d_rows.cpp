@@ -43,6 +43,8 @@ int r3d_rad_gemm_nt_q(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
+int64_t r3d_rad_gemm_nt_q_scratch(const RadArgs* a);
+int64_t r3d_rad_gemm_nt_q_fp8_scratch(const RadArgs* a);
 int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s);
 int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a);
 int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s);
@@ -253,13 +255,16 @@ const RadKernelInfo kRows[] = {
      "mxfp4a8 prefill GEMM on gfx950 block-scaled MFMA: up to 256 weight rows x 256 tokens "
      "per workgroup, a three-deep direct-to-LDS ring, e2m1 weights with their E8M0 scales "
      "fed to v_mfma_scale_f32_16x16x128_f8f6f4 as is, e4m3 activations, one MFMA per "
-     "128-of-K activation group scaled by a_scale in f32",
+     "128-of-K activation group scaled by a_scale in f32; up to M = 128 on a narrow N, K "
+     "split across workgroups into f32 partials in launch scratch, summed in chunk order",
      "K a multiple of 128; 16-byte aligned A/B bases and A pitch; ragged M/N tiles clamp "
-     "their loads and are never stored; M derives from numel(y)/N",
+     "their loads and are never stored; M derives from numel(y)/N; scratch optional (the "
+     "hook sizes the split's partials; without them the unsplit arms run)",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), e2m1 b with E8M0 b_scale per (row, 32 K), "
      "bf16 y; b_ref accepted and ignored; a_sum refused",
      RAD_DOMAIN_DEVICE, kPrioTile, cMxfp4Tile, 2, nullptr, 0, nullptr,
-     nullptr, nullptr, r3d_rad_gemm_nt_q, nullptr, nullptr, nullptr, nullptr, nullptr},
+     nullptr, nullptr, r3d_rad_gemm_nt_q, r3d_rad_gemm_nt_q_scratch, nullptr, nullptr,
+     nullptr, nullptr},
 
     {"gemm_nt_q_mxfp4_decode", "gemm_nt_q", "gemm",
      "mxfp4a8 decode-band GEMV on gfx950: M <= 4 one wave per 4 weight rows (whole 128-byte "
@@ -276,13 +281,16 @@ const RadKernelInfo kRows[] = {
     {"gemm_nt_q_fp8a8", "gemm_nt_q", "gemm",
      "fp8a8 prefill GEMM on gfx950 block-scaled MFMA: 128x128 output tile over a three-deep "
      "direct-to-LDS ring, e4m3 on both operands, one MFMA per 128-of-K scale group flushed as "
-     "(sub * a_scale) * b_scale in the oracle's order",
+     "(sub * a_scale) * b_scale in the oracle's order; up to M = 128 on a narrow N, K split "
+     "across workgroups into f32 partials in launch scratch, summed in chunk order",
      "K a multiple of 128; 16-byte aligned A/B bases and pitches; b_scale either the 128x128 "
-     "block grid or a per-row grid; M derives from numel(y)/N",
+     "block grid or a per-row grid; M derives from numel(y)/N; scratch optional (the hook "
+     "sizes the split's partials; without them the unsplit arms run)",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), fp8_e4m3 b with bf16 scale per 128x128 "
      "tile (or per row), bf16 y; a_sum and b_ref refused",
      RAD_DOMAIN_DEVICE, kPrioTile, cFp8Tile, 3, nullptr, 0, nullptr,
-     nullptr, nullptr, r3d_rad_gemm_nt_q_fp8, nullptr, nullptr, nullptr, nullptr, nullptr},
+     nullptr, nullptr, r3d_rad_gemm_nt_q_fp8, r3d_rad_gemm_nt_q_fp8_scratch, nullptr, nullptr,
+     nullptr, nullptr},
 
     {"gemm_nt_q_fp8a8_decode", "gemm_nt_q", "gemm",
      "fp8a8 decode-band GEMV on gfx950: M <= 4 one wave per 4 weight rows (two whole-line "

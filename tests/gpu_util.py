@@ -39,17 +39,27 @@ def y_buffer(M, N, dev):
     return Guarded(host, dev)
 
 
-def run_row(row, dtype, A, AS, B, BS, M, N, K, dev, y_shape=None, extra=None, tunables=None):
-    """Launch `row` on guarded copies of the operands; returns (rc, Y uint16 [M,N], guards_ok)."""
+def run_row(row, dtype, A, AS, B, BS, M, N, K, dev, y_shape=None, extra=None, tunables=None,
+            scratch=None):
+    """Launch `row` on guarded copies of the operands; returns (rc, Y uint16 [M,N], guards_ok).
+    scratch: None (no launch scratch), "hook" (the bytes the row's scratch hook asks for) or
+    a byte count -- a guarded buffer, poisoned, handed over as RadArgs::scratch."""
     gA, gAS, gB, gBS = (Guarded(x, dev) for x in (A, AS, B, BS))
     gY = y_buffer(M, N, dev)
     ops = R.GemmOperands(gA.t, gAS.t, gB.t, gBS.t, gY.t, dtype=dtype, N=N, K=K,
                          extra_params=extra, y_shape=y_shape, tunables=tunables)
+    held = [gA, gAS, gB, gBS, gY]
+    if scratch is not None:
+        nbytes = R.row_scratch_bytes(row, ops) if scratch == "hook" else int(scratch)
+        if nbytes > 0:
+            gS = Guarded(np.zeros(nbytes, np.uint8), dev, fill=0x5A)
+            ops.set_scratch(gS.t, nbytes)
+            held.append(gS)
     stream = torch.cuda.current_stream().cuda_stream
     rc = R.launch_row(row, ops, stream)
     torch.cuda.synchronize()
     Y = gY.t.cpu().numpy().view(np.uint16).reshape(M, N)
-    ok = all(g.guards_intact() for g in (gA, gAS, gB, gBS, gY))
+    ok = all(g.guards_intact() for g in held)
     return rc, Y, ok
 
 

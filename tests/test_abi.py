@@ -250,6 +250,69 @@ def test_decode_band_bound_and_tile_any_m():
             assert rc == R.RAD_OK and g["arm"] == arm and g.get("passes") == passes, (M, N, d)
 
 
+def _splitk(N, K, bn=128, units=256, min_steps=4):
+    """kc, cst of the tile rows' K split, from its stated rule: units aim at one per CU
+    over ceil(N / bn) tiles, at least min_steps K steps a chunk, no empty chunk."""
+    tiles, steps = -(-N // bn), K // 128
+    kc = min(units // tiles, steps // min_steps)
+    if kc < 2:
+        return 0, 0
+    cst = -(-steps // kc)
+    kc = -(-steps // cst)
+    return (kc, cst) if kc >= 2 else (0, 0)
+
+
+def test_tile_splitk_hook_and_arm():
+    """The tile rows' scratch hook sizes split K's f32 partial planes (kc * M * N * 4) up to
+    M = 128 on a narrow N and returns 0 elsewhere; with that scratch the launch describes
+    the split arm, with less (or misaligned) the unsplit arms it had before."""
+    rows = {r["name"]: r for r in R.rows()}
+    assert rows["gemm_nt_q_mxfp4"]["scratch"] and rows["gemm_nt_q_fp8a8"]["scratch"]
+    assert not rows["gemm_nt_q_mxfp4_decode"]["scratch"]
+    # the split's tile: up to M = 64 one 64-token group a wave over 256 e2m1 / 128 e4m3
+    # weight rows, else 128 x 128.  Config 2 at M = 64: mxfp4 down 21 tiles x 12 chunks of
+    # 14 steps, qkv 32 x 7 of 6, gate_up 84 x 3 of 14; fp8 down 42 x 6 of 28, gate_up's
+    # 168 tiles fill the chip unsplit; M past 128 and one-chunk K never split
+    assert _splitk(5376, 21504, 256) == (12, 14) and _splitk(8192, 5376, 256) == (7, 6)
+    assert _splitk(21504, 5376, 256) == (3, 14) and _splitk(5376, 21504) == (6, 28)
+    assert _splitk(21504, 5376) == (0, 0) and _splitk(1000, 384) == (0, 0)
+    for mk, row in ((_mx_ops, "gemm_nt_q_mxfp4"), (_f8_ops, "gemm_nt_q_fp8a8")):
+        for M, N, K in [(64, 5376, 21504), (17, 8192, 5376), (32, 8192, 5376), (17, 5376, 21504),
+                        (40, 1000, 2048), (128, 300, 1024), (17, 300, 9216), (17, 300, 2048),
+                        (1, 64, 512), (129, 5376, 21504), (64, 21504, 5376), (64, 1000, 384),
+                        (65, 5376, 21504), (100, 21504, 5376)]:
+            ops, keep = mk(M=M, N=N, K=K)
+            bn = 256 if row == "gemm_nt_q_mxfp4" and M <= 64 else 128
+            kc, cst = _splitk(N, K, bn) if M <= 128 else (0, 0)
+            # e2m1, M <= 32, K <= 8192 where the skinny passes apply: the passes stay
+            passes = 17 <= M <= 64 and -(-M // 16) * min(-(-N // 128), 256) < 300
+            if row == "gemm_nt_q_mxfp4" and M <= 32 and K <= 8192 and passes:
+                kc, cst = 0, 0
+            need = kc * M * N * 4
+            assert R.row_scratch_bytes(row, ops) == need, (row, M, N, K)
+            base = _geom(R.describe(row, ops)[1])["arm"]
+            assert base in ("skinny", "prefill")
+            if not need:
+                continue
+            sc = FakeT(_aligned((64,), np.uint8))
+            ops.set_scratch(sc, need)
+            rc, d = R.describe(row, ops)
+            g = _geom(d)
+            assert rc == R.RAD_OK and g["arm"] == "splitk", d
+            assert (g["kc"], g["cst"], g["partials"]) == (str(kc), str(cst), str(need)), d
+            assert (g["bn"], g["bm"]) == (str(bn), "64" if M <= 64 else "128"), d
+            ops.set_scratch(sc, need - 1)                      # short: the unsplit arm
+            assert _geom(R.describe(row, ops)[1])["arm"] == base
+            ops.set_scratch(FakeT(sc.arr, offset=8), need)     # misaligned: the unsplit arm
+            assert _geom(R.describe(row, ops)[1])["arm"] == base
+    # without y the hook sizes at the M parameter, without either at M = 128
+    _, (a, s, b, bs, _y) = _mx_ops(M=64, N=5376, K=21504)
+    for extra, M in ((None, 128), ([("M", 17)], 17)):
+        ops = R.GemmOperands(a, s, b, bs, None, dtype="mxfp4a8", N=5376, K=21504,
+                             extra_params=extra)
+        assert R.row_scratch_bytes("gemm_nt_q_mxfp4", ops) == (6 if M > 64 else 12) * M * 5376 * 4
+
+
 def test_decode_geometry_policy():
     """M <= 4 runs the quad GEMV, split in K until ~2048 waves (>= 16 groups per chunk),
     while its workgroup LDS (whole-K activation rows) stays <= 48 KB, else the 16-row GEMV;

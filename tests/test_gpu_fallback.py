@@ -1,6 +1,6 @@
 """A failed arm hands its launch to the next one on the same operands, as the reference's
 entries do (src/r3d_gemm_mxfp4.hip:1666-1670 skinny -> tile, :2118-2122 q8x -> legacy
-walk), instead of returning RAD_E_DEVICE at issue time.  The failures are forced from the
+walk; this build's split K -> the unsplit tile walk), instead of returning RAD_E_DEVICE at issue time.  The failures are forced from the
 host with the test lever R3D_GFX950_FAIL_ARM, which makes the named arms report a launch
 failure without launching anything; each setting runs in a child process (the lever is
 read once per process), whose calls must still succeed, log the failure, and match the
@@ -27,7 +27,7 @@ from tests import gpu_util as gu
 from tests.test_gpu_gemm import _mx_case, _f8_case
 dev = torch.device("cuda:0")
 out = []
-for row, dtype, M, N, K in %r:
+for row, dtype, M, N, K, *sc in %r:
     if dtype == "mxfp4a8":
         A, AS, B, BS = _mx_case(M, N, K, M + N)
         Yr, Yf, S = O.quant_dot_mxfp4a8(A, AS, B, BS, nthreads=8)
@@ -35,7 +35,8 @@ for row, dtype, M, N, K in %r:
         A, AS, B, BS = _f8_case(M, N, K, M + N, 1)
         Yr, Yf, S = O.quant_dot_fp8a8(A, AS, B, BS, 1, nthreads=8)
     S8 = O.group8_mag(dtype, A, AS, B, BS, 1, nthreads=8)
-    rc, Y, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, dev)
+    rc, Y, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, dev,
+                               scratch=sc[0] if sc else None)
     c = gu.compare(Y, Yr, Yf, S, K, S8)
     out.append([row, M, rc, guards, c["max_viol"], c["sentinel_left"], c["nan_mismatch"]])
 print("RESULT " + json.dumps(out))
@@ -53,6 +54,10 @@ MX_DEC, MX_TILE, F8_DEC = "gemm_nt_q_mxfp4_decode", "gemm_nt_q_mxfp4", "gemm_nt_
      "line decode GEMV launch FAILED"),
     # the skinny band's passes fail: the prefill pipeline takes M = 17..64
     ("skinny", [(MX_TILE, "mxfp4a8", 40, 1000, 2048)], "skinny line GEMV launch FAILED"),
+    # split K fails (hook-sized scratch handed over): the whole K walk recomputes Y
+    ("splitk", [(MX_TILE, "mxfp4a8", 40, 1000, 2048, "hook"),
+                ("gemm_nt_q_fp8a8", "fp8a8", 64, 520, 4096, "hook")],
+     "split-K prefill launch FAILED"),
 ])
 def test_failed_arm_falls_back(gpu, arms, cases, logged):
     env = dict(os.environ, R3D_GFX950_FAIL_ARM=arms, R3D_DEBUG_GEMM="1")

@@ -57,9 +57,11 @@ def _f8_case(M, N, K, seed, rblk):
 KBENCH_TOL = {"mxfp4a8": 3e-2, "fp8a8": 5e-3}
 
 
-def _check(row, dtype, A, AS, B, BS, M, N, K, gpu, rblk=1, row_rel_max=None, tunables=None):
+def _check(row, dtype, A, AS, B, BS, M, N, K, gpu, rblk=1, row_rel_max=None, tunables=None,
+           scratch=None):
     gu = _gu()
-    rc, Y, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, gpu, tunables=tunables)
+    rc, Y, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, gpu, tunables=tunables,
+                               scratch=scratch)
     assert rc == R.RAD_OK, "row %s refused rc=%d" % (row, rc)
     assert guards, "red zone written"
     if dtype == "mxfp4a8":
@@ -185,6 +187,86 @@ def test_mxfp4_tile(gpu, M, N, K):
 def test_fp8_tile(gpu, M, N, K, rblk):
     A, AS, B, BS = _f8_case(M, N, K, 11 * M + N, rblk)
     _check(F8_TILE, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk)
+
+
+def _split_of(row, dtype, M, N, K):
+    """(kc, cst) the row's describe reports with hook-sized scratch, or None unsplit."""
+    gu = _gu()
+    import torch
+    A = np.zeros((M, K), np.uint8)
+    AS = np.ones((M, K // 128), np.float32)
+    B = np.zeros((N, K // 2 if dtype == "mxfp4a8" else K), np.uint8)
+    BS = (np.zeros((N, K // 32), np.uint8) if dtype == "mxfp4a8"
+          else np.zeros((N, K // 128), np.uint16))
+    ts = [torch.from_numpy(x) for x in (A, AS, B, BS)]
+    y = torch.zeros((M, N), dtype=torch.int16)
+    ops = R.GemmOperands(*ts, y, dtype=dtype, N=N, K=K)
+    need = R.row_scratch_bytes(row, ops)
+    if not need:
+        return None
+    ops.set_scratch(torch.zeros(64, dtype=torch.uint8), need)   # describe reads no memory
+    g = dict(kv.split("=") for kv in R.describe(row, ops)[1].split() if "=" in kv)
+    assert g["arm"] == "splitk", g
+    del gu
+    return int(g["kc"]), int(g["cst"])
+
+
+# split K on the tile rows (M <= 128, narrow N): chunks of equal and unequal length (a
+# one-step last chunk at K = 2688), 18 chunks (K = 9216), ragged N (250: partial
+# four-column groups, scalar stores), one token, the 128-token bound (the 128 x 128 tile
+# past M = 64), config 2's qkv width; token groups wholly past M skip their MFMAs at M = 1,
+# 17, 33, 40
+SPLIT_SHAPES = [(17, 300, 9216), (40, 1000, 2048), (33, 700, 2688), (100, 250, 1536),
+                (1, 64, 1024), (128, 520, 4096), (64, 8192, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
+def test_mxfp4_tile_splitk(gpu, M, N, K):
+    """The split arm against the oracle at the tile rows' bar, scratch guarded; two calls
+    give the same bits (the chunks are summed in one order); without scratch the same
+    operands take the unsplit arms and meet the same bar."""
+    assert _split_of(MX_TILE, "mxfp4a8", M, N, K) is not None
+    A, AS, B, BS = _mx_case(M, N, K, 5 * M + N + K)
+    _, Y1 = _check(MX_TILE, "mxfp4a8", A, AS, B, BS, M, N, K, gpu, scratch="hook")
+    _, Y2 = _check(MX_TILE, "mxfp4a8", A, AS, B, BS, M, N, K, gpu, scratch="hook")
+    assert np.array_equal(Y1, Y2)
+    _check(MX_TILE, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
+@pytest.mark.parametrize("rblk", [1, 128])
+def test_fp8_tile_splitk(gpu, M, N, K, rblk):
+    if rblk == 128 and N <= 128:
+        pytest.skip("one block row is a per-row grid")
+    assert _split_of(F8_TILE, "fp8a8", M, N, K) is not None
+    A, AS, B, BS = _f8_case(M, N, K, 3 * M + N + K + rblk, rblk)
+    _, Y1 = _check(F8_TILE, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk, scratch="hook")
+    _, Y2 = _check(F8_TILE, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk, scratch="hook")
+    assert np.array_equal(Y1, Y2)
+
+
+def test_splitk_short_scratch_runs_unsplit(gpu):
+    """A byte short of the hook's size: the launch takes the unsplit arm, leaves the
+    scratch untouched (its poison and red zones intact) and still meets the bar."""
+    gu = _gu()
+    M, N, K = 40, 1000, 2048
+    A, AS, B, BS = _mx_case(M, N, K, 99)
+    kc, _ = _split_of(MX_TILE, "mxfp4a8", M, N, K)
+    need = kc * M * N * 4
+    gA, gAS, gB, gBS = (gu.Guarded(x, gpu) for x in (A, AS, B, BS))
+    gY = gu.y_buffer(M, N, gpu)
+    gS = gu.Guarded(np.zeros(need - 1, np.uint8), gpu, fill=0x5A)
+    import torch
+    ops = R.GemmOperands(gA.t, gAS.t, gB.t, gBS.t, gY.t, dtype="mxfp4a8", N=N, K=K)
+    ops.set_scratch(gS.t, need - 1)
+    assert R.launch_row(MX_TILE, ops, torch.cuda.current_stream().cuda_stream) == R.RAD_OK
+    torch.cuda.synchronize()
+    assert all(g.guards_intact() for g in (gA, gAS, gB, gBS, gY, gS))
+    assert (gS.t.cpu().numpy() == 0x5A).all()
+    Y = gY.t.cpu().numpy().view(np.uint16).reshape(M, N)
+    Yr, Yf, S = O.quant_dot_mxfp4a8(A, AS, B, BS, nthreads=16)
+    c = gu.compare(Y, Yr, Yf, S, K, O.group8_mag("mxfp4a8", A, AS, B, BS, nthreads=16))
+    assert c["sentinel_left"] == 0 and c["max_viol"] <= 1.0, c
 
 
 @pytest.mark.parametrize("row", [MX_DEC, MX_TILE])
