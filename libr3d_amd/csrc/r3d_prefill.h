@@ -240,12 +240,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(
      * results into accumulators that are never stored.  (Wider tiles issue every MFMA: the
      * branch costs them registers.) */
     const int mlive = WMW == 1 && 16 * (int64_t)wm >= M - m0 ? 0 : WMW;
-    /* the result pair dq[2] alternates by group, or by step (the weight set) at one group a
-     * step */
+    /* the result pair dq[2] alternates group by group along the whole K walk: by the group
+     * index at an even group count a step, also by the step (the weight set) at an odd one */
     auto group = [&](int mi, int set) __attribute__((always_inline)) {
         const int slot = mi & 3;
         const bool live = mi < mlive;
-        const int dc = WMW == 1 ? set : (mi & 1), dp = dc ^ 1;
+        const int dc = ((WMW & 1) ? set : 0) ^ (mi & 1), dp = dc ^ 1;
         if (MODE == PF_MX8) {
             if (live) {
 #pragma unroll
@@ -446,8 +446,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         for (int ni = 0; ni < WNF; ++ni)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float d = WMW == 1 ? (ls ? dq[1][ni][i] : dq[0][ni][i])
-                                         : dq[(WMW - 1) & 1][ni][i];
+                const float d = (WMW & 1) ? ((ls ^ ((WMW - 1) & 1)) ? dq[1][ni][i] : dq[0][ni][i])
+                                          : dq[(WMW - 1) & 1][ni][i];
                 if (F8) {
                     const uint32_t sbb = (uint32_t)(ls ? sbF[1][ni][i] : sbF[0][ni][i]);
                     const float sb = __uint_as_float(sbb << 16);
