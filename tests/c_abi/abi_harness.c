@@ -81,6 +81,10 @@ static const void* const kExports[] = {
     (const void*)r3d_rad_rmsnorm_quant_fp8, (const void*)r3d_rad_gemm_nt_q_gated_fp8,
     (const void*)r3d_rad_gemm_nt_q_gated_fp8_scratch, (const void*)r3d_gfx950_describe,
     (const void*)r3d_gfx950_mxfp4a16_stage, (const void*)r3d_gfx950_build_id,
+    (const void*)r3d_rad_gemm_nt_q_scratch, (const void*)r3d_rad_gemm_nt_q_fp8_scratch,
+    (const void*)r3d_rad_logits_gemm_e4m3, (const void*)r3d_gfx950_logits_head_bytes,
+    (const void*)r3d_gfx950_logits_head_header, (const void*)r3d_gfx950_logits_head_join,
+    (const void*)r3d_gfx950_logits_head_split, (const void*)r3d_gfx950_logits_head_forget,
 };
 
 static int table(void) {
@@ -124,6 +128,12 @@ static void* to_dev(const void* h, size_t n) {
 static RadLaunchFn row_launch(const char* name) {
     for (int i = 0; i < rad_kernel_count(); ++i)
         if (strcmp(rad_kernel_at(i)->name, name) == 0) return rad_kernel_at(i)->launch;
+    return NULL;
+}
+
+static RadScratchFn row_scratch(const char* name) {
+    for (int i = 0; i < rad_kernel_count(); ++i)
+        if (strcmp(rad_kernel_at(i)->name, name) == 0) return rad_kernel_at(i)->scratch;
     return NULL;
 }
 
@@ -244,6 +254,60 @@ static int run_prefill_fp8(void) {
     return ok;
 }
 
+/* The mxfp4a8 tile row as an engine drives it: launch scratch sized by the row's own hook
+ * (split K at this narrow N), the table's launch and the export on the same scratch. */
+static int run_splitk_mxfp4(void) {
+    const int64_t M = 40, N = 1000, K = 2048, asc = K / 128, bsc = K / 32;
+    uint8_t* A = malloc(M * K); float* AS = malloc(M * asc * 4);
+    uint8_t* B = malloc(N * K / 2); uint8_t* BS = malloc(N * bsc);
+    for (int64_t i = 0; i < M * K; ++i) A[i] = rnd_e4m3();
+    for (int64_t i = 0; i < M * asc; ++i) AS[i] = 0.001f + 0.01f * (float)(rnd() % 1000) / 1000.f;
+    for (int64_t i = 0; i < N * K / 2; ++i) B[i] = (uint8_t)rnd();
+    for (int64_t i = 0; i < N * bsc; ++i) BS[i] = (uint8_t)(115 + rnd() % 25);
+    void *dA = to_dev(A, M * K), *dAS = to_dev(AS, M * asc * 4), *dB = to_dev(B, N * K / 2),
+         *dBS = to_dev(BS, N * bsc), *dY1 = NULL, *dY2 = NULL, *dS = NULL;
+    CK(hipMalloc(&dY1, M * N * 2)); CK(hipMalloc(&dY2, M * N * 2));
+    CK(hipMemset(dY1, 0xEE, M * N * 2)); CK(hipMemset(dY2, 0xEE, M * N * 2));
+    RadTensor t[7];
+    tensor(&t[0], dA, RAD_F8E4M3, M, K);
+    tensor(&t[1], dAS, RAD_F32, M, asc);
+    tensor(&t[2], dB, RAD_FP4E2M1, N, K);
+    tensor(&t[3], dBS, RAD_E8M0, N, bsc);
+    tensor(&t[4], dY1, RAD_BF16, M, N);
+    memset(&t[5], 0, sizeof t[5]); memset(&t[6], 0, sizeof t[6]);
+    const RadParam p[] = { RAD_STR("dtype", "mxfp4a8"), RAD_INT("N", N), RAD_INT("K", K),
+                           RAD_INT("group", 32) };
+    RadArgs args = { t, 7, p, (int)(sizeof p / sizeof p[0]), NULL, 0, NULL, 0, 0 };
+    RadScratchFn hook = row_scratch("gemm_nt_q_mxfp4");
+    const int64_t need = hook ? hook(&args) : 0;
+    if (need != r3d_rad_gemm_nt_q_scratch(&args) || need <= 0) {
+        printf("split-K hook: %lld bytes\n", (long long)need);
+        return 0;
+    }
+    CK(hipMalloc(&dS, (size_t)need));
+    args.scratch = dS;
+    args.scratch_bytes = need;
+    char desc[512];
+    r3d_gfx950_describe("gemm_nt_q_mxfp4", &args, desc, sizeof desc);
+    printf("split-K plan: %s (hook %lld bytes)\n", desc, (long long)need);
+    RadLaunchFn f = row_launch("gemm_nt_q_mxfp4");
+    const int rc1 = f ? f(&args, NULL) : -1;
+    t[4].data = dY2;
+    const int rc2 = r3d_rad_gemm_nt_q(&args, NULL);
+    CK(hipDeviceSynchronize());
+    uint16_t *Y1 = malloc(M * N * 2), *Y2 = malloc(M * N * 2), *Yr = malloc(M * N * 2);
+    float *Yf = malloc(M * N * 4), *S = malloc(M * N * 4), *S8 = malloc(M * N * 4);
+    CK(hipMemcpy(Y1, dY1, M * N * 2, hipMemcpyDeviceToHost));
+    CK(hipMemcpy(Y2, dY2, M * N * 2, hipMemcpyDeviceToHost));
+    r3d_ref_quant_dot_mxfp4a8(A, K, AS, asc, B, BS, bsc, M, N, K, Yr, N, Yf, S, 1);
+    r3d_ref_group8_mag(0, A, K, AS, asc, B, K / 2, BS, bsc, 1, M, N, K, S8, 1);
+    const int ok = rc1 == RAD_OK && rc2 == RAD_OK && strstr(desc, "arm=splitk") != NULL &&
+                   check("mxfp4a8 split-K tile", M, N, K, Y1, Y2, Yr, Yf, S, S8);
+    hipFree(dA); hipFree(dAS); hipFree(dB); hipFree(dBS); hipFree(dY1); hipFree(dY2); hipFree(dS);
+    free(A); free(AS); free(B); free(BS); free(Y1); free(Y2); free(Yr); free(Yf); free(S); free(S8);
+    return ok;
+}
+
 int main(int argc, char** argv) {
     const char* mode = argc > 1 ? argv[1] : "layout";
     if (strcmp(mode, "layout") == 0) return layout();
@@ -256,8 +320,9 @@ int main(int argc, char** argv) {
         }
         const int a = run_decode_mxfp4();
         const int b = run_prefill_fp8();
-        printf("%s\n", a && b ? "PASS" : "FAIL");
-        return a && b ? 0 : 1;
+        const int c = run_splitk_mxfp4();
+        printf("%s\n", a && b && c ? "PASS" : "FAIL");
+        return a && b && c ? 0 : 1;
     }
     fprintf(stderr, "usage: abi_harness layout|table|run\n");
     return 2;
