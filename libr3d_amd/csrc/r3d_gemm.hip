@@ -20,6 +20,7 @@
 #include "r3d_gemm_kernels.h"
 #include "r3d_gemv_lines.h"
 #include "r3d_gemv_quad.h"
+#include "r3d_gemv_wide.h"
 #include "r3d_plan.h"
 #include "r3d_prefill.h"
 #include "rad_plugin.h"
@@ -215,6 +216,37 @@ static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) 
     return RAD_OK;
 }
 
+/* The skinny-band GEMV of a K split (gemv_wide_kernel): geometry w, kc chunks of w.cg
+ * groups, f32 partial planes at part. */
+static hipError_t wide_launch(const GemmPlan& P, const WideGeom& w, int kc, float* part,
+                              hipStream_t stream) {
+    /* 32-bit lane offsets: a wave's 32 weight rows and the staged activation rows */
+    const int64_t lim = (int64_t)1 << 31;
+    if (32 * P.b_pitch >= lim || w.tw != 2 || P.M > 64) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(w.ntiles * kc)), block(512);
+#define R3D_WIDE(ENC_, D_, NTG_)                                                           \
+    hipLaunchKernelGGL((gemv_wide_kernel<ENC_, 2, D_, NTG_>), grid, block, (size_t)w.lds,    \
+                       stream, P.A, P.AS, P.B, P.BS, part, (int)P.M, (int)P.N, (int)P.K, kc, \
+                       w.cg, (int)w.ntiles, P.rblk, w.sclds, P.a_pitch, P.as_pitch,         \
+                       P.b_pitch, P.bs_pitch)
+#define R3D_WIDE_N(ENC_, D_)                                                                \
+    switch (w.ntg) {                                                                        \
+        case 1: R3D_WIDE(ENC_, D_, 1); break;                                               \
+        case 2: R3D_WIDE(ENC_, D_, 2); break;                                               \
+        case 3: R3D_WIDE(ENC_, D_, 3); break;                                               \
+        default: R3D_WIDE(ENC_, D_, 4); break;                                              \
+    }
+    if (w.ntg < 1 || w.ntg > 4 || (w.d != 1 && w.d != 2)) return hipErrorInvalidValue;
+    if (P.enc == ENC_MXFP4A8) {
+        if (w.d == 2) { R3D_WIDE_N(ENC_MXFP4A8, 2) } else { R3D_WIDE_N(ENC_MXFP4A8, 1) }
+    } else {
+        if (w.d == 2) { R3D_WIDE_N(ENC_FP8A8, 2) } else { R3D_WIDE_N(ENC_FP8A8, 1) }
+    }
+#undef R3D_WIDE_N
+#undef R3D_WIDE
+    return hipGetLastError();
+}
+
 /* The prefill GEMM: mode PF_A8 reads A/AS as given (e4m3 + f32 per 128) against e2m1
  * weights, PF_F8 the same activations against e4m3 weights with bf16 row scales, PF_MX8 the
  * mxfp8 planes the quantiser left in P.scratch.  stage (mxfp4a16 only): 0 both launches, 1
@@ -229,11 +261,14 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
     prefill_geom(P.M, P.N, P.K, mode, cu_count(), &g);
     if (g.tiles > 0x7FFFFFFF || g.grid_m > 0x7FFFFFFF) return RAD_E_SHAPE;
     int cst = 0;
-    PrefillGeom gs{};                                    /* the split's tile */
-    const int kc = part && ((uintptr_t)part & 15) == 0
-                       ? tile_splitk(P.enc, P.M, P.N, P.K, cu_count(), &cst, &gs) : 0;
-    const bool split = kc > 0 && part_bytes >= (int64_t)kc * P.M * P.N * 4 &&
-                       gs.grid_m == 1 && gs.tiles * kc <= 0x7FFFFFFF;
+    PrefillGeom gs{};                                    /* the split's tile (kind 2) */
+    WideGeom gw{};                                       /* or its GEMV (kind 1) */
+    int kc = 0;
+    const int kind = part && ((uintptr_t)part & 15) == 0
+                         ? splitk_plan(P.enc, P.M, P.N, P.K, cu_count(), &kc, &cst, &gs, &gw)
+                         : 0;
+    const bool split = kind != 0 && part_bytes >= (int64_t)kc * P.M * P.N * 4 &&
+                       (kind == 1 || (gs.grid_m == 1 && gs.tiles * kc <= 0x7FFFFFFF));
     /* the skinny band on a narrow N: 16-row passes of the decode GEMVs (each output row is
      * the same arithmetic either way) */
     if (const int passes = split ? 0 : skinny_passes(P.enc, P.M, P.N, cu_count())) {
@@ -335,7 +370,9 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
         hipError_t e = hipSuccess;
         if (forced_fail("splitk")) {
             launch_failed("split-K prefill", hipSuccess);
-        } else if ((e = tiles_launch(gs, kc, cst, reinterpret_cast<float*>(part))) != hipSuccess) {
+        } else if ((e = kind == 1 ? wide_launch(P, gw, kc, reinterpret_cast<float*>(part), stream)
+                                  : tiles_launch(gs, kc, cst, reinterpret_cast<float*>(part)))
+                   != hipSuccess) {
             launch_failed("split-K prefill", e);
         } else {
             const int64_t lanes = P.M * ((P.N + 3) / 4);
@@ -344,8 +381,11 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
                                (int)P.M, (int)P.N, P.Y, P.y_pitch);
             e = hipGetLastError();
             if (e == hipSuccess) {
-                debug_once(mode == PF_F8 ? "fp8a8 split-K prefill" : "mxfp4a8 split-K prefill",
-                           200 + 8 * mode);
+                debug_once(kind == 1 ? (mode == PF_F8 ? "fp8a8 split-K skinny GEMV"
+                                                      : "mxfp4a8 split-K skinny GEMV")
+                                     : (mode == PF_F8 ? "fp8a8 split-K prefill"
+                                                      : "mxfp4a8 split-K prefill"),
+                           200 + 8 * mode + kind);
                 return RAD_OK;
             }
             launch_failed("split-K reduce", e);

@@ -510,9 +510,6 @@ int tile_splitk(int enc, int64_t M, int64_t N, int64_t K, int ncu, int* cst, Pre
     }();
     if (ncu <= 0) ncu = 256;
     const int64_t target = lever >= 0 ? lever : ncu;
-    /* e2m1 weights, short K, two 16-row passes: the passes measured faster (config 2 qkv,
-     * M = 17 / 32: 14.3 / 15.8 us against 16.4 / 17.5 split) */
-    if (enc == ENC_MXFP4A8 && M <= 32 && K <= 8192 && skinny_passes(enc, M, N, ncu)) return 0;
     /* the split's tile: 64 tokens up to M = 64 (256 e2m1 / 128 e4m3 weight rows), else
      * 128 x 128 */
     const int wmf = M <= 64 ? 1 : 2;
@@ -542,9 +539,75 @@ int tile_splitk(int enc, int64_t M, int64_t N, int64_t K, int ncu, int* cst, Pre
     return (int)kc;
 }
 
+/* The skinny-band GEMV's geometry for a K split of at most kc0 chunks: the chunk (cg
+ * groups, a whole number of 128-byte lines) as long as the LDS budget allows. */
+static bool wide_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t kc0, WideGeom* w) {
+    const int G = enc == ENC_MXFP4A8 ? 2 : 1;
+    const int64_t steps = K / 128;
+    w->tw = 2;
+    w->ntg = (int)((M + 15) / 16);
+    w->ntiles = (N + 255) / 256;
+    int64_t cg = (steps + kc0 - 1) / kc0;
+    cg = (cg + G - 1) / G * G;
+    auto lds_of = [&](int64_t c, int64_t* sc) {
+        const int64_t scl = (16 * w->tw * c * 4 + 255) / 256 * 256;
+        if (sc) *sc = scl;
+        return c * w->ntg * 2048 + c * 256 + 8 * scl;
+    };
+    while (cg > G && lds_of(cg, nullptr) > kWideMaxLds) cg -= G;
+    int64_t scl = 0;
+    const int64_t lds = lds_of(cg, &scl);
+    if (lds > kWideMaxLds) return false;
+    w->cg = (int)cg;
+    w->sclds = (int)scl;
+    w->lds = (int)lds;
+    /* two lines in each wave's ring (measured best against one and four) */
+    w->d = cg / G >= 2 ? 2 : 1;
+    return true;
+}
+
+int splitk_plan(int enc, int64_t M, int64_t N, int64_t K, int ncu, int* kc, int* cst,
+                PrefillGeom* g, WideGeom* w) {
+    if ((enc != ENC_MXFP4A8 && enc != ENC_FP8A8) || M < 1 || M > 128 || N < 1 || K < 128)
+        return 0;
+    static const bool tile_only = [] {
+        const char* e = getenv("R3D_GFX950_SPLITK_KERNEL");
+        return e && strcmp(e, "tile") == 0;
+    }();
+    if (M > 64 || tile_only) {
+        int c = 0;
+        const int k = tile_splitk(enc, M, N, K, ncu, &c, g);
+        if (!k) return 0;
+        if (kc) *kc = k;
+        if (cst) *cst = c;
+        return 2;
+    }
+    static const long long lever = [] {
+        const char* e = getenv("R3D_GFX950_SPLITK_UNITS");
+        return e ? atoll(e) : -1LL;
+    }();
+    if (ncu <= 0) ncu = 256;
+    const int64_t target = lever >= 0 ? lever : ncu;
+    /* units aim at the target over the GEMV's 256-row tiles, at least kSplitMinSteps groups a
+     * chunk; the LDS budget may shorten the chunk (more chunks) */
+    const int64_t steps = K / 128;
+    const int64_t ntiles = (N + 255) / 256;
+    int64_t kc0 = target / ntiles;
+    if (kc0 > steps / kSplitMinSteps) kc0 = steps / kSplitMinSteps;
+    if (kc0 < 2) return 0;
+    WideGeom tmp{};
+    WideGeom* wg = w ? w : &tmp;
+    if (!wide_geom(enc, M, N, K, kc0, wg)) return 0;
+    const int64_t kcw = (steps + wg->cg - 1) / wg->cg;
+    if (kcw < 2 || wg->ntiles * kcw > 0x7FFFFFFF) return 0;
+    if (kc) *kc = (int)kcw;
+    if (cst) *cst = wg->cg;
+    return 1;
+}
+
 int64_t tile_splitk_bytes(int enc, int64_t M, int64_t N, int64_t K, int ncu) {
-    const int kc = tile_splitk(enc, M, N, K, ncu, nullptr, nullptr);
-    return kc ? (int64_t)kc * M * N * 4 : 0;
+    int kc = 0;
+    return splitk_plan(enc, M, N, K, ncu, &kc, nullptr, nullptr, nullptr) ? (int64_t)kc * M * N * 4 : 0;
 }
 
 int64_t tile_scratch_bytes(const RadArgs* a, int enc, int ncu) {
@@ -1121,17 +1184,28 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
                  ename, (long long)P.M, (long long)P.N, (long long)P.K,
                  g.mt, g.chunks, g.waves, (long long)g.tiles, (long long)g.blocks, g.steps,
                  P.rblk);
-    } else if (int cst = 0, kc = a->scratch && ((uintptr_t)a->scratch & 15) == 0
-                                  ? tile_splitk(P.enc, P.M, P.N, P.K, 256, &cst, nullptr) : 0;
-               kc && a->scratch_bytes >= (int64_t)kc * P.M * P.N * 4) {
+    } else if (int kc = 0, cst = 0, kind = a->scratch && ((uintptr_t)a->scratch & 15) == 0
+                                  ? splitk_plan(P.enc, P.M, P.N, P.K, 256, &kc, &cst, nullptr,
+                                                nullptr) : 0;
+               kind && a->scratch_bytes >= (int64_t)kc * P.M * P.N * 4) {
         PrefillGeom g{};
-        tile_splitk(P.enc, P.M, P.N, P.K, 256, nullptr, &g);
-        snprintf(buf, (size_t)len,
-                 "arm=splitk enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d tiles=%lld kc=%d cst=%d "
-                 "steps=%d lds=%d partials=%lld (f32 partial planes in scratch, summed in "
-                 "chunk order)",
-                 ename, (long long)P.M, (long long)P.N, (long long)P.K, g.bn, g.bm,
-                 (long long)g.tiles, kc, cst, g.steps, g.lds, (long long)kc * P.M * P.N * 4);
+        WideGeom w{};
+        splitk_plan(P.enc, P.M, P.N, P.K, 256, nullptr, nullptr, &g, &w);
+        if (kind == 1)
+            snprintf(buf, (size_t)len,
+                     "arm=splitk kernel=wide enc=%s M=%lld N=%lld K=%lld bn=%d tiles=%lld kc=%d "
+                     "cst=%d steps=%lld ntg=%d tw=%d depth=%d lds=%d partials=%lld (f32 partial "
+                     "planes in scratch, summed in chunk order)",
+                     ename, (long long)P.M, (long long)P.N, (long long)P.K, 128 * w.tw,
+                     (long long)w.ntiles, kc, cst, (long long)(P.K / 128), w.ntg, w.tw, w.d,
+                     w.lds, (long long)kc * P.M * P.N * 4);
+        else
+            snprintf(buf, (size_t)len,
+                     "arm=splitk kernel=tile enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d tiles=%lld "
+                     "kc=%d cst=%d steps=%d lds=%d partials=%lld (f32 partial planes in scratch, "
+                     "summed in chunk order)",
+                     ename, (long long)P.M, (long long)P.N, (long long)P.K, g.bn, g.bm,
+                     (long long)g.tiles, kc, cst, g.steps, g.lds, (long long)kc * P.M * P.N * 4);
     } else if (const int passes = skinny_passes(P.enc, P.M, P.N, 256)) {
         snprintf(buf, (size_t)len,
                  "arm=skinny enc=%s M=%lld N=%lld K=%lld passes=%d (16-row decode GEMV passes)",

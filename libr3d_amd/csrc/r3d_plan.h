@@ -152,6 +152,16 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
  * R3D_GFX950_SKINNY=0 / 1 turns the passes off / on for every skinny shape. */
 int skinny_passes(int enc, int64_t M, int64_t N, int ncu);
 
+/* The skinny-band GEMV (gemv_wide_kernel, r3d_gemv_wide.h): 8 waves of tw 16-row weight
+ * tiles (256 rows a workgroup at tw = 2) x one K chunk of cg groups; depth d lines in each
+ * wave's register ring; ntg 16-row groups of activations staged in LDS with the chunk. */
+struct WideGeom {
+    int tw, d;
+    int cg, ntg, sclds, lds;
+    int64_t ntiles;
+};
+constexpr int kWideMaxLds = 152 * 1024;
+
 /* Split K on the tile rows (mxfp4a8, fp8a8) up to M = 128, where a narrow N leaves most
  * CUs idle under the prefill pipeline's one tile per 128 weight rows: the K steps are cut
  * into kc chunks of *cst steps (every chunk non-empty), the tile x chunk units write f32
@@ -159,10 +169,14 @@ int skinny_passes(int enc, int64_t M, int64_t N, int ncu);
  * bf16 Y.  The split's tile (*g): up to M = 64 one 64-token group a wave (e2m1 weights: 256
  * rows, e4m3: 128), else the 128 x 128 tile.  Returns kc (0: no split).  Units aim at one
  * per CU (R3D_GFX950_SPLITK_UNITS overrides the target, 0 turns the split off) with at
- * least kSplitMinSteps steps a chunk.  e2m1 weights at M <= 32 with K <= 8192 keep the
- * skinny passes where those apply (measured faster there). */
+ * least kSplitMinSteps steps a chunk. */
 constexpr int kSplitMinSteps = 4;
 int tile_splitk(int enc, int64_t M, int64_t N, int64_t K, int ncu, int* cst, PrefillGeom* g);
+/* The split's kernel: up to M = 64 the skinny-band GEMV (kind 1, *w), else the 128 x 128
+ * prefill tile (kind 2, *g); 0 when no split applies.  *kc and *cst as tile_splitk's.
+ * R3D_GFX950_SPLITK_KERNEL=tile keeps the prefill tile (64 tokens a tile) up to M = 64. */
+int splitk_plan(int enc, int64_t M, int64_t N, int64_t K, int ncu, int* kc, int* cst,
+                PrefillGeom* g, WideGeom* w);
 /* Launch scratch the split needs: kc f32 planes of M x N (0 without a split). */
 int64_t tile_splitk_bytes(int enc, int64_t M, int64_t N, int64_t K, int ncu);
 /* The tile rows' scratch hook: tile_splitk_bytes at the args' N and K and M (numel(y) / N,

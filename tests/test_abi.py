@@ -262,6 +262,26 @@ def _splitk(N, K, bn=128, units=256, min_steps=4):
     return (kc, cst) if kc >= 2 else (0, 0)
 
 
+def _wide_split(N, K, M, mx, units=256, min_steps=4):
+    """kc, cst of the skinny-band GEMV's K split (M <= 64), from its stated rule: units aim
+    at one per CU over ceil(N / 256) tiles with at least min_steps groups a chunk; a chunk is
+    a whole number of 128-byte lines (2 groups at e2m1) and fits the LDS budget with its
+    ceil(M / 16) x 16 staged activation rows."""
+    G = 2 if mx else 1
+    steps, ntiles = K // 128, -(-N // 256)
+    kc0 = min(units // ntiles, steps // min_steps)
+    if kc0 < 2:
+        return 0, 0
+    cg = -(-steps // kc0)
+    cg = -(-cg // G) * G
+    ntg = -(-M // 16)
+    lds = lambda c: c * ntg * 2048 + c * 256 + 8 * (-(-(32 * c * 4) // 256) * 256)
+    while cg > G and lds(cg) > 152 * 1024:
+        cg -= G
+    kc = -(-steps // cg)
+    return (kc, cg) if kc >= 2 else (0, 0)
+
+
 def test_tile_splitk_hook_and_arm():
     """The tile rows' scratch hook sizes split K's f32 partial planes (kc * M * N * 4) up to
     M = 128 on a narrow N and returns 0 elsewhere; with that scratch the launch describes
@@ -269,12 +289,14 @@ def test_tile_splitk_hook_and_arm():
     rows = {r["name"]: r for r in R.rows()}
     assert rows["gemm_nt_q_mxfp4"]["scratch"] and rows["gemm_nt_q_fp8a8"]["scratch"]
     assert not rows["gemm_nt_q_mxfp4_decode"]["scratch"]
-    # the split's tile: up to M = 64 one 64-token group a wave over 256 e2m1 / 128 e4m3
-    # weight rows, else 128 x 128.  Config 2 at M = 64: mxfp4 down 21 tiles x 12 chunks of
-    # 14 steps, qkv 32 x 7 of 6, gate_up 84 x 3 of 14; fp8 down 42 x 6 of 28, gate_up's
-    # 168 tiles fill the chip unsplit; M past 128 and one-chunk K never split
-    assert _splitk(5376, 21504, 256) == (12, 14) and _splitk(8192, 5376, 256) == (7, 6)
-    assert _splitk(21504, 5376, 256) == (3, 14) and _splitk(5376, 21504) == (6, 28)
+    # up to M = 64 the skinny-band GEMV over 256-row tiles, else the 128 x 128 tile.  Config 2
+    # at M = 64: down 21 tiles x 12 chunks of 14 groups, qkv 32 x 7 of 6, gate_up 84 x 3 of
+    # 14 (both encodings); past M = 64 down splits 42 x 6 of 28 and gate_up's 168 tiles fill
+    # the chip unsplit; M past 128 and one-chunk K never split
+    assert _wide_split(5376, 21504, 64, True) == (12, 14) == _wide_split(5376, 21504, 64, False)
+    assert _wide_split(8192, 5376, 64, True) == (7, 6)
+    assert _wide_split(21504, 5376, 64, False) == (3, 14)
+    assert _splitk(5376, 21504) == (6, 28)
     assert _splitk(21504, 5376) == (0, 0) and _splitk(1000, 384) == (0, 0)
     for mk, row in ((_mx_ops, "gemm_nt_q_mxfp4"), (_f8_ops, "gemm_nt_q_fp8a8")):
         for M, N, K in [(64, 5376, 21504), (17, 8192, 5376), (32, 8192, 5376), (17, 5376, 21504),
@@ -282,12 +304,11 @@ def test_tile_splitk_hook_and_arm():
                         (1, 64, 512), (129, 5376, 21504), (64, 21504, 5376), (64, 1000, 384),
                         (65, 5376, 21504), (100, 21504, 5376)]:
             ops, keep = mk(M=M, N=N, K=K)
-            bn = 256 if row == "gemm_nt_q_mxfp4" and M <= 64 else 128
-            kc, cst = _splitk(N, K, bn) if M <= 128 else (0, 0)
-            # e2m1, M <= 32, K <= 8192 where the skinny passes apply: the passes stay
-            passes = 17 <= M <= 64 and -(-M // 16) * min(-(-N // 128), 256) < 300
-            if row == "gemm_nt_q_mxfp4" and M <= 32 and K <= 8192 and passes:
-                kc, cst = 0, 0
+            mx = row == "gemm_nt_q_mxfp4"
+            if M <= 64:
+                kc, cst = _wide_split(N, K, M, mx)
+            else:
+                kc, cst = _splitk(N, K, 128) if M <= 128 else (0, 0)
             need = kc * M * N * 4
             assert R.row_scratch_bytes(row, ops) == need, (row, M, N, K)
             base = _geom(R.describe(row, ops)[1])["arm"]
@@ -300,7 +321,10 @@ def test_tile_splitk_hook_and_arm():
             g = _geom(d)
             assert rc == R.RAD_OK and g["arm"] == "splitk", d
             assert (g["kc"], g["cst"], g["partials"]) == (str(kc), str(cst), str(need)), d
-            assert (g["bn"], g["bm"]) == (str(bn), "64" if M <= 64 else "128"), d
+            if M <= 64:
+                assert (g["kernel"], g["bn"], g["ntg"]) == ("wide", "256", str(-(-M // 16))), d
+            else:
+                assert (g["kernel"], g["bn"], g["bm"]) == ("tile", "128", "128"), d
             ops.set_scratch(sc, need - 1)                      # short: the unsplit arm
             assert _geom(R.describe(row, ops)[1])["arm"] == base
             ops.set_scratch(FakeT(sc.arr, offset=8), need)     # misaligned: the unsplit arm

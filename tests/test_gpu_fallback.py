@@ -4,7 +4,8 @@ walk; this build's split K -> the unsplit tile walk), instead of returning RAD_E
 host with the test lever R3D_GFX950_FAIL_ARM, which makes the named arms report a launch
 failure without launching anything; each setting runs in a child process (the lever is
 read once per process), whose calls must still succeed, log the failure, and match the
-oracle within the bar of tests/test_gpu_gemm.py."""
+oracle within the bar of tests/test_gpu_gemm.py.  The same child runs the tile rows' K split
+with each of its two kernels (R3D_GFX950_SPLITK_KERNEL) against the same bar."""
 import json
 import os
 import subprocess
@@ -65,6 +66,27 @@ def test_failed_arm_falls_back(gpu, arms, cases, logged):
                        capture_output=True, text=True, timeout=300)
     assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
     assert logged in p.stderr, p.stderr[-2000:]
+    line = [l for l in p.stdout.splitlines() if l.startswith("RESULT ")][-1]
+    for row, M, rc, guards, viol, unwritten, nan_mm in json.loads(line[7:]):
+        assert rc == 0 and guards, (row, M, rc)
+        assert viol <= 1.0 and unwritten == 0 and nan_mm == 0, (row, M, viol, unwritten)
+
+
+@pytest.mark.parametrize("env,cases,kernel", [
+    # up to M = 64 the split runs the skinny-band GEMV by default; the lever keeps the
+    # prefill tile of 64 tokens (one token group a wave), which must meet the same bar
+    ({"R3D_GFX950_SPLITK_KERNEL": "tile"},
+     [(MX_TILE, "mxfp4a8", 40, 1000, 2048, "hook"), (MX_TILE, "mxfp4a8", 17, 300, 9216, "hook"),
+      ("gemm_nt_q_fp8a8", "fp8a8", 33, 700, 2688, "hook")], "split-K prefill"),
+    ({}, [(MX_TILE, "mxfp4a8", 40, 1000, 2048, "hook"),
+          ("gemm_nt_q_fp8a8", "fp8a8", 33, 700, 2688, "hook")], "split-K skinny GEMV"),
+])
+def test_split_kernel_lever(gpu, env, cases, kernel):
+    env = dict(os.environ, R3D_DEBUG_GEMM="1", **env)
+    p = subprocess.run([sys.executable, "-c", _CHILD % (ROOT, cases)], env=env,
+                       capture_output=True, text=True, timeout=300)
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    assert kernel + " launched" in p.stderr, p.stderr[-2000:]
     line = [l for l in p.stdout.splitlines() if l.startswith("RESULT ")][-1]
     for row, M, rc, guards, viol, unwritten, nan_mm in json.loads(line[7:]):
         assert rc == 0 and guards, (row, M, rc)
