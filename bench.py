@@ -245,15 +245,27 @@ def main():
             for M in (1, 4, 16):
                 _, A, AS = synth.activations(M, K, 0x5EED + 20 + M)
                 c = Case("mxfp4a8", A, AS, B, BS, M, N, K, copies_for(B.nbytes + BS.nbytes), dev)
-                wall, kern = time_case(c, "gemm_nt_q_mxfp4_decode", ksteps, 10, stream)
+                row = "gemm_nt_q_mxfp4_decode"
+                rec = {"K": K, "N": N}
+                # the row as an engine runs it: with the launch scratch its hook asks for
+                # (the K split where it applies), and the GEMV alone without scratch
+                if c.hook_scratch(row):
+                    c.ops = [R.GemmOperands(c.a, c.as_, b, bs, c.y, dtype="mxfp4a8", N=N, K=K)
+                             for b, bs in zip(c.b, c.bs)]
+                    _, k0 = time_case(c, row, ksteps, 10, stream)
+                    rec.update({"kernel_us_noscratch": round(k0 * 1e6, 3),
+                                "arm_noscratch": R.describe(row, c.ops[0])[1].split()[1]})
+                    c.hook_scratch(row)
+                wall, kern = time_case(c, row, ksteps, 10, stream)
                 nb = mx_bytes(M, N, K)
                 gbs = nb / kern / 1e9
-                extra["c2_mxfp4_%s_M%d" % (name, M)] = {
-                    "K": K, "N": N, "kernel_us": round(kern * 1e6, 3),
-                    "GBps_kernel": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                    "GBps_wall": round(nb * ksteps / wall / 1e9, 1)}
-                log("[bench] C2 %s M=%d: %.2f us, %.1f GB/s (%.1f%%)" % (
-                    name, M, kern * 1e6, gbs, 100 * gbs / HBM_PEAK_GBS))
+                rec.update({"kernel_us": round(kern * 1e6, 3), "GBps_kernel": round(gbs, 1),
+                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                            "GBps_wall": round(nb * ksteps / wall / 1e9, 1),
+                            "arm": " ".join(R.describe(row, c.ops[0])[1].split()[:2])})
+                extra["c2_mxfp4_%s_M%d" % (name, M)] = rec
+                log("[bench] C2 %s M=%d: %.2f us, %.1f GB/s (%.1f%%) %s" % (
+                    name, M, kern * 1e6, gbs, 100 * gbs / HBM_PEAK_GBS, rec["arm"]))
                 del c
         # C3 as configured: bf16 activations quantised in-library to mxfp8, mxfp4a16 row;
         # its GEMM kernel alone carries the compute roofline
@@ -414,8 +426,7 @@ def run_case(name, dev, stream, steps, warmup):
         row = "gemm_nt_q_mxfp4" if name.startswith("skinny_") else "gemm_nt_q_mxfp4_decode"
     copies = 1 if name == "c0" else copies_for(B.nbytes + BS.nbytes)
     c = Case(dtype, A, AS, B, BS, M, N, K, copies, dev)
-    if name.startswith("skinny_"):
-        res["scratch_bytes"] = c.hook_scratch(row)          # split K where it applies
+    res["scratch_bytes"] = c.hook_scratch(row)              # split K where it applies
     wall, kern = time_case(c, row, steps, warmup, stream)
     res.update({"M": M, "K": K, "N": N, "row": row, "bytes": nb, "copies": copies,
                 "kernel_us": round(kern * 1e6, 3), "GBps": round(nb / kern / 1e9, 1),
@@ -779,6 +790,14 @@ def bench_c4(dev, stream, steps=5):
     keep.append((b, bs, ops))
     launches.append((f8_dec, ops))
     total += f8_bytes(M, V, H)
+    # each launch gets the launch scratch its row's hook asks for, from one arena (the
+    # launches run in order on one stream, as an engine's would): down's K split at M = 4
+    needs = [R.row_scratch_bytes("gemm_nt_q_mxfp4_decode" if fn is mx_dec
+                                 else "gemm_nt_q_fp8a8_decode", o) for fn, o in launches]
+    arena = torch.empty(max(max(needs), 256), dtype=torch.uint8, device=dev)
+    for (fn, o), need in zip(launches, needs):
+        if need > 0:
+            o.set_scratch(arena, need)
     torch.cuda.synchronize()
 
     def step(st):
@@ -796,7 +815,8 @@ def bench_c4(dev, stream, steps=5):
     res = {"c4_decode_step_eager": {"bytes": total, "ms": round(eager * 1e3, 3),
                                     "GBps": round(total / eager / 1e9, 1),
                                     "frac_hbm": round(total / eager / 1e9 / HBM_PEAK_GBS, 4),
-                                    "launches": len(launches)}}
+                                    "launches": len(launches),
+                                    "split_launches": sum(1 for n in needs if n > 0)}}
     try:
         s2 = torch.cuda.Stream()
         with torch.cuda.stream(s2):
@@ -848,7 +868,7 @@ def bench_c4(dev, stream, steps=5):
         "lm_head": "logits_gemm_e4m3 (bf16 x, joined e4m3 + bf16 scale head, f32 logits)"}
     log("[bench] C4 decode step with the e4m3 logits head: eager %.3f ms (%.1f GB/s)" % (
         e4 * 1e3, total_e4 / e4 / 1e9))
-    del keep, launches, blob
+    del keep, launches, blob, arena
     return res
 
 

@@ -63,6 +63,19 @@ int64_t r3d_rad_gemm_nt_q_fp8_scratch(const RadArgs* a);
  * Takes a bf16 activation row at M = 1 as the mxfp4a8 decode entry does. */
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
 
+/* Scratch hooks (RadKernelInfo::scratch) of the two decode rows, r3d_rad_gemm_nt_q_mxfp4_decode
+ * and r3d_rad_gemm_nt_q_fp8_decode.  No counterpart in the reference, whose decode rows take
+ * no scratch: where the quad GEMV does not take the launch (M = 5..16, or an M <= 4 shape
+ * whose activation rows it cannot stage) on a plane of at least 2^26 weights, and no
+ * "splitk" tunable pins the GEMV's split, these rows split K across workgroups into f32
+ * partial planes in RadArgs::scratch and sum them in order on the same stream.  The hook
+ * returns the bytes of those planes (kc * M * N * 4 at the N and K parameters and M =
+ * numel(y) / N -- without y the M parameter, else 16), 0 when no split applies.  The
+ * scratch is optional: a launch without it, or with less, or at an address that is not
+ * 16-byte aligned, runs the decode GEMVs (never a refusal). */
+int64_t r3d_rad_gemm_nt_q_mxfp4_decode_scratch(const RadArgs* a);
+int64_t r3d_rad_gemm_nt_q_fp8_decode_scratch(const RadArgs* a);
+
 /* gemm_nt_q at dtype "mxfp4a16", prefill row (any M).  No counterpart in the reference:
  * the bf16-activation variant of the mxfp4 prefill (a bf16 [M, K], a_scale absent,
  * weights as mxfp4a8), for engines that feed unquantised activations.  The launch

@@ -176,12 +176,81 @@ static int launch_lines(const GemmPlan& P, const LinesGeom& g, hipStream_t strea
     return RAD_OK;
 }
 
+/* The skinny-band GEMV of a K split (gemv_wide_kernel): geometry w, kc chunks of w.cg
+ * groups, f32 partial planes at part. */
+static hipError_t wide_launch(const GemmPlan& P, const WideGeom& w, int kc, float* part,
+                              hipStream_t stream) {
+    /* 32-bit lane offsets: a wave's 32 weight rows and the staged activation rows */
+    const int64_t lim = (int64_t)1 << 31;
+    if (32 * P.b_pitch >= lim || w.tw != 2 || P.M > 64) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(w.ntiles * kc)), block(512);
+#define R3D_WIDE(ENC_, D_, NTG_)                                                           \
+    hipLaunchKernelGGL((gemv_wide_kernel<ENC_, 2, D_, NTG_>), grid, block, (size_t)w.lds,    \
+                       stream, P.A, P.AS, P.B, P.BS, part, (int)P.M, (int)P.N, (int)P.K, kc, \
+                       w.cg, (int)w.ntiles, P.rblk, w.sclds, P.a_pitch, P.as_pitch,         \
+                       P.b_pitch, P.bs_pitch)
+#define R3D_WIDE_N(ENC_, D_)                                                                \
+    switch (w.ntg) {                                                                        \
+        case 1: R3D_WIDE(ENC_, D_, 1); break;                                               \
+        case 2: R3D_WIDE(ENC_, D_, 2); break;                                               \
+        case 3: R3D_WIDE(ENC_, D_, 3); break;                                               \
+        default: R3D_WIDE(ENC_, D_, 4); break;                                              \
+    }
+    if (w.ntg < 1 || w.ntg > 4 || w.d != 1) return hipErrorInvalidValue;
+    if (P.enc == ENC_MXFP4A8) {
+        R3D_WIDE_N(ENC_MXFP4A8, 1)
+    } else {
+        R3D_WIDE_N(ENC_FP8A8, 1)
+    }
+#undef R3D_WIDE_N
+#undef R3D_WIDE
+    return hipGetLastError();
+}
+
+/* The in-order sum of kc f32 partial planes of M x N at part into bf16 Y. */
+static hipError_t splitk_reduce(const GemmPlan& P, int kc, const float* part, hipStream_t stream) {
+    const int64_t lanes = P.M * ((P.N + 3) / 4);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
+                       stream, part, kc, (int)P.M, (int)P.N, P.Y, P.y_pitch);
+    return hipGetLastError();
+}
+
+/* The skinny-band GEMV's K split, then the reduce; RAD_OK, or RAD_E_DEVICE (reported as
+ * `what`) when a launch fails, for the caller's unsplit arms to recompute every element of
+ * Y.  decode: the decode rows' split (named so in the R3D_DEBUG_GEMM line). */
+static int launch_wide_split(const GemmPlan& P, const WideGeom& w, int kc, float* part,
+                             hipStream_t stream, const char* what, bool decode, int key) {
+    hipError_t e = hipSuccess;
+    if (forced_fail("splitk")) return launch_failed(what, hipSuccess);
+    if ((e = wide_launch(P, w, kc, part, stream)) != hipSuccess) return launch_failed(what, e);
+    if ((e = splitk_reduce(P, kc, part, stream)) != hipSuccess)
+        return launch_failed("split-K reduce", e);
+    const bool f8 = P.enc == ENC_FP8A8;
+    debug_once(decode ? (f8 ? "fp8a8 split-K decode GEMV" : "mxfp4a8 split-K decode GEMV")
+                      : (f8 ? "fp8a8 split-K skinny GEMV" : "mxfp4a8 split-K skinny GEMV"),
+               key);
+    return RAD_OK;
+}
+
 /* The decode arms in order of preference -- quad GEMV (M <= 4), line GEMV (M = 5..16),
  * 16-row GEMV (any M <= 16) -- each taking the launch when the one before does not serve
  * the shape or fails to launch (a failed arm wrote nothing: the next one writes all of Y). */
-static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) {
+static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream,
+                         uint8_t* part = nullptr, int64_t part_bytes = 0) {
     QuadGeom qg{};
-    if (quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg, P.xq)) {
+    const bool quad = quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg, P.xq);
+    /* launch scratch: the K split where it applies (decode_split_plan) */
+    if (part && ((uintptr_t)part & 15) == 0 && !P.xq) {
+        int kc = 0;
+        WideGeom w{};
+        if (decode_split_plan(P.enc, P.M, P.N, P.K, cu_count(), quad, splitk, &kc, &w) &&
+            part_bytes >= (int64_t)kc * P.M * P.N * 4 &&
+            launch_wide_split(P, w, kc, reinterpret_cast<float*>(part), stream,
+                              "split-K decode", true, 240 + P.enc) == RAD_OK)
+            return RAD_OK;
+        /* no split, or a failed one: the decode arms below */
+    }
+    if (quad) {
         const int rc = launch_quad(P, qg, stream);
         if (rc == RAD_OK || P.xq) return rc;   /* fused bf16 activations: the quad GEMV only */
     } else if (P.xq) {
@@ -214,37 +283,6 @@ static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream) 
     debug_once(P.enc == ENC_MXFP4A8 ? "mxfp4a8 decode GEMV" : "fp8a8 decode GEMV",
                (P.enc << 4) | (g.mt << 1));
     return RAD_OK;
-}
-
-/* The skinny-band GEMV of a K split (gemv_wide_kernel): geometry w, kc chunks of w.cg
- * groups, f32 partial planes at part. */
-static hipError_t wide_launch(const GemmPlan& P, const WideGeom& w, int kc, float* part,
-                              hipStream_t stream) {
-    /* 32-bit lane offsets: a wave's 32 weight rows and the staged activation rows */
-    const int64_t lim = (int64_t)1 << 31;
-    if (32 * P.b_pitch >= lim || w.tw != 2 || P.M > 64) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(w.ntiles * kc)), block(512);
-#define R3D_WIDE(ENC_, D_, NTG_)                                                           \
-    hipLaunchKernelGGL((gemv_wide_kernel<ENC_, 2, D_, NTG_>), grid, block, (size_t)w.lds,    \
-                       stream, P.A, P.AS, P.B, P.BS, part, (int)P.M, (int)P.N, (int)P.K, kc, \
-                       w.cg, (int)w.ntiles, P.rblk, w.sclds, P.a_pitch, P.as_pitch,         \
-                       P.b_pitch, P.bs_pitch)
-#define R3D_WIDE_N(ENC_, D_)                                                                \
-    switch (w.ntg) {                                                                        \
-        case 1: R3D_WIDE(ENC_, D_, 1); break;                                               \
-        case 2: R3D_WIDE(ENC_, D_, 2); break;                                               \
-        case 3: R3D_WIDE(ENC_, D_, 3); break;                                               \
-        default: R3D_WIDE(ENC_, D_, 4); break;                                              \
-    }
-    if (w.ntg < 1 || w.ntg > 4 || (w.d != 1 && w.d != 2)) return hipErrorInvalidValue;
-    if (P.enc == ENC_MXFP4A8) {
-        if (w.d == 2) { R3D_WIDE_N(ENC_MXFP4A8, 2) } else { R3D_WIDE_N(ENC_MXFP4A8, 1) }
-    } else {
-        if (w.d == 2) { R3D_WIDE_N(ENC_FP8A8, 2) } else { R3D_WIDE_N(ENC_FP8A8, 1) }
-    }
-#undef R3D_WIDE_N
-#undef R3D_WIDE
-    return hipGetLastError();
 }
 
 /* The prefill GEMM: mode PF_A8 reads A/AS as given (e4m3 + f32 per 128) against e2m1
@@ -365,30 +403,25 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
 #undef R3D_PF_L
         return hipGetLastError();
     };
-    if (split) {
-        /* partial planes, then their in-order sum into Y */
+    if (split && kind == 1) {
+        if (launch_wide_split(P, gw, kc, reinterpret_cast<float*>(part), stream,
+                              "split-K prefill", false, 200 + 8 * mode + kind) == RAD_OK)
+            return RAD_OK;
+        /* a failed split: the whole K walk below recomputes every element of Y */
+    } else if (split) {
+        /* the prefill tile's partial planes, then their in-order sum into Y */
         hipError_t e = hipSuccess;
         if (forced_fail("splitk")) {
             launch_failed("split-K prefill", hipSuccess);
-        } else if ((e = kind == 1 ? wide_launch(P, gw, kc, reinterpret_cast<float*>(part), stream)
-                                  : tiles_launch(gs, kc, cst, reinterpret_cast<float*>(part)))
-                   != hipSuccess) {
+        } else if ((e = tiles_launch(gs, kc, cst, reinterpret_cast<float*>(part))) != hipSuccess) {
             launch_failed("split-K prefill", e);
-        } else {
-            const int64_t lanes = P.M * ((P.N + 3) / 4);
-            hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((lanes + 255) / 256)),
-                               dim3(256), 0, stream, reinterpret_cast<const float*>(part), kc,
-                               (int)P.M, (int)P.N, P.Y, P.y_pitch);
-            e = hipGetLastError();
-            if (e == hipSuccess) {
-                debug_once(kind == 1 ? (mode == PF_F8 ? "fp8a8 split-K skinny GEMV"
-                                                      : "mxfp4a8 split-K skinny GEMV")
-                                     : (mode == PF_F8 ? "fp8a8 split-K prefill"
-                                                      : "mxfp4a8 split-K prefill"),
-                           200 + 8 * mode + kind);
-                return RAD_OK;
-            }
+        } else if ((e = splitk_reduce(P, kc, reinterpret_cast<const float*>(part), stream)) !=
+                   hipSuccess) {
             launch_failed("split-K reduce", e);
+        } else {
+            debug_once(mode == PF_F8 ? "fp8a8 split-K prefill" : "mxfp4a8 split-K prefill",
+                       200 + 8 * mode + kind);
+            return RAD_OK;
         }
         /* a failed split: the whole K walk below recomputes every element of Y */
     }
@@ -415,7 +448,9 @@ static int entry(const RadArgs* a, RadStream s, int enc, bool decode) {
     if (rc) return rc;
     if (!chip_ok()) return RAD_E_UNSUPPORTED;
     hipStream_t stream = (hipStream_t)s;
-    if (decode) return launch_decode(P, decode_splitk(a), stream);
+    if (decode)
+        return launch_decode(P, decode_splitk(a), stream, (uint8_t*)a->scratch,
+                             a->scratch ? a->scratch_bytes : 0);
     if (enc == ENC_MXFP4A16) return launch_prefill(P, stream);
     return launch_prefill(P, stream, 0, (uint8_t*)a->scratch, a->scratch ? a->scratch_bytes : 0);
 }
@@ -642,6 +677,9 @@ int r3d_rad_gemm_nt_q_mxfp4_decode(const RadArgs* a, RadStream s) {
         return r3d::entry(x, t, r3d::ENC_MXFP4A8, true);
     });
 }
+int64_t r3d_rad_gemm_nt_q_mxfp4_decode_scratch(const RadArgs* a) {
+    return r3d::decode_scratch_bytes(a, r3d::ENC_MXFP4A8, r3d::cu_count());
+}
 int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s) {
     return r3d::dump_wrap("gemm_nt_q_mxfp4a16", a, s, [](const RadArgs* x, RadStream t) {
         return r3d::entry(x, t, r3d::ENC_MXFP4A16, false);
@@ -665,6 +703,9 @@ int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s) {
     return r3d::dump_wrap("gemm_nt_q_fp8a8_decode", a, s, [](const RadArgs* x, RadStream t) {
         return r3d::entry(x, t, r3d::ENC_FP8A8, true);
     });
+}
+int64_t r3d_rad_gemm_nt_q_fp8_decode_scratch(const RadArgs* a) {
+    return r3d::decode_scratch_bytes(a, r3d::ENC_FP8A8, r3d::cu_count());
 }
 int r3d_gfx950_describe(const char* row, const RadArgs* a, char* buf, int len) {
     return r3d::describe(row, a, buf, len);

@@ -254,6 +254,14 @@ __global__ __launch_bounds__(512) void gemv_wide_kernel(
         __builtin_amdgcn_sched_barrier(0);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* the skipped loads past the chunk */
+    /* every accumulator is complete here, in every lane: the compiler may otherwise sink the
+     * last line's MFMAs (and the per-lane operand selects feeding them) into the stores'
+     * lane-divergent branches, where lanes off the exec mask would hand the MFMA stale
+     * operands */
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+        for (int tg = 0; tg < NTG; ++tg) asm volatile("" : "+v"(acc[tt][tg]));
 
     /* ---- 4. the partial tile: lane l holds rows 4 (l / 16) + i of each weight tile for
      * activation row 16 tg + l % 16 -- four consecutive columns of plane c */

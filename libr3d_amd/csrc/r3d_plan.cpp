@@ -561,8 +561,7 @@ static bool wide_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t kc0, Wid
     w->cg = (int)cg;
     w->sclds = (int)scl;
     w->lds = (int)lds;
-    /* two lines in each wave's ring (measured best against one and four) */
-    w->d = cg / G >= 2 ? 2 : 1;
+    w->d = 1;
     return true;
 }
 
@@ -623,6 +622,33 @@ int64_t tile_scratch_bytes(const RadArgs* a, int enc, int ncu) {
     else if (!rad_args_geti(a, "M", &M) || M <= 0)
         M = 128;
     return tile_splitk_bytes(enc, M, N, K, ncu);
+}
+
+int decode_split_plan(int enc, int64_t M, int64_t N, int64_t K, int ncu, bool quad, int64_t pin,
+                      int* kc, WideGeom* w) {
+    if (quad || pin > 0 || M < 1 || M > 16 || N < 1 || K < 1 || N * K < kDecodeSplitMinWeights)
+        return 0;
+    int cst = 0;
+    return splitk_plan(enc, M, N, K, ncu, kc, &cst, nullptr, w) == 1 ? 1 : 0;
+}
+
+int64_t decode_scratch_bytes(const RadArgs* a, int enc, int ncu) {
+    long long N = 0, K = 0, M = 0;
+    if (!rad_args_geti(a, "N", &N) || !rad_args_geti(a, "K", &K)) return 0;
+    if (N <= 0 || K <= 0 || N > (1LL << 34) || K > (1LL << 27)) return 0;
+    const RadTensor* Y = rad_arg_in(a, 4);
+    const long long yn = Y ? rad_tensor_numel(Y) : 0;
+    if (yn > 0 && yn % N == 0)
+        M = yn / N;
+    else if (!rad_args_geti(a, "M", &M) || M <= 0)
+        M = 16;
+    if (M > 16) return 0;
+    const int64_t pin = decode_splitk(a);
+    QuadGeom qg{};
+    const bool quad = quad_geom(enc, M, N, K, pin, &qg, false);
+    int kc = 0;
+    return decode_split_plan(enc, M, N, K, ncu, quad, pin, &kc, nullptr) ? (int64_t)kc * M * N * 4
+                                                                          : 0;
 }
 
 int band_row_pitch(const RadTensor* t, int64_t cols, int64_t* pitch) {
@@ -1155,7 +1181,23 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
     rc = a16 ? plan_mxfp4a16(a, M, N, &P) : mx ? plan_mxfp4a8(a, M, N, &P) : plan_fp8a8(a, M, &P);
     if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
     QuadGeom qg{};
-    if (dec && quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &qg, P.xq)) {
+    const bool quad = quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, decode_splitk(a), &qg, P.xq);
+    auto wide_line = [&](const WideGeom& w, int kc, const char* arm) {
+        snprintf(buf, (size_t)len,
+                 "arm=%s kernel=wide enc=%s M=%lld N=%lld K=%lld bn=%d tiles=%lld kc=%d "
+                 "cst=%d steps=%lld ntg=%d tw=%d depth=%d lds=%d partials=%lld (f32 partial "
+                 "planes in scratch, summed in chunk order)",
+                 arm, ename, (long long)P.M, (long long)P.N, (long long)P.K, 128 * w.tw,
+                 (long long)w.ntiles, kc, w.cg, (long long)(P.K / 128), w.ntg, w.tw, w.d,
+                 w.lds, (long long)kc * P.M * P.N * 4);
+    };
+    int dkc = 0;
+    WideGeom dw{};
+    if (dec && !P.xq && a->scratch && ((uintptr_t)a->scratch & 15) == 0 &&
+        decode_split_plan(P.enc, P.M, P.N, P.K, 256, quad, decode_splitk(a), &dkc, &dw) &&
+        a->scratch_bytes >= (int64_t)dkc * P.M * P.N * 4) {
+        wide_line(dw, dkc, "splitk");
+    } else if (dec && quad) {
         snprintf(buf, (size_t)len,
                  "arm=decode kernel=quad enc=%s M=%lld N=%lld K=%lld mt=%d qpw=%d chunks=%d "
                  "waves=%d quads=%lld blocks=%lld groups=%d depth=%d lds=%d rblk=%d xq=%d",
@@ -1192,13 +1234,7 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
         WideGeom w{};
         splitk_plan(P.enc, P.M, P.N, P.K, 256, nullptr, nullptr, &g, &w);
         if (kind == 1)
-            snprintf(buf, (size_t)len,
-                     "arm=splitk kernel=wide enc=%s M=%lld N=%lld K=%lld bn=%d tiles=%lld kc=%d "
-                     "cst=%d steps=%lld ntg=%d tw=%d depth=%d lds=%d partials=%lld (f32 partial "
-                     "planes in scratch, summed in chunk order)",
-                     ename, (long long)P.M, (long long)P.N, (long long)P.K, 128 * w.tw,
-                     (long long)w.ntiles, kc, cst, (long long)(P.K / 128), w.ntg, w.tw, w.d,
-                     w.lds, (long long)kc * P.M * P.N * 4);
+            wide_line(w, kc, "splitk");
         else
             snprintf(buf, (size_t)len,
                      "arm=splitk kernel=tile enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d tiles=%lld "

@@ -154,7 +154,9 @@ int skinny_passes(int enc, int64_t M, int64_t N, int ncu);
 
 /* The skinny-band GEMV (gemv_wide_kernel, r3d_gemv_wide.h): 8 waves of tw 16-row weight
  * tiles (256 rows a workgroup at tw = 2) x one K chunk of cg groups; depth d lines in each
- * wave's register ring; ntg 16-row groups of activations staged in LDS with the chunk. */
+ * wave's register ring (1: measured at least as fast as 2 and 4 on every config 2 shape at
+ * M = 4..64, and 10 % faster at M = 64); ntg 16-row groups of activations staged in LDS with
+ * the chunk. */
 struct WideGeom {
     int tw, d;
     int cg, ntg, sclds, lds;
@@ -182,6 +184,20 @@ int64_t tile_splitk_bytes(int enc, int64_t M, int64_t N, int64_t K, int ncu);
 /* The tile rows' scratch hook: tile_splitk_bytes at the args' N and K and M (numel(y) / N,
  * else the "M" param, else 128 -- the largest M the split takes); 0 without N or K. */
 int64_t tile_scratch_bytes(const RadArgs* a, int enc, int ncu);
+
+/* The decode rows' K split over launch scratch: the skinny-band GEMV's split (splitk_plan
+ * kind 1) takes the launch where the decode arm would be the line GEMV (M = 5..16) or the
+ * 16-row GEMV (an M <= 4 shape the quad GEMV cannot stage), on a plane of at least
+ * kDecodeSplitMinWeights weights and with no pinned split (pin > 0: the row's "splitk"
+ * tunable).  Measured on MI355X at config 2's shapes: gate_up / down M = 16 20.7 / 25.9 us
+ * on the line GEMV, 16.9 / 16.7 us split; qkv (N K = 44 M) is faster unsplit at every M.
+ * quad: the quad GEMV takes this launch.  Returns 1 with *kc chunks of geometry *w, else 0. */
+constexpr int64_t kDecodeSplitMinWeights = (int64_t)1 << 26;
+int decode_split_plan(int enc, int64_t M, int64_t N, int64_t K, int ncu, bool quad, int64_t pin,
+                      int* kc, WideGeom* w);
+/* The decode rows' scratch hook: the split's kc f32 planes of M x N at the args' N, K and M
+ * (numel(y) / N, else the "M" param, else 16), 0 where the split does not apply. */
+int64_t decode_scratch_bytes(const RadArgs* a, int enc, int ncu);
 
 /* The band rows' operand walk (src/r3d_band.hip:419-449 of the reference): a rank-1 tensor
  * of exactly `cols` unit-stride elements is one row read by every row (pitch 0); rank 2

@@ -45,6 +45,8 @@ int r3d_rad_gemm_nt_q_fp8(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_fp8_decode(const RadArgs* a, RadStream s);
 int64_t r3d_rad_gemm_nt_q_scratch(const RadArgs* a);
 int64_t r3d_rad_gemm_nt_q_fp8_scratch(const RadArgs* a);
+int64_t r3d_rad_gemm_nt_q_mxfp4_decode_scratch(const RadArgs* a);
+int64_t r3d_rad_gemm_nt_q_fp8_decode_scratch(const RadArgs* a);
 int r3d_rad_gemm_nt_q_mxfp4a16(const RadArgs* a, RadStream s);
 int64_t r3d_rad_gemm_nt_q_mxfp4a16_scratch(const RadArgs* a);
 int r3d_rad_quant_act_fp8(const RadArgs* a, RadStream s);
@@ -269,14 +271,17 @@ const RadKernelInfo kRows[] = {
     {"gemm_nt_q_mxfp4_decode", "gemm_nt_q", "gemm",
      "mxfp4a8 decode-band GEMV on gfx950: M <= 4 one wave per 4 weight rows (whole 128-byte "
      "lines straight into the MFMA's fp4 operand, E8M0 bytes as its scale operand), M 5..16 "
-     "one wave per 32 rows; split-K folded through LDS in chunk order",
+     "one wave per 32 rows; split-K folded through LDS in chunk order; on planes of 2^26+ "
+     "weights past the quad GEMV, K split across workgroups into f32 partials in launch "
+     "scratch, summed in chunk order",
      "M <= 16 (decode and speculative verify; widened from the reference's 8); K a multiple "
-     "of 128; N any (dead rows clamp their loads and never store); M derives from numel(y)/N",
+     "of 128; N any (dead rows clamp their loads and never store); M derives from numel(y)/N; "
+     "scratch optional (the hook sizes the split's partials; without them the GEMVs run)",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), e2m1 b with E8M0 b_scale per (row, 32 K), "
      "bf16 y; b_ref accepted and ignored; a_sum refused",
      RAD_DOMAIN_DEVICE, kPrioDecode, cMxfp4Decode, 3, tSplitK, 1, nullptr,
-     nullptr, nullptr, r3d_rad_gemm_nt_q_mxfp4_decode, nullptr, nullptr, nullptr, nullptr,
-     nullptr},
+     nullptr, nullptr, r3d_rad_gemm_nt_q_mxfp4_decode, r3d_rad_gemm_nt_q_mxfp4_decode_scratch,
+     nullptr, nullptr, nullptr, nullptr},
 
     {"gemm_nt_q_fp8a8", "gemm_nt_q", "gemm",
      "fp8a8 prefill GEMM on gfx950 block-scaled MFMA: 128x128 output tile over a three-deep "
@@ -295,14 +300,16 @@ const RadKernelInfo kRows[] = {
     {"gemm_nt_q_fp8a8_decode", "gemm_nt_q", "gemm",
      "fp8a8 decode-band GEMV on gfx950: M <= 4 one wave per 4 weight rows (two whole-line "
      "loads per 128-of-K group into the MFMA's fp8 operand), M 5..16 one wave per 32 rows; "
-     "(sub * a_scale) * b_scale per group, split-K folded through LDS in chunk order",
+     "(sub * a_scale) * b_scale per group, split-K folded through LDS in chunk order; on "
+     "planes of 2^26+ weights past the quad GEMV, K split across workgroups into f32 partials "
+     "in launch scratch, summed in chunk order",
      "M <= 16; K a multiple of 128; N any; b_scale either the 128x128 block grid or a per-row "
-     "grid",
+     "grid; scratch optional (the hook sizes the split's partials; without them the GEMVs run)",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), fp8_e4m3 b with bf16 scale per 128x128 "
      "tile (or per row), bf16 y; a_sum and b_ref refused",
      RAD_DOMAIN_DEVICE, kPrioDecode, cFp8Decode, 4, tSplitK, 1, nullptr,
-     nullptr, nullptr, r3d_rad_gemm_nt_q_fp8_decode, nullptr, nullptr, nullptr, nullptr,
-     nullptr},
+     nullptr, nullptr, r3d_rad_gemm_nt_q_fp8_decode, r3d_rad_gemm_nt_q_fp8_decode_scratch,
+     nullptr, nullptr, nullptr, nullptr},
 
     {"gemm_nt_q_mxfp4a16", "gemm_nt_q", "gemm",
      "mxfp4 prefill GEMM with bf16 activations on gfx950: the activations are quantised to "

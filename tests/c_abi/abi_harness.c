@@ -82,7 +82,8 @@ static const void* const kExports[] = {
     (const void*)r3d_rad_gemm_nt_q_gated_fp8_scratch, (const void*)r3d_gfx950_describe,
     (const void*)r3d_gfx950_mxfp4a16_stage, (const void*)r3d_gfx950_build_id,
     (const void*)r3d_rad_gemm_nt_q_scratch, (const void*)r3d_rad_gemm_nt_q_fp8_scratch,
-    (const void*)r3d_rad_logits_gemm_e4m3, (const void*)r3d_gfx950_logits_head_bytes,
+    (const void*)r3d_rad_gemm_nt_q_mxfp4_decode_scratch,
+    (const void*)r3d_rad_gemm_nt_q_fp8_decode_scratch, (const void*)r3d_rad_logits_gemm_e4m3, (const void*)r3d_gfx950_logits_head_bytes,
     (const void*)r3d_gfx950_logits_head_header, (const void*)r3d_gfx950_logits_head_join,
     (const void*)r3d_gfx950_logits_head_split, (const void*)r3d_gfx950_logits_head_forget,
 };

@@ -63,6 +63,15 @@ def run_row(row, dtype, A, AS, B, BS, M, N, K, dev, y_shape=None, extra=None, tu
     return rc, Y, ok
 
 
+def hook_bytes(row, dtype, M, N, K):
+    """The launch scratch `row`'s hook asks for at M x N x K (the hook reads only N, K and
+    y's element count, so the other operands are stand-ins)."""
+    t = torch.zeros((1, 16), dtype=torch.uint8)
+    y = torch.zeros((M, N), dtype=torch.int16)
+    ops = R.GemmOperands(t, t, t, t, y, dtype=dtype, N=N, K=K)
+    return R.row_scratch_bytes(row, ops)
+
+
 def record(case, row, shape, c, Y=None, Yref_bits=None):
     """Append one parity record (JSON line) to the file named by R3D_PARITY_LOG, if set:
     the case, the row, the shape, the comparison figures and, given both outputs, the

@@ -288,7 +288,6 @@ def test_tile_splitk_hook_and_arm():
     the split arm, with less (or misaligned) the unsplit arms it had before."""
     rows = {r["name"]: r for r in R.rows()}
     assert rows["gemm_nt_q_mxfp4"]["scratch"] and rows["gemm_nt_q_fp8a8"]["scratch"]
-    assert not rows["gemm_nt_q_mxfp4_decode"]["scratch"]
     # up to M = 64 the skinny-band GEMV over 256-row tiles, else the 128 x 128 tile.  Config 2
     # at M = 64: down 21 tiles x 12 chunks of 14 groups, qkv 32 x 7 of 6, gate_up 84 x 3 of
     # 14 (both encodings); past M = 64 down splits 42 x 6 of 28 and gate_up's 168 tiles fill
@@ -335,6 +334,52 @@ def test_tile_splitk_hook_and_arm():
         ops = R.GemmOperands(a, s, b, bs, None, dtype="mxfp4a8", N=5376, K=21504,
                              extra_params=extra)
         assert R.row_scratch_bytes("gemm_nt_q_mxfp4", ops) == (6 if M > 64 else 12) * M * 5376 * 4
+
+
+def test_decode_split_hook_and_arm():
+    """The decode rows' scratch hook sizes the skinny-band GEMV's K split (kc * M * N * 4)
+    where the quad GEMV does not take the launch and the plane holds at least 2^26 weights,
+    with no pinned split; with that scratch the launch describes the split, with less, a
+    misaligned one or a pinned split the GEMV it had before."""
+    rows = {r["name"]: r for r in R.rows()}
+    assert rows["gemm_nt_q_mxfp4_decode"]["scratch"] and rows["gemm_nt_q_fp8a8_decode"]["scratch"]
+    for mk, row in ((_mx_ops, "gemm_nt_q_mxfp4_decode"), (_f8_ops, "gemm_nt_q_fp8a8_decode")):
+        mx = row == "gemm_nt_q_mxfp4_decode"
+        # config 2's gate_up / down / qkv at M = 16, 4 and 1, and both sides of 2^26 weights
+        for M, N, K, split in [(16, 21504, 5376, True), (16, 5376, 21504, True),
+                               (16, 8192, 5376, False), (8, 5376, 21504, True),
+                               (4, 5376, 21504, True), (4, 21504, 5376, False),
+                               (1, 5376, 21504, False), (5, 2048, 32768, True),
+                               (5, 2048, 32512, False)]:
+            ops, keep = mk(M=M, N=N, K=K)
+            base = _geom(R.describe(row, ops)[1])
+            assert base["arm"] == "decode"
+            assert split == (base["kernel"] != "quad" and N * K >= 1 << 26), (row, M, N, K)
+            kc, cst = _wide_split(N, K, M, mx) if split else (0, 0)
+            need = kc * M * N * 4
+            assert R.row_scratch_bytes(row, ops) == need, (row, M, N, K)
+            if not need:
+                continue
+            sc = FakeT(_aligned((64,), np.uint8))
+            ops.set_scratch(sc, need)
+            rc, d = R.describe(row, ops)
+            g = _geom(d)
+            assert rc == R.RAD_OK and g["arm"] == "splitk" and g["kernel"] == "wide", d
+            assert (g["kc"], g["cst"], g["partials"]) == (str(kc), str(cst), str(need)), d
+            ops.set_scratch(sc, need - 1)                      # short: the GEMV
+            assert _geom(R.describe(row, ops)[1])["kernel"] == base["kernel"]
+            ops.set_scratch(FakeT(sc.arr, offset=8), need)     # misaligned: the GEMV
+            assert _geom(R.describe(row, ops)[1])["kernel"] == base["kernel"]
+            del ops, keep
+    # a pinned split keeps the GEMV and asks for no scratch
+    ops, _ = _mx_ops(M=16, N=5376, K=21504, tunables=[("splitk", 2)])
+    assert R.row_scratch_bytes("gemm_nt_q_mxfp4_decode", ops) == 0
+    # without y the hook sizes at the M parameter, without either at M = 16
+    _, (a, s, b, bs, _y) = _mx_ops(M=16, N=5376, K=21504)
+    for extra, M in ((None, 16), ([("M", 8)], 8)):
+        ops = R.GemmOperands(a, s, b, bs, None, dtype="mxfp4a8", N=5376, K=21504,
+                             extra_params=extra)
+        assert R.row_scratch_bytes("gemm_nt_q_mxfp4_decode", ops) == 12 * M * 5376 * 4
 
 
 def test_decode_geometry_policy():

@@ -24,9 +24,9 @@ TENSOR_REL_MAX = 2e-3
 NT = 16
 
 
-def _run(row, dtype, A, AS, B, BS, M, N, K, gpu):
+def _run(row, dtype, A, AS, B, BS, M, N, K, gpu, scratch=None):
     from tests import gpu_util as gu
-    rc, Y, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, gpu)
+    rc, Y, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, gpu, scratch=scratch)
     assert rc == R.RAD_OK, rc
     assert guards
     return Y
@@ -73,12 +73,19 @@ C2_SHAPES = {"gate_up": (5376, 21504), "down": (21504, 5376), "qkv": (5376, 8192
 @pytest.mark.parametrize("shape", sorted(C2_SHAPES))
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_c2_mxfp4_decode(gpu, shape, M):
+    """Without launch scratch (the decode GEMVs), and with the scratch the row's hook asks
+    for where it asks for any (the K split: gate_up and down at M = 4 / 16 past the quad
+    GEMV)."""
+    from tests import gpu_util as gu
     K, N = C2_SHAPES[shape]
     _, A, AS = synth.activations(M, K, 0x5EED + 20 + M)
     B, BS = synth.mxfp4_weights(N, K, 0x5EED + 21 + K)
-    Y = _run("gemm_nt_q_mxfp4_decode", "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
-    _grade(Y, A, AS, B, BS, K, "mxfp4a8", case="C2 %s M=%d" % (shape, M),
-           row="gemm_nt_q_mxfp4_decode")
+    row = "gemm_nt_q_mxfp4_decode"
+    Y = _run(row, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+    _grade(Y, A, AS, B, BS, K, "mxfp4a8", case="C2 %s M=%d" % (shape, M), row=row)
+    if gu.hook_bytes(row, "mxfp4a8", M, N, K):
+        Y = _run(row, "mxfp4a8", A, AS, B, BS, M, N, K, gpu, scratch="hook")
+        _grade(Y, A, AS, B, BS, K, "mxfp4a8", case="C2 %s M=%d split-K" % (shape, M), row=row)
 
 
 # config 4's other per-layer shapes (q, k / v, o) at its decode batch M = 4; gate/up and

@@ -59,6 +59,11 @@ MX_DEC, MX_TILE, F8_DEC = "gemm_nt_q_mxfp4_decode", "gemm_nt_q_mxfp4", "gemm_nt_
     ("splitk", [(MX_TILE, "mxfp4a8", 40, 1000, 2048, "hook"),
                 ("gemm_nt_q_fp8a8", "fp8a8", 64, 520, 4096, "hook")],
      "split-K prefill launch FAILED"),
+    # the decode rows' split fails: the line GEMV (M = 9) and the 16-row GEMV (M = 4 on
+    # activation rows the quad GEMV cannot stage) take the launch
+    ("splitk", [(MX_DEC, "mxfp4a8", 9, 1024, 65536, "hook"),
+                (F8_DEC, "fp8a8", 4, 3200, 21504, "hook")],
+     "split-K decode launch FAILED"),
 ])
 def test_failed_arm_falls_back(gpu, arms, cases, logged):
     env = dict(os.environ, R3D_GFX950_FAIL_ARM=arms, R3D_DEBUG_GEMM="1")

@@ -245,6 +245,36 @@ def test_fp8_tile_splitk(gpu, M, N, K, rblk):
     assert np.array_equal(Y1, Y2)
 
 
+# split K on the decode rows (planes of 2^26+ weights past the quad GEMV): 17..64 chunks,
+# a short last chunk (K = 25856), ragged M (5, 9) and N (2600: a partial last tile and dead
+# rows), an M = 4 shape whose activation rows the quad GEMV cannot stage
+DEC_SPLIT_SHAPES = [(16, 2048, 32768), (5, 1024, 65536), (9, 2600, 25856), (4, 3200, 21504)]
+
+
+@pytest.mark.parametrize("M,N,K", DEC_SPLIT_SHAPES)
+def test_mxfp4_decode_splitk(gpu, M, N, K):
+    """The decode row's split arm against the oracle at the decode rows' bar, scratch
+    guarded; two calls give the same bits; without scratch the GEMV meets the same bar."""
+    gu = _gu()
+    assert gu.hook_bytes(MX_DEC, "mxfp4a8", M, N, K) > 0
+    A, AS, B, BS = _mx_case(M, N, K, 7 * M + N + K)
+    _, Y1 = _check(MX_DEC, "mxfp4a8", A, AS, B, BS, M, N, K, gpu, scratch="hook")
+    _, Y2 = _check(MX_DEC, "mxfp4a8", A, AS, B, BS, M, N, K, gpu, scratch="hook")
+    assert np.array_equal(Y1, Y2)
+    _check(MX_DEC, "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+
+
+@pytest.mark.parametrize("M,N,K", DEC_SPLIT_SHAPES)
+@pytest.mark.parametrize("rblk", [1, 128])
+def test_fp8_decode_splitk(gpu, M, N, K, rblk):
+    gu = _gu()
+    assert gu.hook_bytes(F8_DEC, "fp8a8", M, N, K) > 0
+    A, AS, B, BS = _f8_case(M, N, K, 5 * M + N + K + rblk, rblk)
+    _, Y1 = _check(F8_DEC, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk, scratch="hook")
+    _, Y2 = _check(F8_DEC, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk, scratch="hook")
+    assert np.array_equal(Y1, Y2)
+
+
 def test_splitk_short_scratch_runs_unsplit(gpu):
     """A byte short of the hook's size: the launch takes the unsplit arm, leaves the
     scratch untouched (its poison and red zones intact) and still meets the bar."""
