@@ -1,5 +1,6 @@
-/* r3d_gemv_wide.h -- gfx950 GEMV for the tile rows' skinny band with K split across
- * workgroups (gemm_nt_q at mxfp4a8 and fp8a8, up to 64 activation rows).
+/* r3d_gemv_wide.h -- gfx950 GEMV with K split across workgroups over launch scratch
+ * (gemm_nt_q at mxfp4a8 and fp8a8, up to 64 activation rows): the tile rows' skinny band
+ * and the decode rows' launches past the quad GEMV on large planes.
  *
  * The skinny band streams weights like a decode GEMV and reads each weight byte against up
  * to 64 activation rows.  A workgroup of 8 waves owns 256 weight rows (a wave TW = 2 tiles
