@@ -745,12 +745,13 @@ def bench_c4(dev, stream, steps=5):
     gate/up/down in mxfp4a8 plus an fp8a8 lm_head (K=5376, N=262144).  Weights are random
     codes generated on the device (bandwidth does not depend on values; NaN-free); the
     435 launches run eagerly and as one captured HIP graph; then eagerly again with the
-    reference's own lm_head row, logits_gemm_e4m3 over the joined e4m3 head."""
+    reference's own lm_head row, logits_gemm_e4m3 over the joined e4m3 head.  Last, the
+    same bytes in the engine's joined layouts -- q/k/v as one N = 8192 plane (config 2's
+    qkv shape) and gate/up as one N = 43008 plane (the [M, 2n] gate_up plane the gated row
+    consumes) -- 249 launches, eagerly and as a graph."""
     import torch
     import libr3d_amd as R
     M, H, I, L, V = 4, 5376, 21504, 62, 262144
-    shapes = [("q", H, 4096), ("k", H, 2048), ("v", H, 2048), ("o", 4096, H),
-              ("gate", H, I), ("up", H, I), ("down", I, H)]
     g = torch.Generator(device=dev)
     g.manual_seed(0x5EED + 4)
 
@@ -765,66 +766,64 @@ def bench_c4(dev, stream, steps=5):
         a = codes(M * K, True).view(M, K)
         s = torch.full((M, K // 128), 0.01, dtype=torch.float32, device=dev)
         acts[K] = (a, s)
-    y_bufs = {}
-    launches = []
     mx_dec = R.row_launcher("gemm_nt_q_mxfp4_decode")
     f8_dec = R.row_launcher("gemm_nt_q_fp8a8_decode")
-    keep = []
-    total = 0
-    for layer in range(L):
-        for name, K, N in shapes:
-            b = codes(N * K // 2, False).view(N, K // 2)
-            bs = (127 - torch.randint(0, 9, (N, K // 32), dtype=torch.int32, device=dev,
-                                      generator=g)).to(torch.uint8)
-            y = y_bufs.setdefault(N, torch.empty((M, N), dtype=torch.int16, device=dev))
-            a, s = acts[K]
-            ops = R.GemmOperands(a, s, b, bs, y, dtype="mxfp4a8", N=N, K=K)
-            keep.append((b, bs, ops))
-            launches.append((mx_dec, ops))
-            total += mx_bytes(M, N, K)
-    b = codes(V * H, True).view(V, H)
-    bs = torch.full((V, H // 128), 0x3C00, dtype=torch.int16, device=dev)   # bf16 0.0078125
-    y = torch.empty((M, V), dtype=torch.int16, device=dev)
-    a, s = acts[H]
-    ops = R.GemmOperands(a, s, b, bs, y, dtype="fp8a8", N=V, K=H)
-    keep.append((b, bs, ops))
-    launches.append((f8_dec, ops))
-    total += f8_bytes(M, V, H)
-    # each launch gets the launch scratch its row's hook asks for, from one arena (the
-    # launches run in order on one stream, as an engine's would): down's K split at M = 4
-    needs = [R.row_scratch_bytes("gemm_nt_q_mxfp4_decode" if fn is mx_dec
-                                 else "gemm_nt_q_fp8a8_decode", o) for fn, o in launches]
-    arena = torch.empty(max(max(needs), 256), dtype=torch.uint8, device=dev)
-    for (fn, o), need in zip(launches, needs):
-        if need > 0:
-            o.set_scratch(arena, need)
-    torch.cuda.synchronize()
 
-    def step(st):
+    def build(shapes):
+        """-> (launches, kept tensors, bytes, split launches) for 62 layers of `shapes` and
+        the fp8a8 lm_head; every launch gets the scratch its row's hook asks for from one
+        arena (the launches run in order on one stream, as an engine's would)."""
+        y_bufs, launches, keep, total = {}, [], [], 0
+        for layer in range(L):
+            for name, K, N in shapes:
+                b = codes(N * K // 2, False).view(N, K // 2)
+                bs = (127 - torch.randint(0, 9, (N, K // 32), dtype=torch.int32, device=dev,
+                                          generator=g)).to(torch.uint8)
+                y = y_bufs.setdefault(N, torch.empty((M, N), dtype=torch.int16, device=dev))
+                a, s = acts[K]
+                ops = R.GemmOperands(a, s, b, bs, y, dtype="mxfp4a8", N=N, K=K)
+                keep.append((b, bs, ops))
+                launches.append((mx_dec, ops))
+                total += mx_bytes(M, N, K)
+        b = codes(V * H, True).view(V, H)
+        bs = torch.full((V, H // 128), 0x3C00, dtype=torch.int16, device=dev)   # bf16 2^-7
+        y = torch.empty((M, V), dtype=torch.int16, device=dev)
+        a, s = acts[H]
+        ops = R.GemmOperands(a, s, b, bs, y, dtype="fp8a8", N=V, K=H)
+        keep.append((b, bs, ops))
+        launches.append((f8_dec, ops))
+        total += f8_bytes(M, V, H)
+        needs = [R.row_scratch_bytes("gemm_nt_q_mxfp4_decode" if fn is mx_dec
+                                     else "gemm_nt_q_fp8a8_decode", o) for fn, o in launches]
+        arena = torch.empty(max(max(needs), 256), dtype=torch.uint8, device=dev)
+        keep.append(arena)
+        for (fn, o), need in zip(launches, needs):
+            if need > 0:
+                o.set_scratch(arena, need)
+        torch.cuda.synchronize()
+        return launches, keep, total, sum(1 for n in needs if n > 0)
+
+    def step(launches, st):
         for fn, o in launches:
             fn(o, st)
 
-    step(stream)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step(stream)
-    torch.cuda.synchronize()
-    eager = (time.perf_counter() - t0) / steps
+    def eager(launches):
+        step(launches, stream)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(launches, stream)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
 
-    res = {"c4_decode_step_eager": {"bytes": total, "ms": round(eager * 1e3, 3),
-                                    "GBps": round(total / eager / 1e9, 1),
-                                    "frac_hbm": round(total / eager / 1e9 / HBM_PEAK_GBS, 4),
-                                    "launches": len(launches),
-                                    "split_launches": sum(1 for n in needs if n > 0)}}
-    try:
+    def graphed(launches):
         s2 = torch.cuda.Stream()
         with torch.cuda.stream(s2):
-            step(s2.cuda_stream)
+            step(launches, s2.cuda_stream)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=s2):
-            step(s2.cuda_stream)
+            step(launches, s2.cuda_stream)
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
@@ -832,12 +831,24 @@ def bench_c4(dev, stream, steps=5):
         for _ in range(steps):
             graph.replay()
         torch.cuda.synchronize()
-        gt = (time.perf_counter() - t0) / steps
-        res["c4_decode_step_graph"] = {"bytes": total, "ms": round(gt * 1e3, 3),
-                                       "GBps": round(total / gt / 1e9, 1),
-                                       "frac_hbm": round(total / gt / 1e9 / HBM_PEAK_GBS, 4)}
+        return (time.perf_counter() - t0) / steps
+
+    def rec(total, t, **kw):
+        r = {"bytes": total, "ms": round(t * 1e3, 3), "GBps": round(total / t / 1e9, 1),
+             "frac_hbm": round(total / t / 1e9 / HBM_PEAK_GBS, 4)}
+        r.update(kw)
+        return r
+
+    separate = [("q", H, 4096), ("k", H, 2048), ("v", H, 2048), ("o", 4096, H),
+                ("gate", H, I), ("up", H, I), ("down", I, H)]
+    launches, keep, total, nsplit = build(separate)
+    te = eager(launches)
+    res = {"c4_decode_step_eager": rec(total, te, launches=len(launches), split_launches=nsplit)}
+    try:
+        tg = graphed(launches)
+        res["c4_decode_step_graph"] = rec(total, tg)
         log("[bench] C4 decode step: eager %.3f ms (%.1f GB/s), graph %.3f ms (%.1f GB/s)" % (
-            eager * 1e3, total / eager / 1e9, gt * 1e3, total / gt / 1e9))
+            te * 1e3, total / te / 1e9, tg * 1e3, total / tg / 1e9))
     except Exception as e:          # graph capture unavailable: report eager only
         res["c4_decode_step_graph"] = {"error": repr(e)[:200]}
         log("[bench] C4 graph capture failed: %r" % (e,))
@@ -854,21 +865,31 @@ def bench_c4(dev, stream, steps=5):
     lops = R.LogitsOperands(xh, blob, yl, n_vocab=V, n_embd=H)
     launches[-1] = (R.row_launcher("logits_gemm_e4m3"), lops)
     total_e4 = total - f8_bytes(M, V, H) + V * H + V * scols * 2 + M * H * 2 + M * V * 4
-    step(stream)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step(stream)
-    torch.cuda.synchronize()
-    e4 = (time.perf_counter() - t0) / steps
+    t4 = eager(launches)
     R.forget_head(blob)
-    res["c4_decode_step_eager_e4m3_head"] = {
-        "bytes": total_e4, "ms": round(e4 * 1e3, 3), "GBps": round(total_e4 / e4 / 1e9, 1),
-        "frac_hbm": round(total_e4 / e4 / 1e9 / HBM_PEAK_GBS, 4),
-        "lm_head": "logits_gemm_e4m3 (bf16 x, joined e4m3 + bf16 scale head, f32 logits)"}
+    res["c4_decode_step_eager_e4m3_head"] = rec(
+        total_e4, t4, lm_head="logits_gemm_e4m3 (bf16 x, joined e4m3 + bf16 scale head, f32 logits)")
     log("[bench] C4 decode step with the e4m3 logits head: eager %.3f ms (%.1f GB/s)" % (
-        e4 * 1e3, total_e4 / e4 / 1e9))
-    del keep, launches, blob, arena
+        t4 * 1e3, total_e4 / t4 / 1e9))
+    del keep, launches, blob
+    torch.cuda.empty_cache()
+    # the joined layouts: the same weight bytes in 4 launches a layer
+    joined = [("qkv", H, 8192), ("o", 4096, H), ("gate_up", H, 2 * I), ("down", I, H)]
+    launches, keep, total_j, nsplit = build(joined)     # the activation rows read once less
+    tj = eager(launches)
+    res["c4_decode_step_eager_joined"] = rec(
+        total_j, tj, launches=len(launches), split_launches=nsplit,
+        layout="q/k/v joined (N = 8192) and gate/up joined (N = 43008): the same weight bytes")
+    try:
+        tjg = graphed(launches)
+        res["c4_decode_step_graph_joined"] = rec(total_j, tjg)
+    except Exception as e:
+        res["c4_decode_step_graph_joined"] = {"error": repr(e)[:200]}
+        tjg = float("nan")
+    log("[bench] C4 decode step, joined q/k/v and gate/up planes: eager %.3f ms (%.1f GB/s), "
+        "graph %.3f ms" % (tj * 1e3, total_j / tj / 1e9, tjg * 1e3))
+    del keep, launches
+    torch.cuda.empty_cache()
     return res
 
 
