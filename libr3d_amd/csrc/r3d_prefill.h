@@ -472,6 +472,13 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     /* ---- split K: the f32 partial tile goes to plane kci of part ([kc][M][N], 16-byte
      * aligned), four consecutive columns a lane */
     if (KS && part) {
+        /* every accumulator complete in every lane before the lane-divergent stores (the
+         * compiler may otherwise sink the last MFMAs into them, where lanes off the exec
+         * mask would hand the MFMA stale operands) */
+#pragma unroll
+        for (int ni = 0; ni < WNF; ++ni)
+#pragma unroll
+            for (int mi = 0; mi < WMW; ++mi) asm volatile("" : "+v"(acc[ni][mi]));
         float* pp = part + (int64_t)kci * M * N;
         const bool v4 = (N & 3) == 0;
 #pragma unroll
