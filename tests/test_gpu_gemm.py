@@ -189,6 +189,10 @@ def test_fp8_tile(gpu, M, N, K, rblk):
     _check(F8_TILE, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk)
 
 
+def _geom(desc):
+    return dict(kv.split("=") for kv in desc.split() if "=" in kv)
+
+
 def _split_of(row, dtype, M, N, K):
     """(kc, cst) the row's describe reports with hook-sized scratch, or None unsplit."""
     gu = _gu()
@@ -273,6 +277,51 @@ def test_fp8_decode_splitk(gpu, M, N, K, rblk):
     _, Y1 = _check(F8_DEC, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk, scratch="hook")
     _, Y2 = _check(F8_DEC, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk, scratch="hook")
     assert np.array_equal(Y1, Y2)
+
+
+@pytest.mark.parametrize("row,dtype,M,N,K", [
+    (MX_DEC, "mxfp4a8", 5, 2048, 32768), (MX_TILE, "mxfp4a8", 40, 1000, 2048),
+    (F8_TILE, "fp8a8", 33, 700, 2688), (F8_DEC, "fp8a8", 9, 2048, 32768)])
+def test_splitk_padded_views(gpu, row, dtype, M, N, K):
+    """The K split on padded-pitch views of the operands (activation, a_scale, scale rows,
+    Y, and the e4m3 weight rows; the e2m1 plane must be dense, as the reference's FP4 rule
+    requires): the partial planes and their sum follow the pitches, and Y's padding columns
+    are never written."""
+    import torch
+    gu = _gu()
+    mx = dtype == "mxfp4a8"
+    if mx:
+        A, AS, B, BS = _mx_case(M, N, K, 11 * M + N)
+    else:
+        A, AS, B, BS = _f8_case(M, N, K, 11 * M + N, 1)
+
+    def padded(x, extra):
+        w = np.zeros((x.shape[0], x.shape[1] + extra), x.dtype)
+        w[:, :x.shape[1]] = x
+        return w
+
+    hosts = [padded(A, 128), padded(AS, 4), padded(B, 0 if mx else 64), padded(BS, 8)]
+    g = [gu.Guarded(h, gpu) for h in hosts]
+    views = [gg.t[:, :x.shape[1]] for gg, x in zip(g, (A, AS, B, BS))]
+    gY = gu.Guarded(np.full((M, N + 8), gu.Y_SENTINEL, np.uint16), gpu)
+    ops = R.GemmOperands(*views, gY.t[:, :N], dtype=dtype, N=N, K=K)
+    need = R.row_scratch_bytes(row, ops)
+    assert need > 0
+    gS = gu.Guarded(np.zeros(need, np.uint8), gpu, fill=0x5A)
+    ops.set_scratch(gS.t, need)
+    assert _geom(R.describe(row, ops)[1])["arm"] == "splitk"
+    assert R.launch_row(row, ops, torch.cuda.current_stream().cuda_stream) == R.RAD_OK
+    torch.cuda.synchronize()
+    assert all(gg.guards_intact() for gg in g + [gY, gS])
+    Yp = gY.t.cpu().numpy().view(np.uint16).reshape(M, N + 8)
+    assert (Yp[:, N:] == gu.Y_SENTINEL).all()
+    if mx:
+        Yr, Yf, S = O.quant_dot_mxfp4a8(A, AS, B, BS, nthreads=16)
+    else:
+        Yr, Yf, S = O.quant_dot_fp8a8(A, AS, B, BS, 1, nthreads=16)
+    S8 = O.group8_mag(dtype, A, AS, B, BS, 1, nthreads=16)
+    c = gu.compare(np.ascontiguousarray(Yp[:, :N]), Yr, Yf, S, K, S8)
+    assert c["sentinel_left"] == 0 and c["nan_mismatch"] == 0 and c["max_viol"] <= 1.0, c
 
 
 def test_splitk_short_scratch_runs_unsplit(gpu):
