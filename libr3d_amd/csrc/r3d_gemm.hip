@@ -362,18 +362,20 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
     /* one launch of the tile kernel of geometry g over g.tiles x ukc units (ukc = 1: the
      * whole K walk into bf16 Y; else chunks of ucst steps into the f32 planes at pp) */
     auto tiles_launch = [&](const PrefillGeom& g, int ukc, int ucst, float* pp) -> hipError_t {
-        const dim3 grid((unsigned)(g.tiles * ukc)), block(512);
-#define R3D_PF_L(MODE_, WNF_, WMF_) PrefillLayout<WNF_, WMF_, 3, MODE_ == PF_F8 ? 2 : 1>
-#define R3D_PF(MODE_, WNF_, WMF_)                                                          \
-    static_assert(R3D_PF_L(MODE_, WNF_, WMF_)::LDS ==                                      \
-                      3 * prefill_stage_bytes(WNF_, WMF_, MODE_ == PF_F8 ? 2 : 1),          \
+        const dim3 grid((unsigned)(g.tiles * ukc)), block((unsigned)(64 * g.wv));
+#define R3D_PF_L(MODE_, WNF_, WMF_, WV_) PrefillLayout<WNF_, WMF_, 3, MODE_ == PF_F8 ? 2 : 1, WV_>
+#define R3D_PFW(MODE_, WNF_, WMF_, WV_)                                                    \
+    static_assert(R3D_PF_L(MODE_, WNF_, WMF_, WV_)::LDS ==                                 \
+                      3 * prefill_stage_bytes(WNF_, WMF_, MODE_ == PF_F8 ? 2 : 1, WV_),     \
                   "host and kernel ring sizes differ");                                    \
-    if ((int)R3D_PF_L(MODE_, WNF_, WMF_)::LDS != g.lds) return hipErrorInvalidValue;        \
-    hipLaunchKernelGGL((prefill_kernel<MODE_, WNF_, WMF_>), grid, block,                    \
-                       (size_t)(R3D_PF_L(MODE_, WNF_, WMF_)::LDS),                          \
+    if ((int)R3D_PF_L(MODE_, WNF_, WMF_, WV_)::LDS != g.lds || g.wv != WV_)                 \
+        return hipErrorInvalidValue;                                                        \
+    hipLaunchKernelGGL((prefill_kernel<MODE_, WNF_, WMF_, WV_>), grid, block,               \
+                       (size_t)(R3D_PF_L(MODE_, WNF_, WMF_, WV_)::LDS),                     \
                        stream, A, AS, P.B, (const uint8_t*)P.BS, P.Y, (int)P.M, (int)P.N,  \
                        g.steps, (int)g.grid_m, (int)g.tiles, P.rblk, a_pitch, as_pitch,     \
                        P.b_pitch, P.bs_pitch, P.y_pitch, ukc, ucst, pp)
+#define R3D_PF(MODE_, WNF_, WMF_) R3D_PFW(MODE_, WNF_, WMF_, 8)
         if (mode == PF_MX8) {
             switch (g.wnf) {
                 case 8: R3D_PF(PF_MX8, 8, 4); break;
@@ -384,6 +386,8 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
         } else if (mode == PF_F8) {
             if (g.wmf == 1) {
                 R3D_PF(PF_F8, 4, 1);                    /* split K up to 64 tokens */
+            } else if (g.wv == 4) {
+                R3D_PFW(PF_F8, 4, 8, 4);                /* 128 x 256, one wave a SIMD */
             } else {
                 R3D_PF(PF_F8, 4, 2);
             }
@@ -400,6 +404,7 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
             }
         }
 #undef R3D_PF
+#undef R3D_PFW
 #undef R3D_PF_L
         return hipGetLastError();
     };
@@ -428,8 +433,10 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
     const hipError_t e = tiles_launch(g, 1, g.steps, nullptr);
     if (e != hipSuccess) return launch_failed("prefill", e);
     debug_once(mode == PF_MX8 ? "mxfp4a16 prefill (mxfp8 quantiser + MFMA)"
-               : mode == PF_F8 ? "fp8a8 prefill" : "mxfp4a8 prefill",
-               160 + 8 * mode + g.wnf);
+               : mode == PF_F8 ? (g.wv == 4 ? "fp8a8 prefill, 128 x 256 on four waves"
+                                            : "fp8a8 prefill")
+               : "mxfp4a8 prefill",
+               160 + 8 * mode + g.wnf + (g.wv == 4 ? 4 : 0));
     return RAD_OK;
 }
 

@@ -454,6 +454,16 @@ bool lines_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, 
  * 32 wnf weight rows.  Workgroups run one per CU, so the launch
  * takes ceil(tiles / ncu) rounds; a round costs about wnf + 1/2 fragment-steps (the
  * fixed activation reads of a step).  The cheapest total wins, ties to the larger tile. */
+/* R3D_GFX950_F8_TILE: "128" keeps the e4m3 prefill on the 128 x 128 tile at every M,
+ * "256" takes the 128 x 256 tile at every M past 128 (default: by round cost) */
+static int f8_tile_lever() {
+    static const int v = [] {
+        const char* e = getenv("R3D_GFX950_F8_TILE");
+        return e && strcmp(e, "128") == 0 ? 128 : e && strcmp(e, "256") == 0 ? 256 : 0;
+    }();
+    return v;
+}
+
 void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeom* g) {
     /* e4m3 weights: two 8-register operand sets, the row scales and two f32 result sets per
      * fragment hold the tile at 4 fragment pairs (at 6, 185 registers spill) */
@@ -478,13 +488,28 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
     g->wnf = best;
     g->wmf = wmw;
     g->nst = 3;
-    g->bn = 32 * best;
-    g->bm = 64 * wmw;
+    g->wv = 8;
+    /* e4m3 weights past 128 tokens: four waves (one a SIMD, 512 registers each) hold a
+     * 128 x 256 tile -- a quarter fewer bytes per MFMA than the 128 x 128 tile.  A round of
+     * those tiles takes 1.71x a round of 128 x 128 tiles (config 3's shape: 387 us over 6
+     * rounds against 416 over 11), so it runs where its rounds cost less. */
+    if (mode == PF_F8 && M > 128 && f8_tile_lever() != 128) {
+        const int64_t rn = (N + 127) / 128;
+        const int64_t r8 = (rn * ((M + 127) / 128) + ncu - 1) / ncu;
+        const int64_t r4 = (rn * ((M + 255) / 256) + ncu - 1) / ncu;
+        if (f8_tile_lever() == 256 || 171 * r4 < 100 * r8) {
+            g->wnf = 4;
+            g->wmf = 8;
+            g->wv = 4;
+        }
+    }
+    g->bn = 32 * g->wnf;
+    g->bm = 8 * g->wv * g->wmf;
     g->grid_m = (M + g->bm - 1) / g->bm;
     g->grid_n = (N + g->bn - 1) / g->bn;
     g->tiles = g->grid_m * g->grid_n;
     g->steps = (int)(K / 128);
-    g->lds = g->nst * prefill_stage_bytes(g->wnf, g->wmf, mode == PF_F8 ? 2 : 1);
+    g->lds = g->nst * prefill_stage_bytes(g->wnf, g->wmf, mode == PF_F8 ? 2 : 1, g->wv);
 }
 
 int skinny_passes(int enc, int64_t M, int64_t N, int ncu) {
@@ -528,6 +553,7 @@ int tile_splitk(int enc, int64_t M, int64_t N, int64_t K, int ncu, int* cst, Pre
         g->wnf = wnf;
         g->wmf = wmf;
         g->nst = 3;
+        g->wv = 8;
         g->bn = (int)bn;
         g->bm = 64 * wmf;
         g->grid_m = 1;
@@ -1251,9 +1277,9 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
         PrefillGeom g{};
         prefill_geom(P.M, P.N, P.K, mode, 256, &g);
         snprintf(buf, (size_t)len,
-                 "arm=prefill enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d grid=%lldx%lld "
+                 "arm=prefill enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d waves=%d grid=%lldx%lld "
                  "tiles=%lld nst=%d lds=%d steps=%d rblk=%d",
-                 ename, (long long)P.M, (long long)P.N, (long long)P.K, g.bn, g.bm,
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K, g.bn, g.bm, g.wv,
                  (long long)g.grid_n, (long long)g.grid_m, (long long)g.tiles, g.nst, g.lds,
                  g.steps, P.rblk);
     }

@@ -92,6 +92,7 @@ struct LinesGeom {
  * a workgroup of 8 waves (2 x 4) owns bn = 32 wnf weight rows x bm = 64 wmf tokens. */
 struct PrefillGeom {
     int wnf, wmf, nst;       /* 16-row fragments per wave along N / M; ring depth */
+    int wv;                  /* waves per workgroup: 8, or 4 (one a SIMD) */
     int bn, bm;
     int64_t grid_m, grid_n, tiles;
     int steps;               /* K / 128 */

@@ -57,8 +57,8 @@ __device__ __forceinline__ void r3d_mfma_mx_inplace(r3d_f32x4& acc, r3d_i32x4 a,
         : "v"(a), "v"(b), "v"(sa), "v"(sb));
 }
 
-template <int MODE, int WNF, int WMW>
-__global__ __launch_bounds__(512) void prefill_kernel(
+template <int MODE, int WNF, int WMW, int WV = 8>
+__global__ __launch_bounds__(64 * WV) void prefill_kernel(
     const uint8_t* __restrict__ A, const void* __restrict__ ASv,
     const uint8_t* __restrict__ B, const uint8_t* __restrict__ BS,
     uint16_t* __restrict__ Y,
@@ -68,11 +68,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     constexpr bool F8 = MODE == PF_F8;                   /* e4m3 weights, bf16 row scales */
     constexpr int WH = F8 ? 2 : 1;                        /* 1 KB images per weight fragment */
     constexpr int WB = 64 * WH;                           /* weight bytes per row per step */
-    using L = PrefillLayout<WNF, WMW, 3, WH>;
+    using L = PrefillLayout<WNF, WMW, 3, WH, WV>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     /* 0 .. 7 */
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     /* 0 .. WV-1 */
     const int li = lane & 15, q = lane >> 4;
 
     /* The grid is tiles x kc units: unit u is K chunk u / tiles (steps [cst c, cst c + cst)
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
      * for 4 x 8; measured 1-1.5 % faster). */
     /* the split runs on the tiles of up to 128 tokens of the flushed modes only; the other
      * instantiations compile it out (it costs them registers) and take kc = 1 */
-    constexpr bool KS = MODE != PF_MX8 && WMW <= 2;
+    constexpr bool KS = MODE != PF_MX8 && WMW <= 2 && WV == 8;
     const int bid = blockIdx.x;
     const int units = KS ? tiles * kc : tiles;
     const int per = units >> 3, rem = units & 7, x = bid & 7;
@@ -114,9 +114,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     const int64_t wk = WB * s0, ak = 128 * s0, wsk = (F8 ? 2 : 4) * s0, ask = 4 * s0;
     const __amdgpu_buffer_rsrc_t rB = r3d_rsrc(B + n0 * b_pitch + wk, (N - n0) * b_pitch - wk);
     const __amdgpu_buffer_rsrc_t rA = r3d_rsrc(A + m0 * a_pitch + ak, (M - m0) * a_pitch - ak);
-    /* scales: waves 0-3 fetch the weight rows' scales (E8M0 dwords; e4m3 weights: the bf16
-     * of the row's scale row n / rblk), waves 4-7 the tokens' */
-    const bool wsc = wave < 4;
+    /* scales: at 8 waves, waves 0-3 fetch the weight rows' scales (E8M0 dwords; e4m3
+     * weights: the bf16 of the row's scale row n / rblk), waves 4-7 the tokens'; at 4 waves
+     * every wave fetches 64 of each (wsc: this wave's first scale load is the weights') */
+    const bool wsc = WV == 4 || wave < 4;
     const int64_t sr0 = F8 ? n0 / rblk : n0;             /* first scale row of the tile */
     const int64_t srn = F8 ? (N - 1) / rblk + 1 : N;     /* scale rows */
     const int64_t ws_pitch = F8 ? 2 * bs_pitch : bs_pitch;    /* bytes */
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
 #pragma unroll
     for (int i = 0; i < L::WLD; ++i) {
         /* image j: fragment j / WH, 64-byte half j % WH (e4m3 rows are two halves) */
-        const int j = wave + 8 * i;
+        const int j = wave + WV * i;
         const int jr = j < WH * L::WFR ? j : WH * L::WFR - 1;    /* pad slots reload the last */
         int64_t n = n0 + 16 * (jr / WH) + lr;
         if (n > N - 1) n = N - 1;
@@ -155,10 +156,22 @@ __global__ __launch_bounds__(512) void prefill_kernel(
         }
     }
     const int sxdst = (wsc ? L::S : L::AS) + 256 * (wave & 3);
+    /* 4 waves: the tokens' scales are each wave's second scale load */
+    const __amdgpu_buffer_rsrc_t rSA =
+        r3d_rsrc(reinterpret_cast<const uint8_t*>(ASv) + m0 * xs_pitch + ask,
+                 (M - m0) * xs_pitch - ask);
+    uint32_t saoff;
+    {
+        const int r0 = 64 * (wave & 3) + lane;
+        int64_t m = m0 + (r0 < L::BM ? r0 : L::BM - 1);
+        if (m > M - 1) m = M - 1;
+        saoff = (uint32_t)((m - m0) * xs_pitch);
+    }
+    const int sadst = L::AS + 256 * (wave & 3);
     uint32_t aoff[L::ALD];
 #pragma unroll
     for (int i = 0; i < L::ALD; ++i) {
-        const int j = wave + 8 * i;                          /* fragment j/2, half j%2 */
+        const int j = wave + WV * i;                         /* fragment j/2, half j%2 */
         int64_t m = m0 + 16 * (j >> 1) + lr;
         if (m > M - 1) m = M - 1;
         aoff[i] = (uint32_t)((m - m0) * a_pitch + 64 * (j & 1) + 16 * lc);
@@ -166,14 +179,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(
     /* load k (0 .. LOADS-1) of stage s into ring slot st */
     auto load = [&](int k, int s, uint8_t* st) __attribute__((always_inline)) {
         if (k < L::WLD)
-            r3d_buf_lds<16>(rB, st + L::W + 1024 * (wave + 8 * k), woff[k], WB * s);
+            r3d_buf_lds<16>(rB, st + L::W + 1024 * (wave + WV * k), woff[k], WB * s);
         else if (k == L::WLD && F8 && wsc)
             r3d_buf_lds<2>(rSX, st + sxdst, sxoff, 2 * s);        /* one bf16 per weight row */
         else if (k == L::WLD)
             r3d_buf_lds<4>(rSX, st + sxdst, sxoff, 4 * s);
+        else if (WV == 4 && k == L::WLD + 1)
+            r3d_buf_lds<4>(rSA, st + sadst, saoff, 4 * s);        /* the tokens' scales */
         else
-            r3d_buf_lds<16>(rA, st + L::A + 1024 * (wave + 8 * (k - L::WLD - 1)),
-                            aoff[k - L::WLD - 1], 128 * s);
+            r3d_buf_lds<16>(rA, st + L::A + 1024 * (wave + WV * (k - L::WLD - L::SLD)),
+                            aoff[k - L::WLD - L::SLD], 128 * s);
     };
     /* a stage's loads go out in WMW parts, one per fragment group, so the load issue
      * never stalls a wave for a whole stage at once */
@@ -292,7 +307,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
             sprev = af[slot];        /* this group's scale, kept past the slot's refill */
         }
     };
-    /* Flushed modes (PF_A8, PF_F8) with four token fragments per wave: ONE weight operand
+    /* Flushed modes (PF_A8, PF_F8) with four (or eight) token fragments per wave: ONE weight operand
      * set -- fragment ni of step s + 1 is read into it right after the last group's MFMA on
      * fragment ni of step s, WNF MFMAs before its first use -- and the MFMA results in a
      * ring of RR, each flushed LAG MFMAs after its issue (past the result latency), so the
@@ -300,7 +315,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(
      * The flush of MFMA t (index mi * WNF + ni in the step) uses its group's a_scale: the
      * current group's, or sprev for the group before (the previous step's last group at
      * mi = 0), and at e4m3 weights the row scales of its step's set. */
-    constexpr bool SS = MODE != PF_MX8 && WMW == 4;
+    constexpr bool SS = MODE != PF_MX8 && (WMW == 4 || WMW == 8);
     constexpr int RR = 4, LAG = RR - 1;
     static_assert(!SS || ((WMW * WNF) % RR == 0 && LAG < WNF), "result ring period");
     r3d_f32x4 dqr[RR];

@@ -617,7 +617,7 @@ def test_prefill_tile_choice_fills_the_last_round():
     assert (g["arm"], g["bn"], g["bm"], g["tiles"], g["steps"]) == ("prefill", "224", "256", "768", "42")
     assert int(g["lds"]) <= 160 * 1024
     # the f32-a_scale mode takes the same tile at config 3, 128-token tiles up to 128
-    # tokens; e4m3 weights run 128 x 128
+    # tokens; e4m3 weights run 128 x 256 on four waves past 128 tokens, 128 x 128 up to it
     ops, _ = _mx_ops(M=2048, N=21504, K=5376)
     g = _geom(R.describe("gemm_nt_q_mxfp4", ops)[1])
     assert (g["bn"], g["bm"], g["tiles"]) == ("224", "256", "768")
@@ -626,7 +626,16 @@ def test_prefill_tile_choice_fills_the_last_round():
     assert (g["bn"], g["bm"]) == ("128", "128")
     ops, _ = _f8_ops(M=2048, N=21504, K=5376)
     g = _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])
-    assert (g["arm"], g["bn"], g["bm"]) == ("prefill", "128", "128")
+    assert (g["arm"], g["bn"], g["bm"], g["waves"], g["tiles"]) == ("prefill", "128", "256", "4", "1344")
+    assert int(g["lds"]) <= 160 * 1024
+    ops, _ = _f8_ops(M=128, N=21504, K=5376)
+    g = _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])
+    assert (g["arm"], g["bn"], g["bm"], g["waves"]) == ("prefill", "128", "128", "8")
+    # the wider tile only where its rounds (1.71x as long) cost less: 3 of 128 x 128 at
+    # M = 512 against 2 of 128 x 256
+    ops, _ = _f8_ops(M=512, N=21504, K=5376)
+    g = _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])
+    assert (g["bn"], g["bm"], g["waves"]) == ("128", "128", "8")
     # few tiles: the narrowest tile spreads the work over more CUs
     ops, _ = _mx_ops(M=256, N=4096, K=1024)
     g = _geom(R.describe("gemm_nt_q_mxfp4", ops)[1])

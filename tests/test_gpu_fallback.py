@@ -5,7 +5,8 @@ host with the test lever R3D_GFX950_FAIL_ARM, which makes the named arms report 
 failure without launching anything; each setting runs in a child process (the lever is
 read once per process), whose calls must still succeed, log the failure, and match the
 oracle within the bar of tests/test_gpu_gemm.py.  The same child runs the tile rows' K split
-with each of its two kernels (R3D_GFX950_SPLITK_KERNEL) against the same bar."""
+with each of its two kernels (R3D_GFX950_SPLITK_KERNEL), and the e4m3 prefill on its
+four-wave tile (R3D_GFX950_F8_TILE), against the same bar."""
 import json
 import os
 import subprocess
@@ -85,6 +86,12 @@ def test_failed_arm_falls_back(gpu, arms, cases, logged):
       ("gemm_nt_q_fp8a8", "fp8a8", 33, 700, 2688, "hook")], "split-K prefill"),
     ({}, [(MX_TILE, "mxfp4a8", 40, 1000, 2048, "hook"),
           ("gemm_nt_q_fp8a8", "fp8a8", 33, 700, 2688, "hook")], "split-K skinny GEMV"),
+    # the e4m3 prefill's 128 x 256 four-wave tile forced at shapes its cost rule leaves to
+    # the 128 x 128 one: ragged tokens and weight rows, one and several steps, both sides
+    # of a 256-token tile
+    ({"R3D_GFX950_F8_TILE": "256"},
+     [("gemm_nt_q_fp8a8", "fp8a8", 300, 1000, 1024), ("gemm_nt_q_fp8a8", "fp8a8", 129, 130, 128),
+      ("gemm_nt_q_fp8a8", "fp8a8", 513, 388, 2688)], "fp8a8 prefill, 128 x 256 on four waves"),
 ])
 def test_split_kernel_lever(gpu, env, cases, kernel):
     env = dict(os.environ, R3D_DEBUG_GEMM="1", **env)
