@@ -361,7 +361,8 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
         return RAD_E_UNSUPPORTED;
     /* one launch of the tile kernel of geometry g over g.tiles x ukc units (ukc = 1: the
      * whole K walk into bf16 Y; else chunks of ucst steps into the f32 planes at pp) */
-    auto tiles_launch = [&](const PrefillGeom& g, int ukc, int ucst, float* pp) -> hipError_t {
+    auto tiles_launch = [&](const PrefillGeom& g, int ukc, int ucst, float* pp,
+                            const GemmPlan& Q) -> hipError_t {
         const dim3 grid((unsigned)(g.tiles * ukc)), block((unsigned)(64 * g.wv));
 #define R3D_PF_L(MODE_, WNF_, WMF_, WV_) PrefillLayout<WNF_, WMF_, 3, MODE_ == PF_F8 ? 2 : 1, WV_>
 #define R3D_PFW(MODE_, WNF_, WMF_, WV_)                                                    \
@@ -372,9 +373,9 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
         return hipErrorInvalidValue;                                                        \
     hipLaunchKernelGGL((prefill_kernel<MODE_, WNF_, WMF_, WV_>), grid, block,               \
                        (size_t)(R3D_PF_L(MODE_, WNF_, WMF_, WV_)::LDS),                     \
-                       stream, A, AS, P.B, (const uint8_t*)P.BS, P.Y, (int)P.M, (int)P.N,  \
-                       g.steps, (int)g.grid_m, (int)g.tiles, P.rblk, a_pitch, as_pitch,     \
-                       P.b_pitch, P.bs_pitch, P.y_pitch, ukc, ucst, pp)
+                       stream, A, AS, Q.B, (const uint8_t*)Q.BS, Q.Y, (int)Q.M, (int)Q.N,  \
+                       g.steps, (int)g.grid_m, (int)g.tiles, Q.rblk, a_pitch, as_pitch,     \
+                       Q.b_pitch, Q.bs_pitch, Q.y_pitch, ukc, ucst, pp)
 #define R3D_PF(MODE_, WNF_, WMF_) R3D_PFW(MODE_, WNF_, WMF_, 8)
         if (mode == PF_MX8) {
             switch (g.wnf) {
@@ -418,7 +419,8 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
         hipError_t e = hipSuccess;
         if (forced_fail("splitk")) {
             launch_failed("split-K prefill", hipSuccess);
-        } else if ((e = tiles_launch(gs, kc, cst, reinterpret_cast<float*>(part))) != hipSuccess) {
+        } else if ((e = tiles_launch(gs, kc, cst, reinterpret_cast<float*>(part), P)) !=
+                   hipSuccess) {
             launch_failed("split-K prefill", e);
         } else if ((e = splitk_reduce(P, kc, reinterpret_cast<const float*>(part), stream)) !=
                    hipSuccess) {
@@ -430,7 +432,30 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
         }
         /* a failed split: the whole K walk below recomputes every element of Y */
     }
-    const hipError_t e = tiles_launch(g, 1, g.steps, nullptr);
+    /* e4m3 weights on the four-wave tile: whole rounds of it over the first n1 weight rows,
+     * the rest on the 128 x 128 tile (prefill_f8_split_n) */
+    if (mode == PF_F8 && g.wv == 4) {
+        const int64_t n1 = prefill_f8_split_n(P.M, P.N, cu_count());
+        PrefillGeom g1{}, g2{};
+        if (n1 > 0) {
+            prefill_geom(P.M, n1, P.K, mode, cu_count(), &g1);
+            prefill_geom(P.M, P.N - n1, P.K, mode, cu_count(), &g2);
+        }
+        if (n1 > 0 && n1 % 128 == 0 && g1.wv == 4 && g2.wv == 8) {
+            GemmPlan P1 = P, P2 = P;
+            P1.N = n1;
+            P2.N = P.N - n1;
+            P2.B = P.B + n1 * P.b_pitch;
+            P2.BS = reinterpret_cast<const uint16_t*>(P.BS) + (n1 / P.rblk) * P.bs_pitch;
+            P2.Y = P.Y + n1;
+            hipError_t e = tiles_launch(g1, 1, g1.steps, nullptr, P1);
+            if (e == hipSuccess) e = tiles_launch(g2, 1, g2.steps, nullptr, P2);
+            if (e != hipSuccess) return launch_failed("prefill", e);
+            debug_once("fp8a8 prefill, 128 x 256 on four waves plus a 128 x 128 remainder", 190);
+            return RAD_OK;
+        }
+    }
+    const hipError_t e = tiles_launch(g, 1, g.steps, nullptr, P);
     if (e != hipSuccess) return launch_failed("prefill", e);
     debug_once(mode == PF_MX8 ? "mxfp4a16 prefill (mxfp8 quantiser + MFMA)"
                : mode == PF_F8 ? (g.wv == 4 ? "fp8a8 prefill, 128 x 256 on four waves"

@@ -496,8 +496,13 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
     if (mode == PF_F8 && M > 128 && f8_tile_lever() != 128) {
         const int64_t rn = (N + 127) / 128;
         const int64_t r8 = (rn * ((M + 127) / 128) + ncu - 1) / ncu;
-        const int64_t r4 = (rn * ((M + 255) / 256) + ncu - 1) / ncu;
-        if (f8_tile_lever() == 256 || 171 * r4 < 100 * r8) {
+        int64_t c4 = 171 * ((rn * ((M + 255) / 256) + ncu - 1) / ncu);
+        if (const int64_t n1 = prefill_f8_split_n(M, N, ncu)) {   /* whole rounds + remainder */
+            const int64_t r1 = ((n1 / 128) * ((M + 255) / 256) + ncu - 1) / ncu;
+            const int64_t r2 = (((N - n1 + 127) / 128) * ((M + 127) / 128) + ncu - 1) / ncu;
+            c4 = 171 * r1 + 100 * r2;
+        }
+        if (f8_tile_lever() == 256 || c4 < 100 * r8) {
             g->wnf = 4;
             g->wmf = 8;
             g->wv = 4;
@@ -510,6 +515,21 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
     g->tiles = g->grid_m * g->grid_n;
     g->steps = (int)(K / 128);
     g->lds = g->nst * prefill_stage_bytes(g->wnf, g->wmf, mode == PF_F8 ? 2 : 1, g->wv);
+}
+
+int64_t prefill_f8_split_n(int64_t M, int64_t N, int ncu) {
+    if (ncu <= 0) ncu = 256;
+    if (M <= 128 || N <= 128) return 0;
+    const int64_t rn = (N + 127) / 128, mt = (M + 255) / 256;
+    const int64_t tiles = rn * mt;
+    const int64_t whole = tiles / ncu;                  /* whole rounds of the wide tile */
+    if (whole < 1 || tiles % ncu == 0) return 0;
+    const int64_t n1t = whole * ncu / mt;               /* weight tiles inside them */
+    if (n1t < 1 || n1t >= rn) return 0;
+    const int64_t t2 = ((N - 128 * n1t + 127) / 128) * ((M + 127) / 128);
+    const int64_t r1 = (n1t * mt + ncu - 1) / ncu, r2 = (t2 + ncu - 1) / ncu;
+    const int64_t rall = (tiles + ncu - 1) / ncu;
+    return 171 * r1 + 100 * r2 < 171 * rall ? 128 * n1t : 0;
 }
 
 int skinny_passes(int enc, int64_t M, int64_t N, int ncu) {
@@ -1278,10 +1298,11 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
         prefill_geom(P.M, P.N, P.K, mode, 256, &g);
         snprintf(buf, (size_t)len,
                  "arm=prefill enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d waves=%d grid=%lldx%lld "
-                 "tiles=%lld nst=%d lds=%d steps=%d rblk=%d",
+                 "tiles=%lld nst=%d lds=%d steps=%d rblk=%d nsplit=%lld",
                  ename, (long long)P.M, (long long)P.N, (long long)P.K, g.bn, g.bm, g.wv,
                  (long long)g.grid_n, (long long)g.grid_m, (long long)g.tiles, g.nst, g.lds,
-                 g.steps, P.rblk);
+                 g.steps, P.rblk,
+                 (long long)(mode == PF_F8 && g.wv == 4 ? prefill_f8_split_n(P.M, P.N, 256) : 0));
     }
     return RAD_OK;
 }

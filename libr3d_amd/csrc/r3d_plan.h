@@ -153,6 +153,12 @@ void prefill_geom(int64_t M, int64_t N, int64_t K, int mode, int ncu, PrefillGeo
  * R3D_GFX950_SKINNY=0 / 1 turns the passes off / on for every skinny shape. */
 int skinny_passes(int enc, int64_t M, int64_t N, int ncu);
 
+/* The e4m3 prefill on its four-wave 128 x 256 tile when the tile count leaves the last round
+ * part full: weight rows [0, n1) run as whole rounds of that tile and [n1, N) as a second
+ * launch on the 128 x 128 tile, where that costs less (a round of the four-wave tile counts
+ * 1.71 rounds of the other).  Returns n1 (a multiple of 128), or 0 for one launch over N. */
+int64_t prefill_f8_split_n(int64_t M, int64_t N, int ncu);
+
 /* The skinny-band GEMV (gemv_wide_kernel, r3d_gemv_wide.h): 8 waves of tw 16-row weight
  * tiles (256 rows a workgroup at tw = 2) x one K chunk of cg groups; depth d lines in each
  * wave's register ring (1: measured at least as fast as 2 and 4 on every config 2 shape at

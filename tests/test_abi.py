@@ -631,11 +631,28 @@ def test_prefill_tile_choice_fills_the_last_round():
     ops, _ = _f8_ops(M=128, N=21504, K=5376)
     g = _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])
     assert (g["arm"], g["bn"], g["bm"], g["waves"]) == ("prefill", "128", "128", "8")
-    # the wider tile only where its rounds (1.71x as long) cost less: 3 of 128 x 128 at
-    # M = 512 against 2 of 128 x 256
-    ops, _ = _f8_ops(M=512, N=21504, K=5376)
+    # the wider tile only where its rounds (1.71x as long) cost less: one round of either
+    # at M = 256, N = 4096
+    ops, _ = _f8_ops(M=256, N=4096, K=1024)
     g = _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])
     assert (g["bn"], g["bm"], g["waves"]) == ("128", "128", "8")
+    # at M = 512, N = 21504: 3 rounds of 128 x 128, against one round of 128 x 256 over the
+    # first 16384 weight rows and one of 128 x 128 over the rest (1.71 + 1)
+    ops, _ = _f8_ops(M=512, N=21504, K=5376)
+    g = _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])
+    assert (g["bn"], g["bm"], g["waves"], g["nsplit"]) == ("128", "256", "4", "16384")
+    # config 3's 1344 four-wave tiles are 5.25 rounds: the first 20480 weight rows run as 5
+    # whole rounds, the last 1024 as one launch of 128 x 128 tiles (5 x 1.71 + 1 < 6 x 1.71)
+    ops, _ = _f8_ops(M=2048, N=21504, K=5376)
+    assert _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])["nsplit"] == "20480"
+    # the remainder launch can make the four-wave tile pay where it alone would not:
+    # 260 tiles at M = 512, N = 16640 are 1 round + 4 tiles
+    ops, _ = _f8_ops(M=512, N=16640, K=1024)
+    g = _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])
+    assert (g["waves"], g["nsplit"]) == ("4", "16384"), g
+    ops, _ = _f8_ops(M=512, N=16384, K=1024)                  # 256 tiles: one whole round
+    g = _geom(R.describe("gemm_nt_q_fp8a8", ops)[1])
+    assert (g["waves"], g["nsplit"]) == ("4", "0"), g
     # few tiles: the narrowest tile spreads the work over more CUs
     ops, _ = _mx_ops(M=256, N=4096, K=1024)
     g = _geom(R.describe("gemm_nt_q_mxfp4", ops)[1])

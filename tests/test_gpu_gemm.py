@@ -324,6 +324,27 @@ def test_splitk_padded_views(gpu, row, dtype, M, N, K):
     assert c["sentinel_left"] == 0 and c["nan_mismatch"] == 0 and c["max_viol"] <= 1.0, c
 
 
+@pytest.mark.parametrize("rblk", [1, 128])
+def test_fp8_prefill_wide_tile_with_remainder(gpu, rblk):
+    """The e4m3 prefill's four-wave 128 x 256 tile over whole rounds of weight rows, and the
+    remaining rows as a second launch on the 128 x 128 tile (both scale grids: the second
+    launch's weight-scale rows start n1 / rblk rows in)."""
+    M, N, K = 512, 16640, 1024
+    ops_desc = _f8_desc(M, N, K, rblk)
+    assert (ops_desc["waves"], ops_desc["nsplit"]) == ("4", "16384"), ops_desc
+    A, AS, B, BS = _f8_case(M, N, K, 77 + rblk, rblk)
+    _check(F8_TILE, "fp8a8", A, AS, B, BS, M, N, K, gpu, rblk=rblk)
+
+
+def _f8_desc(M, N, K, rblk):
+    import torch
+    rows = N if rblk == 1 else (N + 127) // 128
+    ts = [torch.zeros((M, K), dtype=torch.uint8), torch.zeros((M, K // 128), dtype=torch.float32),
+          torch.zeros((N, K), dtype=torch.uint8), torch.zeros((rows, K // 128), dtype=torch.int16)]
+    ops = R.GemmOperands(*ts, torch.zeros((M, N), dtype=torch.int16), dtype="fp8a8", N=N, K=K)
+    return _geom(R.describe(F8_TILE, ops)[1])
+
+
 def test_splitk_short_scratch_runs_unsplit(gpu):
     """A byte short of the hook's size: the launch takes the unsplit arm, leaves the
     scratch untouched (its poison and red zones intact) and still meets the bar."""
