@@ -3,8 +3,11 @@
     python -m libr3d_amd.build            # or: python libr3d_amd/build.py
 
 hipcc compiles the HIP kernels for --offload-arch=gfx950 with packed-fp32 code
-generation switched off; the host C++ (row table, plans) goes into the same shared
-object.  The oracle (oracle/Makefile) is test infrastructure and is built beside it.
+generation switched off and matrix-core results written to ordinary VGPRs
+(-amdgpu-mfma-vgpr-form: the kernels scale and add every MFMA result with VALU
+instructions, which read only VGPRs; with results in AGPRs each element first needs a
+v_accvgpr_read, a third of the e4m3 prefill tile's VALU work).  The host C++ (row table,
+plans) goes into the same shared object.  The oracle (oracle/Makefile) is test infrastructure and is built beside it.
 """
 import hashlib
 import os
@@ -23,6 +26,7 @@ SOURCES = ["r3d_gemm.hip", "r3d_logits.hip", "r3d_noalloc.hip", "r3d_plan.cpp", 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function",
     "-I" + os.path.join(ROOT, "include"), "-I" + CSRC,
 ]

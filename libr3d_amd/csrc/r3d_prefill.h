@@ -215,12 +215,28 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
     /* PF_F8: the e4m3 weight operands and, per fragment, the bf16 scales (4-byte slots) of
      * the lane's four result rows 4q .. 4q + 3; zero until the first step's are read, so
      * the first (empty) deferred flush multiplies zeros */
+    /* e4m3 weights on the single-operand-set walk (SS below) */
+    constexpr bool SSF = F8 && (WMW == 4 || WMW == 8);
     r3d_i32x8 wF[2][WNF];
     r3d_i32x4 sbF[2][WNF];
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int a = 0; a < WNF; ++a) sbF[b][a] = r3d_i32x4{0, 0, 0, 0};
+    /* the single-operand-set walk (SS below) holds the same bf16 scales two to a register:
+     * rows 4q, 4q + 1 in word 0 (low, high half), rows 4q + 2, 4q + 3 in word 1 */
+    uint32_t sbP[2][WNF][2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int a = 0; a < WNF; ++a) sbP[b][a][0] = sbP[b][a][1] = 0u;
+    auto pack_sb = [&](const uint8_t* src, int set, int ni) __attribute__((always_inline)) {
+        const r3d_i32x4 v = *reinterpret_cast<const r3d_i32x4*>(src);
+        /* bytes 0-1 of v[0] then bytes 0-1 of v[1] (v_perm_b32: selector bytes 0-3 pick
+         * the second source, 4-7 the first) */
+        sbP[set][ni][0] = __builtin_amdgcn_perm((uint32_t)v[1], (uint32_t)v[0], 0x05040100u);
+        sbP[set][ni][1] = __builtin_amdgcn_perm((uint32_t)v[3], (uint32_t)v[2], 0x05040100u);
+    };
     r3d_i32x8 ar[4];
     int ax[4];
     float af[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -244,7 +260,10 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
                 const r3d_i32x4 hi =
                     *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + 1024 + rd);
                 wF[set][ni] = r3d_i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                sbF[set][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::S + 4 * (16 * f + 4 * q));
+                if (SSF)
+                    pack_sb(st + L::S + 4 * (16 * f + 4 * q), set, ni);
+                else
+                    sbF[set][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::S + 4 * (16 * f + 4 * q));
             } else {
                 wS[set][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 1024 * f + rd);
                 xS[set][ni] = st[L::S + 4 * (16 * f + li) + q];
@@ -327,7 +346,7 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
             const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + rd);
             const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + 1024 + rd);
             wF[0][ni] = r3d_i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            sbF[sset][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::S + 4 * (16 * f + 4 * q));
+            pack_sb(st + L::S + 4 * (16 * f + 4 * q), sset, ni);
         } else {
             wS[0][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 1024 * f + rd);
             xS[0][ni] = st[L::S + 4 * (16 * f + li) + q];
@@ -342,9 +361,9 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             if (F8) {
-                const int sbi = before ? (set ? sbF[0][nf][i] : sbF[1][nf][i])
-                                       : (set ? sbF[1][nf][i] : sbF[0][nf][i]);
-                const float sb = __uint_as_float((uint32_t)sbi << 16);
+                const uint32_t pw = before ? (set ? sbP[0][nf][i >> 1] : sbP[1][nf][i >> 1])
+                                           : (set ? sbP[1][nf][i >> 1] : sbP[0][nf][i >> 1]);
+                const float sb = __uint_as_float((i & 1) ? (pw & 0xFFFF0000u) : (pw << 16));
                 acc[nf][mf][i] = acc[nf][mf][i] + (d[i] * sv) * sb;
             } else {
                 acc[nf][mf][i] = acc[nf][mf][i] + d[i] * sv;
