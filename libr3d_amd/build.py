@@ -43,10 +43,11 @@ def _run(cmd, cwd=None):
 
 
 def source_id():
-    """SHA-256 (hex) of every file under libr3d_amd/csrc and include, in name order, each
-    hashed as "<path relative to the repo root>\n<bytes>" -- the identity the library
-    reports through r3d_gfx950_build_id()."""
+    """SHA-256 (hex) of the compile flags, then of every file under libr3d_amd/csrc and
+    include, in name order, each hashed as "<path relative to the repo root>\n<bytes>" --
+    the identity the library reports through r3d_gfx950_build_id()."""
     h = hashlib.sha256()
+    h.update((" ".join(f for f in FLAGS if not f.startswith("-I")) + "\n").encode())
     files = []
     for d in (CSRC, os.path.join(ROOT, "include")):
         for name in os.listdir(d):
