@@ -119,27 +119,49 @@ int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a);
  * joined-planes blob (rad_planes.h: "codes" e4m3 [n_vocab, n_embd] dense, "scale" bf16 /
  * f16 / f32 per (1 or 128 rows, 128 columns)), f32 logits [M, n_vocab], M =
  * numel(logits) / n_vocab.  Replaces src/r3d_gemm_logits.hip:144-226
- * (r3d_rad_logits_gemm_e4m3).  The first launch over a blob in device memory reads its
- * header with one synchronous copy (cached per device and address); see
+ * (r3d_rad_logits_gemm_e4m3).  n_embd a multiple of 4 at any alignment of x, codes and
+ * scale (off a multiple of 16 or off 16-byte alignment: a slower dword walk).  The first
+ * launch over a blob in device memory reads its header and entries with a copy on the
+ * launch stream and waits for it (cached per device and address; refused with
+ * RAD_E_UNSUPPORTED under graph capture -- launch once first); see
  * r3d_gfx950_logits_head_forget. */
 int r3d_rad_logits_gemm_e4m3(const RadArgs* a, RadStream s);
 
-/* The joined head's byte layout, in host memory.  These replace the reference row's
- * layout hooks (src/r3d_gemm_logits.hip:233-272: r3d_layout_head / r3d_relayout_head /
- * r3d_unrelayout_head), which join radiance's encoded planes through its rad_planes
- * helpers; here the two planes are passed directly.
+/* The logits_gemm_e4m3 row's weight-layout hooks (host only).  Replace
+ * src/r3d_gemm_logits.hip:233-272 (r3d_layout_head / r3d_relayout_head /
+ * r3d_unrelayout_head, registered at src/r3d_rows.cpp:1598-1599).  They admit the head
+ * (operand 1) as an untransformed "affine" encoding whose selected planes are "codes"
+ * (tiled 1 x 1, e4m3, [n_vocab, n_embd]) then "scale" (tiled bf16 / f16 / f32, block
+ * (1 or 128) x 128, [ceil(n_vocab / block), ceil(n_embd / 128)]) with n_embd a multiple of
+ * 4 the launch can stage, and answer with the canonical rad.planes join (rad_planes.h):
+ * layout gives its tag and bytes, relayout writes it into host memory dst, unrelayout
+ * reads the planes back.  Any other operand: RAD_E_UNSUPPORTED (stored as is); any other
+ * head, a plain one without that encoding included: declined (RAD_E_DTYPE, or RAD_E_SHAPE
+ * for grids that disagree). */
+int r3d_layout_head(const RadParam* p, int n_p, int operand, const RadEncoding* enc,
+                    const int* sel, const RadTensor* planes, int n, RadLayout* out);
+int r3d_relayout_head(const RadParam* p, int n_p, int operand, const RadEncoding* enc,
+                      const int* sel, const RadTensor* planes, int n, void* dst,
+                      int64_t dst_bytes);
+int r3d_unrelayout_head(const RadParam* p, int n_p, int operand, const RadEncoding* enc,
+                        const int* sel, const void* src, int64_t src_bytes,
+                        const RadTensor* planes, int n);
+
+/* The same join for a caller holding the two planes directly, no counterpart in the
+ * reference (it is what r3d_relayout_head writes for the head's encoding), in host memory:
  *   _bytes: the blob's size for n_vocab x n_embd codes and a scale plane of scale_dtype
  *           (RAD_BF16 / RAD_F16 / RAD_F32) with scale_block_rows (1 or 128) rows per
  *           element, or a negative RAD_E_* code;
- *   _header: the same, and the header itself into *out (the planes go at its entries'
- *           offsets: a caller can stream them straight into device memory);
- *   _join:  writes header, codes (rows codes_pitch bytes apart) and scale (rows
+ *   _header: the same, and the blob's header and entries into *out (the planes go at the
+ *           entries' offsets: a caller can stream them straight into device memory);
+ *   _join:  writes header, entries, codes (rows codes_pitch bytes apart) and scale (rows
  *           scale_pitch_bytes apart, (n_embd + 127) / 128 elements each) into dst;
- *   _split: the inverse, into dense planes (either pointer may be null). */
+ *   _split: the inverse, into dense planes (either pointer may be null), after checking
+ *           each plane's dtype, grid, pitch and extent against the blob. */
 int64_t r3d_gfx950_logits_head_bytes(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,
                                      int64_t scale_block_rows);
 int64_t r3d_gfx950_logits_head_header(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,
-                                      int64_t scale_block_rows, RadPlanesHeader* out);
+                                      int64_t scale_block_rows, RadPlanesHead* out);
 int r3d_gfx950_logits_head_join(const uint8_t* codes, int64_t codes_pitch, const void* scale,
                                 int64_t scale_pitch_bytes, int64_t n_vocab, int64_t n_embd,
                                 uint32_t scale_dtype, int64_t scale_block_rows, void* dst,
@@ -165,7 +187,9 @@ int r3d_rad_gemm_nt_q_mxfp4a16_noalloc(const RadArgs* a, RadStream s);
 
 /* Host-only diagnostic with no counterpart in the reference: runs `row`'s preamble and
  * plan on `a` and writes the chosen arm and launch geometry (or the refusal) into buf.
- * Launches nothing, touches no device memory.  Returns the plan's status code. */
+ * Launches nothing and copies nothing from the device: a logits head's header is read in
+ * place when the blob is host-accessible, else taken from the copy an earlier launch
+ * cached (RAD_E_UNSUPPORTED when there is none).  Returns the plan's status code. */
 int r3d_gfx950_describe(const char* row, const RadArgs* a, char* buf, int len);
 
 /* Diagnostic with no counterpart in the reference: one stage of a gemm_nt_q_mxfp4a16 call
@@ -176,10 +200,11 @@ int r3d_gfx950_describe(const char* row, const RadArgs* a, char* buf, int len);
  * call would take the skinny band's decode passes (no quantiser stage there). */
 int r3d_gfx950_mxfp4a16_stage(const RadArgs* a, RadStream s, int stage);
 
-/* Build identity with no counterpart in the reference: the SHA-256 (hex) of the sources
- * this library was compiled from -- every file under libr3d_amd/csrc and include, in name
- * order, each as "<relative path>\n<bytes>" -- so a test harness can tell whether the
- * binary it loaded was built from the tree beside it. */
+/* Build identity with no counterpart in the reference: the SHA-256 (hex) of the compile
+ * flags and of the sources this library was compiled from -- the flags as one line, then
+ * every file under libr3d_amd/csrc and include, in name order, each as "<relative
+ * path>\n<bytes>" -- so a test harness can tell whether the binary it loaded was built
+ * from the tree beside it. */
 const char* r3d_gfx950_build_id(void);
 
 #ifdef __cplusplus

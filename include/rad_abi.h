@@ -17,6 +17,14 @@
  *                 (src/r3d_rows.cpp:1033-1036, 1601-1675).
  *   RadOpSchema   {op, params, n_params, operands, n_operands, prose}
  *                 (src/r3d_rows.cpp:793-850).
+ *   RadEncoding   {scheme, n_planes, transform[], plane[]}, RadEncPlane {role, kind,
+ *                 dtype, block[2]}, RadLayout {tag, ...} and the three weight-layout hook
+ *                 signatures, from the hooks' uses (src/r3d_gemm_logits.hip:233-272,
+ *                 src/r3d_gemm_w2a8.hip:1362-1436, src/r3d_rows.cpp:1353-1358): roles and
+ *                 the scheme are fixed-size strings compared with strncmp(.., RAD_ENC_STR),
+ *                 `transform[0]` non-zero means a rotated encoding, `kind` is
+ *                 RAD_PLANE_TILED for a plain element grid, and at declare time the plane
+ *                 tensors carry geometry with null data.
  * Enum VALUES and the array bound RAD_MAX_RANK are not recoverable from the reference
  * and are this header's own; the whole dependency is isolated here so the real v1.11.0
  * header can replace this file without touching any other source.
@@ -38,7 +46,8 @@ typedef void* RadStream;
 
 enum RadDtype {
     RAD_F32 = 0, RAD_BF16, RAD_F16, RAD_F8E4M3, RAD_F8E5M2, RAD_FP4E2M1, RAD_E8M0,
-    RAD_U8, RAD_I8, RAD_I16, RAD_I32, RAD_U32, RAD_I64, RAD_BOOL
+    RAD_U8, RAD_I8, RAD_I16, RAD_I32, RAD_U32, RAD_I64, RAD_BOOL,
+    RAD_U4, RAD_U2                        /* sub-byte code planes (src/r3d_gemm_w2a8.hip:1382,1388) */
 };
 
 /* Return codes: RAD_OK is zero, every refusal non-zero (entries test `if (rc)`). */
@@ -107,10 +116,50 @@ typedef struct RadTunable {
 
 enum RadDomain { RAD_DOMAIN_HOST = 0, RAD_DOMAIN_DEVICE = 1 };
 
+/* A weight's encoding as the engine declares it to a row's layout hooks. */
+#define RAD_ENC_STR 16
+#define RAD_ENC_MAX_PLANES 4
+
+enum RadPlaneKind { RAD_PLANE_TILED = 0 };   /* one element per block[0] x block[1] weights */
+
+typedef struct RadEncPlane {
+    char     role[RAD_ENC_STR];           /* "codes", "scale", "zero", ... NUL-padded */
+    uint32_t kind;                        /* RadPlaneKind */
+    uint32_t dtype;                       /* RadDtype of one element */
+    int64_t  block[2];                    /* weight rows x cols one element covers */
+} RadEncPlane;
+
+typedef struct RadEncoding {
+    char        scheme[RAD_ENC_STR];      /* "affine", ... */
+    int         n_planes;
+    uint32_t    transform[RAD_ENC_MAX_PLANES];   /* [0] non-zero: a rotated encoding */
+    RadEncPlane plane[RAD_ENC_MAX_PLANES];
+} RadEncoding;
+
+/* What a layout hook answers: the name of the device layout and the bytes its relayout
+ * writes. */
+typedef struct RadLayout {
+    const char* tag;
+    int64_t     bytes;
+} RadLayout;
+
 typedef int     (*RadInitFn)(void);
 typedef void    (*RadFiniFn)(void);
 typedef int     (*RadLaunchFn)(const RadArgs* a, RadStream s);
 typedef int64_t (*RadScratchFn)(const RadArgs* a);
+/* Weight-layout hooks, host only.  `operand` is the schema index of the weight, `sel[i]`
+ * the encoding plane that planes[i] holds.  layout: RAD_OK and *out, RAD_E_UNSUPPORTED for
+ * "store the operand as it is", any other code declines the row for this weight.
+ * relayout writes the device form into dst (host memory of dst_bytes); unrelayout reads
+ * it back into the planes. */
+typedef int (*RadLayoutFn)(const RadParam* p, int n_p, int operand, const RadEncoding* enc,
+                           const int* sel, const RadTensor* planes, int n, RadLayout* out);
+typedef int (*RadRelayoutFn)(const RadParam* p, int n_p, int operand, const RadEncoding* enc,
+                             const int* sel, const RadTensor* planes, int n, void* dst,
+                             int64_t dst_bytes);
+typedef int (*RadUnrelayoutFn)(const RadParam* p, int n_p, int operand,
+                               const RadEncoding* enc, const int* sel, const void* src,
+                               int64_t src_bytes, const RadTensor* planes, int n);
 
 typedef struct RadKernelInfo {
     const char*          name;
@@ -130,10 +179,10 @@ typedef struct RadKernelInfo {
     RadFiniFn            fini;
     RadLaunchFn          launch;
     RadScratchFn         scratch;
-    const void*          layout;          /* weight layout hooks: unused by these rows */
-    const void*          relayout;
-    const void*          opd_shape;
-    const void*          unrelayout;
+    RadLayoutFn          layout;          /* weight layout hooks (null: none) */
+    RadRelayoutFn        relayout;
+    const void*          opd_shape;       /* unused by these rows */
+    RadUnrelayoutFn      unrelayout;
 } RadKernelInfo;
 
 enum RadParamReq { RAD_REQUIRED = 0, RAD_OPTIONAL = 1, RAD_DERIVED = 2 };

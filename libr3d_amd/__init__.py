@@ -21,7 +21,9 @@ __all__ = [
     "launch_row", "gemm_nt_q", "describe", "GemmOperands", "QuantActOperands", "quant_act_fp8",
     "GatedQuantOperands", "GatedGemmOperands", "RmsNormQuantOperands", "build_id",
     "check_build_id", "mxfp4a16_stage", "LogitsOperands", "logits_gemm", "head_bytes",
-    "join_head", "split_head", "forget_head", "head_header",
+    "join_head", "split_head", "forget_head", "head_header", "RadEncoding", "RadEncPlane",
+    "RadLayout", "RadPlanesHeader", "RadPlanesEntry", "head_encoding", "layout_head",
+    "relayout_head", "unrelayout_head",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -33,7 +35,7 @@ RAD_OK, RAD_E_UNSUPPORTED, RAD_E_SHAPE, RAD_E_STRIDE, RAD_E_DTYPE, RAD_E_INVAL, 
 # enum RadDtype (include/rad_abi.h)
 DT = {name: i for i, name in enumerate(
     ["F32", "BF16", "F16", "F8E4M3", "F8E5M2", "FP4E2M1", "E8M0", "U8", "I8", "I16", "I32",
-     "U32", "I64", "BOOL"])}
+     "U32", "I64", "BOOL", "U4", "U2"])}
 RAD_P_INT, RAD_P_STR, RAD_P_F64 = 0, 1, 2
 RAD_C_EQ, RAD_C_LE, RAD_C_GE, RAD_C_DIV, RAD_C_IN = range(5)
 
@@ -80,6 +82,35 @@ class RadKernelInfo(ctypes.Structure):
                 ("scratch", ctypes.c_void_p), ("layout", ctypes.c_void_p),
                 ("relayout", ctypes.c_void_p), ("opd_shape", ctypes.c_void_p),
                 ("unrelayout", ctypes.c_void_p)]
+
+
+RAD_ENC_STR, RAD_ENC_MAX_PLANES, RAD_PLANE_TILED = 16, 4, 0
+
+
+class RadEncPlane(ctypes.Structure):
+    _fields_ = [("role", ctypes.c_char * RAD_ENC_STR), ("kind", ctypes.c_uint32),
+                ("dtype", ctypes.c_uint32), ("block", ctypes.c_int64 * 2)]
+
+
+class RadEncoding(ctypes.Structure):
+    _fields_ = [("scheme", ctypes.c_char * RAD_ENC_STR), ("n_planes", ctypes.c_int),
+                ("transform", ctypes.c_uint32 * RAD_ENC_MAX_PLANES),
+                ("plane", RadEncPlane * RAD_ENC_MAX_PLANES)]
+
+
+class RadLayout(ctypes.Structure):
+    _fields_ = [("tag", ctypes.c_char_p), ("bytes", ctypes.c_int64)]
+
+
+class RadPlanesHeader(ctypes.Structure):          # include/rad_planes.h
+    _fields_ = [("magic", ctypes.c_uint32), ("n_planes", ctypes.c_uint32),
+                ("transform", ctypes.c_uint32 * 4), ("bytes", ctypes.c_int64)]
+
+
+class RadPlanesEntry(ctypes.Structure):
+    _fields_ = [("role", ctypes.c_char * 16), ("dtype", ctypes.c_uint32), ("kind", ctypes.c_uint32),
+                ("block", ctypes.c_int64 * 2), ("rows", ctypes.c_int64), ("cols", ctypes.c_int64),
+                ("row_bytes", ctypes.c_int64), ("offset", ctypes.c_int64)]
 
 
 class RadParamSpec(ctypes.Structure):
@@ -147,6 +178,15 @@ def lib():
         L.r3d_gfx950_logits_head_split.restype = ctypes.c_int
         L.r3d_gfx950_logits_head_split.argtypes = [ctypes.c_void_p, _i64, ctypes.c_void_p,
                                                    ctypes.c_void_p]
+        _hook = [ctypes.POINTER(RadParam), ctypes.c_int, ctypes.c_int, ctypes.POINTER(RadEncoding),
+                 ctypes.POINTER(ctypes.c_int), ctypes.POINTER(RadTensor), ctypes.c_int]
+        L.r3d_layout_head.restype = ctypes.c_int
+        L.r3d_layout_head.argtypes = _hook + [ctypes.POINTER(RadLayout)]
+        L.r3d_relayout_head.restype = ctypes.c_int
+        L.r3d_relayout_head.argtypes = _hook + [ctypes.c_void_p, _i64]
+        L.r3d_unrelayout_head.restype = ctypes.c_int
+        L.r3d_unrelayout_head.argtypes = _hook[:5] + [ctypes.c_void_p, _i64,
+                                                       ctypes.POINTER(RadTensor), ctypes.c_int]
         L.r3d_gfx950_logits_head_forget.restype = None
         L.r3d_gfx950_logits_head_forget.argtypes = [ctypes.c_void_p]
         _LIB = L
@@ -190,7 +230,8 @@ def rows():
                  _s(k.constraints[c].sval)) for c in range(k.n_constraints)]
         out.append({"name": _s(k.name), "op": _s(k.op), "priority": k.priority,
                     "domain": k.domain, "constraints": cons, "launch": k.launch,
-                    "scratch": k.scratch})
+                    "scratch": k.scratch, "layout": k.layout, "relayout": k.relayout,
+                    "opd_shape": k.opd_shape, "unrelayout": k.unrelayout})
     return out
 
 
@@ -544,20 +585,22 @@ def head_bytes(n_vocab, n_embd, scale_dtype="bf16", scale_block_rows=1):
                                                   scale_block_rows))
 
 
-HEADER_BYTES = 328                          # sizeof(RadPlanesHeader)
+HEAD_BYTES = 320                  # sizeof(RadPlanesHead): the header, then 4 entries
+HEADER_BYTES = 32 + 2 * 72        # a two-plane blob's header and its two entries
 
 
 def head_header(n_vocab, n_embd, scale_dtype="bf16", scale_block_rows=1):
-    """(header uint8 [HEADER_BYTES], codes offset, scale offset, blob bytes) of a joined
-    head, so its planes can be written straight into device memory at those offsets."""
+    """(header and entries uint8 [HEADER_BYTES], codes offset, scale offset, blob bytes) of
+    a joined head, so its planes can be written straight into device memory at those
+    offsets."""
     import numpy as np
-    h = np.zeros(HEADER_BYTES, np.uint8)
+    h = np.zeros(HEAD_BYTES, np.uint8)
     nb = int(lib().r3d_gfx950_logits_head_header(n_vocab, n_embd, DT[_SCALE_DT[scale_dtype]],
                                                  scale_block_rows, h.ctypes.data))
     if nb < 0:
         raise ValueError("head refused (%d)" % nb)
-    e = h[40:].view(np.int64)          # entries from byte 40: 9 int64 each, offset last
-    return h, int(e[8]), int(e[17]), nb
+    e = h[32:].view(np.int64)          # entries from byte 32: 9 int64 each, offset last
+    return h[:HEADER_BYTES].copy(), int(e[8]), int(e[17]), nb
 
 
 def join_head(codes, scale, scale_dtype="bf16", scale_block_rows=1):
@@ -593,6 +636,81 @@ def split_head(blob, n_vocab, n_embd, scale_dtype="bf16", scale_block_rows=1):
     if rc != RAD_OK:
         raise ValueError("split refused (%d)" % rc)
     return codes, scale
+
+
+def head_encoding(scale_dtype="bf16", scale_block_rows=1, scheme="affine", roles=("codes", "scale"),
+                  code_dtype="F8E4M3", code_block=(1, 1), kinds=(RAD_PLANE_TILED, RAD_PLANE_TILED),
+                  transform0=0, n_planes=2):
+    """A RadEncoding of a joined lm_head as an engine would declare it (every field
+    overridable, so tests can hand the hooks what they must decline)."""
+    enc = RadEncoding()
+    enc.scheme = scheme.encode()
+    enc.n_planes = n_planes
+    enc.transform[0] = transform0
+    sdt = DT[_SCALE_DT.get(scale_dtype, scale_dtype)]
+    for i, (role, kind, dt, blk) in enumerate([
+            (roles[0], kinds[0], DT[code_dtype], code_block),
+            (roles[1], kinds[1], sdt, (scale_block_rows, 128))]):
+        enc.plane[i].role = role.encode()
+        enc.plane[i].kind = kind
+        enc.plane[i].dtype = dt
+        enc.plane[i].block[0], enc.plane[i].block[1] = blk
+    return enc
+
+
+def _head_hook_args(enc, codes, scale, sel, params):
+    """ctypes arguments shared by the three hooks: params, encoding, selection and the two
+    plane tensors (numpy arrays, (array, dtype name) pairs, or (shape, dtype name) pairs for
+    geometry only, as at declare time)."""
+    import numpy as np
+    ps = (RadParam * max(1, len(params)))()
+    keep = []
+    for i, (k, v) in enumerate(params):
+        kb = k.encode()
+        keep.append(kb)
+        ps[i].kind, ps[i].key, ps[i].ival = RAD_P_INT, kb, int(v)
+    ts = (RadTensor * 2)()
+    for i, (arr, dt) in enumerate([(codes, "F8E4M3"), (scale, None)]):
+        if isinstance(arr, tuple) and isinstance(arr[0], np.ndarray):
+            arr, dt = arr                      # (array, dtype name)
+        if isinstance(arr, tuple):
+            shape, dname = arr
+            data = None
+        else:
+            shape, data = arr.shape, arr.ctypes.data
+            dname = dt or {np.dtype(np.float32): "F32", np.dtype(np.uint16): "BF16"}[arr.dtype]
+        ts[i].data = data
+        ts[i].dtype = DT[dname]
+        ts[i].rank = len(shape)
+        for j, n in enumerate(shape):
+            ts[i].shape[j] = n
+        ts[i].stride[len(shape) - 1] = 1
+        if len(shape) == 2:
+            ts[i].stride[0] = shape[1]
+    sl = (ctypes.c_int * 2)(*sel)
+    return ps, len(params), enc, sl, ts, keep
+
+
+def layout_head(enc, codes, scale, operand=1, sel=(0, 1), params=(), n=2):
+    """r3d_layout_head: (status, tag, bytes)."""
+    ps, n_p, enc, sl, ts, keep = _head_hook_args(enc, codes, scale, sel, params)
+    out = RadLayout()
+    rc = lib().r3d_layout_head(ps, n_p, operand, ctypes.byref(enc), sl, ts, n, ctypes.byref(out))
+    return rc, (_s(out.tag) if out.tag else None), int(out.bytes)
+
+
+def relayout_head(enc, codes, scale, dst, operand=1, sel=(0, 1), params=()):
+    """r3d_relayout_head into the numpy uint8 buffer dst: the status."""
+    ps, n_p, enc, sl, ts, keep = _head_hook_args(enc, codes, scale, sel, params)
+    return lib().r3d_relayout_head(ps, n_p, operand, ctypes.byref(enc), sl, ts, 2,
+                                   dst.ctypes.data, dst.size)
+
+
+def unrelayout_head(enc, src, codes, scale, operand=1, sel=(0, 1), params=()):
+    """r3d_unrelayout_head from the numpy uint8 blob src into codes / scale: the status."""
+    ps, n_p, enc, sl, ts, keep = _head_hook_args(enc, codes, scale, sel, params)
+    return lib().r3d_unrelayout_head(ps, n_p, operand, ctypes.byref(enc), sl, src.ctypes.data,
+                                     src.size, ts, 2)
 
 
 def forget_head(lm_head):

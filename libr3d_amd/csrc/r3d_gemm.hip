@@ -17,6 +17,7 @@
 
 #include "r3d_band.h"
 #include "r3d_dump.h"
+#include "r3d_gemm_any.h"
 #include "r3d_gemm_kernels.h"
 #include "r3d_gemv_lines.h"
 #include "r3d_gemv_quad.h"
@@ -232,11 +233,48 @@ static int launch_wide_split(const GemmPlan& P, const WideGeom& w, int kc, float
     return RAD_OK;
 }
 
+/* The any-alignment GEMM (r3d_gemm_any.h) over A / AS as given: mode PF_A8 (e2m1 weights,
+ * e4m3 A + f32 a_scale), PF_F8 (e4m3 weights) or PF_MX8 (e2m1 weights, mxfp8 A). */
+static int launch_any(const GemmPlan& P, int mode, const uint8_t* A, const void* AS,
+                      int64_t a_pitch, int64_t as_pitch, hipStream_t stream) {
+    /* 32-bit lane offsets over one wave's 32 rows of every operand */
+    const int64_t lim = (int64_t)1 << 31;
+    const int64_t bsz = mode == PF_F8 ? 2 : 1, asz = mode == PF_MX8 ? 1 : 4;
+    if (32 * P.b_pitch >= lim || 32 * a_pitch >= lim || 32 * P.bs_pitch * bsz >= lim ||
+        32 * as_pitch * asz >= lim)
+        return RAD_E_UNSUPPORTED;
+    const int tm = P.M <= 16 ? 1 : 2;
+    const int64_t gx = (P.N + 127) / 128, gy = (P.M + 16 * tm - 1) / (16 * tm);
+    if (gx > 0x7FFFFFFF || gy > 65535) return RAD_E_SHAPE;
+    const dim3 grid((unsigned)gx, (unsigned)gy), block(256);
+#define R3D_ANY(MODE_, TM_)                                                                 \
+    hipLaunchKernelGGL((gemm_any_kernel<MODE_, TM_>), grid, block, 0, stream, A, AS, P.B,      \
+                       (const uint8_t*)P.BS, P.Y, (int)P.M, (int)P.N, (int)(P.K / 128),      \
+                       P.rblk, a_pitch, as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch)
+    if (mode == PF_F8) {
+        if (tm == 1) R3D_ANY(PF_F8, 1); else R3D_ANY(PF_F8, 2);
+    } else if (mode == PF_MX8) {
+        if (tm == 1) R3D_ANY(PF_MX8, 1); else R3D_ANY(PF_MX8, 2);
+    } else {
+        if (tm == 1) R3D_ANY(PF_A8, 1); else R3D_ANY(PF_A8, 2);
+    }
+#undef R3D_ANY
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return launch_failed("any-alignment GEMM", e);
+    debug_once(mode == PF_F8 ? "fp8a8 any-alignment GEMM"
+               : mode == PF_MX8 ? "mxfp4a16 any-alignment GEMM" : "mxfp4a8 any-alignment GEMM",
+               120 + 2 * mode + (tm - 1));
+    return RAD_OK;
+}
+
 /* The decode arms in order of preference -- quad GEMV (M <= 4), line GEMV (M = 5..16),
  * 16-row GEMV (any M <= 16) -- each taking the launch when the one before does not serve
  * the shape or fails to launch (a failed arm wrote nothing: the next one writes all of Y). */
 static int launch_decode(const GemmPlan& P, int64_t splitk, hipStream_t stream,
                          uint8_t* part = nullptr, int64_t part_bytes = 0) {
+    if (P.ua & UA_GEMM)
+        return launch_any(P, P.enc == ENC_FP8A8 ? PF_F8 : PF_A8, P.A, P.AS, P.a_pitch,
+                          P.as_pitch, stream);
     QuadGeom qg{};
     const bool quad = quad_fits(P) && quad_geom(P.enc, P.M, P.N, P.K, splitk, &qg, P.xq);
     /* launch scratch: the K split where it applies (decode_split_plan) */
@@ -298,18 +336,20 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
     PrefillGeom g{};
     prefill_geom(P.M, P.N, P.K, mode, cu_count(), &g);
     if (g.tiles > 0x7FFFFFFF || g.grid_m > 0x7FFFFFFF) return RAD_E_SHAPE;
+    if ((P.ua & UA_GEMM) && mode != PF_MX8)
+        return launch_any(P, mode, P.A, P.AS, P.a_pitch, P.as_pitch, stream);
     int cst = 0;
     PrefillGeom gs{};                                    /* the split's tile (kind 2) */
     WideGeom gw{};                                       /* or its GEMV (kind 1) */
     int kc = 0;
-    const int kind = part && ((uintptr_t)part & 15) == 0
+    const int kind = part && ((uintptr_t)part & 15) == 0 && !P.ua
                          ? splitk_plan(P.enc, P.M, P.N, P.K, cu_count(), &kc, &cst, &gs, &gw)
                          : 0;
     const bool split = kind != 0 && part_bytes >= (int64_t)kc * P.M * P.N * 4 &&
                        (kind == 1 || (gs.grid_m == 1 && gs.tiles * kc <= 0x7FFFFFFF));
     /* the skinny band on a narrow N: 16-row passes of the decode GEMVs (each output row is
      * the same arithmetic either way) */
-    if (const int passes = split ? 0 : skinny_passes(P.enc, P.M, P.N, cu_count())) {
+    if (const int passes = split || P.ua ? 0 : skinny_passes(P.enc, P.M, P.N, cu_count())) {
         GemmPlan S = P;
         S.M = 16;
         LinesGeom lg{};
@@ -340,10 +380,16 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
         uint8_t* SX = P.scratch + qbytes;
         const int64_t qblocks = P.M;                     /* one workgroup per row */
         if (qblocks > 0x7FFFFFFF) return RAD_E_SHAPE;
-        if (stage != 2)
-            hipLaunchKernelGGL(quant_mx8_kernel, dim3((unsigned)qblocks), dim3(256), 0, stream,
-                               reinterpret_cast<const uint16_t*>(P.A), P.a_pitch, Q, P.K, SX,
-                               P.K / 32, P.M, (int)P.K);
+        if (stage != 2) {
+            if (P.ua & UA_QUANT)
+                hipLaunchKernelGGL(quant_mx8_kernel<true>, dim3((unsigned)qblocks), dim3(256), 0,
+                                   stream, reinterpret_cast<const uint16_t*>(P.A), P.a_pitch, Q,
+                                   P.K, SX, P.K / 32, P.M, (int)P.K);
+            else
+                hipLaunchKernelGGL(quant_mx8_kernel<false>, dim3((unsigned)qblocks), dim3(256), 0,
+                                   stream, reinterpret_cast<const uint16_t*>(P.A), P.a_pitch, Q,
+                                   P.K, SX, P.K / 32, P.M, (int)P.K);
+        }
         if (stage == 1) {
             const hipError_t e = hipGetLastError();
             return e == hipSuccess ? RAD_OK : RAD_E_DEVICE;
@@ -352,6 +398,7 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
         AS = SX;
         a_pitch = P.K;
         as_pitch = P.K / 32;
+        if (P.ua & UA_GEMM) return launch_any(P, PF_MX8, A, AS, a_pitch, as_pitch, stream);
     }
     /* the kernel addresses 256 rows of any operand with 32-bit lane offsets */
     const int64_t lim = (int64_t)1 << 31;

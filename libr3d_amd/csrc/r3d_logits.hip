@@ -33,11 +33,13 @@
 #include <hip/hip_fp16.h>
 
 #include <mutex>
+#include <stddef.h>
 #include <stdio.h>
 #include <string.h>
 
 #include "r3d_device.h"
 #include "r3d_dump.h"
+#include "r3d_gemm_any.h"
 #include "r3d_plan.h"
 #include "rad_planes.h"
 #include "rad_plugin.h"
@@ -66,16 +68,38 @@ __device__ __forceinline__ float lg_scale(__amdgpu_buffer_rsrc_t rs, uint32_t of
     return __half2float(__ushort_as_half((unsigned short)v));
 }
 
-/* The device copy of the header still describes the planes the host planned from. */
+/* One scale element at any alignment (the dword walk): widened exactly. */
+template <int SDT>
+__device__ __forceinline__ float lg_scale_any(const AnyBuf& b, uint32_t off) {
+    const uint32_t v = any_ld4(b, off);
+    if (SDT == 2) return __uint_as_float(v);
+    if (SDT == 0) return __uint_as_float(v << 16);
+    return __half2float(__ushort_as_half((unsigned short)(v & 0xFFFFu)));
+}
+
+/* The device copy of the header still describes the planes the host planned from.  Read
+ * by aligned dwords (the blob may start at any byte). */
 __device__ __forceinline__ bool lg_header_ok(const LogitsGuard& g) {
-    const RadPlanesHeader* h = reinterpret_cast<const RadPlanesHeader*>(g.header);
-    if (h->magic != RAD_PLANES_MAGIC || h->version != RAD_PLANES_VERSION || h->n_planes != 2)
+    const int ne = (g.ic > g.is ? g.ic : g.is) + 1;
+    const uint32_t eb = (uint32_t)sizeof(RadPlanesHeader), es = (uint32_t)sizeof(RadPlanesEntry);
+    const AnyBuf hb = any_buf(g.header, eb + es * ne);
+    auto u32 = [&](uint32_t o) { return any_ld4(hb, o); };
+    auto i64 = [&](uint32_t o) {
+        return (int64_t)((uint64_t)any_ld4(hb, o) | ((uint64_t)any_ld4(hb, o + 4) << 32));
+    };
+    if (u32(offsetof(RadPlanesHeader, magic)) != RAD_PLANES_MAGIC ||
+        u32(offsetof(RadPlanesHeader, n_planes)) != 2)
         return false;
-    const RadPlanesEntry& c = h->entry[g.ic];
-    const RadPlanesEntry& s = h->entry[g.is];
-    return c.dtype == RAD_F8E4M3 && c.offset == g.c_off && c.rows == g.c_rows &&
-           c.cols == g.c_cols && s.dtype == g.s_dtype && s.offset == g.s_off &&
-           s.rows == g.s_rows && s.row_bytes == g.s_row_bytes && s.block[0] == g.s_br;
+    const uint32_t c = eb + es * g.ic, s = eb + es * g.is;
+    return u32(c + offsetof(RadPlanesEntry, dtype)) == RAD_F8E4M3 &&
+           i64(c + offsetof(RadPlanesEntry, offset)) == g.c_off &&
+           i64(c + offsetof(RadPlanesEntry, rows)) == g.c_rows &&
+           i64(c + offsetof(RadPlanesEntry, cols)) == g.c_cols &&
+           u32(s + offsetof(RadPlanesEntry, dtype)) == g.s_dtype &&
+           i64(s + offsetof(RadPlanesEntry, offset)) == g.s_off &&
+           i64(s + offsetof(RadPlanesEntry, rows)) == g.s_rows &&
+           i64(s + offsetof(RadPlanesEntry, row_bytes)) == g.s_row_bytes &&
+           i64(s + offsetof(RadPlanesEntry, block)) == g.s_br;
 }
 
 constexpr uint32_t kLgOob = 0x80000000u;     /* past every buffer's num_records: reads 0 */
@@ -114,7 +138,7 @@ __device__ __forceinline__ float lg_unit_elem(const r3d_i32x4& u, int i) {
     return __half2float(__ushort_as_half((unsigned short)h));
 }
 
-template <int D, int XG, int SDT>
+template <int D, int XG, int SDT, bool UA>
 __global__ __launch_bounds__(512) void logits_e4m3_kernel(
     const uint16_t* __restrict__ X, int64_t x_pitch, const uint8_t* __restrict__ codes,
     const uint8_t* __restrict__ scale, int64_t s_pitch, int64_t s_bytes, int br,
@@ -135,7 +159,17 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
     for (int i = threadIdx.x; i < live * cpr; i += blockDim.x) {
         const int m = i / cpr, c = i - m * cpr;
         r3d_i32x4 v = {0, 0, 0, 0};
-        if (8 * c < K) v = *reinterpret_cast<const r3d_i32x4*>(X + (int64_t)(mb + m) * x_pitch + 8 * c);
+        const uint16_t* xp = X + (int64_t)(mb + m) * x_pitch + 8 * c;
+        if (UA) {                                     /* element by element, zero past K */
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t lo = 8 * c + 2 * j < K ? xp[2 * j] : 0u;
+                const uint32_t hi = 8 * c + 2 * j + 1 < K ? xp[2 * j + 1] : 0u;
+                v[j] = (int)(lo | (hi << 16));
+            }
+        } else if (8 * c < K) {
+            v = *reinterpret_cast<const r3d_i32x4*>(xp);
+        }
         *reinterpret_cast<r3d_i32x4*>(lg_lds + m * xrow + 16 * c) = v;
     }
     __syncthreads();
@@ -156,6 +190,10 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
     const int nb_pad = 2 * nw_pad;                    /* scale blocks in a table */
     float* tab = reinterpret_cast<float*>(lg_lds + xbytes) + (size_t)wave * 16 * nb_pad;
     const __amdgpu_buffer_rsrc_t rs = r3d_rsrc(scale, s_bytes);
+    const AnyBuf rsa = any_buf(scale, s_bytes);       /* the dword walk's view of the plane */
+    auto sload = [&](uint32_t off) -> float {
+        return UA ? lg_scale_any<SDT>(rsa, off) : lg_scale<SDT>(rs, off);
+    };
     /* table value i of chunk k: row 16 chunk + i % 16, block i / 16 (zero past N and K) */
     auto tab_off = [&](int k, int i) -> uint32_t {
         const int64_t row = (ch0 + (int64_t)k * stride) * 16 + (i & 15);
@@ -164,7 +202,7 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
                                               : kLgOob;
     };
     auto tab_sync = [&](int k, float* tab, int from) {   /* values from..end, loaded and written */
-        for (int i = from + l; i < 16 * nb_pad; i += 64) tab[i] = lg_scale<SDT>(rs, tab_off(k, i));
+        for (int i = from + l; i < 16 * nb_pad; i += 64) tab[i] = sload(tab_off(k, i));
     };
     /* how chunk k's scales are fetched: 1 by 16-byte unit, 2 one scale row by element, 0 by
      * table value (wave-uniform) */
@@ -173,6 +211,7 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
     auto tab_kind = [&](int k) -> int {
         if (k >= nch) return 0;
         if (br != 1) return 2;
+        if (UA) return 0;
         const int64_t row0 = (ch0 + (int64_t)k * stride) * 16;
         if (N - row0 < 16 || (span & 15) || nunits > 64 * kLgTU ||
             ((reinterpret_cast<uintptr_t>(scale) + row0 * s_pitch * ESZ) & 15))
@@ -197,14 +236,14 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
             for (int j = 0; j < 4 * kLgTU; ++j) {
                 const int b = l + 64 * j;
                 if (64 * j < nwin)
-                    tu[j >> 2][j & 3] = __float_as_int(lg_scale<SDT>(
-                        rs, b < nwin ? (uint32_t)((srow * s_pitch + b) * ESZ) : kLgOob));
+                    tu[j >> 2][j & 3] = __float_as_int(
+                        sload(b < nwin ? (uint32_t)((srow * s_pitch + b) * ESZ) : kLgOob));
             }
         } else {
 #pragma unroll
             for (int j = 0; j < 4 * kLgTU; ++j)
                 if (64 * j < 16 * nb_pad)
-                    tu[j >> 2][j & 3] = __float_as_int(lg_scale<SDT>(rs, tab_off(k, l + 64 * j)));
+                    tu[j >> 2][j & 3] = __float_as_int(sload(tab_off(k, l + 64 * j)));
         }
     };
     auto tab_write = [&](int k, const r3d_i32x4* tu) __attribute__((always_inline)) {
@@ -236,8 +275,8 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
             if (nb_pad > 64 * 4 * kLgTU) {            /* per-128-rows grids of very long K */
                 const int64_t srow = ((ch0 + (int64_t)k * stride) * 16) / br;
                 for (int b = 64 * 4 * kLgTU + l; b < nb_pad; b += 64) {
-                    const float v = lg_scale<SDT>(rs, b < nwin ? (uint32_t)((srow * s_pitch + b) * ESZ)
-                                                               : kLgOob);
+                    const float v = sload(b < nwin ? (uint32_t)((srow * s_pitch + b) * ESZ)
+                                                   : kLgOob);
                     r3d_f32x4* t = reinterpret_cast<r3d_f32x4*>(tab + 16 * b);
                     t[0] = t[1] = t[2] = t[3] = r3d_f32x4{v, v, v, v};
                 }
@@ -257,11 +296,27 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
     auto issue = [&](r3d_i32x4* dst) __attribute__((always_inline)) {
         const int64_t row0 = (ch0 + (int64_t)lk * stride) * 16;
         const int64_t rows_here = lk >= nch ? 0 : (N - row0 < 16 ? N - row0 : 16);
-        const __amdgpu_buffer_rsrc_t rc = r3d_rsrc(codes + (lk >= nch ? 0 : row0 * K), rows_here * K);
+        const uint8_t* cbase = codes + (lk >= nch ? 0 : row0 * K);
         const int k = 256 * lw + kl;
+        if (UA) {
+            /* dword loads funnel-shifted; the bytes past K of a row (a partial piece: K is a
+             * multiple of 4, k of 16) are zeroed, as are rows past the chunk's */
+            const AnyBuf cu = any_buf(cbase, rows_here * K);
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-            dst[g] = r3d_buf_ld16_stream(rc, k < K ? (uint32_t)((4 * g + lr) * K + k) : kLgOob);
+            for (int g = 0; g < 4; ++g) {
+                const bool in = k < K && 4 * g + lr < rows_here;
+                r3d_i32x4 v = any_ld16(cu, in ? (uint32_t)((4 * g + lr) * K + k) : kAnyOob, false);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (k + 4 * j >= K) v[j] = 0;
+                dst[g] = v;
+            }
+        } else {
+            const __amdgpu_buffer_rsrc_t rc = r3d_rsrc(cbase, rows_here * K);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                dst[g] = r3d_buf_ld16_stream(rc, k < K ? (uint32_t)((4 * g + lr) * K + k) : kLgOob);
+        }
         if (++lw == nw_pad) { lw = 0; ++lk; }
     };
 #pragma unroll
@@ -347,53 +402,98 @@ __global__ __launch_bounds__(512) void logits_e4m3_kernel(
 /* ------------------------------------------------------------------ the blob's header */
 
 /* Host copies of device-resident headers, per (device, blob): the first launch over a
- * blob in device memory reads its header with one synchronous copy, later launches reuse
- * it (and the kernel re-checks it against the device copy before reading a plane).  A blob
- * in pinned or managed memory is read in place every launch. */
+ * blob in device memory reads its header and entries with a copy on the launch stream,
+ * later launches reuse them (and the kernel re-checks them against the device copy before
+ * reading a plane).  A blob in host-accessible memory is read in place every launch. */
 struct HeadCacheEntry {
     int dev;
     const void* blob;
-    RadPlanesHeader h;
+    RadPlanesHead h;
 };
 static std::mutex g_head_mu;
 static HeadCacheEntry g_head[16];
 static int g_head_n = 0, g_head_next = 0;
 
-static bool head_copy(const void* blob, RadPlanesHeader* out) {
-    if (!blob) return false;
+/* Where a blob lives: 1 host memory the device can read too (pinned, managed), 2 device
+ * memory, 0 anything else -- ordinary host memory HIP does not know (also when no device
+ * is present), readable by the host only -- and -1 for null. */
+static int blob_kind(const void* blob) {
+    if (!blob) return -1;
     hipPointerAttribute_t at;
     memset(&at, 0, sizeof at);
     if (hipPointerGetAttributes(&at, blob) != hipSuccess) {
-        (void)hipGetLastError();                      /* unregistered host memory */
-        return false;
+        (void)hipGetLastError();
+        return 0;
     }
     if (at.type == hipMemoryTypeHost || at.type == hipMemoryTypeManaged ||
-        at.type == hipMemoryTypeUnified) {
-        memcpy(out, blob, sizeof *out);
-        return rad_planes_header(out) != nullptr;
-    }
-    if (at.type != hipMemoryTypeDevice) return false;
+        at.type == hipMemoryTypeUnified)
+        return 1;
+    return at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeArray ? 2 : 0;
+}
+
+/* The header, then the n_planes entries it announces (none when it is not a planes
+ * header: the plan then refuses it), read in place from host-readable memory; false for
+ * a null blob. */
+static bool head_read_host(const void* blob, RadPlanesHead* out) {
+    if (!blob) return false;
+    memset(out, 0, sizeof *out);
+    memcpy(&out->h, blob, sizeof out->h);
+    const RadPlanesHeader* h = rad_planes_header(blob);
+    if (h) memcpy(out->e, rad_planes_entries(h), h->n_planes * sizeof(RadPlanesEntry));
+    return true;
+}
+
+static bool head_cached(int dev, const void* blob, RadPlanesHead* out) {
+    std::lock_guard<std::mutex> lk(g_head_mu);
+    for (int i = 0; i < g_head_n; ++i)
+        if (g_head[i].dev == dev && g_head[i].blob == blob) {
+            *out = g_head[i].h;
+            return true;
+        }
+    return false;
+}
+
+/* The launch's view of the header: in place, cached, or (first launch over a device blob)
+ * copied on `stream` -- the header, then the entries it announces -- and synchronised, so
+ * the copy is ordered after the stream's earlier writes to the blob.  A first launch under
+ * graph capture is refused (RAD_E_UNSUPPORTED): the copy and the wait cannot be captured. */
+static int head_copy(const void* blob, hipStream_t stream, RadPlanesHead* out) {
+    const int kind = blob_kind(blob);
+    if (kind == 1) return head_read_host(blob, out) && rad_planes_header(blob) ? RAD_OK : RAD_E_DTYPE;
+    if (kind != 2) return RAD_E_DTYPE;          /* the kernel could not read it */
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    {
-        std::lock_guard<std::mutex> lk(g_head_mu);
-        for (int i = 0; i < g_head_n; ++i)
-            if (g_head[i].dev == dev && g_head[i].blob == blob) {
-                *out = g_head[i].h;
-                return true;
-            }
-    }
-    if (hipMemcpy(out, blob, sizeof *out, hipMemcpyDeviceToHost) != hipSuccess) {
+    if (hipGetDevice(&dev) != hipSuccess) return RAD_E_DEVICE;
+    if (head_cached(dev, blob, out)) return RAD_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
         (void)hipGetLastError();
-        return false;
+        return RAD_E_DEVICE;
     }
-    if (!rad_planes_header(out)) return false;
+    if (cs != hipStreamCaptureStatusNone) {
+        fprintf(stderr, "libr3d_gfx950: logits_gemm_e4m3: the first launch over a device-"
+                        "resident head is under graph capture; launch once before capturing\n");
+        return RAD_E_UNSUPPORTED;
+    }
+    memset(out, 0, sizeof *out);
+    if (hipMemcpyAsync(&out->h, blob, sizeof out->h, hipMemcpyDeviceToHost, stream) != hipSuccess ||
+        hipStreamSynchronize(stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return RAD_E_DEVICE;
+    }
+    if (!rad_planes_header(&out->h)) return RAD_E_DTYPE;
+    if (hipMemcpyAsync(out->e, rad_planes_entries(reinterpret_cast<const RadPlanesHeader*>(blob)),
+                       out->h.n_planes * sizeof(RadPlanesEntry), hipMemcpyDeviceToHost,
+                       stream) != hipSuccess ||
+        hipStreamSynchronize(stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return RAD_E_DEVICE;
+    }
     std::lock_guard<std::mutex> lk(g_head_mu);
     HeadCacheEntry& e = g_head[g_head_n < 16 ? g_head_n++ : (g_head_next++ & 15)];
     e.dev = dev;
     e.blob = blob;
     e.h = *out;
-    return true;
+    return RAD_OK;
 }
 
 static void head_forget(const void* blob) {
@@ -405,20 +505,28 @@ static void head_forget(const void* blob) {
     g_head_next = 0;
 }
 
+bool logits_head_peek(const void* blob, RadPlanesHead* out) {
+    const int kind = blob_kind(blob);
+    if (kind == 0 || kind == 1) return head_read_host(blob, out);
+    int dev = 0;
+    return kind == 2 && hipGetDevice(&dev) == hipSuccess && head_cached(dev, blob, out);
+}
+
 /* ---------------------------------------------------------------------- the row entry */
 
 /* Workgroups of `waves` waves of this instantiation one compute unit holds at `lds` bytes
  * of LDS (the register count answered once by the runtime). */
-template <int D, int XG, int SDT>
+template <int D, int XG, int SDT, bool UA>
 static int logits_per_cu(int waves, int lds) {
     static int regs[9];
     if (!regs[waves]) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&logits_e4m3_kernel<D, XG, SDT>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLogitsLds);
+        (void)hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&logits_e4m3_kernel<D, XG, SDT, UA>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, kLogitsLds);
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &n, reinterpret_cast<const void*>(&logits_e4m3_kernel<D, XG, SDT>), waves * 64,
-                0) != hipSuccess || n < 1)
+                &n, reinterpret_cast<const void*>(&logits_e4m3_kernel<D, XG, SDT, UA>),
+                waves * 64, 0) != hipSuccess || n < 1)
             n = 1;
         (void)hipGetLastError();
         regs[waves] = n;
@@ -428,12 +536,12 @@ static int logits_per_cu(int waves, int lds) {
     return n < 1 ? 1 : n;
 }
 
-template <int D, int XG, int SDT>
+template <int D, int XG, int SDT, bool UA>
 static hipError_t launch_logits_t(const LogitsPlan& P, hipStream_t stream) {
-    const LogitsGeom g = logits_geom(P, cu_count(), logits_per_cu<D, XG, SDT>(P.waves, P.lds));
+    const LogitsGeom g = logits_geom(P, cu_count(), logits_per_cu<D, XG, SDT, UA>(P.waves, P.lds));
     const int esz = SDT == 2 ? 4 : 2;
     const int64_t s_bytes = P.guard.s_rows * P.s_pitch * esz;
-    hipLaunchKernelGGL((logits_e4m3_kernel<D, XG, SDT>),
+    hipLaunchKernelGGL((logits_e4m3_kernel<D, XG, SDT, UA>),
                        dim3((unsigned)g.blocks, (unsigned)g.passes), dim3(P.waves * 64),
                        (size_t)P.lds, stream, P.X, P.x_pitch, P.codes, P.scale, P.s_pitch,
                        s_bytes, P.br, P.Y, P.y_pitch, (int)P.N, (int)P.K, (int)P.M, P.mt,
@@ -441,67 +549,39 @@ static hipError_t launch_logits_t(const LogitsPlan& P, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int D, int XG>
+template <int D, int XG, bool UA>
 static hipError_t launch_logits_dx(const LogitsPlan& P, hipStream_t s) {
-    return P.sdt == 0 ? launch_logits_t<D, XG, 0>(P, s)
-         : P.sdt == 1 ? launch_logits_t<D, XG, 1>(P, s)
-                      : launch_logits_t<D, XG, 2>(P, s);
+    return P.sdt == 0 ? launch_logits_t<D, XG, 0, UA>(P, s)
+         : P.sdt == 1 ? launch_logits_t<D, XG, 1, UA>(P, s)
+                      : launch_logits_t<D, XG, 2, UA>(P, s);
 }
 
+template <bool UA>
+static hipError_t launch_logits_u(const LogitsPlan& P, hipStream_t stream) {
+    /* 5..8 activation rows a pass: two groups of 4, one window in flight (the plan's rule) */
+    return P.mt > 4        ? launch_logits_dx<1, 2, UA>(P, stream)
+         : P.depth == 3    ? launch_logits_dx<3, 1, UA>(P, stream)
+         : P.depth == 2    ? launch_logits_dx<2, 1, UA>(P, stream)
+                           : launch_logits_dx<1, 1, UA>(P, stream);
+}
 
 static int logits_entry(const RadArgs* a, RadStream s) {
     LogitsPlan P{};
     int rc = plan_logits_e4m3(a, nullptr, &P, true);
     if (rc) return rc;
     if (!chip_ok()) return RAD_E_UNSUPPORTED;
-    RadPlanesHeader hc;
-    if (!head_copy(rad_arg_in(a, 1)->data, &hc)) return RAD_E_DTYPE;
+    hipStream_t stream = (hipStream_t)s;
+    RadPlanesHead hc;
+    rc = head_copy(rad_arg_in(a, 1)->data, stream, &hc);
+    if (rc) return rc;
     rc = plan_logits_e4m3(a, &hc, &P, false);
     if (rc) return rc;
-    hipStream_t stream = (hipStream_t)s;
-    /* 5..8 activation rows a pass: two groups of 4, one window in flight (the plan's rule) */
-    const hipError_t e = P.mt > 4        ? launch_logits_dx<1, 2>(P, stream)
-                       : P.depth == 3    ? launch_logits_dx<3, 1>(P, stream)
-                       : P.depth == 2    ? launch_logits_dx<2, 1>(P, stream)
-                                         : launch_logits_dx<1, 1>(P, stream);
+    const hipError_t e = P.ua ? launch_logits_u<true>(P, stream) : launch_logits_u<false>(P, stream);
     if (e != hipSuccess) {
         fprintf(stderr, "libr3d_gfx950: logits_e4m3 launch FAILED (%s)\n", hipGetErrorName(e));
         return RAD_E_DEVICE;
     }
     return RAD_OK;
-}
-
-/* ------------------------------------------------------------------ joining the planes */
-
-/* The joined head's layout (header, then the codes and the scale plane each at a 256-byte
- * boundary), written into *h when given; the blob's bytes, or minus a RAD_E_* code. */
-static int64_t head_layout(int64_t N, int64_t K, uint32_t sdt, int64_t br, RadPlanesHeader* h) {
-    if (N <= 0 || K <= 0 || N > 0x7FFFFFFLL || K > 0x7FFFFFFLL) return -RAD_E_SHAPE;
-    if (sdt != RAD_BF16 && sdt != RAD_F16 && sdt != RAD_F32) return -RAD_E_DTYPE;
-    if (br != 1 && br != 128) return -RAD_E_SHAPE;
-    const int64_t esz = sdt == RAD_F32 ? 4 : 2;
-    const int64_t srows = (N + br - 1) / br, scols = (K + 127) / 128;
-    auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
-    const int64_t c_off = up((int64_t)sizeof(RadPlanesHeader));
-    const int64_t s_off = up(c_off + N * K);
-    if (h) {
-        memset(h, 0, sizeof *h);
-        h->magic = RAD_PLANES_MAGIC;
-        h->version = RAD_PLANES_VERSION;
-        h->n_planes = 2;
-        RadPlanesEntry& c = h->entry[0];
-        strncpy(c.role, "codes", RAD_PLANES_ROLE);
-        c.dtype = RAD_F8E4M3;
-        c.block[0] = 1; c.block[1] = 1;
-        c.rows = N; c.cols = K; c.row_bytes = K; c.offset = c_off;
-        RadPlanesEntry& e = h->entry[1];
-        strncpy(e.role, "scale", RAD_PLANES_ROLE);
-        e.dtype = sdt;
-        e.block[0] = br; e.block[1] = 128;
-        e.rows = srows; e.cols = scols; e.row_bytes = scols * esz; e.offset = s_off;
-        h->bytes = s_off + srows * scols * esz;
-    }
-    return s_off + srows * scols * esz;
 }
 
 }  // namespace r3d
@@ -510,63 +590,6 @@ extern "C" {
 
 int r3d_rad_logits_gemm_e4m3(const RadArgs* a, RadStream s) {
     return r3d::dump_wrap("logits_gemm_e4m3", a, s, r3d::logits_entry);
-}
-
-int64_t r3d_gfx950_logits_head_bytes(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,
-                                     int64_t scale_block_rows) {
-    return r3d::head_layout(n_vocab, n_embd, scale_dtype, scale_block_rows, nullptr);
-}
-
-int64_t r3d_gfx950_logits_head_header(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,
-                                      int64_t scale_block_rows, RadPlanesHeader* out) {
-    if (!out) return -RAD_E_INVAL;
-    return r3d::head_layout(n_vocab, n_embd, scale_dtype, scale_block_rows, out);
-}
-
-int r3d_gfx950_logits_head_join(const uint8_t* codes, int64_t codes_pitch, const void* scale,
-                                int64_t scale_pitch_bytes, int64_t n_vocab, int64_t n_embd,
-                                uint32_t scale_dtype, int64_t scale_block_rows, void* dst,
-                                int64_t dst_bytes) {
-    RadPlanesHeader h;
-    const int64_t need = r3d::head_layout(n_vocab, n_embd, scale_dtype, scale_block_rows, &h);
-    if (need < 0) return (int)-need;
-    if (!codes || !scale || !dst || dst_bytes < need) return RAD_E_SHAPE;
-    const RadPlanesEntry& c = h.entry[0];
-    const RadPlanesEntry& e = h.entry[1];
-    if (codes_pitch < n_embd || scale_pitch_bytes < e.row_bytes) return RAD_E_STRIDE;
-    uint8_t* d = (uint8_t*)dst;
-    memset(d, 0, (size_t)need);
-    memcpy(d, &h, sizeof h);
-    for (int64_t i = 0; i < n_vocab; ++i)
-        memcpy(d + c.offset + i * n_embd, codes + i * codes_pitch, (size_t)n_embd);
-    for (int64_t i = 0; i < e.rows; ++i)
-        memcpy(d + e.offset + i * e.row_bytes, (const uint8_t*)scale + i * scale_pitch_bytes,
-               (size_t)e.row_bytes);
-    return RAD_OK;
-}
-
-int r3d_gfx950_logits_head_split(const void* blob, int64_t blob_bytes, uint8_t* codes,
-                                 void* scale) {
-    if (!blob || blob_bytes < (int64_t)sizeof(RadPlanesHeader)) return RAD_E_SHAPE;
-    const RadPlanesHeader* h = rad_planes_header(blob);
-    const RadPlanesEntry* c = nullptr;
-    const RadPlanesEntry* e = nullptr;
-    if (!h || h->n_planes != 2 || !rad_planes_find(blob, "codes", &c) ||
-        !rad_planes_find(blob, "scale", &e))
-        return RAD_E_DTYPE;
-    if (h->bytes > blob_bytes || c->offset + c->rows * c->row_bytes > h->bytes ||
-        e->offset + e->rows * e->row_bytes > h->bytes)
-        return RAD_E_SHAPE;
-    const int64_t esz = e->dtype == RAD_F32 ? 4 : 2;
-    const uint8_t* b = (const uint8_t*)blob;
-    if (codes)
-        for (int64_t i = 0; i < c->rows; ++i)
-            memcpy(codes + i * c->cols, b + c->offset + i * c->row_bytes, (size_t)c->cols);
-    if (scale)
-        for (int64_t i = 0; i < e->rows; ++i)
-            memcpy((uint8_t*)scale + i * e->cols * esz, b + e->offset + i * e->row_bytes,
-                   (size_t)(e->cols * esz));
-    return RAD_OK;
 }
 
 void r3d_gfx950_logits_head_forget(const void* blob) { r3d::head_forget(blob); }

@@ -109,11 +109,16 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     if (!inner_contig(A) || !inner_contig(B) || !inner_contig(Y)) return RAD_E_STRIDE;
     if ((K & 1) || row_stride(B, K) != K) return RAD_E_STRIDE;   /* nibble rows packed */
 
-    /* gfx950 gates: whole 128-wide MFMA steps, 16-byte operand walks. */
+    /* gfx950 gates: whole 128-wide MFMA steps.  The fast arms walk A and B in 16-byte
+     * pieces and the scale plane in dwords; anything else takes the any-alignment arm
+     * (the fused bf16 producer has none: the reference's rows take e4m3 A only). */
     if (K % 128) return RAD_E_UNSUPPORTED;
     const int64_t a_pitch = row_stride(A, K) * (xq ? 2 : 1);     /* bytes */
-    if (!aligned16(A->data) || !aligned16(B->data) || (a_pitch & 15)) return RAD_E_UNSUPPORTED;
-    if ((uintptr_t)BS->data & 3) return RAD_E_UNSUPPORTED;      /* dword scale walk */
+    const int64_t bs_pitch = row_stride(BS, bs_cols);
+    const bool fast = aligned16(A->data) && aligned16(B->data) && !(a_pitch & 15) &&
+                      !((uintptr_t)BS->data & 3) && !(bs_pitch & 3) &&
+                      (xq || !((uintptr_t)AS->data & 3));
+    if (!fast && xq) return RAD_E_UNSUPPORTED;
 
     P->enc = ENC_MXFP4A8;
     P->xq = xq;
@@ -127,11 +132,11 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     P->b_pitch = K / 2;
     P->y_pitch = row_stride(Y, N);
     P->as_pitch = xq ? as_cols : row_stride(AS, as_cols);
-    P->bs_pitch = row_stride(BS, bs_cols);
-    if (P->bs_pitch & 3) return RAD_E_UNSUPPORTED;               /* dword scale walk */
+    P->bs_pitch = bs_pitch;
     P->as_cols = (int)as_cols;
     P->bs_cols = (int)bs_cols;
     P->rblk = 1;
+    P->ua = fast ? 0 : UA_GEMM;
     return RAD_OK;
 }
 
@@ -176,8 +181,11 @@ int plan_mxfp4a16(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
 
     if (K % 128) return RAD_E_UNSUPPORTED;
     const int64_t a_pitch = row_stride(A, K);                 /* bf16 elements */
-    if (!aligned16(A->data) || !aligned16(B->data) || (a_pitch & 7)) return RAD_E_UNSUPPORTED;
-    if ((uintptr_t)BS->data & 3) return RAD_E_UNSUPPORTED;
+    const int64_t bs_pitch = row_stride(BS, bs_cols);
+    /* the quantiser walks A in 16-byte pieces, the GEMM B in 16-byte pieces and the scale
+     * plane in dwords; anything else takes the element-wise quantiser / any-alignment GEMM */
+    const bool qfast = aligned16(A->data) && !(a_pitch & 7);
+    const bool gfast = aligned16(B->data) && !((uintptr_t)BS->data & 3) && !(bs_pitch & 3);
     if (!a->scratch || !aligned16(a->scratch) ||
         a->scratch_bytes < mxfp4a16_scratch_bytes(M, K))
         return RAD_E_UNSUPPORTED;
@@ -193,12 +201,12 @@ int plan_mxfp4a16(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     P->b_pitch = K / 2;
     P->y_pitch = row_stride(Y, N);
     P->as_pitch = K / 32;                                     /* of the scratch E8M0 plane */
-    P->bs_pitch = row_stride(BS, bs_cols);
-    if (P->bs_pitch & 3) return RAD_E_UNSUPPORTED;               /* dword scale walk */
+    P->bs_pitch = bs_pitch;
     P->as_cols = (int)(K / 32);
     P->bs_cols = (int)bs_cols;
     P->rblk = 1;
     P->scratch = (uint8_t*)a->scratch;
+    P->ua = (qfast ? 0 : UA_QUANT) | (gfast ? 0 : UA_GEMM);
     return RAD_OK;
 }
 
@@ -251,9 +259,13 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
 
     if (!inner_contig(A) || !inner_contig(B) || !inner_contig(Y)) return RAD_E_STRIDE;
 
+    /* the fast arms walk A and B in 16-byte pieces; anything else takes the any-alignment
+     * arm (the fused bf16 producer has none: the reference's rows take e4m3 A only) */
     const int64_t a_pitch = row_stride(A, K) * (xq ? 2 : 1), b_pitch = row_stride(B, K);
-    if (!aligned16(A->data) || !aligned16(B->data) || (a_pitch & 15) || (b_pitch & 15))
-        return RAD_E_UNSUPPORTED;
+    const bool fast = aligned16(A->data) && aligned16(B->data) && !(a_pitch & 15) &&
+                      !(b_pitch & 15) && !((uintptr_t)BS->data & 1) &&
+                      (xq || !((uintptr_t)AS->data & 3));
+    if (!fast && xq) return RAD_E_UNSUPPORTED;
 
     P->enc = ENC_FP8A8;
     P->xq = xq;
@@ -271,6 +283,7 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
     P->as_cols = (int)as_cols;
     P->bs_cols = (int)bs_cols;
     P->rblk = rblk;
+    P->ua = fast ? 0 : UA_GEMM;
     return RAD_OK;
 }
 
@@ -935,11 +948,52 @@ int plan_gemm_gated(const RadArgs* a, GemmPlan* G, GatedPlan* E) {
     return RAD_OK;
 }
 
+bool logits_shape(int64_t M, int64_t K, LogitsShape* out) {
+    const int64_t nw = (K + 255) / 256;
+    /* Shape: waves a workgroup and windows in flight.  Activation rows are staged
+     * nw_pad * 512 + 16 bytes apart, at most 8 rows a pass, and 5..8 rows keep one window
+     * in flight (registers); the first shape with LDS for min(M, 8) rows beside the waves'
+     * scale tables wins, else the first with room for one row.  R3D_LOGITS_SHAPE="W,D"
+     * (W 4|8 waves, D 1..3 windows) is tried first (a tuning lever, read once). */
+    const int64_t want = M < 8 ? M : 8;
+    static const char* lever = getenv("R3D_LOGITS_SHAPE");
+    int shapes[5][2] = {{0, 0}, {8, 2}, {8, 1}, {4, 2}, {4, 1}};
+    int lw = 0, ld = 0;
+    if (lever && sscanf(lever, "%d,%d", &lw, &ld) == 2 && (lw == 4 || lw == 8) && ld >= 1 && ld <= 3) {
+        shapes[0][0] = lw;
+        shapes[0][1] = ld;
+    }
+    for (int pass = 0; pass < 2; ++pass)
+        for (const auto& sh : shapes) {
+            if (!sh[0]) continue;
+            const int np = (int)((nw + sh[1]) / (sh[1] + 1) * (sh[1] + 1));
+            const int64_t xr = (int64_t)np * 512 + 16, st = (int64_t)sh[0] * 16 * 2 * np * 4;
+            int64_t rows = (kLogitsLds - st) / xr;
+            if (rows < 1) continue;
+            if (rows > want) rows = want;
+            if (rows > 4 && sh[1] > 1) rows = 4;
+            /* first pass: a shape that holds the wanted rows (the lever: any that fits) */
+            if (pass == 0 && rows < want && &sh != &shapes[0]) continue;
+            if (out) {
+                out->waves = sh[0];
+                out->depth = sh[1];
+                out->nw_pad = np;
+                out->xrow = xr;
+                out->stab = st;
+                out->mt = rows;
+            }
+            return true;
+        }
+    return false;
+}
+
 /* The reference entry's gates, in its order and with its codes (src/r3d_gemm_logits.hip:
- * 149-186), then this build's: K a multiple of 16 (16-byte code walks; the reference takes a
- * multiple of 4), 16-byte aligned x rows and codes plane, the codes plane inside the blob's
- * byte count, and one staged activation row within kLogitsMaxXLds of LDS. */
-int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, bool args_only) {
+ * 149-186), then this build's: the codes plane inside the blob's byte count, 32-bit
+ * buffer offsets, and one staged activation row within the compute unit's LDS (n_embd up
+ * to 40448).  n_embd a multiple of 16 with 16-byte aligned x rows and codes plane and an
+ * element-aligned scale plane takes the fast walk; any other multiple of 4 at any
+ * alignment the dword walk (ua). */
+int plan_logits_e4m3(const RadArgs* a, const RadPlanesHead* hh, LogitsPlan* P, bool args_only) {
     const RadTensor* X = rad_arg_in(a, 0);
     const RadTensor* W = rad_arg_in(a, 1);
     const RadTensor* Y = rad_arg_in(a, 2);
@@ -963,7 +1017,8 @@ int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, 
     if (x_pitch < K || y_pitch < N) return RAD_E_STRIDE;
     if (args_only) return RAD_OK;
 
-    if (!h || h->n_planes != 2) return RAD_E_DTYPE;
+    const RadPlanesHeader* h = hh ? &hh->h : nullptr;
+    if (!h || h->magic != RAD_PLANES_MAGIC || h->n_planes != 2) return RAD_E_DTYPE;
     if (h->transform[0]) return RAD_E_UNSUPPORTED;
     const RadPlanesEntry* ec = nullptr;
     const RadPlanesEntry* es = nullptr;
@@ -986,70 +1041,34 @@ int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, 
     if (es->row_bytes < scols * ssz || es->row_bytes % ssz || es->offset < 0 || ec->offset < 0)
         return RAD_E_STRIDE;
     if (h->bytes < ec->offset + N * K) return RAD_E_SHAPE;
-    if (K % 16) return RAD_E_UNSUPPORTED;
-    if (!aligned16(X->data) || (x_pitch & 7) || !aligned16(pc) || ((uintptr_t)ps % ssz))
-        return RAD_E_UNSUPPORTED;
     /* buffer offsets are 32-bit: one wave's rows of codes and the whole scale plane */
     if (64 * K > 0x7FFFFFFFLL || es->rows * es->row_bytes > 0x7FFFFFFFLL) return RAD_E_UNSUPPORTED;
-    const int nwin = (int)scols;
-    const int64_t nw = (K + 255) / 256;
-    /* Shape: waves a workgroup and windows in flight.  Activation rows are staged
-     * nw_pad * 512 + 16 bytes apart, at most 8 rows a pass, and 5..8 rows keep one window
-     * in flight (registers); the first shape with LDS for min(M, 8) rows beside the waves'
-     * scale tables wins, else the first with room for one row.  R3D_LOGITS_SHAPE="W,D"
-     * (W 4|8 waves, D 1..3 windows) is tried first (a tuning lever, read once). */
-    const int64_t want = M < 8 ? M : 8;
-    static const char* lever = getenv("R3D_LOGITS_SHAPE");
-    int shapes[5][2] = {{0, 0}, {8, 2}, {8, 1}, {4, 2}, {4, 1}};
-    int lw = 0, ld = 0;
-    if (lever && sscanf(lever, "%d,%d", &lw, &ld) == 2 && (lw == 4 || lw == 8) && ld >= 1 && ld <= 3) {
-        shapes[0][0] = lw;
-        shapes[0][1] = ld;
-    }
-    int wv = 0, dp = 0, nw_pad = 0;
-    int64_t xrow = 0, stab = 0, mt = 0;
-    for (int pass = 0; pass < 2 && !wv; ++pass)
-        for (const auto& sh : shapes) {
-            if (!sh[0]) continue;
-            const int np = (int)((nw + sh[1]) / (sh[1] + 1) * (sh[1] + 1));
-            const int64_t xr = (int64_t)np * 512 + 16, st = (int64_t)sh[0] * 16 * 2 * np * 4;
-            int64_t rows = (kLogitsLds - st) / xr;
-            if (rows < 1) continue;
-            if (rows > want) rows = want;
-            if (rows > 4 && sh[1] > 1) rows = 4;
-            /* first pass: a shape that holds the wanted rows (the lever: any that fits) */
-            if (pass == 0 && rows < want && &sh != &shapes[0]) continue;
-            wv = sh[0];
-            dp = sh[1];
-            nw_pad = np;
-            xrow = xr;
-            stab = st;
-            mt = rows;
-            break;
-        }
-    if (!wv) return RAD_E_UNSUPPORTED;
-    if ((M + mt - 1) / mt > 65535) return RAD_E_UNSUPPORTED;      /* passes ride grid.y */
+    LogitsShape sh{};
+    if (!logits_shape(M, K, &sh)) return RAD_E_UNSUPPORTED;
+    if ((M + sh.mt - 1) / sh.mt > 65535) return RAD_E_UNSUPPORTED;   /* passes ride grid.y */
+    P->ua = (K % 16) || !aligned16(X->data) || (x_pitch & 7) || !aligned16(pc) ||
+            ((uintptr_t)ps % ssz);
     P->X = (const uint16_t*)X->data;
     P->codes = (const uint8_t*)pc;
     P->scale = (const uint8_t*)ps;
     P->Y = (float*)Y->data;
     P->sdt = es->dtype == RAD_BF16 ? 0 : es->dtype == RAD_F16 ? 1 : 2;
     P->br = (int)es->block[0];
-    P->mt = (int)mt;
-    P->nwin = nwin;
-    P->nw_pad = nw_pad;
-    P->xrow = (int)xrow;
-    P->waves = wv;
-    P->depth = dp;
+    P->mt = (int)sh.mt;
+    P->nwin = (int)scols;
+    P->nw_pad = sh.nw_pad;
+    P->xrow = (int)sh.xrow;
+    P->waves = sh.waves;
+    P->depth = sh.depth;
     P->M = M; P->N = N; P->K = K;
     P->x_pitch = x_pitch;
     P->s_pitch = es->row_bytes / ssz;
     P->y_pitch = y_pitch;
-    P->lds = (int)(mt * xrow + stab);
+    P->lds = (int)(sh.mt * sh.xrow + sh.stab);
     LogitsGuard& g = P->guard;
     g.header = (const uint8_t*)W->data;
-    g.ic = (int32_t)(ec - h->entry);
-    g.is = (int32_t)(es - h->entry);
+    g.ic = (int32_t)(ec - rad_planes_entries(h));
+    g.is = (int32_t)(es - rad_planes_entries(h));
     g.c_off = ec->offset; g.c_rows = ec->rows; g.c_cols = ec->cols;
     g.s_off = es->offset; g.s_rows = es->rows; g.s_row_bytes = es->row_bytes; g.s_br = es->block[0];
     g.s_dtype = es->dtype; g.pad = 0;
@@ -1161,19 +1180,26 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
         return RAD_OK;
     }
     if (strstr(row, "logits_gemm") != nullptr) {
-        /* host-memory operands here (describe launches nothing): the blob's header is read
-         * where it lies */
+        /* describe copies nothing from the device: the blob's header is read in place when
+         * it is host-accessible, else taken from the copy an earlier launch cached */
         const RadTensor* W = rad_arg_in(a, 1);
         LogitsPlan L{};
         int rc = plan_logits_e4m3(a, nullptr, &L, true);
-        if (!rc) rc = plan_logits_e4m3(a, W ? rad_planes_header(W->data) : nullptr, &L, false);
+        RadPlanesHead hc;
+        if (!rc && !logits_head_peek(W->data, &hc)) {
+            snprintf(buf, (size_t)len, "refused rc=%d (the blob's header is in device memory "
+                     "and no launch has cached it: not host-readable)", RAD_E_UNSUPPORTED);
+            return RAD_E_UNSUPPORTED;
+        }
+        if (!rc) rc = plan_logits_e4m3(a, &hc, &L, false);
         if (rc) { snprintf(buf, (size_t)len, "refused rc=%d (plan)", rc); return rc; }
         const LogitsGeom g = logits_geom(L, 256, 1);
         snprintf(buf, (size_t)len,
                  "arm=logits M=%lld N=%lld K=%lld mt=%d passes=%lld depth=%d wg_waves=%d "
-                 "chunks=%lld blocks=%d br=%d sdt=%d nwin=%d lds=%d",
+                 "chunks=%lld blocks=%d br=%d sdt=%d nwin=%d lds=%d walk=%s",
                  (long long)L.M, (long long)L.N, (long long)L.K, L.mt, (long long)g.passes,
-                 L.depth, L.waves, (long long)g.chunks, g.blocks, L.br, L.sdt, L.nwin, L.lds);
+                 L.depth, L.waves, (long long)g.chunks, g.blocks, L.br, L.sdt, L.nwin, L.lds,
+                 L.ua ? "dword" : "vector");
         return RAD_OK;
     }
     if (strstr(row, "rmsnorm_quant_fp8") != nullptr) {
@@ -1239,6 +1265,16 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
     };
     int dkc = 0;
     WideGeom dw{};
+    if (P.ua & UA_GEMM) {
+        snprintf(buf, (size_t)len,
+                 "arm=any kernel=any enc=%s M=%lld N=%lld K=%lld tm=%d grid=%lldx%lld rblk=%d "
+                 "quant=%s (operands off 16-byte alignment: dword loads, funnel-shifted)",
+                 ename, (long long)P.M, (long long)P.N, (long long)P.K, P.M <= 16 ? 1 : 2,
+                 (long long)((P.N + 127) / 128),
+                 (long long)((P.M + (P.M <= 16 ? 15 : 31)) / (P.M <= 16 ? 16 : 32)), P.rblk,
+                 !a16 ? "none" : (P.ua & UA_QUANT) ? "elementwise" : "vector");
+        return RAD_OK;
+    }
     if (dec && !P.xq && a->scratch && ((uintptr_t)a->scratch & 15) == 0 &&
         decode_split_plan(P.enc, P.M, P.N, P.K, 256, quad, decode_splitk(a), &dkc, &dw) &&
         a->scratch_bytes >= (int64_t)dkc * P.M * P.N * 4) {
@@ -1298,11 +1334,12 @@ int describe(const char* row, const RadArgs* a, char* buf, int len) {
         prefill_geom(P.M, P.N, P.K, mode, 256, &g);
         snprintf(buf, (size_t)len,
                  "arm=prefill enc=%s M=%lld N=%lld K=%lld bn=%d bm=%d waves=%d grid=%lldx%lld "
-                 "tiles=%lld nst=%d lds=%d steps=%d rblk=%d nsplit=%lld",
+                 "tiles=%lld nst=%d lds=%d steps=%d rblk=%d nsplit=%lld quant=%s",
                  ename, (long long)P.M, (long long)P.N, (long long)P.K, g.bn, g.bm, g.wv,
                  (long long)g.grid_n, (long long)g.grid_m, (long long)g.tiles, g.nst, g.lds,
                  g.steps, P.rblk,
-                 (long long)(mode == PF_F8 && g.wv == 4 ? prefill_f8_split_n(P.M, P.N, 256) : 0));
+                 (long long)(mode == PF_F8 && g.wv == 4 ? prefill_f8_split_n(P.M, P.N, 256) : 0),
+                 !a16 ? "none" : (P.ua & UA_QUANT) ? "elementwise" : "vector");
     }
     return RAD_OK;
 }

@@ -32,7 +32,12 @@ struct GemmPlan {
                                 absent -- quantised in the kernel with quant_act_fp8's
                                 arithmetic */
     uint8_t* scratch;        /* mxfp4a16: e4m3 codes [M, K] then E8M0 [M, K/32] */
+    int ua;                  /* operands off the fast arms' alignment: UA_GEMM -- A, B or a
+                                scale plane (the any-alignment GEMM, r3d_gemm_any.h, takes the
+                                launch); UA_QUANT -- mxfp4a16's bf16 A (its quantiser reads it
+                                element by element) */
 };
+enum { UA_GEMM = 1, UA_QUANT = 2 };
 
 /* Launch scratch the mxfp4a16 row needs at M rows: the e4m3 plane (rounded up to 256
  * bytes) followed by the E8M0 plane. */
@@ -280,7 +285,7 @@ int64_t gemm_gated_scratch_bytes(const RadArgs* a);   /* 64 * N * 2, or 0 withou
  * blob's (W->data) plus the header's offsets; `guard` carries what the kernel re-checks
  * against the device copy of the header before it reads a plane. */
 struct LogitsGuard {
-    const uint8_t* header;   /* the blob's first byte (its header) */
+    const uint8_t* header;   /* the blob's first byte (its header, then its entries) */
     int32_t ic, is;          /* entry indices of "codes" and "scale" */
     int64_t c_off, c_rows, c_cols;
     int64_t s_off, s_rows, s_row_bytes, s_br;
@@ -301,10 +306,25 @@ struct LogitsPlan {
     int64_t M, N, K;
     int64_t x_pitch, s_pitch, y_pitch;   /* elements */
     int lds;                 /* dynamic LDS bytes per workgroup: x rows, then scale tables */
+    int ua;                  /* n_embd off a multiple of 16, or x / codes / scale off the fast
+                                walk's alignment: every piece read by dwords, funnel-shifted */
     LogitsGuard guard;
 };
-/* `h` null: the gates that need no header (args_only); else a host copy of the header. */
-int plan_logits_e4m3(const RadArgs* a, const RadPlanesHeader* h, LogitsPlan* P, bool args_only);
+/* `h` null: the gates that need no header (args_only); else a host copy of the blob's
+ * header and entries. */
+int plan_logits_e4m3(const RadArgs* a, const RadPlanesHead* h, LogitsPlan* P, bool args_only);
+/* The kernel's shape for M activation rows of n_embd K: waves a workgroup, windows in
+ * flight, padded windows, LDS row pitch, scale-table bytes and rows a pass; false when no
+ * shape stages even one activation row (K too long for the compute unit's LDS). */
+struct LogitsShape {
+    int waves, depth, nw_pad;
+    int64_t xrow, stab, mt;
+};
+bool logits_shape(int64_t M, int64_t K, LogitsShape* s);
+/* The header (and entries) of the blob at `blob` without copying from device memory: read
+ * in place when the blob is host-accessible, else this device's cached copy from an
+ * earlier launch; false when neither exists. */
+bool logits_head_peek(const void* blob, RadPlanesHead* out);
 constexpr int kLogitsLds = 160 * 1024;         /* LDS of one compute unit */
 /* The grid: 16-row chunks dealt to waves blocks * waves apart, at most per_cu workgroups
  * per compute unit (what one unit holds at once); blocks.y = passes over the activation

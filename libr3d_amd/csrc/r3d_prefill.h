@@ -697,6 +697,9 @@ __device__ __forceinline__ void r3d_quant_mx8_chunk(r3d_i32x4 raw, uint8_t* q, u
     if (write_scale) *sx = (uint8_t)(e + 127);
 }
 
+/* UA: the bf16 plane at any element alignment (base or pitch off 16 bytes), each chunk
+ * read element by element. */
+template <bool UA>
 __global__ __launch_bounds__(256) void quant_mx8_kernel(
     const uint16_t* __restrict__ X, int64_t x_pitch, uint8_t* __restrict__ Q, int64_t q_pitch,
     uint8_t* __restrict__ SX, int64_t sx_pitch, int64_t M, int K) {
@@ -710,8 +713,16 @@ __global__ __launch_bounds__(256) void quant_mx8_kernel(
         r3d_i32x4 raw[kQU];
 #pragma unroll
         for (int u = 0; u < kQU; ++u)
-            if (c0 + 256 * u < per_row)
-                raw[u] = *reinterpret_cast<const r3d_i32x4*>(xr + 8 * (c0 + 256 * u));
+            if (c0 + 256 * u < per_row) {
+                const uint16_t* p = xr + 8 * (c0 + 256 * u);
+                if (UA) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        raw[u][j] = (int)((uint32_t)p[2 * j] | ((uint32_t)p[2 * j + 1] << 16));
+                } else {
+                    raw[u] = *reinterpret_cast<const r3d_i32x4*>(p);
+                }
+            }
 #pragma unroll
         for (int u = 0; u < kQU; ++u) {
             const int c = c0 + 256 * u;

@@ -55,6 +55,12 @@ int r3d_rad_rmsnorm_quant_fp8(const RadArgs* a, RadStream s);
 int r3d_rad_gemm_nt_q_gated_fp8(const RadArgs* a, RadStream s);
 int64_t r3d_rad_gemm_nt_q_gated_fp8_scratch(const RadArgs* a);
 int r3d_rad_logits_gemm_e4m3(const RadArgs* a, RadStream s);
+int r3d_layout_head(const RadParam*, int, int, const RadEncoding*, const int*, const RadTensor*,
+                    int, RadLayout*);
+int r3d_relayout_head(const RadParam*, int, int, const RadEncoding*, const int*,
+                      const RadTensor*, int, void*, int64_t);
+int r3d_unrelayout_head(const RadParam*, int, int, const RadEncoding*, const int*, const void*,
+                        int64_t, const RadTensor*, int);
 }
 
 namespace {
@@ -368,20 +374,22 @@ const RadKernelInfo kRows[] = {
      nullptr, nullptr, r3d_rad_gemm_nt_q_gated_fp8, r3d_rad_gemm_nt_q_gated_fp8_scratch,
      nullptr, nullptr, nullptr, nullptr},
 
-    /* The layout hooks stay null: radiance's encoding and layout structures are not part of
-     * this build's ABI headers, so the head is joined by r3d_gfx950_logits_head_join (the
-     * same blob the reference's relayout hook writes, src/r3d_gemm_logits.hip:233-272). */
+    /* The layout hooks (r3d_head.cpp) admit exactly the joined e4m3 + block-scale head the
+     * launch reads and answer with the canonical rad.planes join; a plain head is declined
+     * at declare time (this library has no bf16 head row to claim it first). */
     {"logits_gemm_e4m3", "logits_gemm", "vocab",
      "lm_head GEMV on gfx950 bf16 MFMA: e4m3 codes widened exactly to bf16 in registers "
      "(v_cvt_scalef32_pk_bf16_fp8), 16 activation rows staged once per workgroup in LDS, "
      "16 head rows per MFMA streamed from HBM with 16-byte buffer loads, the block scale "
      "applied once per 128-column window in f32",
      "codes [n_vocab, n_embd] e4m3 dense, scale per (1 or 128 rows, 128 cols); n_embd a "
-     "multiple of 16; M derives from numel(logits)/n_vocab, up to 16 rows a pass (fewer "
+     "multiple of 4 up to 40448 (off a multiple of 16, or x / codes / scale off alignment: "
+     "a slower dword walk); M derives from numel(logits)/n_vocab, up to 8 rows a pass (fewer "
      "where LDS holds fewer rows of n_embd), passes ride grid.y",
-     "bf16 x, joined e4m3 + bf16/f16/f32 head, f32 logits",
+     "bf16 x, joined e4m3 + bf16/f16/f32 head (rad.planes), f32 logits",
      RAD_DOMAIN_DEVICE, kPrioTile, cLogitsRow, 3, nullptr, 0, nullptr,
-     nullptr, nullptr, r3d_rad_logits_gemm_e4m3, nullptr, nullptr, nullptr, nullptr, nullptr},
+     nullptr, nullptr, r3d_rad_logits_gemm_e4m3, nullptr, r3d_layout_head, r3d_relayout_head,
+     nullptr, r3d_unrelayout_head},
 };
 
 bool row_hidden(const RadKernelInfo& k) {

@@ -7,9 +7,15 @@
  *
  *   abi_harness layout   JSON: sizeof / offsetof of every ABI structure (no GPU)
  *   abi_harness table    JSON: ABI version, plugin identity, schemas and rows (no GPU)
- *   abi_harness run      one mxfp4a8 decode launch (M = 3) and one fp8a8 prefill launch
- *                        (M = 130) on the GPU, each through RadKernelInfo::launch and the
- *                        named export, checked against the oracle; exit 0 when both pass
+ *   abi_harness hooks    the logits row's weight-layout hooks through RadKernelInfo with a
+ *                        hand-built RadEncoding: accepted and declined encodings, the
+ *                        relayout against the library's join, the unrelayout round trip
+ *                        (no GPU); exit 0 when every check passes
+ *   abi_harness run      one mxfp4a8 decode launch (M = 3), one fp8a8 prefill launch
+ *                        (M = 130) and a split-K launch on the GPU, each through
+ *                        RadKernelInfo::launch and the named export, and one logits launch
+ *                        over a head the relayout hook joined (n_embd 260: the dword walk),
+ *                        checked against the oracle; exit 0 when all pass
  */
 #include <math.h>
 #include <stddef.h>
@@ -22,6 +28,7 @@
 
 #include "r3d_gfx950.h"
 #include "rad_abi.h"
+#include "rad_planes.h"
 #include "r3d_oracle.h"
 
 #define FIELD(T, f) printf("\"%s.%s\": [%zu, %zu], ", #T, #f, offsetof(T, f), sizeof(((T*)0)->f))
@@ -61,6 +68,21 @@ static int layout(void) {
     printf("\"sizeof.RadOpSchema\": %zu, ", sizeof(RadOpSchema));
     FIELD(RadOpSchema, op); FIELD(RadOpSchema, params); FIELD(RadOpSchema, n_params);
     FIELD(RadOpSchema, operands); FIELD(RadOpSchema, n_operands); FIELD(RadOpSchema, prose);
+    printf("\"sizeof.RadEncPlane\": %zu, ", sizeof(RadEncPlane));
+    FIELD(RadEncPlane, role); FIELD(RadEncPlane, kind); FIELD(RadEncPlane, dtype);
+    FIELD(RadEncPlane, block);
+    printf("\"sizeof.RadEncoding\": %zu, ", sizeof(RadEncoding));
+    FIELD(RadEncoding, scheme); FIELD(RadEncoding, n_planes); FIELD(RadEncoding, transform);
+    FIELD(RadEncoding, plane);
+    printf("\"sizeof.RadLayout\": %zu, ", sizeof(RadLayout));
+    FIELD(RadLayout, tag); FIELD(RadLayout, bytes);
+    printf("\"sizeof.RadPlanesHeader\": %zu, ", sizeof(RadPlanesHeader));
+    FIELD(RadPlanesHeader, magic); FIELD(RadPlanesHeader, n_planes);
+    FIELD(RadPlanesHeader, transform); FIELD(RadPlanesHeader, bytes);
+    printf("\"sizeof.RadPlanesEntry\": %zu, ", sizeof(RadPlanesEntry));
+    FIELD(RadPlanesEntry, role); FIELD(RadPlanesEntry, dtype); FIELD(RadPlanesEntry, kind);
+    FIELD(RadPlanesEntry, block); FIELD(RadPlanesEntry, rows); FIELD(RadPlanesEntry, cols);
+    FIELD(RadPlanesEntry, row_bytes); FIELD(RadPlanesEntry, offset);
     printf("\"sizeof.RadPluginInfo\": %zu, ", sizeof(RadPluginInfo));
     FIELD(RadPluginInfo, kind); FIELD(RadPluginInfo, name); FIELD(RadPluginInfo, version);
     FIELD(RadPluginInfo, description); FIELD(RadPluginInfo, targets);
@@ -86,6 +108,7 @@ static const void* const kExports[] = {
     (const void*)r3d_rad_gemm_nt_q_fp8_decode_scratch, (const void*)r3d_rad_logits_gemm_e4m3, (const void*)r3d_gfx950_logits_head_bytes,
     (const void*)r3d_gfx950_logits_head_header, (const void*)r3d_gfx950_logits_head_join,
     (const void*)r3d_gfx950_logits_head_split, (const void*)r3d_gfx950_logits_head_forget,
+    (const void*)r3d_layout_head, (const void*)r3d_relayout_head, (const void*)r3d_unrelayout_head,
 };
 
 static int table(void) {
@@ -309,6 +332,160 @@ static int run_splitk_mxfp4(void) {
     return ok;
 }
 
+/* ------------------------------------------------------------------ layout hooks */
+static const RadKernelInfo* row_info(const char* name) {
+    for (int i = 0; i < rad_kernel_count(); ++i)
+        if (strcmp(rad_kernel_at(i)->name, name) == 0) return rad_kernel_at(i);
+    return NULL;
+}
+
+/* The encoding an engine declares for a joined e4m3 head: "affine", codes (tiled 1 x 1
+ * e4m3) and scale (tiled bf16, block br x 128). */
+static void head_enc(RadEncoding* e, int64_t br) {
+    memset(e, 0, sizeof *e);
+    strcpy(e->scheme, "affine");
+    e->n_planes = 2;
+    strcpy(e->plane[0].role, "codes");
+    e->plane[0].kind = RAD_PLANE_TILED; e->plane[0].dtype = RAD_F8E4M3;
+    e->plane[0].block[0] = 1; e->plane[0].block[1] = 1;
+    strcpy(e->plane[1].role, "scale");
+    e->plane[1].kind = RAD_PLANE_TILED; e->plane[1].dtype = RAD_BF16;
+    e->plane[1].block[0] = br; e->plane[1].block[1] = 128;
+}
+
+/* A synthetic N x K head: e4m3 codes (no NaN) and bf16 scales near 2^-7, per (br, 128). */
+static void head_planes(int64_t N, int64_t K, int64_t br, uint8_t* codes, uint16_t* scale) {
+    for (int64_t i = 0; i < N * K; ++i) codes[i] = rnd_e4m3();
+    const int64_t sr = (N + br - 1) / br, sc = (K + 127) / 128;
+    for (int64_t i = 0; i < sr * sc; ++i) scale[i] = (uint16_t)(0x3C00 + (rnd() & 0x7F));
+}
+
+#define HOOK_CK(cond, what) do { if (!(cond)) { \
+    fprintf(stderr, "hooks: %s FAILED\n", what); ok = 0; } } while (0)
+
+static int hooks(void) {
+    int ok = 1;
+    const RadKernelInfo* k = row_info("logits_gemm_e4m3");
+    if (!k || !k->layout || !k->relayout || !k->unrelayout) {
+        fprintf(stderr, "hooks: logits_gemm_e4m3 row or its hooks missing\n");
+        return 1;
+    }
+    const int64_t N = 300, K = 260, br = 1, sr = N, sc = (K + 127) / 128;
+    uint8_t* codes = malloc((size_t)(N * K));
+    uint16_t* scale = malloc((size_t)(sr * sc * 2));
+    head_planes(N, K, br, codes, scale);
+    RadEncoding enc;
+    head_enc(&enc, br);
+    const int sel[2] = {0, 1};
+    RadTensor pl[2];
+    tensor(&pl[0], NULL, RAD_F8E4M3, N, K);              /* declare time: geometry only */
+    tensor(&pl[1], NULL, RAD_BF16, sr, sc);
+    RadParam p[2] = {RAD_INT("n_vocab", N), RAD_INT("n_embd", K)};
+    RadLayout lay;
+    memset(&lay, 0, sizeof lay);
+    HOOK_CK(k->layout(p, 2, 1, &enc, sel, pl, 2, &lay) == RAD_OK, "layout accepts the head");
+    const int64_t nb = r3d_gfx950_logits_head_bytes(N, K, RAD_BF16, br);
+    HOOK_CK(lay.tag && strcmp(lay.tag, RAD_PLANES_TAG) == 0 && lay.bytes == nb, "layout tag / bytes");
+    uint8_t* blob = malloc((size_t)nb);
+    uint8_t* ref = malloc((size_t)nb);
+    HOOK_CK(k->relayout(p, 2, 1, &enc, sel, pl, 2, blob, nb) == RAD_E_INVAL,
+            "relayout refuses planes without data");
+    pl[0].data = codes;
+    pl[1].data = scale;
+    HOOK_CK(k->relayout(p, 2, 1, &enc, sel, pl, 2, blob, nb - 1) == RAD_E_SHAPE,
+            "relayout refuses a short destination");
+    HOOK_CK(k->relayout(p, 2, 1, &enc, sel, pl, 2, blob, nb) == RAD_OK, "relayout");
+    HOOK_CK(r3d_gfx950_logits_head_join(codes, K, scale, sc * 2, N, K, RAD_BF16, br, ref, nb) ==
+                RAD_OK && memcmp(blob, ref, (size_t)nb) == 0,
+            "relayout writes the library's join, byte for byte");
+    uint8_t* c2 = calloc((size_t)(N * K), 1);
+    uint16_t* s2 = calloc((size_t)(sr * sc), 2);
+    RadTensor back[2];
+    tensor(&back[0], c2, RAD_F8E4M3, N, K);
+    tensor(&back[1], s2, RAD_BF16, sr, sc);
+    HOOK_CK(k->unrelayout(p, 2, 1, &enc, sel, blob, nb, back, 2) == RAD_OK &&
+                memcmp(c2, codes, (size_t)(N * K)) == 0 &&
+                memcmp(s2, scale, (size_t)(sr * sc * 2)) == 0,
+            "unrelayout round trip");
+    /* declines */
+    RadEncoding e2 = enc;
+    strcpy(e2.scheme, "none");
+    HOOK_CK(k->layout(p, 2, 1, &e2, sel, pl, 2, &lay) == RAD_E_DTYPE, "non-affine declined");
+    e2 = enc;
+    e2.transform[0] = 1;
+    HOOK_CK(k->layout(p, 2, 1, &e2, sel, pl, 2, &lay) == RAD_E_DTYPE, "rotated declined");
+    e2 = enc;
+    e2.plane[0].dtype = RAD_I8;
+    HOOK_CK(k->layout(p, 2, 1, &e2, sel, pl, 2, &lay) == RAD_E_DTYPE, "int8 codes declined");
+    HOOK_CK(k->layout(p, 2, 1, NULL, NULL, pl, 1, &lay) == RAD_E_DTYPE, "plain head declined");
+    HOOK_CK(k->layout(p, 2, 0, &enc, sel, pl, 2, &lay) == RAD_E_UNSUPPORTED,
+            "another operand stored as is");
+    printf("%s\n", ok ? "PASS" : "FAIL");
+    free(codes); free(scale); free(blob); free(ref); free(c2); free(s2);
+    return ok ? 0 : 1;
+}
+
+/* The logits row over a head the relayout hook joined, n_embd 260 (off a multiple of 16:
+ * the dword walk), M = 3, checked per element against the oracle within
+ * (2K + 300) 2^-24 S. */
+static int run_logits_relayout(void) {
+    const RadKernelInfo* k = row_info("logits_gemm_e4m3");
+    const int64_t M = 3, N = 300, K = 260, br = 1, sr = N, sc = (K + 127) / 128;
+    uint8_t* codes = malloc((size_t)(N * K));
+    uint16_t* scale = malloc((size_t)(sr * sc * 2));
+    head_planes(N, K, br, codes, scale);
+    RadEncoding enc;
+    head_enc(&enc, br);
+    const int sel[2] = {0, 1};
+    RadTensor pl[2];
+    tensor(&pl[0], codes, RAD_F8E4M3, N, K);
+    tensor(&pl[1], scale, RAD_BF16, sr, sc);
+    RadParam p[4] = {RAD_INT("M", M), RAD_INT("n_vocab", N), RAD_INT("n_embd", K),
+                     RAD_STR("dtype", "bf16")};
+    RadLayout lay;
+    if (!k || k->layout(p, 4, 1, &enc, sel, pl, 2, &lay) != RAD_OK) {
+        fprintf(stderr, "logits relayout: layout declined\n");
+        return 0;
+    }
+    uint8_t* blob = malloc((size_t)lay.bytes);
+    if (k->relayout(p, 4, 1, &enc, sel, pl, 2, blob, lay.bytes) != RAD_OK) {
+        fprintf(stderr, "logits relayout: relayout refused\n");
+        return 0;
+    }
+    uint16_t* x = malloc((size_t)(M * K * 2));
+    for (int64_t i = 0; i < M * K; ++i) x[i] = (uint16_t)(0x3E00 + (rnd() & 0x1FF)) ^ (uint16_t)((rnd() & 1) << 15);
+    float* Y = malloc((size_t)(M * N * 4));
+    float* Yr = malloc((size_t)(M * N * 4));
+    float* S = malloc((size_t)(M * N * 4));
+    void* dx = to_dev(x, (size_t)(M * K * 2));
+    void* dw = to_dev(blob, (size_t)lay.bytes);
+    void* dy = NULL;
+    CK(hipMalloc(&dy, (size_t)(M * N * 4)));
+    CK(hipMemset(dy, 0xFF, (size_t)(M * N * 4)));
+    RadTensor t[3];
+    tensor(&t[0], dx, RAD_BF16, M, K);
+    memset(&t[1], 0, sizeof t[1]);
+    t[1].data = dw; t[1].dtype = RAD_U8; t[1].rank = 1; t[1].shape[0] = lay.bytes; t[1].stride[0] = 1;
+    tensor(&t[2], dy, RAD_F32, M, N);
+    const RadArgs a = {t, 3, p, 4, NULL, 0, NULL, 0, 0};
+    const int rc = k->launch(&a, NULL);
+    CK(hipDeviceSynchronize());
+    CK(hipMemcpy(Y, dy, (size_t)(M * N * 4), hipMemcpyDeviceToHost));
+    r3d_ref_logits_e4m3(x, K, codes, scale, 0, sc, (int)br, M, N, K, Yr, N, S, 4);
+    int bad = 0;
+    for (int64_t i = 0; i < M * N; ++i) {
+        const double tol = (2.0 * K + 300.0) * ldexp(1.0, -24) * S[i] + 1e-30;
+        if (!(fabs((double)Y[i] - (double)Yr[i]) <= tol)) ++bad;
+    }
+    printf("logits over the relayout hook's blob (M=%lld N=%lld K=%lld): rc=%d, %d of %lld "
+           "outside the bound\n", (long long)M, (long long)N, (long long)K, rc, bad,
+           (long long)(M * N));
+    r3d_gfx950_logits_head_forget(dw);
+    CK(hipFree(dx)); CK(hipFree(dw)); CK(hipFree(dy));
+    free(codes); free(scale); free(blob); free(x); free(Y); free(Yr); free(S);
+    return rc == RAD_OK && bad == 0;
+}
+
 int main(int argc, char** argv) {
     const char* mode = argc > 1 ? argv[1] : "layout";
     if (strcmp(mode, "layout") == 0) return layout();
@@ -322,9 +499,11 @@ int main(int argc, char** argv) {
         const int a = run_decode_mxfp4();
         const int b = run_prefill_fp8();
         const int c = run_splitk_mxfp4();
-        printf("%s\n", a && b && c ? "PASS" : "FAIL");
-        return a && b && c ? 0 : 1;
+        const int d = run_logits_relayout();
+        printf("%s\n", a && b && c && d ? "PASS" : "FAIL");
+        return a && b && c && d ? 0 : 1;
     }
-    fprintf(stderr, "usage: abi_harness layout|table|run\n");
+    if (strcmp(mode, "hooks") == 0) return hooks();
+    fprintf(stderr, "usage: abi_harness layout|table|hooks|run\n");
     return 2;
 }

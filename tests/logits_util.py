@@ -7,11 +7,13 @@ import numpy as np
 from libr3d_amd import synth
 
 MAGIC = 0x534E4C50
-HEADER_BYTES = 328                       # 40 + 4 entries x 72
-ENTRY0 = 40
-ENTRY_BYTES = 72
+HDR = 32                                 # magic, n_planes, transform[4], bytes
+ENTRY0 = HDR                             # the entries follow the header
+ENTRY_BYTES = 72                         # role[16], dtype, kind, block[2], rows, cols, row_bytes, offset
+HEADER_BYTES = HDR + 2 * ENTRY_BYTES     # a two-plane blob's header and entries
 DT_CODE = {"F32": 0, "BF16": 1, "F16": 2, "F8E4M3": 3, "F8E5M2": 4, "U8": 7}
 SDT = {"bf16": "BF16", "f16": "F16", "f32": "F32"}
+TILED = 0
 
 
 def up256(v):
@@ -19,32 +21,35 @@ def up256(v):
 
 
 def header(N, K, sdt="bf16", br=1):
-    """The header the library's join writes for an N x K head (uint8 [328])."""
+    """The header and entries of an N x K head's blob, written the way the reference's tools
+    write a joined blob (tools/bench_skinny.cpp:206-220): header at 0 with magic, n_planes,
+    transform[0] and bytes; the entries right after it; the first plane at the header and
+    entries rounded up to 256 bytes, the next at its end rounded up (uint8 [HEADER_BYTES])."""
     esz = 4 if sdt == "f32" else 2
     srows, scols = (N + br - 1) // br, (K + 127) // 128
     c_off = up256(HEADER_BYTES)
     s_off = up256(c_off + N * K)
     h = np.zeros(HEADER_BYTES, np.uint8)
-    u32 = h[:40].view(np.uint32)
-    u32[0], u32[1], u32[2] = MAGIC, 1, 2
-    h[32:40].view(np.int64)[0] = s_off + srows * scols * esz
+    u32 = h[:24].view(np.uint32)
+    u32[0], u32[1] = MAGIC, 2
+    h[24:32].view(np.int64)[0] = s_off + srows * scols * esz
     for i, (role, dt, blk, rows, cols, rb, off) in enumerate([
             ("codes", DT_CODE["F8E4M3"], (1, 1), N, K, K, c_off),
             ("scale", DT_CODE[SDT[sdt]], (br, 128), srows, scols, scols * esz, s_off)]):
         e = h[ENTRY0 + i * ENTRY_BYTES: ENTRY0 + (i + 1) * ENTRY_BYTES]
         e[:len(role)] = np.frombuffer(role.encode(), np.uint8)
-        e[16:20].view(np.uint32)[0] = dt
+        e[16:24].view(np.uint32)[:] = [dt, TILED]
         e[24:72].view(np.int64)[:] = [blk[0], blk[1], rows, cols, rb, off]
     return h
 
 
 def set_field(h, field, value, entry=None):
     """Overwrite one header field in place (entry 0 = codes, 1 = scale)."""
-    top = {"magic": (0, np.uint32), "version": (4, np.uint32), "n_planes": (8, np.uint32),
-           "transform0": (12, np.uint32), "bytes": (32, np.int64)}
-    ent = {"dtype": (16, np.uint32), "block0": (24, np.int64), "block1": (32, np.int64),
-           "rows": (40, np.int64), "cols": (48, np.int64), "row_bytes": (56, np.int64),
-           "offset": (64, np.int64)}
+    top = {"magic": (0, np.uint32), "n_planes": (4, np.uint32), "transform0": (8, np.uint32),
+           "bytes": (24, np.int64)}
+    ent = {"dtype": (16, np.uint32), "kind": (20, np.uint32), "block0": (24, np.int64),
+           "block1": (32, np.int64), "rows": (40, np.int64), "cols": (48, np.int64),
+           "row_bytes": (56, np.int64), "offset": (64, np.int64)}
     if field == "role":
         b = ENTRY0 + entry * ENTRY_BYTES
         h[b:b + 16] = 0

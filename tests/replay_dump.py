@@ -320,12 +320,12 @@ def head_planes(blob):
     """(codes [N, K] uint8, scale grid (uint16 bits or float32), scale dtype name, rows per
     scale row) out of a joined head (include/rad_planes.h's layout)."""
     b = np.asarray(blob, np.uint8)
-    u32 = b[:40].view(np.uint32)
-    if u32[0] != 0x534E4C50 or u32[1] != 1:
+    u32 = b[:24].view(np.uint32)        # magic, n_planes, transform[4]; then bytes (i64)
+    if u32[0] != 0x534E4C50 or not 1 <= u32[1] <= 4:
         raise ValueError("no joined-planes header")
     ents = {}
-    for i in range(int(u32[2])):
-        e = b[40 + 72 * i: 40 + 72 * (i + 1)]
+    for i in range(int(u32[1])):        # the entries follow the 32-byte header
+        e = b[32 + 72 * i: 32 + 72 * (i + 1)]
         role = bytes(e[:16]).split(b"\0")[0].decode()
         dt = int(e[16:20].view(np.uint32)[0])
         blk0, blk1, rows, cols, rb, off = (int(v) for v in e[24:72].view(np.int64))

@@ -433,7 +433,7 @@ def test_decode_geometry_policy():
 
 @pytest.mark.parametrize("case,rc", [
     ("dtype", R.RAD_E_UNSUPPORTED), ("a_sum", R.RAD_E_UNSUPPORTED), ("pb1", R.RAD_E_UNSUPPORTED),
-    ("k_ragged", R.RAD_E_UNSUPPORTED), ("a_misaligned", R.RAD_E_UNSUPPORTED),
+    ("k_ragged", R.RAD_E_UNSUPPORTED), ("a_misaligned", R.RAD_OK),
     ("no_n", R.RAD_E_SHAPE), ("y_ragged", R.RAD_E_SHAPE), ("bs_grid", R.RAD_E_UNSUPPORTED),
     ("y_dtype", R.RAD_E_UNSUPPORTED), ("b_ref_ok", R.RAD_OK), ("a_small", R.RAD_E_SHAPE),
 ])
@@ -476,6 +476,8 @@ def test_mxfp4_plan_refusals(case, rc):
         ops._t[4].dtype = R.DT["F32"]
     got, d = R.describe("gemm_nt_q_mxfp4_decode", ops)
     assert got == rc, (case, d)
+    if case == "a_misaligned":              # taken, on the any-alignment arm
+        assert d.startswith("arm=any "), d
 
 
 @pytest.mark.parametrize("case,rc", [
@@ -882,3 +884,79 @@ def test_rmsnorm_quant_plan_and_refusals():
     ops = _rms_ops()
     ops.args.n_t = 4
     assert R.describe(G, ops)[0] == R.RAD_E_INVAL                        # n_t < 5
+
+
+def _shift(t, off, extra_cols=0):
+    """The same tensor viewed `off` bytes past an aligned base (its own storage widened so
+    the view stays inside it)."""
+    rows, cols = t.arr.shape if t.arr.ndim == 2 else (1, t.arr.shape[0])
+    pitch = cols + extra_cols
+    base = _aligned((rows * pitch + 16,), t.arr.dtype)
+    v = FakeT(base, offset=off)
+    v.shape = t.shape
+    v.stride = lambda dim=None, p=pitch: (p, 1) if dim is None else (p, 1)[dim]
+    return v
+
+
+@pytest.mark.parametrize("row,dtype", [("gemm_nt_q_mxfp4", "mxfp4a8"),
+                                       ("gemm_nt_q_mxfp4_decode", "mxfp4a8"),
+                                       ("gemm_nt_q_fp8a8", "fp8a8"),
+                                       ("gemm_nt_q_fp8a8_decode", "fp8a8")])
+@pytest.mark.parametrize("which,off", [("a", 1), ("a", 4), ("a", 8), ("b", 1), ("b", 4),
+                                       ("b", 8), ("bs", 1), ("bs", 2), ("pitch", 0)])
+@pytest.mark.parametrize("M", [1, 4, 40, 300])
+def test_any_alignment_taken(row, dtype, which, off, M):
+    """Operands the reference's rows accept at any alignment (src/r3d_gemm_fp8a8.hip:985-990,
+    1090-1095) are taken, never refused at issue time: A, B or the weight-scale plane at
+    1-, 4- or 8-byte offsets, or an A row pitch off 16 bytes, go to the any-alignment arm."""
+    if "decode" in row and M > 16:
+        pytest.skip("past the decode band")
+    N, K = 200, 512
+    mk = _mx_ops if dtype == "mxfp4a8" else _f8_ops
+    ops, (a, s, b, bs, y) = mk(M=M, N=N, K=K)
+    if which == "bs" and dtype == "fp8a8" and off == 1:
+        pytest.skip("a bf16 plane on an odd byte: not an element-aligned tensor")
+    if which == "a":
+        a = _shift(a, off)
+    elif which == "b":
+        b = _shift(b, off)
+    elif which == "bs":
+        bs = _shift(bs, off)
+    elif which == "pitch":
+        a = _shift(a, 0, extra_cols=4)             # row pitch K + 20: off 16 bytes
+    ops = R.GemmOperands(a, s, b, bs, y, dtype=dtype, N=N, K=K)
+    rc, d = R.describe(row, ops)
+    assert rc == R.RAD_OK, (row, which, off, d)
+    if which == "bs" and dtype == "fp8a8":
+        return                  # bf16 row scales are read by the element: the fast arms
+    assert d.startswith("arm=any "), (row, which, off, d)
+    g = _geom(d)
+    assert g["tm"] == ("1" if M <= 16 else "2") and g["grid"] == "2x%d" % (
+        (M + 15) // 16 if M <= 16 else (M + 31) // 32), d
+
+
+def test_any_alignment_mxfp4a16_and_fused():
+    """The bf16-in row: a misaligned bf16 A takes the element-wise quantiser, a misaligned
+    weight plane the any-alignment GEMM; the decode rows' fused bf16 producer (no
+    counterpart in the reference, whose rows take e4m3 A only) still needs aligned rows."""
+    M, N, K = 64, 256, 512
+    a = FakeT(_aligned((M, K), np.uint16))
+    b = FakeT(_aligned((N, K // 2), np.uint8))
+    bs = FakeT(_aligned((N, K // 32), np.uint8))
+    y = FakeT(_aligned((M, N), np.uint16))
+    need = R.lib().r3d_rad_gemm_nt_q_mxfp4a16_scratch
+    for av, bv, quant, arm in [(a, b, "vector", "prefill"), (_shift(a, 2), b, "elementwise", "prefill"),
+                               (a, _shift(b, 1), "vector", "any"),
+                               (_shift(a, 0, extra_cols=4), _shift(b, 4), "elementwise", "any")]:
+        ops = R.GemmOperands(av, None, bv, bs, y, dtype="mxfp4a16", N=N, K=K, M=M)
+        sc = FakeT(_aligned((M * K + M * K // 32 + 256,), np.uint8))
+        ops.set_scratch(sc, sc.arr.size)
+        rc, d = R.describe("gemm_nt_q_mxfp4a16", ops)
+        assert rc == R.RAD_OK and d.startswith("arm=%s " % arm), d
+        if quant:
+            assert _geom(d)["quant"] == quant, d
+    for dtype, row in [("mxfp4a8", "gemm_nt_q_mxfp4_decode"), ("fp8a8", "gemm_nt_q_fp8a8_decode")]:
+        ops = _xq_ops(dtype, 1, 256, 512)
+        ops._t[0].data = ops._t[0].data + 2
+        rc, d = R.describe(row, ops)
+        assert rc == R.RAD_E_UNSUPPORTED, d

@@ -16,7 +16,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HARNESS = os.path.join(ROOT, "tests", "c_abi", "abi_harness")
 
 MIRRORS = ["RadTensor", "RadParam", "RadTunableValue", "RadArgs", "RadConstraint",
-           "RadKernelInfo", "RadParamSpec", "RadOperandSpec", "RadOpSchema", "RadPluginInfo"]
+           "RadKernelInfo", "RadParamSpec", "RadOperandSpec", "RadOpSchema", "RadPluginInfo",
+           "RadEncPlane", "RadEncoding", "RadLayout", "RadPlanesHeader", "RadPlanesEntry"]
 
 
 def _harness(mode, timeout=60):
@@ -62,6 +63,13 @@ def test_c_table_matches_python_view():
     assert [r[0] for r in t["rows"]] == [r["name"] for r in rows]
     for c, p in zip(t["rows"], rows):
         assert c[1:] == [p["op"], p["priority"], len(p["constraints"]), 1]
+
+
+def test_c_harness_calls_the_layout_hooks():
+    """The logits row's hooks through RadKernelInfo from C, with a hand-built RadEncoding:
+    layout / relayout / unrelayout on an accepted head, and the declines."""
+    out = _harness("hooks")
+    assert out.returncode == 0 and out.stdout.strip() == "PASS", out.stdout + out.stderr
 
 
 def test_library_built_from_this_tree():

@@ -25,7 +25,7 @@ def test_join_layout_and_round_trip(N, K, sdt, br):
              else rng.integers(0, 65536, sshape, dtype=np.uint16))
     blob = R.join_head(codes, scale, sdt, br)
     h = LU.header(N, K, sdt, br)
-    assert blob.size == R.head_bytes(N, K, sdt, br) == h[32:40].view(np.int64)[0]
+    assert blob.size == R.head_bytes(N, K, sdt, br) == h[24:32].view(np.int64)[0]
     assert np.array_equal(blob[:LU.HEADER_BYTES], h)           # the header, byte for byte
     c_off, s_off = LU.up256(LU.HEADER_BYTES), LU.up256(LU.up256(LU.HEADER_BYTES) + N * K)
     assert np.array_equal(blob[c_off:c_off + N * K].reshape(N, K), codes)
@@ -134,9 +134,9 @@ def _hdr(N=1000, K=5376, sdt="bf16", br=1, **fields):
     (dict(ydt="BF16"), R.RAD_E_UNSUPPORTED),                    # logits are f32
     (dict(xdt="F32"), R.RAD_E_UNSUPPORTED),                     # x is bf16
     (dict(K=130, h=LU.header(1000, 130)), R.RAD_E_UNSUPPORTED),  # K % 4 (reference gate)
-    (dict(K=132, h=LU.header(1000, 132)), R.RAD_E_UNSUPPORTED),  # K % 16 (16-byte walks)
     (dict(h=_hdr(magic=0)), R.RAD_E_DTYPE),                      # no header
     (dict(h=_hdr(n_planes=3)), R.RAD_E_DTYPE),
+    (dict(h=_hdr(n_planes=0)), R.RAD_E_DTYPE),
     (dict(h=_hdr(transform0=1)), R.RAD_E_UNSUPPORTED),
     (dict(h=_hdr(role__1="zero")), R.RAD_E_DTYPE),
     (dict(h=_hdr(dtype__0=4)), R.RAD_E_SHAPE),                   # e5m2 codes
@@ -151,12 +151,145 @@ def _hdr(N=1000, K=5376, sdt="bf16", br=1, **fields):
     (dict(h=_hdr(bytes=1024)), R.RAD_E_SHAPE),                   # scale past the blob
     (dict(h=_hdr(row_bytes__1=82)), R.RAD_E_STRIDE),             # scale rows shorter than 42
     (dict(h=_hdr(offset__0=200000)), R.RAD_E_SHAPE),             # codes past the blob
-    (dict(h=_hdr(offset__0=520)), R.RAD_E_UNSUPPORTED),          # codes not 16-byte aligned
     (dict(M=1, N=4, K=80000, h=LU.header(4, 80000)), R.RAD_E_UNSUPPORTED),  # a row past LDS
 ])
 def test_plan_refusals(case, rc):
     ops, keep = _ops(**case)
     assert _desc(ops)[0] == rc, (case, _desc(ops))
+
+
+@pytest.mark.parametrize("case", [
+    dict(K=132, N=10, h=LU.header(10, 132)),                     # K % 16: the dword walk
+    dict(K=260, N=10, h=LU.header(10, 260), sdt="f16"),
+    dict(h=_hdr(offset__0=520)),                                 # codes off 16-byte alignment
+    dict(h=_hdr(offset__0=513)),                                 # codes on an odd byte
+    dict(N=10, K=256, h=_hdr(N=10, K=256, offset__1=4097, bytes=4097 + 40)),  # scale off 2 B
+])
+def test_plan_takes_any_alignment(case):
+    """Every operand the reference's entry accepts (n_embd a multiple of 4, any alignment,
+    src/r3d_gemm_logits.hip:166) is taken: off a multiple of 16 or off alignment, on the
+    slower dword walk; aligned multiples of 16 stay on the vector walk."""
+    ops, keep = _ops(**case)
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK and g["walk"] == "dword", (case, g)
+    ops, keep = _ops(M=2, N=10, K=256, h=LU.header(10, 256))
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK and g["walk"] == "vector"
+
+
+def test_reference_style_blob_accepted():
+    """A blob written the way the reference's tools write one (tools/bench_skinny.cpp:
+    206-220: zeroed, header fields magic / n_planes / transform[0] / bytes, the entries
+    right after the header with kind = RAD_PLANE_TILED, planes at rad_planes_round offsets)
+    is what the library's join writes, byte for byte, and what its plan accepts."""
+    N, K = 300, 256
+    h = LU.header(N, K)
+    assert h[8:24].view(np.uint32).tolist() == [0, 0, 0, 0]       # transform[], zero
+    hb, c_off, s_off, nb = R.head_header(N, K)
+    assert np.array_equal(hb, h) and c_off == 256 and s_off == LU.up256(256 + N * K)
+    ops, keep = _ops(M=1, N=N, K=K, h=h)
+    assert _desc(ops)[0] == R.RAD_OK
+
+
+# ------------------------------------------------------------------ the layout hooks
+def _planes(N, K, sdt, br, rng):
+    codes = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    sshape = ((N + br - 1) // br, (K + 127) // 128)
+    scale = (rng.standard_normal(sshape).astype(np.float32) if sdt == "f32"
+             else rng.integers(0, 65536, sshape, dtype=np.uint16))
+    return codes, (scale, LU.SDT[sdt])
+
+
+@pytest.mark.parametrize("N,K,sdt,br", [(300, 208, "bf16", 1), (257, 132, "f16", 128),
+                                        (5, 1040, "f32", 1), (129, 128, "bf16", 128)])
+def test_hooks_accept_and_round_trip(N, K, sdt, br):
+    """The hooks admit the joined e4m3 head: layout answers the canonical rad.planes join and
+    its size, relayout writes exactly the bytes the library's join writes, unrelayout reads
+    the planes back, and the plan accepts the blob."""
+    rng = np.random.default_rng(N * K)
+    codes, (scale, sname) = _planes(N, K, sdt, br, rng)
+    enc = R.head_encoding(sdt, br)
+    geo = ((N, K), "F8E4M3"), (scale.shape, sname)                 # declare time: no data
+    rc, tag, nb = R.layout_head(enc, *geo, params=[("n_vocab", N), ("n_embd", K)])
+    assert rc == R.RAD_OK and tag == "rad.planes" and nb == R.head_bytes(N, K, sdt, br)
+    assert R.relayout_head(enc, *geo, np.zeros(nb, np.uint8)) == R.RAD_E_INVAL   # no data yet
+    dst = np.full(nb, 0xAB, np.uint8)
+    assert R.relayout_head(enc, codes, (scale, sname), dst) == R.RAD_OK
+    assert np.array_equal(dst, R.join_head(codes, scale, sdt, br))
+    assert R.relayout_head(enc, codes, (scale, sname), np.zeros(nb - 1, np.uint8)) == R.RAD_E_SHAPE
+    c2, s2 = np.zeros_like(codes), np.zeros_like(scale)
+    assert R.unrelayout_head(enc, dst, c2, (s2, sname)) == R.RAD_OK
+    assert np.array_equal(c2, codes) and np.array_equal(s2, scale)
+    bad = dst.copy()
+    bad[:4] = 0                                                    # no magic
+    assert R.unrelayout_head(enc, bad, c2, (s2, sname)) == R.RAD_E_DTYPE
+    ops, keep = _ops(M=1, N=N, K=K, sdt=sdt, br=br, h=dst[:LU.HEADER_BYTES].copy())
+    assert _desc(ops)[0] == R.RAD_OK
+
+
+def _declines():
+    N, K = 64, 256
+    base = dict(sdt="bf16", br=1, N=N, K=K)
+    return [
+        (dict(base, enc=dict(scheme="none")), R.RAD_E_DTYPE),
+        (dict(base, enc=dict(transform0=1)), R.RAD_E_DTYPE),       # rotated ("givens")
+        (dict(base, enc=dict(roles=("scale", "codes"))), R.RAD_E_DTYPE),
+        (dict(base, enc=dict(roles=("codes", "zero"))), R.RAD_E_DTYPE),
+        (dict(base, enc=dict(code_dtype="F8E5M2")), R.RAD_E_DTYPE),
+        (dict(base, enc=dict(code_dtype="I8")), R.RAD_E_DTYPE),    # int8 heads: the host's
+        (dict(base, enc=dict(code_block=(1, 2))), R.RAD_E_DTYPE),
+        (dict(base, enc=dict(kinds=(1, 0))), R.RAD_E_DTYPE),       # codes not tiled
+        (dict(base, enc=dict(kinds=(0, 1))), R.RAD_E_DTYPE),
+        (dict(base, enc=dict(n_planes=3)), R.RAD_E_DTYPE),
+        (dict(base, sdt="U8"), R.RAD_E_DTYPE),                      # u8 scales
+        (dict(base, br=2), R.RAD_E_DTYPE),                          # scale block 2 x 128
+        (dict(base, sel=(0, 2)), R.RAD_E_DTYPE),                    # selection past n_planes
+        (dict(base, K=130), R.RAD_E_DTYPE),                         # n_embd % 4
+        (dict(base, K=80000, N=4), R.RAD_E_DTYPE),                  # a row past the LDS
+        (dict(base, srows=63), R.RAD_E_SHAPE),                      # grids disagree
+        (dict(base, params=[("n_vocab", 65)]), R.RAD_E_SHAPE),
+        (dict(base, operand=0), R.RAD_E_UNSUPPORTED),               # x: stored as it is
+        (dict(base, operand=2), R.RAD_E_UNSUPPORTED),
+    ]
+
+
+@pytest.mark.parametrize("case,rc", _declines())
+def test_hooks_decline(case, rc):
+    """What the reference's hook declines (src/r3d_gemm_logits.hip:233-253), and what this
+    row's launch would refuse, declined at declare time instead of refused at issue."""
+    N, K, sdt, br = case["N"], case["K"], case["sdt"], case["br"]
+    sname = LU.SDT.get(sdt, sdt)
+    enc = R.head_encoding(sname if sdt not in LU.SDT else sdt, br, **case.get("enc", {}))
+    srows = case.get("srows", (N + max(br, 1) - 1) // max(br, 1))
+    geo = ((N, K), "F8E4M3"), ((srows, (K + 127) // 128), sname)
+    got = R.layout_head(enc, *geo, operand=case.get("operand", 1), sel=case.get("sel", (0, 1)),
+                        params=case.get("params", ()))[0]
+    assert got == rc, (case, got)
+
+
+def test_hooks_decline_a_plain_head():
+    """A head without the two-plane encoding (a plain bf16 lm_head: no encoding, or one
+    plane) is declined (RAD_E_DTYPE), so it resolves past this row -- the library has no
+    bf16 head row declared ahead of it to claim such heads, as the reference's
+    logits_gemm_bf16 does (src/r3d_rows.cpp:1570-1585)."""
+    import ctypes
+    L = R.lib()
+    t = (R.RadTensor * 2)()
+    t[0].dtype, t[0].rank, t[0].shape[0], t[0].shape[1] = R.DT["BF16"], 2, 64, 256
+    out = R.RadLayout()
+    assert L.r3d_layout_head(None, 0, 1, None, None, t, 1, ctypes.byref(out)) == R.RAD_E_DTYPE
+    enc = R.head_encoding()
+    sel = (ctypes.c_int * 2)(0, 1)
+    assert L.r3d_layout_head(None, 0, 1, ctypes.byref(enc), sel, t, 1,
+                             ctypes.byref(out)) == R.RAD_E_DTYPE
+
+
+def test_row_registers_the_hooks():
+    row = {r["name"]: r for r in R.rows()}["logits_gemm_e4m3"]
+    assert row["layout"] and row["relayout"] and row["unrelayout"] and not row["opd_shape"]
+    for r in R.rows():                                # no other row declares weight hooks
+        if r["name"] != "logits_gemm_e4m3":
+            assert not (r["layout"] or r["relayout"] or r["unrelayout"]), r["name"]
 
 
 def test_plan_shape_and_stride_refusals():
@@ -171,13 +304,16 @@ def test_plan_shape_and_stride_refusals():
     assert _desc(ops)[0] == R.RAD_E_STRIDE
     ops, keep = _ops(strides={0: [5000, 1]})
     assert _desc(ops)[0] == R.RAD_E_STRIDE
-    # x rows 8-element aligned with a longer pitch are taken; a 16-byte misaligned x is not
+    # x rows 8-element aligned with a longer pitch take the vector walk; a 16-byte
+    # misaligned x pitch the dword walk
     ops, keep = _ops(M=2, K=256, N=10, h=LU.header(10, 256), shapes={0: [2, 256]},
                      strides={0: [264, 1]})
-    assert _desc(ops)[0] == R.RAD_OK
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK and g["walk"] == "vector"
     ops, keep = _ops(M=2, K=256, N=10, h=LU.header(10, 256), shapes={0: [2, 256]},
                      strides={0: [260, 1]})
-    assert _desc(ops)[0] == R.RAD_E_UNSUPPORTED
+    rc, g = _desc(ops)
+    assert rc == R.RAD_OK and g["walk"] == "dword"
     # M comes from numel(logits) / n_vocab, not the M parameter
     x = HostT(_aligned((6, 256), np.uint16))
     w = HostT(_aligned((LU.HEADER_BYTES,), np.uint8))
