@@ -8,9 +8,13 @@ the weight planes rotate over enough copies to exceed 1 GiB, well past the 256 M
 Infinity Cache.  `value` is algorithmic bytes per step (weights + scales + activations +
 output, counted once) times steps over the wall time between two synchronised points.
 `roofline.achieved` divides the same bytes by the kernel's average duration measured with
-HIP events on the launch stream.  The other configs (C0, C2, C3, C4) are reported under
-`extra`.  The CPU baseline is the C restatement of libref (oracle/) on the host's cores,
-timed on a bounded sample.  One GPU only: --gpus above 1 exits with a message.
+HIP events on the launch stream.  The headline times exactly --steps launches after
+exactly --warmup; it runs after the `floors` leg (the stream probe's ceilings and the
+launch floor on the same box), which also leaves the GPU at its working clocks.  The other
+configs (C0, C2, C3, C4) are reported under `extra`, each timed over at least 30 ms of GPU
+time.  The CPU baseline is the C restatement of libref (oracle/) on every host core this
+process may use, timed on a bounded sample.  One GPU only: --gpus above 1 exits with a
+message.
 """
 import argparse
 import json
@@ -83,11 +87,17 @@ def copies_for(nbytes):
     return max(1, int(np.ceil(ROTATE_BYTES / nbytes)))
 
 
-def time_case(case, row, steps, warmup, stream):
-    """-> (wall seconds for `steps` back-to-back launches between two synchronised points,
+EXTRA_MIN_S = 0.03     # GPU time every non-headline measurement runs for, at least
+
+
+def time_case(case, row, steps, warmup, stream, min_s=EXTRA_MIN_S):
+    """-> (wall seconds for the timed back-to-back launches between two synchronised points,
     average launch duration in seconds from HIP events recorded on the launch stream
     around the same launches -- the GPU-side span divided by the launch count, which is
-    what rocprofv3's per-kernel average measures plus the back-to-back dispatch gaps)."""
+    what rocprofv3's per-kernel average measures plus the back-to-back dispatch gaps).
+    At least `steps` launches are timed, and (min_s) enough for min_s seconds of GPU time,
+    after `warmup` untimed ones; case.last_steps holds the count.  The headline passes
+    min_s = None: exactly the --steps / --warmup it was given."""
     import torch
     import libr3d_amd as R
     launch = R.row_launcher(row)
@@ -97,6 +107,15 @@ def time_case(case, row, steps, warmup, stream):
         assert rc == 0, "row %s refused: %d" % (row, rc)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    if min_s:
+        e0.record()
+        for i in range(5):
+            launch(case.ops[(warmup + i) % n], stream)
+        e1.record()
+        torch.cuda.synchronize()
+        est = e0.elapsed_time(e1) * 1e-3 / 5
+        steps = max(steps, int(np.ceil(min_s / max(est, 1e-7))))
+    case.last_steps = steps
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record()
@@ -109,6 +128,99 @@ def time_case(case, row, steps, warmup, stream):
     return wall, kern
 
 
+def time_min(launch, min_s=0.03, warm=10):
+    """Average seconds per call of launch(i) for i = 0, 1, ... back to back on the current
+    stream (HIP events around the timed calls): `warm` untimed calls, a short probe, then
+    enough calls for at least min_s of GPU time -- so clocks and queues are steady whatever
+    the kernel's length."""
+    import torch
+    for i in range(warm):
+        launch(i)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(5):
+        launch(i)
+    e1.record()
+    torch.cuda.synchronize()
+    n = max(20, int(np.ceil(min_s / max(e0.elapsed_time(e1) * 1e-3 / 5, 1e-7))))
+    e0.record()
+    for i in range(n):
+        launch(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / n, n
+
+
+FLOOR_SIZES = {          # algorithmic bytes of the decode workloads the floors stand beside
+    "c2_qkv_M1": lambda: mx_bytes(1, 8192, 5376),
+    "c2_gate_up_M1": lambda: mx_bytes(1, 21504, 5376),
+    "c1": lambda: f8_bytes(1, 21504, 5376),
+    "lm_head_M4": lambda: f8_bytes(4, 262144, 5376),
+}
+
+
+def bench_floors(dev, stream, min_s=0.03):
+    """The ceilings the decode GEMVs are held against, from committed code: at each decode
+    workload's byte count, rotated over > 1 GiB like the GEMVs' weights, (a) the library's
+    read-only stream probe (r3d_gfx950_stream_probe: 1 KB loads 8 deep, best of the runs a
+    wave and waves a workgroup listed), (b) a stock torch kernel that only reads the bytes
+    (an int32 sum), and (c) the empty-kernel launch floor at 1 / 1344 / 5376 workgroups."""
+    import torch
+    import libr3d_amd as R
+    L = R.lib()
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    out = {}
+    for name, fn in FLOOR_SIZES.items():
+        nb = (fn() + 1023) // 1024 * 1024
+        bufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(copies_for(nb))]
+        for b in bufs:
+            b.view(torch.int32)[: nb // 4].fill_(0x01020304)
+        rec = {"bytes": nb, "copies": len(bufs), "probe": {}}
+        best = None
+        for kb in (16, 22, 32, 64, 128):
+            for wpg in (4, 8):
+                def go(i, kb=kb, wpg=wpg):
+                    rc = L.r3d_gfx950_stream_probe(ctypes_ptr(bufs[i % len(bufs)]), nb, wpg, kb,
+                                                   ctypes_ptr(sink), ctypes_ptr_stream(stream))
+                    assert rc == 0, rc
+                t, n = time_min(go, min_s)
+                rec["probe"]["%dKBx%d" % (kb, wpg)] = round(t * 1e6, 3)
+                if best is None or t < best[0]:
+                    best = (t, "%d KB a wave, %d waves a workgroup" % (kb, wpg))
+        rec["probe_us"] = round(best[0] * 1e6, 3)
+        rec["probe_best"] = best[1]
+        rec["probe_GBps"] = round(nb / best[0] / 1e9, 1)
+        rec["probe_frac_hbm"] = round(nb / best[0] / 1e9 / HBM_PEAK_GBS, 4)
+        t, n = time_min(lambda i: torch.sum(bufs[i % len(bufs)].view(torch.int32)), min_s)
+        rec["torch_sum_us"] = round(t * 1e6, 3)
+        rec["torch_sum_GBps"] = round(nb / t / 1e9, 1)
+        out[name] = rec
+        log("[bench] floor %s (%d B): probe %.2f us (%.1f%% of HBM, %s), torch sum %.2f us" % (
+            name, nb, best[0] * 1e6, 100 * rec["probe_frac_hbm"], best[1], t * 1e6))
+        del bufs
+        torch.cuda.empty_cache()
+    empty = {}
+    for wgs in (1, 1344, 5376):
+        def go(i, wgs=wgs):
+            L.r3d_gfx950_stream_probe(ctypes_ptr(sink), 0, 4, 4 * wgs, ctypes_ptr(sink),
+                                      ctypes_ptr_stream(stream))
+        t, n = time_min(go, min_s)
+        empty["%d_workgroups" % wgs] = round(t * 1e6, 3)
+    out["empty_kernel_us"] = empty
+    log("[bench] launch floor (empty kernel, back to back): %s us" % empty)
+    return out
+
+
+def ctypes_ptr(t):
+    import ctypes
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def ctypes_ptr_stream(s):
+    import ctypes
+    return ctypes.c_void_p(s)
+
+
 def cpu_baseline(seconds=10.0):
     """The oracle (libref restatement, OpenMP over output rows) on config 1, repeated for
     about `seconds` of wall time."""
@@ -117,7 +229,12 @@ def cpu_baseline(seconds=10.0):
     M, K, N = 1, 5376, 21504
     A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 10)
     B, BS = synth.fp8_weights(N, K, 0x5EED + 11)
-    nth = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    nth = min(avail, omp) if omp > 0 else avail
     O.quant_dot_fp8a8(A, AS, B, BS, 1, nthreads=nth)         # warm
     calls, t0 = 0, time.perf_counter()
     while True:
@@ -137,9 +254,12 @@ def cpu_baseline(seconds=10.0):
     except OSError:
         pass
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": nth, "kind": "port",
+            "nproc": os.cpu_count(), "affinity_cores": avail,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "cpu_model": cpu,
             "sample": "config 1 (fp8a8 GEMV M=1 K=5376 N=21504), full problem x %d calls, "
                       "%.1f s wall, oracle/ C restatement of libref quant_dot, OpenMP %d "
-                      "threads on %s" % (calls, el, nth, cpu or "host CPU")}
+                      "threads (every core this process may run on, capped by OMP_NUM_THREADS "
+                      "when set) on %s" % (calls, el, nth, cpu or "host CPU")}
 
 
 def main():
@@ -151,6 +271,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--floors", action="store_true",
+                    help="only measure the HBM stream ceilings and the launch floor, print JSON")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy (counter calibration for PMC runs)")
     ap.add_argument("--c3-only", action="store_true",
@@ -182,9 +304,20 @@ def main():
     if args.c3_only:
         print(json.dumps(bench_c3(dev, stream, steps=args.steps, warmup=args.warmup)), flush=True)
         return
+    if args.floors:
+        print(json.dumps(bench_floors(dev, stream)), flush=True)
+        return
     if args.case:
         print(json.dumps(run_case(args.case, dev, stream, args.steps, args.warmup)), flush=True)
         return
+
+    # ---- the ceilings first: the stream probe and the launch floor on this box (they also
+    # leave the GPU at its working clocks, as a serving loop keeps it, before the headline's
+    # own --warmup launches)
+    floors = None
+    if not args.quick and not args.no_extra:
+        log("[bench] floors: HBM stream ceilings and the launch floor")
+        floors = bench_floors(dev, stream)
 
     # ---- headline: config 1, fp8a8 decode GEMV, cold
     M, K, N = 1, 5376, 21504
@@ -194,7 +327,8 @@ def main():
     nbytes = f8_bytes(M, N, K)
     c1 = Case("fp8a8", A, AS, B, BS, M, N, K, copies_for(B.nbytes), dev)
     torch.cuda.synchronize()
-    wall, kern = time_case(c1, "gemm_nt_q_fp8a8_decode", args.steps, args.warmup, stream)
+    wall, kern = time_case(c1, "gemm_nt_q_fp8a8_decode", args.steps, args.warmup, stream,
+                           min_s=None)
     value = nbytes * args.steps / wall / 1e9
     achieved = nbytes / kern / 1e9
     log("[bench] config 1: wall %.2f GB/s, kernel %.2f us -> %.1f GB/s (%.1f%% of HBM peak)"
@@ -226,6 +360,8 @@ def main():
     }
 
     extra = {}
+    if floors is not None:
+        extra["floors"] = floors
     if not args.quick and not args.no_extra:
         ksteps = max(20, args.steps // 4)
         # C0: cache-fit parity config
@@ -261,7 +397,8 @@ def main():
                 gbs = nb / kern / 1e9
                 rec.update({"kernel_us": round(kern * 1e6, 3), "GBps_kernel": round(gbs, 1),
                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                            "GBps_wall": round(nb * ksteps / wall / 1e9, 1),
+                            "GBps_wall": round(nb * c.last_steps / wall / 1e9, 1),
+                            "launches": c.last_steps,
                             "arm": " ".join(R.describe(row, c.ops[0])[1].split()[:2])})
                 extra["c2_mxfp4_%s_M%d" % (name, M)] = rec
                 log("[bench] C2 %s M=%d: %.2f us, %.1f GB/s (%.1f%%) %s" % (
@@ -431,7 +568,7 @@ def run_case(name, dev, stream, steps, warmup):
     res.update({"M": M, "K": K, "N": N, "row": row, "bytes": nb, "copies": copies,
                 "kernel_us": round(kern * 1e6, 3), "GBps": round(nb / kern / 1e9, 1),
                 "frac_hbm": round(nb / kern / 1e9 / HBM_PEAK_GBS, 4),
-                "GBps_wall": round(nb * steps / wall / 1e9, 1),
+                "GBps_wall": round(nb * c.last_steps / wall / 1e9, 1), "steps": c.last_steps,
                 "plan": R.describe(row, c.ops[0])[1]})
     return res
 
@@ -472,7 +609,8 @@ def bench_lm_head_e4m3(M, dev, stream, steps, warmup, res):
                 "kernel": "r3d::logits_e4m3_kernel<%d, %d, 0>" % (2 if M <= 4 else 1, 1 if M <= 4 else 2),
                 "kernel_us": round(kern * 1e6, 3),
                 "GBps": round(nb / kern / 1e9, 1), "frac_hbm": round(nb / kern / 1e9 / HBM_PEAK_GBS, 4),
-                "GBps_wall": round(nb * steps / wall / 1e9, 1)})
+                "GBps_wall": round(nb * _Case.last_steps / wall / 1e9, 1),
+                "steps": _Case.last_steps})
     return res
 
 

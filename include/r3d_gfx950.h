@@ -200,6 +200,16 @@ int r3d_gfx950_describe(const char* row, const RadArgs* a, char* buf, int len);
  * call would take the skinny band's decode passes (no quantiser stage there). */
 int r3d_gfx950_mxfp4a16_stage(const RadArgs* a, RadStream s, int stage);
 
+/* Measurement diagnostic with no counterpart in the reference: a read-only stream over
+ * `bytes` of device memory at src on `s` -- each wave one contiguous run of kb KB read by
+ * 1 KB loads (64 lanes x 16 bytes, non-temporal) kept 8 deep in flight, waves_per_wg
+ * (1..8) waves a workgroup -- the ceiling an HBM-bound kernel of that access pattern and
+ * size is held against.  bytes = 0 launches kb waves that do nothing (the launch floor).
+ * sink: a device dword written only if the XOR of the data hits a fixed value.  RAD_OK,
+ * RAD_E_INVAL for a bad argument, RAD_E_DEVICE if the launch fails. */
+int r3d_gfx950_stream_probe(const void* src, int64_t bytes, int waves_per_wg, int64_t kb,
+                            uint32_t* sink, RadStream s);
+
 /* Build identity with no counterpart in the reference: the SHA-256 (hex) of the compile
  * flags and of the sources this library was compiled from -- the flags as one line, then
  * every file under libr3d_amd/csrc and include, in name order, each as "<relative

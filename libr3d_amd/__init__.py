@@ -187,6 +187,9 @@ def lib():
         L.r3d_unrelayout_head.restype = ctypes.c_int
         L.r3d_unrelayout_head.argtypes = _hook[:5] + [ctypes.c_void_p, _i64,
                                                        ctypes.POINTER(RadTensor), ctypes.c_int]
+        L.r3d_gfx950_stream_probe.restype = ctypes.c_int
+        L.r3d_gfx950_stream_probe.argtypes = [ctypes.c_void_p, _i64, ctypes.c_int, _i64,
+                                              ctypes.c_void_p, ctypes.c_void_p]
         L.r3d_gfx950_logits_head_forget.restype = None
         L.r3d_gfx950_logits_head_forget.argtypes = [ctypes.c_void_p]
         _LIB = L

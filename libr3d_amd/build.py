@@ -22,7 +22,7 @@ LIB = os.path.join(PKG, "libr3d_gfx950.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["r3d_gemm.hip", "r3d_logits.hip", "r3d_noalloc.hip", "r3d_plan.cpp", "r3d_rows.cpp",
-           "r3d_dump.cpp", "r3d_head.cpp"]
+           "r3d_dump.cpp", "r3d_head.cpp", "r3d_probe.hip"]
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

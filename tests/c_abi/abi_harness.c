@@ -109,6 +109,7 @@ static const void* const kExports[] = {
     (const void*)r3d_gfx950_logits_head_header, (const void*)r3d_gfx950_logits_head_join,
     (const void*)r3d_gfx950_logits_head_split, (const void*)r3d_gfx950_logits_head_forget,
     (const void*)r3d_layout_head, (const void*)r3d_relayout_head, (const void*)r3d_unrelayout_head,
+    (const void*)r3d_gfx950_stream_probe,
 };
 
 static int table(void) {
