@@ -1,6 +1,6 @@
 /* r3d_logits.hip -- the gfx950 logits_gemm_e4m3 row: logits over a joined e4m3 +
- * block-scale lm_head (the reference's row is src/r3d_gemm_logits.hip:72-226, its layout
- * hooks :233-272).
+ * block-scale lm_head (the reference's row is src/r3d_gemm_logits.hip:72-226; its layout
+ * hooks, :233-272, are r3d_head.cpp's).
  *
  *     y[m, n] = sum_k x[m, k] * e4m3(codes[n, k]) * scale[n / br, k / 128]     (f32 out)
  *
@@ -9,26 +9,19 @@
  * NaN included); x is bf16 already.  v_mfma_f32_16x16x32_bf16 therefore forms every product
  * x * code exactly -- 8 x 4 significant bits -- and sums 32 of them at f32 accuracy (worst
  * measured on MI355X: 5.9 * 2^-24 of the sum of magnitudes per instruction, C included).
- * The scale, which need not be a power of two, is applied once per 128-wide window, in f32:
- * tot = fma(scale, window_sum, tot).  This differs from the reference's order (one fma per
+ * The scale, which need not be a power of two, is applied once per 128-wide block, in f32:
+ * tot = fma(scale, block_sum, tot).  This differs from the reference's order (one fma per
  * product, code * scale rounded first) only in where the f32 roundings fall; both stay
- * within (window count + 4 * 66) * 2^-24 * sum |x * code * scale| of the exact sum.
+ * within (block count + 4 * 66) * 2^-24 * sum |x * code * scale| of the exact sum.
  *
- * Layout of one step (a 128-wide K window, w):
- *   A = 16 activation rows, staged once per workgroup in LDS as bf16 (rows mb .. mb+mt,
- *       zero past K up to a multiple of 4 windows), lane (m = l%16, q = l/16) reading its
- *       row's columns [128w + 16q, +16) and [128w + 64 + 16q, +16);
- *   B = 16 head rows streamed from HBM: lane (r = l%16, q) loads 16 code bytes of row r at
- *       each of those two column ranges (buffer loads: a chunk past K or a row past N reads
- *       zero), and each 8-byte half feeds one of the four MFMAs of the window;
- *   D = lane (r, q) holds x rows 4q .. 4q+3 for head row r, so its four accumulators share
- *       one scale: lane (r, q) loads row r's scale for window 4t + q once every four windows
- *       and the window's value comes from lane r + 16 (w % 4) by one ds_bpermute.
- * A wave owns G groups of 16 head rows (a chunk), so one A fragment from LDS feeds G x 4
- * MFMAs; chunks are dealt to waves blocks * 8 apart.  The codes of window w + 1 are in
- * flight while window w computes.  Bytes per head row: K codes + 2 or 4 per 128 columns
- * of scale (br = 1) -- the kernel is bound by HBM, the MFMAs run at a few percent.
- */
+ * The walk (logits_e4m3_kernel below): 16 head rows a chunk, in 256-wide windows; one
+ * buffer_load_dwordx4 a lane reads 4 head rows x 256 contiguous bytes ("the quad trick":
+ * MFMA A row i = (head row i % 4, K slot i / 4), B column j = (K slot j / 4, activation
+ * row j % 4), the products where the slots agree are used); activation rows staged once
+ * per workgroup in LDS; each chunk's scales in an LDS table; waves walk chunks
+ * blocks * waves apart with a register ring running across chunk boundaries.  n_embd off a
+ * multiple of 16, or x, codes or scale off the vector walk's alignment, take the same walk
+ * with every piece read by aligned dwords and funnel-shifted (UA). */
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 

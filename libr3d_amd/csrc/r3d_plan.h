@@ -298,7 +298,7 @@ struct LogitsPlan {
     float* Y;
     int sdt;                 /* scale element: 0 bf16, 1 f16, 2 f32 */
     int br;                  /* weight rows per scale row: 1 or 128 */
-    int mt;                  /* activation rows per pass (1..16); passes = ceil(M / mt) */
+    int mt;                  /* activation rows per pass (1..8); passes = ceil(M / mt) */
     int nwin;                /* 128-wide scale blocks along K */
     int nw_pad;              /* 256-wide code windows, padded to the ring's unroll */
     int xrow;                /* LDS pitch of one staged activation row, bytes */

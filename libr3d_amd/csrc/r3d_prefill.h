@@ -400,6 +400,16 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
                 issue_part(1, s + 3, cur);
                 read_a(nxt, 1);
             }
+#ifdef R3D_PF_SCHED
+            if (F8) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    /* the group's LDS reads */
+#pragma unroll
+                for (int k = 0; k < WNF; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, R3D_PF_SCHED, 0);
+                }
+            }
+#endif
             __builtin_amdgcn_sched_barrier(0);
         }
     };

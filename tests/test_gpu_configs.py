@@ -103,11 +103,21 @@ def test_c4_mxfp4_attention_shapes(gpu, shape):
     _grade(Y, A, AS, B, BS, K, "mxfp4a8", case="C4 %s M=4" % shape, row="gemm_nt_q_mxfp4_decode")
 
 
+def _all_written(Y):
+    """Every one of the M x N outputs was written (Y starts as the sentinel everywhere; the
+    oracle grades sampled rows, this holds all of them) and none is NaN (the config's
+    operands carry no NaN code or scale)."""
+    from tests import gpu_util as gu
+    assert not np.any(Y == gu.Y_SENTINEL), np.argwhere(Y == gu.Y_SENTINEL)[:8]
+    assert not np.any(np.isnan(O.bf16_to_f32(Y))), np.argwhere(np.isnan(O.bf16_to_f32(Y)))[:8]
+
+
 def test_c3_mxfp4_prefill_sampled(gpu):
     M, K, N = 2048, 5376, 21504
     _, A, AS = synth.activations(M, K, 0x5EED + 30)
     B, BS = synth.mxfp4_weights(N, K, 0x5EED + 31)
     Y = _run("gemm_nt_q_mxfp4", "mxfp4a8", A, AS, B, BS, M, N, K, gpu)
+    _all_written(Y)
     rows = np.sort(np.random.default_rng(3).choice(M, size=12, replace=False))
     _grade(Y[rows], A[rows], AS[rows], B, BS, K, "mxfp4a8", case="C3 mxfp4a8 (12 sampled rows)",
            row="gemm_nt_q_mxfp4")
@@ -152,6 +162,7 @@ def test_c3_shape_fp8a8_prefill_sampled(gpu, rblk):
     if rblk == 128:
         BS = BS[::128].copy()                 # one scale row per 128 weight rows
     Y = _run("gemm_nt_q_fp8a8", "fp8a8", A, AS, B, BS, M, N, K, gpu)
+    _all_written(Y)
     rows = np.sort(np.random.default_rng(5).choice(M, size=12, replace=False))
     _grade(Y[rows], A[rows], AS[rows], B, BS, K, "fp8a8", rblk,
            case="C3 shape fp8a8 rblk=%d (12 sampled rows)" % rblk, row="gemm_nt_q_fp8a8")

@@ -1,8 +1,8 @@
 """r3d_rad_gemm_nt_q_mxfp4a16_noalloc (run by pytest last): the mxfp4a16 row with its quantiser scratch in a
 static device buffer instead of RadArgs::scratch.  Through the C ABI it must give exactly
 the bytes of the allocating row on the same operands, on two calls in a row (the second
-smaller, over the first call's leftovers), and refuse a call whose scratch need passes the
-buffer (RAD_E_SHAPE, nothing launched)."""
+smaller, over the first call's leftovers), refuse a call whose scratch need passes the
+buffer (RAD_E_SHAPE, nothing launched), and leave the device's free memory unchanged."""
 import ctypes
 
 import numpy as np
@@ -70,3 +70,25 @@ def test_noalloc_refuses_past_the_buffer(gpu):
     torch.cuda.synchronize()
     assert rc == R.RAD_E_SHAPE
     assert np.all(gY.t.cpu().numpy().view(np.uint16) == gu.Y_SENTINEL)   # nothing launched
+
+
+@pytest.mark.gpu
+def test_noalloc_allocates_nothing(gpu):
+    """After a first call (which looks the device's buffer up and loads the kernels), calls
+    leave the device's free memory (hipMemGetInfo) and torch's allocated bytes unchanged:
+    the entry allocates nothing."""
+    M, N, K = 513, 1000, 1152
+    x, b, bs = _operands(M, N, K, 13, gpu)
+    y = torch.empty((M, N), dtype=torch.int16, device=gpu)
+    ops = R.GemmOperands(x, None, b, bs, y, dtype="mxfp4a16", N=N, K=K, group=32, M=M)
+    f = _noalloc()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert f(ctypes.byref(ops.args), stream) == R.RAD_OK
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    used0 = torch.cuda.memory_allocated()
+    for _ in range(3):
+        assert f(ctypes.byref(ops.args), stream) == R.RAD_OK
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0 and torch.cuda.memory_allocated() == used0, (free0, free1)
