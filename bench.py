@@ -5,7 +5,8 @@
 A "step" is one gemm_nt_q launch over one batch.  The headline workload is BASELINE's
 config 1 -- the fp8a8 W8A8 decode GEMV at M=1, K=5376, N=21504 -- read cold from HBM:
 the weight planes rotate over enough copies to exceed 1 GiB, well past the 256 MB
-Infinity Cache.  `value` is algorithmic bytes per step (weights + scales + activations +
+Infinity Cache; each copy is read once (a read-only stream) before the warm-up, as a
+serving loop's weights have been.  `value` is algorithmic bytes per step (weights + scales + activations +
 output, counted once) times steps over the wall time between two synchronised points.
 `roofline.achieved` divides the same bytes by the kernel's average duration measured with
 HIP events on the launch stream.  The headline times exactly --steps launches after
@@ -69,6 +70,22 @@ class Case:
         self.ops = [R.GemmOperands(self.a, self.as_, b, bs, self.y, dtype=dtype, N=N, K=K)
                     for b, bs in zip(self.b, self.bs)]
         self.scratch = None
+        self.sink = torch.zeros(4, dtype=torch.int32, device=dev)
+        self.touched = False
+
+    def touch(self, stream):
+        """Read every weight copy once (the library's read-only stream probe), so the timed
+        launches find the inputs resident as a serving loop's weights are: the first read
+        of a freshly written copy runs 25-80 % slower than every later one."""
+        if self.touched:
+            return
+        import libr3d_amd as R
+        L = R.lib()
+        for t in self.b + self.bs:
+            rc = L.r3d_gfx950_stream_probe(ctypes_ptr(t), t.numel() * t.element_size(), 8, 22,
+                                           ctypes_ptr(self.sink), ctypes_ptr_stream(stream))
+            assert rc == 0, rc
+        self.touched = True
 
     def hook_scratch(self, row):
         """Hand every call the launch scratch `row`'s hook asks for (one buffer: the calls
@@ -102,11 +119,15 @@ def time_case(case, row, steps, warmup, stream, min_s=EXTRA_MIN_S):
     import libr3d_amd as R
     launch = R.row_launcher(row)
     n = len(case.ops)
+    if hasattr(case, "touch"):   # rotated weight copies: read each once first
+        case.touch(stream)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()                  # the events' device objects exist before the timed region
+    e1.record()
     for i in range(warmup):
         rc = launch(case.ops[i % n], stream)
         assert rc == 0, "row %s refused: %d" % (row, rc)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
     if min_s:
         e0.record()
         for i in range(5):
@@ -350,7 +371,8 @@ def main():
         "data": "synthetic (seeded; BASELINE config 1 distributions)",
         "config": {"workload": "config 1: gemm_nt_q fp8a8 decode GEMV, M=1 K=5376 N=21504, "
                                "per-row bf16 weight scales, per-token a_scale, cold HBM "
-                               "(weights rotated over >1 GiB)",
+                               "(weights rotated over >1 GiB, each copy read once before "
+                               "the warm-up)",
                    "row": "gemm_nt_q_fp8a8_decode", "bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
