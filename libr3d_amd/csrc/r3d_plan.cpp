@@ -322,8 +322,12 @@ void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGe
 
 bool quad_fits(const GemmPlan& P) { return 8 * P.b_pitch < ((int64_t)1 << 31); }
 
-/* Quad geometry: split K until about env_quad_waves() waves are in flight, keeping >= 16
- * groups per chunk. */
+/* Quad geometry: split K until about env_quad_waves() waves are in flight (default 2048
+ * at one activation row, 1280 at 2..4), keeping >= 16 groups per chunk.  A split doubles
+ * the workgroups, and every workgroup stages the whole-K activation rows: at four rows
+ * those are as many bytes as a quarter of its weights (o, K = 4096 N = 5376, M = 4: 5.28 us
+ * unsplit against 6.11 split in two), while one row is cheap enough that more waves pay
+ * (C2 down, K = 21504 N = 5376, M = 1: 12.73 split against 13.06). */
 bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, QuadGeom* g,
                int xq) {
     if (M < 1 || M > 4 || N < 1 || K < 128 || K % 128 != 0) return false;
@@ -334,7 +338,7 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     g->groups = (int)(K / 128);
     g->quads = (N + 3) / 4;
     g->nblk = (N + 4 * g->qpw - 1) / (4 * g->qpw);
-    const int64_t target = env_quad_waves();
+    const int64_t target = env_quad_waves() > 0 ? env_quad_waves() : g->mt == 1 ? 2048 : 1280;
     int c = 1;
     if (force_chunks > 0) {
         c = (int)force_chunks;
@@ -1101,7 +1105,7 @@ int64_t env_quad_waves() {
     static const int64_t v = [] {
         const char* e = getenv("R3D_GFX950_QWAVES");
         const int64_t w = e ? (int64_t)atoll(e) : 0;
-        return w > 0 ? w : (int64_t)2048;
+        return w > 0 ? w : (int64_t)0;
     }();
     return v;
 }
