@@ -323,7 +323,8 @@ def main():
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream().cuda_stream
     if args.c3_only:
-        print(json.dumps(bench_c3(dev, stream, steps=args.steps, warmup=args.warmup)), flush=True)
+        print(json.dumps(bench_c3(dev, stream, steps=args.steps, warmup=args.warmup, min_s=None)),
+              flush=True)
         return
     if args.floors:
         print(json.dumps(bench_floors(dev, stream)), flush=True)
@@ -463,8 +464,8 @@ def main():
         del c
         torch.cuda.empty_cache()
         extra.update(bench_quant(dev, stream))
-        extra.update(bench_fused_decode(dev, stream, ksteps))
-        extra.update(bench_gated(dev, stream, ksteps))
+        extra.update(bench_fused_decode(dev, stream))
+        extra.update(bench_gated(dev, stream))
         extra.update(bench_skinny(dev, stream, ksteps))
         extra.update(bench_c4(dev, stream, steps=5))
         torch.cuda.empty_cache()
@@ -636,7 +637,7 @@ def bench_lm_head_e4m3(M, dev, stream, steps, warmup, res):
     return res
 
 
-def bench_c3(dev, stream, steps=10, warmup=3):
+def bench_c3(dev, stream, steps=10, warmup=3, min_s=EXTRA_MIN_S):
     """Config 3 as written: M=2048, K=5376, N=21504, mxfp4 weights (E8M0 exponents in
     [-8, 0]), bf16 N(0,1) activations quantised by the row itself to mxfp8 (e4m3 + E8M0
     per 32) -- gemm_nt_q_mxfp4a16, quantiser and GEMM both inside the timed launches."""
@@ -656,27 +657,31 @@ def bench_c3(dev, stream, steps=10, warmup=3):
     scratch = torch.empty(need, dtype=torch.uint8, device=dev)
     ops.set_scratch(scratch)
     launch = R.row_launcher("gemm_nt_q_mxfp4a16")
-    for _ in range(warmup):
-        assert launch(ops, stream) == 0
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(steps):
-        launch(ops, stream)
-    e1.record()
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) * 1e-3 / steps
+    assert launch(ops, stream) == 0
+    if min_s:
+        t, n = time_min(lambda i: launch(ops, stream), min_s, warm=warmup)
+    else:                        # exactly `steps` launches after `warmup` (profiling runs)
+        for _ in range(warmup):
+            launch(ops, stream)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            launch(ops, stream)
+        e1.record()
+        torch.cuda.synchronize()
+        t, n = e0.elapsed_time(e1) * 1e-3 / steps, steps
     tf = 2.0 * M * N * K / t / 1e12
     log("[bench] C3 mxfp4a16 prefill (quantiser + GEMM): %.1f us, %.1f TFLOP/s (%.1f%% of fp8 dense)"
         % (t * 1e6, tf, 100 * tf / FP8_PEAK_TFLOPS))
-    return {"c3_mxfp4a16_prefill": {"M": M, "K": K, "N": N, "op_us": round(t * 1e6, 1),
+    return {"c3_mxfp4a16_prefill": {"M": M, "K": K, "N": N, "op_us": round(t * 1e6, 1), "launches": n,
                                     "TFLOPs": round(tf, 1),
                                     "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
                                     "includes": "bf16->mxfp8 quantiser + block-scaled MFMA GEMM"}}
 
 
-def bench_quant(dev, stream, steps=50):
+def bench_quant(dev, stream):
     """The quant_act_fp8 producer (bf16 in, e4m3 codes + f32 scale per 128 out) on the
     configs' activation shapes: config 3's 2048 x 5376 and a decode step's 4 x 5376."""
     import torch
@@ -689,17 +694,8 @@ def bench_quant(dev, stream, steps=50):
         s = torch.empty((M, n // g), dtype=torch.float32, device=dev)
         ops = R.QuantActOperands(x, q, s, n=n, group=g, M=M, x_dtype="BF16")
         f = R.row_launcher("quant_act_fp8_act")
-        for _ in range(3):
-            assert f(ops, stream) == 0
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(steps):
-            f(ops, stream)
-        e1.record()
-        torch.cuda.synchronize()
-        t = e0.elapsed_time(e1) * 1e-3 / steps
+        assert f(ops, stream) == 0
+        t, _ = time_min(lambda i: f(ops, stream), EXTRA_MIN_S)
         nb = M * n * 2 + M * n + M * (n // g) * 4
         res["quant_act_fp8_M%d" % M] = {"n": n, "group": g, "kernel_us": round(t * 1e6, 2),
                                          "GBps": round(nb / t / 1e9, 1),
@@ -711,15 +707,8 @@ def bench_quant(dev, stream, steps=50):
         o = torch.empty((M, n), dtype=torch.int16, device=dev)
         rops = R.RmsNormQuantOperands(x, r, w, q, s, o, n=n, group=g, M=M)
         fr = R.row_launcher("rmsnorm_quant_fp8")
-        for _ in range(3):
-            assert fr(rops, stream) == 0
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(steps):
-            fr(rops, stream)
-        e1.record()
-        torch.cuda.synchronize()
-        t = e0.elapsed_time(e1) * 1e-3 / steps
+        assert fr(rops, stream) == 0
+        t, _ = time_min(lambda i: fr(rops, stream), EXTRA_MIN_S)
         nb = M * n * 2 * 4 + n * 4 + M * n + M * (n // g) * 4    # x, residual in/out, out, w, q, s
         res["rmsnorm_quant_fp8_M%d" % M] = {"n": n, "group": g, "kernel_us": round(t * 1e6, 2),
                                              "GBps": round(nb / t / 1e9, 1)}
@@ -728,17 +717,21 @@ def bench_quant(dev, stream, steps=50):
     return res
 
 
-def bench_fused_decode(dev, stream, steps=50):
+def bench_fused_decode(dev, stream):
     """A decode call fed bf16 activations, two ways, cold weights: the quant_act_fp8 row then
     the decode row (two launches), and the decode row taking the bf16 rows itself (the
-    producer fused into its LDS staging, one launch; M = 1 only).  Config 1's shape (fp8a8) and
-    config 2's gate_up (mxfp4a8)."""
+    producer fused into its LDS staging, one launch: the default at M = 1, the rows' "fuse"
+    tunable at M = 4).  Config 1's shape (fp8a8), config 2's gate_up (mxfp4a8) and C4's o
+    (mxfp4a8, K = 4096 N = 5376)."""
     import torch
     import libr3d_amd as R
     from libr3d_amd import synth
     res = {}
     for name, dtype, M, K, N in (("c1_fp8a8_M1", "fp8a8", 1, 5376, 21504),
-                                 ("c2_mxfp4_gate_up_M1", "mxfp4a8", 1, 5376, 21504)):
+                                 ("c2_mxfp4_gate_up_M1", "mxfp4a8", 1, 5376, 21504),
+                                 ("c1_fp8a8_M4", "fp8a8", 4, 5376, 21504),
+                                 ("c2_mxfp4_gate_up_M4", "mxfp4a8", 4, 5376, 21504),
+                                 ("c4_mxfp4_o_M4", "mxfp4a8", 4, 4096, 5376)):
         if dtype == "fp8a8":
             B, BS = synth.fp8_weights(N, K, 0x5EED + 11)
             BS = BS.view(np.int16)
@@ -758,21 +751,13 @@ def bench_fused_decode(dev, stream, steps=50):
         y = torch.empty((M, N), dtype=torch.int16, device=dev)
         qa = R.QuantActOperands(x, q, sc, n=K, group=128, M=M, x_dtype="BF16")
         two = [R.GemmOperands(q, sc, b, s_, y, dtype=dtype, N=N, K=K) for b, s_ in zip(bs, bss)]
-        one = [R.GemmOperands(x, None, b, s_, y, dtype=dtype, N=N, K=K) for b, s_ in zip(bs, bss)]
+        tv = [("fuse", 1)] if M > 1 else None
+        one = [R.GemmOperands(x, None, b, s_, y, dtype=dtype, N=N, K=K, tunables=tv)
+               for b, s_ in zip(bs, bss)]
         fq, fg = R.row_launcher("quant_act_fp8_act"), R.row_launcher(row)
 
         def timed(body):
-            for i in range(10):
-                body(i)
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            e0.record()
-            for i in range(steps):
-                body(i)
-            e1.record()
-            torch.cuda.synchronize()
-            return e0.elapsed_time(e1) * 1e-3 / steps
+            return time_min(body, EXTRA_MIN_S)[0]
 
         def unfused(i):
             assert fq(qa, stream) == 0 and fg(two[i % copies], stream) == 0
@@ -791,7 +776,7 @@ def bench_fused_decode(dev, stream, steps=50):
     return res
 
 
-def bench_gated(dev, stream, steps=50):
+def bench_gated(dev, stream):
     """gemm_nt_q_gated at fp8a8 on config 1's plane read as a gate_up pair (N = 2n = 21504,
     K = 5376, per-row weight scales, cold), silu: the gated row against its two rows
     (gemm_nt_q, then gated_quant_fp8) at M = 1 and 4 -- the same kernels, so the gap is the
@@ -827,17 +812,7 @@ def bench_gated(dev, stream, steps=50):
                       ("gemm_nt_q_gated_fp8a8", "gemm_nt_q_fp8a8_decode", "gated_quant_fp8_act"))
 
         def timed(body):
-            for i in range(10):
-                body(i)
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            e0.record()
-            for i in range(steps):
-                body(i)
-            e1.record()
-            torch.cuda.synchronize()
-            return e0.elapsed_time(e1) * 1e-3 / steps
+            return time_min(body, EXTRA_MIN_S)[0]
 
         def one(i):
             assert fg(fused[i % copies], stream) == 0

@@ -54,6 +54,11 @@ class RadTunableValue(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("value", ctypes.c_longlong)]
 
 
+class RadTunable(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("values", ctypes.POINTER(ctypes.c_longlong)),
+                ("n_values", ctypes.c_int), ("def", ctypes.c_int), ("prose", ctypes.c_char_p)]
+
+
 class RadArgs(ctypes.Structure):
     _fields_ = [("t", ctypes.POINTER(RadTensor)), ("n_t", ctypes.c_int),
                 ("p", ctypes.POINTER(RadParam)), ("n_p", ctypes.c_int),
@@ -76,7 +81,7 @@ class RadKernelInfo(ctypes.Structure):
                 ("summary", ctypes.c_char_p), ("limits", ctypes.c_char_p),
                 ("formats", ctypes.c_char_p), ("domain", ctypes.c_int),
                 ("priority", ctypes.c_int), ("constraints", ctypes.POINTER(RadConstraint)),
-                ("n_constraints", ctypes.c_int), ("tunables", ctypes.c_void_p),
+                ("n_constraints", ctypes.c_int), ("tunables", ctypes.POINTER(RadTunable)),
                 ("n_tunables", ctypes.c_int), ("replaces", ctypes.c_char_p),
                 ("init", ctypes.c_void_p), ("fini", ctypes.c_void_p), ("launch", ctypes.c_void_p),
                 ("scratch", ctypes.c_void_p), ("layout", ctypes.c_void_p),
@@ -231,8 +236,9 @@ def rows():
         k = L.rad_kernel_at(i).contents
         cons = [(_s(k.constraints[c].key), k.constraints[c].op, k.constraints[c].ival,
                  _s(k.constraints[c].sval)) for c in range(k.n_constraints)]
+        tun = [_s(k.tunables[t].name) for t in range(k.n_tunables)]
         out.append({"name": _s(k.name), "op": _s(k.op), "priority": k.priority,
-                    "domain": k.domain, "constraints": cons, "launch": k.launch,
+                    "domain": k.domain, "constraints": cons, "tunables": tun, "launch": k.launch,
                     "scratch": k.scratch, "layout": k.layout, "relayout": k.relayout,
                     "opd_shape": k.opd_shape, "unrelayout": k.unrelayout})
     return out

@@ -89,7 +89,6 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
     /* mxfp4 scale rows contiguous (pitch = K/32) in a 16-byte aligned plane: 1 KB staging loads */
     const int sc16 = P.enc == ENC_MXFP4A8 && P.bs_pitch == P.K / 32 &&
                      ((uintptr_t)P.BS & 15) == 0;
-    if (P.xq && g.mt != 1) return RAD_E_UNSUPPORTED;    /* the fused producer is MT = 1 only */
     if ((g.wv != 4 && g.wv != 7 && g.wv != 8) || (g.qpw == 2 && g.wv != 4) ||
         (g.wv == 7 && (g.chunks != 1 || P.xq)))
         return RAD_E_UNSUPPORTED;
@@ -101,8 +100,8 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
                        g.chunks, P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, sc16,        \
                        P.a_pitch, P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch)
 #define R3D_QUAD(ENC_, MT_, D_)                                                              \
-    if (P.xq && g.wv == 8) R3D_QUADW(ENC_, MT_, 1, D_, (MT_ == 1), 8);                       \
-    else if (P.xq) R3D_QUAD1(ENC_, MT_, 1, D_, (MT_ == 1));                                  \
+    if (P.xq && g.wv == 8) R3D_QUADW(ENC_, MT_, 1, D_, 1, 8);                                \
+    else if (P.xq) R3D_QUAD1(ENC_, MT_, 1, D_, 1);                                           \
     else if (g.qpw == 2) R3D_QUAD1(ENC_, MT_, 2, D_, 0);                                     \
     else if (g.wv == 8) R3D_QUADW(ENC_, MT_, 1, D_, 0, 8);                                   \
     else if (g.wv == 7) R3D_QUADW(ENC_, MT_, 1, D_, 0, 7);                                   \

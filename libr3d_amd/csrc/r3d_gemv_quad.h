@@ -230,14 +230,14 @@ __global__ __launch_bounds__(64 * WV) void gemv_quad_kernel(
      * amax * (1/448)), q = e4m3_rne(clamp(x * (1 / sc), +-448)) -- the codes and scales the
      * quant_act_fp8 row writes, so the products are those of the unfused pair.  A lane takes
      * one 16-byte chunk (8 values) of the [MT][K / 8] chunk space per block of 64 chunks; a
-     * group is 16 consecutive chunks, i.e. 16 lanes, reduced by 4 xor-shuffles.  Wave w
-     * takes blocks w, w + 4, ...; XU blocks per batch, the first batch's loads issued
-     * before the weight ring is primed (so waiting for them never waits for weights).  One
-     * batch covers K <= 2048 * WV; a longer K takes more batches, whose loads wait behind
-     * the ring's.  MT = 1 only: every workgroup re-reads the bf16 rows (twice the bytes of the
-     * e4m3 images) and re-quantises them, which at MT = 4 costs more than the separate
-     * producer launch it saves. */
-    static_assert(!XQ || MT == 1, "the fused producer is built for one activation row");
+     * group is 16 consecutive chunks, i.e. 16 lanes, reduced by 4 xor-shuffles (a row's
+     * K / 8 chunks are whole groups, so no group straddles two rows).  Wave w takes blocks
+     * w, w + WV, ...; XU blocks per batch, the first batch's loads issued before the weight
+     * ring is primed (so waiting for them never waits for weights).  One batch covers
+     * MT * K <= 2048 * WV; more takes further batches, whose loads wait behind the ring's.
+     * Every workgroup re-reads the bf16 rows (twice the bytes of the e4m3 images) and
+     * re-quantises them: at MT = 4 that costs more than the producer launch it saves at the
+     * benchmark shapes, so the plan takes MT = 4 only when the engine asks (tunable "fuse"). */
     constexpr int XU = XQ ? 4 : 1;
     const int cpr = K >> 3, nchunk = MT * cpr;
     const int nxb = (nchunk + 63) >> 6;

@@ -96,7 +96,7 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     if (N <= 0 || K <= 0 || M <= 0) return RAD_E_SHAPE;
     if (M > kDimMax || N > kDimMax || K > kDimMax) return RAD_E_SHAPE;
     if (rad_tensor_numel(A) < M * K || rad_tensor_numel(B) < N * K) return RAD_E_SHAPE;
-    if (xq && M != 1) return RAD_E_UNSUPPORTED;    /* fused producer: M = 1 only */
+    if (xq && M > (decode_fuse(a) ? 4 : 1)) return RAD_E_UNSUPPORTED;   /* fused producer */
 
     /* Scale grids derived from the operands, then pinned to b 32 / a 128. */
     if (BS->rank != 2 || BS->stride[1] != 1 || BS->shape[0] < N) return RAD_E_UNSUPPORTED;
@@ -235,7 +235,7 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
     if (M <= 0) return RAD_E_SHAPE;
     if (M > kDimMax || N > kDimMax || K > kDimMax) return RAD_E_SHAPE;
     if (rad_tensor_numel(A) < M * K || rad_tensor_numel(B) < N * K) return RAD_E_SHAPE;
-    if (xq && M != 1) return RAD_E_UNSUPPORTED;    /* fused producer: M = 1 only */
+    if (xq && M > (decode_fuse(a) ? 4 : 1)) return RAD_E_UNSUPPORTED;   /* fused producer */
 
     if (BS->rank != 2 || BS->stride[1] != 1) return RAD_E_UNSUPPORTED;
     if (!xq && (AS->rank != 2 || AS->stride[1] != 1 || AS->shape[0] < M)) return RAD_E_UNSUPPORTED;
@@ -1159,6 +1159,13 @@ int env_quad_depth(int enc) {
     }();
     (void)enc;   /* 4 steps measured best for both encodings on MI355X at the 27B shapes */
     return v > 0 ? v : 4;
+}
+
+bool decode_fuse(const RadArgs* a) {
+    if (a && a->tv)
+        for (int i = 0; i < a->n_tv; ++i)
+            if (a->tv[i].name && strcmp(a->tv[i].name, "fuse") == 0) return a->tv[i].value > 0;
+    return false;
 }
 
 int64_t decode_splitk(const RadArgs* a) {

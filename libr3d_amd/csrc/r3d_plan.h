@@ -28,9 +28,9 @@ struct GemmPlan {
                                                                 (mxfp4a16 A: elements) */
     int as_cols, bs_cols;
     int rblk;                /* fp8a8 weight-scale rows per scale row: 1 or 128 */
-    int xq;                  /* decode rows at M = 1: A is a bf16 row (a_pitch bytes), AS
-                                absent -- quantised in the kernel with quant_act_fp8's
-                                arithmetic */
+    int xq;                  /* decode rows at M = 1 (M <= 4 with the "fuse" tunable): A is
+                                bf16 rows (a_pitch bytes), AS absent -- quantised in the
+                                kernel with quant_act_fp8's arithmetic */
     uint8_t* scratch;        /* mxfp4a16: e4m3 codes [M, K] then E8M0 [M, K/32] */
     int ua;                  /* operands off the fast arms' alignment: UA_GEMM -- A, B or a
                                 scale plane (the any-alignment GEMM, r3d_gemm_any.h, takes the
@@ -108,8 +108,10 @@ int64_t grid_block(int64_t ext, int64_t blocks);
 int64_t row_stride(const RadTensor* t, int64_t cols);
 
 /* Format gates (src/r3d_gemm_mxfp4.hip:1521-1582 and src/r3d_gemm_fp8a8.hip:852-924)
- * plus this build's gfx950 gates: K % 128 == 0 and 16-byte aligned A/B bases and
- * pitches.  M must already be numel(Y)/N.  Returns RAD_OK or the refusal code. */
+ * plus this build's gfx950 gate K % 128 == 0.  Operands off the fast arms' alignment
+ * (16-byte A/B bases and pitches, 4-byte mxfp4 / 2-byte fp8 scale planes, 4-byte
+ * a_scale) set ua = UA_GEMM: the any-alignment arm.  M must already be numel(Y)/N.
+ * Returns RAD_OK or the refusal code. */
 int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P);
 int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P);
 /* The bf16-in mxfp4 row: A bf16 [M, K], a_scale absent, weights as mxfp4a8, and launch
@@ -358,6 +360,9 @@ int env_lines_tw();         /* R3D_GFX950_LTW: 16-row tiles per wave of the line
 /* The decode rows' "splitk" tunable (RadArgs::tv): chunks per tile, 0 = the policy.  An
  * engine-chosen value wins over R3D_GFX950_SPLITK. */
 int64_t decode_splitk(const RadArgs* a);
+/* The decode rows' "fuse" tunable: 1 lets a bf16 activation call at M = 2..4 quantise
+ * inside the quad GEMV (default 0: only M = 1 is fused; the engine runs the producer). */
+bool decode_fuse(const RadArgs* a);
 
 /* Human-readable plan + geometry for `row` without launching anything. */
 int describe(const char* row, const RadArgs* a, char* buf, int len);

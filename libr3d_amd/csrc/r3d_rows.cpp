@@ -250,12 +250,17 @@ const RadConstraint cLogitsRow[] = {
 
 enum { kPrioTile = 1000, kPrioDecode = 1100 };
 
-/* The decode rows' split-K lever: waves per 16-row weight tile (0 = the library's policy,
- * which targets ~2048 waves in flight). */
+/* The decode rows' levers: split K (waves per weight tile; 0 = the library's policy,
+ * which targets ~1280-2048 waves in flight) and the fused producer beyond one row. */
 const long long kSplitKValues[] = {0, 1, 2, 4, 8};
+const long long kFuseValues[] = {0, 1};
 const RadTunable tSplitK[] = {
     {"splitk", kSplitKValues, 5, 0,
      "K chunks per 16-row weight tile, folded through LDS in chunk order; 0 = fill the CUs"},
+    {"fuse", kFuseValues, 2, 0,
+     "1: bf16 activations (no a_scale) at M = 2..4 are quantised inside the quad GEMV like "
+     "the M = 1 call; 0: refused there, so the engine runs quant_act_fp8 first (measured "
+     "faster at the 27B decode shapes)"},
 };
 
 const RadKernelInfo kRows[] = {
@@ -265,9 +270,10 @@ const RadKernelInfo kRows[] = {
      "fed to v_mfma_scale_f32_16x16x128_f8f6f4 as is, e4m3 activations, one MFMA per "
      "128-of-K activation group scaled by a_scale in f32; up to M = 128 on a narrow N, K "
      "split across workgroups into f32 partials in launch scratch, summed in chunk order",
-     "K a multiple of 128; 16-byte aligned A/B bases and A pitch; ragged M/N tiles clamp "
-     "their loads and are never stored; M derives from numel(y)/N; scratch optional (the "
-     "hook sizes the split's partials; without them the unsplit arms run)",
+     "K a multiple of 128; operands at any alignment (off 16 bytes: the dword-walk arm); "
+     "ragged M/N tiles clamp their loads and are never stored; M derives from numel(y)/N; "
+     "scratch optional (the hook sizes the split's partials; without them the unsplit arms "
+     "run)",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), e2m1 b with E8M0 b_scale per (row, 32 K), "
      "bf16 y; b_ref accepted and ignored; a_sum refused",
      RAD_DOMAIN_DEVICE, kPrioTile, cMxfp4Tile, 2, nullptr, 0, nullptr,
@@ -285,7 +291,7 @@ const RadKernelInfo kRows[] = {
      "scratch optional (the hook sizes the split's partials; without them the GEMVs run)",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), e2m1 b with E8M0 b_scale per (row, 32 K), "
      "bf16 y; b_ref accepted and ignored; a_sum refused",
-     RAD_DOMAIN_DEVICE, kPrioDecode, cMxfp4Decode, 3, tSplitK, 1, nullptr,
+     RAD_DOMAIN_DEVICE, kPrioDecode, cMxfp4Decode, 3, tSplitK, 2, nullptr,
      nullptr, nullptr, r3d_rad_gemm_nt_q_mxfp4_decode, r3d_rad_gemm_nt_q_mxfp4_decode_scratch,
      nullptr, nullptr, nullptr, nullptr},
 
@@ -294,9 +300,10 @@ const RadKernelInfo kRows[] = {
      "direct-to-LDS ring, e4m3 on both operands, one MFMA per 128-of-K scale group flushed as "
      "(sub * a_scale) * b_scale in the oracle's order; up to M = 128 on a narrow N, K split "
      "across workgroups into f32 partials in launch scratch, summed in chunk order",
-     "K a multiple of 128; 16-byte aligned A/B bases and pitches; b_scale either the 128x128 "
-     "block grid or a per-row grid; M derives from numel(y)/N; scratch optional (the hook "
-     "sizes the split's partials; without them the unsplit arms run)",
+     "K a multiple of 128; operands at any alignment (off 16 bytes: the dword-walk arm); "
+     "b_scale either the 128x128 block grid or a per-row grid; M derives from numel(y)/N; "
+     "scratch optional (the hook sizes the split's partials; without them the unsplit arms "
+     "run)",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), fp8_e4m3 b with bf16 scale per 128x128 "
      "tile (or per row), bf16 y; a_sum and b_ref refused",
      RAD_DOMAIN_DEVICE, kPrioTile, cFp8Tile, 3, nullptr, 0, nullptr,
@@ -313,7 +320,7 @@ const RadKernelInfo kRows[] = {
      "grid; scratch optional (the hook sizes the split's partials; without them the GEMVs run)",
      "fp8_e4m3 a with f32 a_scale per (row, 128 K), fp8_e4m3 b with bf16 scale per 128x128 "
      "tile (or per row), bf16 y; a_sum and b_ref refused",
-     RAD_DOMAIN_DEVICE, kPrioDecode, cFp8Decode, 4, tSplitK, 1, nullptr,
+     RAD_DOMAIN_DEVICE, kPrioDecode, cFp8Decode, 4, tSplitK, 2, nullptr,
      nullptr, nullptr, r3d_rad_gemm_nt_q_fp8_decode, r3d_rad_gemm_nt_q_fp8_decode_scratch,
      nullptr, nullptr, nullptr, nullptr},
 
@@ -323,8 +330,9 @@ const RadKernelInfo kRows[] = {
      "v_mfma_scale_f32_16x16x128_f8f6f4, which accumulates in place; up to 256 x 256 "
      "output tile per workgroup over a three-deep direct-to-LDS ring",
      "K a multiple of 128; a_scale absent; launch scratch >= M*K (rounded to 256) + M*K/32 "
-     "bytes, 16-byte aligned (the row's scratch hook sizes it from M and K); A rows 16-byte "
-     "aligned; M derives from numel(y)/N",
+     "bytes, 16-byte aligned (the row's scratch hook sizes it from M and K); A and B at any "
+     "alignment (off 16 bytes: the element-wise quantiser / dword-walk arm); M derives from "
+     "numel(y)/N",
      "bf16 a, e2m1 b with E8M0 b_scale per (row, 32 K), bf16 y; b_ref accepted and ignored; "
      "a_scale and a_sum refused",
      RAD_DOMAIN_DEVICE, kPrioTile, cMxfp4A16, 2, nullptr, 0, nullptr,

@@ -47,6 +47,9 @@ static int layout(void) {
     FIELD(RadArgs, t); FIELD(RadArgs, n_t); FIELD(RadArgs, p); FIELD(RadArgs, n_p);
     FIELD(RadArgs, tv); FIELD(RadArgs, n_tv); FIELD(RadArgs, scratch);
     FIELD(RadArgs, scratch_bytes); FIELD(RadArgs, flags);
+    printf("\"sizeof.RadTunable\": %zu, ", sizeof(RadTunable));
+    FIELD(RadTunable, name); FIELD(RadTunable, values); FIELD(RadTunable, n_values);
+    FIELD(RadTunable, def); FIELD(RadTunable, prose);
     printf("\"sizeof.RadConstraint\": %zu, ", sizeof(RadConstraint));
     FIELD(RadConstraint, key); FIELD(RadConstraint, op); FIELD(RadConstraint, ival);
     FIELD(RadConstraint, sval);

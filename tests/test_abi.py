@@ -552,6 +552,28 @@ def test_fused_producer_plan(dtype, row):
     assert R.describe(tile, _xq_ops(dtype, 64, 512, 1024))[0] == R.RAD_E_UNSUPPORTED
 
 
+@pytest.mark.parametrize("dtype,row", [("mxfp4a8", "gemm_nt_q_mxfp4_decode"),
+                                       ("fp8a8", "gemm_nt_q_fp8a8_decode")])
+def test_fused_producer_beyond_one_row_on_request(dtype, row):
+    """The "fuse" tunable extends the fused producer to M = 2..4 (the quad GEMV's four
+    activation images), and only there: M = 5.. stays refused, as do shapes whose four
+    whole-K rows the workgroup cannot stage (K = 21504), and "fuse" = 0 is the default."""
+    fuse = [("fuse", 1)]
+    for M, N, K in [(2, 64, 256), (3, 5376, 4096), (4, 21504, 5376), (4, 2048, 5376)]:
+        rc, d = R.describe(row, _xq_ops(dtype, M, N, K, tunables=fuse))
+        assert rc == R.RAD_OK, (M, N, K, d)
+        g = _geom(d)
+        assert g["kernel"] == "quad" and g["xq"] == "1" and g["mt"] == "4", d
+        assert R.describe(row, _xq_ops(dtype, M, N, K, tunables=[("fuse", 0)]))[0] == \
+            R.RAD_E_UNSUPPORTED
+    for ops in (_xq_ops(dtype, 5, 512, 1024, tunables=fuse),
+                _xq_ops(dtype, 16, 512, 1024, tunables=fuse),
+                _xq_ops(dtype, 4, 5376, 21504, tunables=fuse)):
+        assert R.describe(row, ops)[0] == R.RAD_E_UNSUPPORTED
+    names = [t for r in R.rows() if r["name"] == row for t in r.get("tunables", [])]
+    assert names == ["splitk", "fuse"], names
+
+
 _QWV_SCRIPT = r"""
 import sys
 sys.path.insert(0, %r)

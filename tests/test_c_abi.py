@@ -15,7 +15,7 @@ import libr3d_amd as R
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HARNESS = os.path.join(ROOT, "tests", "c_abi", "abi_harness")
 
-MIRRORS = ["RadTensor", "RadParam", "RadTunableValue", "RadArgs", "RadConstraint",
+MIRRORS = ["RadTensor", "RadParam", "RadTunableValue", "RadTunable", "RadArgs", "RadConstraint",
            "RadKernelInfo", "RadParamSpec", "RadOperandSpec", "RadOpSchema", "RadPluginInfo",
            "RadEncPlane", "RadEncoding", "RadLayout", "RadPlanesHeader", "RadPlanesEntry"]
 

@@ -4,9 +4,10 @@ products (src/r3d_gemm_mxfp4.hip:14-15, src/r3d_gemm_fp8a8.hip:9-15).
 
 Two bars: (1) Y bit-identical to the unfused pair -- the quant_act_fp8 row, then the same
 decode row on its codes and scales; (2) Y within the GEMM bar of the oracle's composition
-(oracle quant_act_fp8, then the oracle GEMM).  The fused path is the M = 1 decode call; shapes cover one
-and several producer batches per wave (K past 8192), split K, a padded activation view, and
-special values (an all-zero group, subnormals, an outlier, an Inf, a NaN).
+(oracle quant_act_fp8, then the oracle GEMM).  The fused path is the M = 1 decode call, and
+M = 2..4 when the engine sets the rows' "fuse" tunable; shapes cover one and several
+producer batches per wave (K past 8192), split K, a padded activation view, and special
+values (an all-zero group, subnormals, an outlier, an Inf, a NaN).
 """
 import numpy as np
 import pytest
@@ -124,3 +125,30 @@ def test_fused_decode_special_values(gpu, dtype):
         xs[0, pos] = bits
         Y = _check(dtype, xs, N, K, gpu, seed=5)
         assert np.isnan(O.bf16_to_f32(Y)).all(), pos
+
+
+@pytest.mark.parametrize("dtype", ["mxfp4a8", "fp8a8"])
+@pytest.mark.parametrize("M", [2, 3, 4])
+@pytest.mark.parametrize("N,K", [(21504, 5376), (2048, 5376), (5376, 4096), (100, 128),
+                                 (3000, 8192)])
+def test_fused_decode_rows_on_request(gpu, dtype, M, N, K):
+    """The "fuse" tunable: M = 2..4 bf16 rows quantised in the quad GEMV's four activation
+    images (one producer batch per wave up to M K = 16384, two beyond), bit-identical to
+    the producer row followed by the decode row."""
+    _check(dtype, _x(M, K, 31 * M + K), N, K, gpu, seed=M + N, tunables=[("fuse", 1)])
+
+
+@pytest.mark.parametrize("dtype", ["mxfp4a8", "fp8a8"])
+def test_fused_decode_rows_view_split_values(gpu, dtype):
+    fuse = [("fuse", 1)]
+    _check(dtype, _x(3, 2048, 41), 512, 2048, gpu, pitch=2048 + 64, tunables=fuse)
+    _check(dtype, _x(4, 4096, 42), 768, 4096, gpu, tunables=fuse + [("splitk", 4)])
+    x = _x(4, 1024, 43).copy()
+    x[1, :128] = 0                                                    # an all-zero group
+    x[2, 300] = synth.bf16_bits(np.array([3.0e4], np.float32))[0]     # an outlier
+    Y = _check(dtype, x, 384, 1024, gpu, seed=9, tunables=fuse)
+    assert not np.isnan(O.bf16_to_f32(Y)).any()
+    x[3, 700] = 0x7FC0                                                # a NaN poisons row 3 only
+    Y = _check(dtype, x, 384, 1024, gpu, seed=9, tunables=fuse)
+    Yf = O.bf16_to_f32(Y)
+    assert np.isnan(Yf[3]).all() and not np.isnan(Yf[:3]).any()
