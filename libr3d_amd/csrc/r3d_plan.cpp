@@ -392,7 +392,11 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
         /* the deepest supported ring that no wave's step count falls below */
         static const int kDepths[] = {8, 4, 2, 1};
         const int ns_min = (g->groups / c + 3) / 4;
-        const int want = env_quad_depth(enc);
+        /* four steps, or eight at mxfp4a8 where every wave walks 16+ steps (one 1 KB load
+         * a step, so eight fit its registers at full occupancy): C2 down at M = 1, 21 steps
+         * a chunk, 12.86 -> 12.59 us; at 11 steps (gate_up, config 1) two to eight tie */
+        const int want = env_quad_depth(enc) > 0 ? env_quad_depth(enc)
+                       : enc == ENC_MXFP4A8 && ns_min >= 16 ? 8 : 4;
         g->depth = 1;
         for (int d : kDepths)
             if (d <= want && d <= ns_min) { g->depth = d; break; }
@@ -1157,8 +1161,8 @@ int env_quad_depth(int enc) {
         const char* e = getenv("R3D_GFX950_QD");
         return e ? atoi(e) : 0;
     }();
-    (void)enc;   /* 4 steps measured best for both encodings on MI355X at the 27B shapes */
-    return v > 0 ? v : 4;
+    (void)enc;
+    return v > 0 ? v : 0;   /* 0: the policy in quad_geom */
 }
 
 bool decode_fuse(const RadArgs* a) {

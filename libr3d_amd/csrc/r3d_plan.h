@@ -350,7 +350,7 @@ bool env_no_fp8_dec();      /* R3D_NO_FP8_DEC: the fp8a8 decode row */
 bool env_debug();           /* R3D_DEBUG_GEMM: one stderr line per distinct launch arm */
 int64_t env_splitk();       /* R3D_GFX950_SPLITK: force the decode chunk count (0 = policy) */
 int64_t env_quad_waves();   /* R3D_GFX950_QWAVES: waves the quad split aims for (0: unset) */
-int env_quad_depth(int enc);/* R3D_GFX950_QD: quad ring depth 1/2/4/8 (default 4) */
+int env_quad_depth(int enc);/* R3D_GFX950_QD: quad ring depth 1/2/4/8 (0: unset, the policy) */
 int env_quad_qpw();         /* R3D_GFX950_QPW: quads per wave of the quad GEMV, 1 or 2 (default 1) */
 int env_quad_wv();          /* R3D_GFX950_QWV: waves per quad-GEMV workgroup, 4 or 8 (0: policy) */
 int64_t env_lines_waves();  /* R3D_GFX950_LWAVES: waves the line GEMV's split aims for (default 4096) */
