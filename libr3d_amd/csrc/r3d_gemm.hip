@@ -210,8 +210,12 @@ static hipError_t wide_launch(const GemmPlan& P, const WideGeom& w, int kc, floa
 /* The in-order sum of kc f32 partial planes of M x N at part into bf16 Y. */
 static hipError_t splitk_reduce(const GemmPlan& P, int kc, const float* part, hipStream_t stream) {
     const int64_t lanes = P.M * ((P.N + 3) / 4);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
-                       stream, part, kc, (int)P.M, (int)P.N, P.Y, P.y_pitch);
+    if (lanes <= 32768)
+        hipLaunchKernelGGL((splitk_reduce_kernel<64, 16>), dim3((unsigned)((lanes + 63) / 64)),
+                           dim3(64), 0, stream, part, kc, (int)P.M, (int)P.N, P.Y, P.y_pitch);
+    else
+        hipLaunchKernelGGL((splitk_reduce_kernel<256, 4>), dim3((unsigned)((lanes + 255) / 256)),
+                           dim3(256), 0, stream, part, kc, (int)P.M, (int)P.N, P.Y, P.y_pitch);
     return hipGetLastError();
 }
 

@@ -583,28 +583,34 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
 }
 
 /* Split K's second kernel: Y[m, n] = bf16(sum over c = 0 .. kc-1 of part[c][m][n]), the
- * chunks added in order from +0 (so every call sums the same way), four columns a lane;
- * the chunk loads go out four at a time ahead of their adds. */
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+ * chunks added in order from +0 (so every call sums the same way), four columns a lane.
+ * BATCH chunk loads go out together ahead of their adds; TH lanes a workgroup.  A
+ * decode-sized Y (a few thousand lanes) takes <64, 16>: its planes, written by the kernel
+ * just before on other CUs, are read from memory once for up to 16 chunks, over many CUs
+ * (C2 down at M = 4: the split call 15.80 -> 15.48 us).  A larger Y (M = 16..64) has the
+ * lanes to hide the latency and keeps <256, 4>, whose fewer registers a lane measured
+ * 1-2 % faster there. */
+template <int TH, int BATCH>
+__global__ __launch_bounds__(TH) void splitk_reduce_kernel(
     const float* __restrict__ part, int kc, int M, int N, uint16_t* __restrict__ Y,
     int64_t y_pitch) {
     const int cpr = (N + 3) >> 2;
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t e = (int64_t)blockIdx.x * TH + threadIdx.x;
     if (e >= (int64_t)M * cpr) return;
     const int m = (int)(e / cpr), n = 4 * (int)(e - (int64_t)m * cpr);
     const int64_t plane = (int64_t)M * N;
     const float* p = part + (int64_t)m * N + n;
     r3d_f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
     if ((N & 3) == 0) {
-        int c = 0;
-        for (; c + 4 <= kc; c += 4) {
-            r3d_f32x4 v[4];
+        for (int c = 0; c < kc; c += BATCH) {
+            r3d_f32x4 v[BATCH];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = *reinterpret_cast<const r3d_f32x4*>(p + (c + j) * plane);
+            for (int j = 0; j < BATCH; ++j)
+                if (c + j < kc) v[j] = *reinterpret_cast<const r3d_f32x4*>(p + (c + j) * plane);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) s += v[j];
+            for (int j = 0; j < BATCH; ++j)
+                if (c + j < kc) s += v[j];
         }
-        for (; c < kc; ++c) s += *reinterpret_cast<const r3d_f32x4*>(p + c * plane);
     } else {
         for (int c = 0; c < kc; ++c)
 #pragma unroll

@@ -61,3 +61,20 @@ def test_shape_sweep(gpu, row, dtype, M, N, K, scratch, rblk):
         assert rc == R.RAD_E_UNSUPPORTED and ok and (Y == gu.Y_SENTINEL).all()
         return
     _check(row, dtype, A, AS, B, BS, M, N, K, gpu, rblk=rblk, scratch=scratch)
+
+
+@pytest.mark.parametrize("row,dtype,M,N,K", [(MX_TILE, "mxfp4a8", 20, 256, 21504),
+                                             (F8_TILE, "fp8a8", 40, 256, 16384),
+                                             (MX_DEC, "mxfp4a8", 8, 3200, 21504)])
+def test_split_many_chunks(gpu, row, dtype, M, N, K):
+    """A narrow N over a long K: one weight tile, so the split cuts K into more than 16
+    chunks and the reduce sums its planes over several load batches (in chunk order)."""
+    from tests import gpu_util as gu
+    seed = M + N + K
+    if dtype == "mxfp4a8":
+        A, AS, B, BS = _mx_case(M, N, K, seed)
+    else:
+        A, AS, B, BS = _f8_case(M, N, K, seed, 1)
+    kc = gu.hook_bytes(row, dtype, M, N, K) // (M * N * 4)        # the hook sizes kc planes
+    assert kc > 16, kc
+    _check(row, dtype, A, AS, B, BS, M, N, K, gpu, scratch="hook")
