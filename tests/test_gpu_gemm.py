@@ -159,6 +159,33 @@ def test_mxfp4_decode_scale_plane_layouts(gpu, pad, offset):
     assert c["sentinel_left"] == 0 and c["max_viol"] <= 1.0, c
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 1001, 5376), (1, 8227, 1024), (1, 700, 5248),
+                                   (4, 777, 2048), (2, 300, 21504)])
+def test_fp8_decode_scale_plane_layouts(gpu, M, N, K):
+    """fp8a8 decode-row weight scales read through the plane's row pitch and base (the quad
+    GEMV; at M = 2, K = 21504 the 16-row GEMV): the same per-row plane as a dense 16-byte
+    aligned view and as a padded, 4-byte aligned view must give bit-identical Y (ragged last
+    workgroups, even and odd group counts), and the dense one must pass the oracle check."""
+    import torch
+    gu = _gu()
+    A, AS, B, BS = _f8_case(M, N, K, 70 + M + N, 1)
+    c, Y_dense = _check(F8_DEC, "fp8a8", A, AS, B, BS, M, N, K, gpu)
+    pad, offset = 3, 4
+    wide = np.zeros((N, K // 128 + pad), np.uint16)
+    wide[:, :K // 128] = BS
+    flat = np.concatenate([np.zeros(offset // 2, np.uint16), wide.reshape(-1)])
+    gA, gAS, gB, gW = (gu.Guarded(x, gpu) for x in (A, AS, B, flat))
+    bs = gW.t[offset // 2:].view(N, K // 128 + pad)[:, :K // 128]
+    gY = gu.y_buffer(M, N, gpu)
+    ops = R.GemmOperands(gA.t, gAS.t, gB.t, bs, gY.t, dtype="fp8a8", N=N, K=K)
+    rc = R.launch_row(F8_DEC, ops, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == R.RAD_OK
+    assert all(g.guards_intact() for g in (gA, gAS, gB, gW, gY))
+    Y_pad = gY.t.cpu().numpy().view(np.uint16).reshape(M, N)
+    assert np.array_equal(Y_pad, Y_dense)
+
+
 @pytest.mark.parametrize("N,K", [(17, 256), (1001, 4096), (4096, 1152), (6, 21504)])
 @pytest.mark.parametrize("rblk", [1, 128])
 def test_fp8_decode_shapes(gpu, N, K, rblk):
