@@ -157,7 +157,10 @@ int r3d_unrelayout_head(const RadParam* p, int n_p, int operand, const RadEncodi
  *   _join:  writes header, entries, codes (rows codes_pitch bytes apart) and scale (rows
  *           scale_pitch_bytes apart, (n_embd + 127) / 128 elements each) into dst;
  *   _split: the inverse, into dense planes (either pointer may be null), after checking
- *           each plane's dtype, grid, pitch and extent against the blob. */
+ *           each plane's dtype, grid, pitch and extent against the blob; the planes take
+ *           the blob's own grids (codes rows x cols bytes, scale rows x cols elements, as
+ *           its entries state: read them first, _header or rad_planes_find, to size the
+ *           destinations). */
 int64_t r3d_gfx950_logits_head_bytes(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,
                                      int64_t scale_block_rows);
 int64_t r3d_gfx950_logits_head_header(int64_t n_vocab, int64_t n_embd, uint32_t scale_dtype,

@@ -88,7 +88,9 @@ static inline const void* rad_planes_find_at(const RadPlanesHeader* h, const voi
     for (uint32_t i = 0; i < h->n_planes; ++i)
         if (strncmp(en[i].role, role, RAD_PLANES_ROLE) == 0) {
             if (e) *e = &en[i];
-            return (const uint8_t*)base + en[i].offset;
+            /* address arithmetic on integers: an offset the reader has not validated yet
+             * (the plan checks it against the blob's extent) cannot overflow a pointer */
+            return (const void*)((uintptr_t)base + (uint64_t)en[i].offset);
         }
     return 0;
 }
@@ -114,6 +116,9 @@ static inline int rad_planes_elem_bits(uint32_t dtype) {
     }
 }
 
+/* The largest row count, column count or row pitch (elements) a plane may have here. */
+#define RAD_PLANES_DIM_MAX ((int64_t)1 << 28)
+
 /* A plane tensor's element grid (rank 1: one row; rank 2: rows x cols, inner stride 1)
  * and its row pitch in elements; RAD_OK or the refusal. */
 static inline int rad_planes_grid(const RadTensor* t, int64_t* rows, int64_t* cols,
@@ -131,6 +136,8 @@ static inline int rad_planes_grid(const RadTensor* t, int64_t* rows, int64_t* co
         return RAD_E_SHAPE;
     }
     if (*rows <= 0 || *cols <= 0 || *pitch < *cols) return RAD_E_SHAPE;
+    /* extents whose products (rows x row bytes, pitch x bits) stay far inside int64 */
+    if (*rows > RAD_PLANES_DIM_MAX || *pitch > RAD_PLANES_DIM_MAX) return RAD_E_SHAPE;
     return RAD_OK;
 }
 
@@ -246,7 +253,10 @@ static inline int rad_planes_unrelayout(const RadEncoding* enc, const int* sel, 
         if (rc) return rc;
         const int64_t need = (cols * bits + 7) / 8;
         if (e->rows != rows || e->cols != cols || e->row_bytes < need) return RAD_E_SHAPE;
-        if (e->offset < 0 || e->offset + rows * e->row_bytes > h->bytes) return RAD_E_SHAPE;
+        int64_t span = 0, end = 0;                 /* the header's own fields: checked sums */
+        if (e->offset < 0 || __builtin_mul_overflow(rows, e->row_bytes, &span) ||
+            __builtin_add_overflow(e->offset, span, &end) || end > h->bytes)
+            return RAD_E_SHAPE;
         if ((pitch * bits) % 8) return RAD_E_STRIDE;
         if (!planes[i].data) return RAD_E_INVAL;
         for (int64_t r = 0; r < rows; ++r)

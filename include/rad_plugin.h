@@ -1,11 +1,12 @@
 /* rad_plugin.h -- host-side argument helpers a radiance kernel row uses, reconstructed
  * from their call sites in the reference (rad_arg_in: src/r3d_gemm_mxfp4.hip:1594-1600;
  * rad_args_geti / rad_args_gets: :1523-1529; rad_tensor_numel: :1536).  Semantics:
- *   rad_arg_in(a, i)      the i-th operand, or null when absent (index past n_t or null
- *                         data pointer);
+ *   rad_arg_in(a, i)      the i-th operand, or null when absent (index past n_t, null
+ *                         data pointer, or a rank past RAD_MAX_RANK);
  *   rad_args_geti/gets    look a parameter up by key, 1 when found with that kind;
  *   rad_args_getf_or      an F64 parameter by key, else the fallback;
- *   rad_tensor_numel      product of the shape (0 for a null tensor).
+ *   rad_tensor_numel      product of the shape (0 for a null tensor, -1 for a negative
+ *                         extent or an int64 overflow).
  */
 #ifndef RAD_PLUGIN_H
 #define RAD_PLUGIN_H
@@ -15,7 +16,9 @@
 
 static inline const RadTensor* rad_arg_in(const RadArgs* a, int i) {
     if (!a || i < 0 || i >= a->n_t || !a->t) return 0;
-    return a->t[i].data ? &a->t[i] : 0;
+    /* a rank past RAD_MAX_RANK has no shape to read: treated as absent (refused by every
+     * row that needs the operand) */
+    return a->t[i].data && a->t[i].rank <= RAD_MAX_RANK ? &a->t[i] : 0;
 }
 
 static inline int rad_args_geti(const RadArgs* a, const char* key, long long* out) {
@@ -46,10 +49,14 @@ static inline double rad_args_getf_or(const RadArgs* a, const char* key, double 
     return fb;
 }
 
+/* Elements of t (the product of its shape); -1 for a negative extent or a product past
+ * int64, which every caller's size check then refuses. */
 static inline long long rad_tensor_numel(const RadTensor* t) {
     if (!t) return 0;
     long long n = 1;
-    for (uint32_t i = 0; i < t->rank && i < RAD_MAX_RANK; ++i) n *= t->shape[i];
+    for (uint32_t i = 0; i < t->rank && i < RAD_MAX_RANK; ++i) {
+        if (t->shape[i] < 0 || __builtin_mul_overflow(n, (long long)t->shape[i], &n)) return -1;
+    }
     return n;
 }
 

@@ -84,8 +84,11 @@ size_t span_bytes(const RadTensor& t) {
     if (!t.data) return 0;
     long long els = 1;
     for (uint32_t r = 0; r < t.rank && r < RAD_MAX_RANK; ++r) {
-        if (t.shape[r] <= 0) return 0;
-        els += (t.shape[r] - 1) * t.stride[r];
+        long long step = 0;
+        if (t.shape[r] <= 0 || t.stride[r] < 0 ||
+            __builtin_mul_overflow((long long)(t.shape[r] - 1), (long long)t.stride[r], &step) ||
+            __builtin_add_overflow(els, step, &els) || els > (1LL << 40))
+            return 0;                                     /* no span a capture could copy */
     }
     switch (t.dtype) {
         case RAD_FP4E2M1: return (size_t)((els + 1) / 2);
@@ -195,7 +198,7 @@ void dump_end(void* handle, const RadArgs* a, RadStream s, int rc) {
         }
         for (int i = 0; i < a->n_t; ++i) {
             const RadTensor& t = a->t[i];
-            const uint32_t rank = t.data ? t.rank : 0;
+            const uint32_t rank = t.data ? (t.rank < RAD_MAX_RANK ? t.rank : RAD_MAX_RANK) : 0;
             fprintf(f, "T\t%d\t%u\t%u", i, t.dtype, rank);
             for (uint32_t r = 0; r < rank; ++r) fprintf(f, "\t%lld", (long long)t.shape[r]);
             for (uint32_t r = 0; r < rank; ++r) fprintf(f, "\t%lld", (long long)t.stride[r]);

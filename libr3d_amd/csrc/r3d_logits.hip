@@ -424,15 +424,16 @@ static int blob_kind(const void* blob) {
     return at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeArray ? 2 : 0;
 }
 
-/* The header, then the n_planes entries it announces (none when it is not a planes
- * header: the plan then refuses it), read in place from host-readable memory; false for
- * a null blob. */
+/* The header, then its entries, read in place from host-readable memory; false for a
+ * null blob.  Entries are read only for the two-plane header the plan accepts: a header
+ * announcing any other count is refused without reading past the entries a two-plane blob
+ * is sure to hold (the blob's extent is not known here). */
 static bool head_read_host(const void* blob, RadPlanesHead* out) {
     if (!blob) return false;
     memset(out, 0, sizeof *out);
     memcpy(&out->h, blob, sizeof out->h);
     const RadPlanesHeader* h = rad_planes_header(blob);
-    if (h) memcpy(out->e, rad_planes_entries(h), h->n_planes * sizeof(RadPlanesEntry));
+    if (h && h->n_planes == 2) memcpy(out->e, rad_planes_entries(h), 2 * sizeof(RadPlanesEntry));
     return true;
 }
 
@@ -473,9 +474,10 @@ static int head_copy(const void* blob, hipStream_t stream, RadPlanesHead* out) {
         (void)hipGetLastError();
         return RAD_E_DEVICE;
     }
-    if (!rad_planes_header(&out->h)) return RAD_E_DTYPE;
+    /* two planes or none: the copy never reaches past what a two-plane blob holds */
+    if (!rad_planes_header(&out->h) || out->h.n_planes != 2) return RAD_E_DTYPE;
     if (hipMemcpyAsync(out->e, rad_planes_entries(reinterpret_cast<const RadPlanesHeader*>(blob)),
-                       out->h.n_planes * sizeof(RadPlanesEntry), hipMemcpyDeviceToHost,
+                       2 * sizeof(RadPlanesEntry), hipMemcpyDeviceToHost,
                        stream) != hipSuccess ||
         hipStreamSynchronize(stream) != hipSuccess) {
         (void)hipGetLastError();

@@ -29,12 +29,17 @@ int64_t row_stride(const RadTensor* t, int64_t cols) {
     if (!t || t->rank < 2) return cols;
     int64_t span = 1;
     for (int i = (int)t->rank - 1; i >= 0; --i) {
-        span *= t->shape[i];
+        if (__builtin_mul_overflow(span, t->shape[i], &span)) break;
         if (span == cols) return i > 0 ? t->stride[i - 1] : cols;
         if (span > cols) break;
     }
     return t->stride[t->rank - 2];
 }
+
+/* A row pitch the kernels can walk: not negative, and below any device allocation (the
+ * reference takes the engine's strides as given; a malformed one is refused here rather
+ * than turned into addresses). */
+static bool pitch_ok(int64_t p) { return p >= 0 && p <= (int64_t(1) << 40); }
 
 static bool inner_contig(const RadTensor* t) {
     return t->rank < 2 || t->stride[t->rank - 1] == 1;
@@ -137,6 +142,9 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     P->bs_cols = (int)bs_cols;
     P->rblk = 1;
     P->ua = fast ? 0 : UA_GEMM;
+    if (!pitch_ok(P->a_pitch) || !pitch_ok(P->b_pitch) || !pitch_ok(P->y_pitch) ||
+        !pitch_ok(P->as_pitch) || !pitch_ok(P->bs_pitch))
+        return RAD_E_STRIDE;
     return RAD_OK;
 }
 
@@ -207,6 +215,9 @@ int plan_mxfp4a16(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
     P->rblk = 1;
     P->scratch = (uint8_t*)a->scratch;
     P->ua = (qfast ? 0 : UA_QUANT) | (gfast ? 0 : UA_GEMM);
+    if (!pitch_ok(P->a_pitch) || !pitch_ok(P->b_pitch) || !pitch_ok(P->y_pitch) ||
+        !pitch_ok(P->as_pitch) || !pitch_ok(P->bs_pitch))
+        return RAD_E_STRIDE;
     return RAD_OK;
 }
 
@@ -284,6 +295,9 @@ int plan_fp8a8(const RadArgs* a, int64_t M, GemmPlan* P) {
     P->bs_cols = (int)bs_cols;
     P->rblk = rblk;
     P->ua = fast ? 0 : UA_GEMM;
+    if (!pitch_ok(P->a_pitch) || !pitch_ok(P->b_pitch) || !pitch_ok(P->y_pitch) ||
+        !pitch_ok(P->as_pitch) || !pitch_ok(P->bs_pitch))
+        return RAD_E_STRIDE;
     return RAD_OK;
 }
 
@@ -728,13 +742,17 @@ int band_row_pitch(const RadTensor* t, int64_t cols, int64_t* pitch) {
     if (t->rank == 2) {
         if (t->stride[1] != 1) return -3;
         *pitch = t->shape[1] == cols ? t->stride[0] : cols;
-        return 0;
+        return pitch_ok(*pitch) ? 0 : -4;         /* a walkable pitch (not in the reference) */
     }
     if (t->rank >= 3) {
         if (t->stride[t->rank - 1] != 1) return -3;
         if (t->shape[t->rank - 1] != cols) { *pitch = cols; return 0; }
-        for (int i = 0; i < (int)t->rank - 1; ++i)
-            if (t->stride[i] != t->shape[i + 1] * t->stride[i + 1]) return -4;
+        for (int i = 0; i < (int)t->rank - 1; ++i) {
+            int64_t span = 0;
+            if (__builtin_mul_overflow(t->shape[i + 1], t->stride[i + 1], &span) ||
+                t->stride[i] != span)
+                return -4;
+        }
         *pitch = cols;
         return 0;
     }
@@ -750,7 +768,7 @@ int plan_quant_act_fp8(const RadArgs* a, QuantPlan* P) {
     if (q->dtype != RAD_F8E4M3 || sc->dtype != RAD_F32) return RAD_E_DTYPE;
     long long v = 0;
     const int64_t n = rad_args_geti(a, "n", &v) ? (int64_t)v : (x->rank >= 2 ? x->shape[1] : 0);
-    if (n <= 0) return RAD_E_SHAPE;
+    if (n <= 0 || n > kDimMax) return RAD_E_SHAPE;
     const int64_t rows = rad_tensor_numel(x) / n;
     if (rows <= 0 || rows > 0xffff) return RAD_E_SHAPE;
     int64_t g = rad_args_geti(a, "group", &v) ? (int64_t)v : n;
@@ -787,7 +805,7 @@ int plan_gated_quant_fp8(const RadArgs* a, GatedPlan* P) {
     long long v = 0;
     const int64_t n = rad_args_geti(a, "n", &v) ? (int64_t)v
                                                 : (gu->rank >= 2 ? gu->shape[1] / 2 : 0);
-    if (n <= 0) return RAD_E_SHAPE;
+    if (n <= 0 || n > kDimMax) return RAD_E_SHAPE;
     const char* act = rad_args_gets(a, "act");
     int64_t g = rad_args_geti(a, "group", &v) ? (int64_t)v : n;
     if (g <= 0 || g > n) g = n;
@@ -1022,7 +1040,7 @@ int plan_logits_e4m3(const RadArgs* a, const RadPlanesHead* hh, LogitsPlan* P, b
     if (Y->rank >= 2 && Y->stride[Y->rank - 1] != 1) return RAD_E_STRIDE;
     const int64_t x_pitch = X->rank >= 2 ? X->stride[X->rank - 2] : K;
     const int64_t y_pitch = Y->rank >= 2 ? Y->stride[Y->rank - 2] : N;
-    if (x_pitch < K || y_pitch < N) return RAD_E_STRIDE;
+    if (x_pitch < K || y_pitch < N || !pitch_ok(x_pitch) || !pitch_ok(y_pitch)) return RAD_E_STRIDE;
     if (args_only) return RAD_OK;
 
     const RadPlanesHeader* h = hh ? &hh->h : nullptr;
@@ -1042,15 +1060,20 @@ int plan_logits_e4m3(const RadArgs* a, const RadPlanesHead* hh, LogitsPlan* P, b
     const int64_t srows = (N + es->block[0] - 1) / es->block[0], scols = (K + 127) / 128;
     if (es->rows != srows || es->cols != scols) return RAD_E_SHAPE;
     if (ec->row_bytes != K) return RAD_E_STRIDE;       /* dense, one byte each */
-    if (h->bytes < es->offset + es->rows * es->row_bytes) return RAD_E_SHAPE;
+    /* extents in overflow-checked arithmetic (header fields are untrusted bytes): an
+     * extent past int64 is past the blob */
+    int64_t s_span = 0, s_end = 0, c_end = 0;
+    const bool s_ovf = __builtin_mul_overflow(es->rows, es->row_bytes, &s_span) ||
+                       __builtin_add_overflow(es->offset, s_span, &s_end);
+    if (s_ovf || h->bytes < s_end) return RAD_E_SHAPE;
 
     /* gfx950 gates */
     const int64_t ssz = es->dtype == RAD_F32 ? 4 : 2;
     if (es->row_bytes < scols * ssz || es->row_bytes % ssz || es->offset < 0 || ec->offset < 0)
         return RAD_E_STRIDE;
-    if (h->bytes < ec->offset + N * K) return RAD_E_SHAPE;
+    if (__builtin_add_overflow(ec->offset, N * K, &c_end) || h->bytes < c_end) return RAD_E_SHAPE;
     /* buffer offsets are 32-bit: one wave's rows of codes and the whole scale plane */
-    if (64 * K > 0x7FFFFFFFLL || es->rows * es->row_bytes > 0x7FFFFFFFLL) return RAD_E_UNSUPPORTED;
+    if (64 * K > 0x7FFFFFFFLL || s_span > 0x7FFFFFFFLL) return RAD_E_UNSUPPORTED;
     LogitsShape sh{};
     if (!logits_shape(M, K, &sh)) return RAD_E_UNSUPPORTED;
     if ((M + sh.mt - 1) / sh.mt > 65535) return RAD_E_UNSUPPORTED;   /* passes ride grid.y */

@@ -982,3 +982,37 @@ def test_any_alignment_mxfp4a16_and_fused():
         ops._t[0].data = ops._t[0].data + 2
         rc, d = R.describe(row, ops)
         assert rc == R.RAD_E_UNSUPPORTED, d
+
+
+def _set_param(ops, key, val):
+    for i in range(ops.args.n_p):
+        if ops.args.p[i].key == key.encode():
+            ops.args.p[i].ival = val
+            return
+    raise KeyError(key)
+
+
+def test_malformed_operands_refused():
+    """Operand metadata no engine would send -- a rank past RAD_MAX_RANK, extents whose
+    product leaves int64, negative or absurd row pitches, a band row width past int32 --
+    is refused with a status instead of being turned into addresses (found by fuzzing the
+    plans under the host address and undefined-behaviour sanitizers)."""
+    rows = ["gemm_nt_q_mxfp4", "gemm_nt_q_mxfp4_decode", "gemm_nt_q_fp8a8", "gemm_nt_q_fp8a8_decode"]
+    for row in rows:
+        mk = _mx_ops if "mxfp4" in row else _f8_ops
+        ops, keep = mk(M=4, N=256, K=256)
+        assert R.describe(row, ops)[0] == R.RAD_OK
+        ops._t[0].rank = 9                                  # A: past RAD_MAX_RANK -> absent
+        assert R.describe(row, ops)[0] != R.RAD_OK
+        ops, keep = mk(M=4, N=256, K=256)
+        ops._t[0].shape[0] = 1 << 62                        # numel past int64
+        assert R.describe(row, ops)[0] == R.RAD_E_SHAPE
+        ops, keep = mk(M=4, N=256, K=256)
+        ops._t[0].stride[0] = -(1 << 62)                    # a negative row pitch
+        assert R.describe(row, ops)[0] == R.RAD_E_STRIDE
+        ops, keep = mk(M=4, N=256, K=256)
+        ops._t[4].stride[0] = 1 << 50                       # Y rows past any allocation
+        assert R.describe(row, ops)[0] == R.RAD_E_STRIDE
+    ops = _gq_ops()
+    _set_param(ops, "n", 1 << 62)                           # 2n past int64
+    assert R.describe("gated_quant_fp8_act", ops)[0] == R.RAD_E_SHAPE
