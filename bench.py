@@ -2,7 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-extra] [--no-cpu]
 
-A "step" is one gemm_nt_q launch over one batch.  The headline workload is BASELINE's
+A "step" is one gemm_nt_q launch over one batch.  The headline workload is BASELINE.json's
 config 1 -- the fp8a8 W8A8 decode GEMV at M=1, K=5376, N=21504 -- read cold from HBM:
 the weight planes rotate over enough copies to exceed 1 GiB, well past the 256 MB
 Infinity Cache; each copy is read once (a read-only stream) before the warm-up, as a

@@ -1,4 +1,4 @@
-"""Seeded synthetic operands for gemm_nt_q (host numpy), shaped like BASELINE's configs.
+"""Seeded synthetic operands for gemm_nt_q (host numpy), shaped like the configs of BASELINE.json.
 
 Weights and activations follow the configs' stated distributions:
   mxfp4a8  e2m1 codes uniform over the 16 codes (two per byte, low nibble = even k),

@@ -9,7 +9,7 @@ classes match; and per element
 product -- the block-scaled MFMA sums each 8 products at a width that truncates bits
 below 2^-13 of the group's largest, measured on MI355X; see oracle/r3d_oracle.h).
 Whole-tensor rel_l2 must stay inside the reference's own kbench tolerances (3e-2
-mxfp4a8, 5e-3 fp8a8; docs/COVERAGE.md:868,1296).  On the BASELINE configs' data
+mxfp4a8, 5e-3 fp8a8; docs/COVERAGE.md:868,1296).  On BASELINE.json's configs' data
 (tests/test_gpu_configs.py) the per-row rel_l2 is held to 2^-8 (one bf16 ulp) as well.
 The operand law of most cases here is the reference probe's (full-range NaN-free e4m3
 codes, tools/probe_m4_entry.cpp:36-40): it maximises cancellation, so it tests the bound,
