@@ -462,6 +462,18 @@ def main():
                                            "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
         log("[bench] C3-shape fp8a8 prefill: %.1f us, %.1f TFLOP/s" % (kern * 1e6, tf))
         del c
+        # and on the reference fp8a8 rows' checkpoint grid: one bf16 scale per 128 x 128
+        # weight tile (the same scales, one row of them per 128 weight rows)
+        c = Case("fp8a8", A8, AS8, B8, BS8[::128].copy(), M, N, K, 1, dev)
+        wall, kern = time_case(c, "gemm_nt_q_fp8a8", 100, 20, stream)
+        tf = 2.0 * M * N * K / kern / 1e12
+        extra["c3_shape_fp8a8_prefill_block128"] = {
+            "M": M, "K": K, "N": N, "kernel_us": round(kern * 1e6, 1), "TFLOPs": round(tf, 1),
+            "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
+            "scales": "one bf16 per 128 x 128 weight tile"}
+        log("[bench] C3-shape fp8a8 prefill, 128 x 128 scale blocks: %.1f us, %.1f TFLOP/s"
+            % (kern * 1e6, tf))
+        del c
         torch.cuda.empty_cache()
         extra.update(bench_quant(dev, stream))
         extra.update(bench_fused_decode(dev, stream))
@@ -485,7 +497,8 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-CASES = (["c0", "c1", "c3_a16", "c3_a16_quant", "c3_a16_gemm", "c3_a8", "c3_f8", "lm_head_M4"] +
+CASES = (["c0", "c1", "c3_a16", "c3_a16_quant", "c3_a16_gemm", "c3_a8", "c3_f8", "c3_f8_b128",
+          "lm_head_M4"] +
          ["c2_%s_M%d" % (s, m) for s in ("gate_up", "down", "qkv") for m in (1, 4, 16)] +
          ["c4_%s_M4" % s for s in ("q", "kv", "o")] +
          ["skinny_%s_M%d" % (s, m) for s in ("gate_up", "down", "qkv") for m in (17, 32, 64)] +
@@ -542,7 +555,7 @@ def run_case(name, dev, stream, steps, warmup):
                         "TFLOPs": round(fl / t / 1e12, 1),
                         "frac_fp8_peak": round(fl / t / 1e12 / FP8_PEAK_TFLOPS, 4)})
         return res
-    if name in ("c3_a8", "c3_f8"):
+    if name in ("c3_a8", "c3_f8", "c3_f8_b128"):
         M, K, N = 2048, 5376, 21504
         if name == "c3_a8":
             _, A, AS = synth.activations(M, K, 0x5EED + 30)
@@ -551,6 +564,8 @@ def run_case(name, dev, stream, steps, warmup):
         else:
             A, AS = synth.fp8_activations_per_token(M, K, 0x5EED + 35)
             B, BS = synth.fp8_weights(N, K, 0x5EED + 36)
+            if name == "c3_f8_b128":
+                BS = BS[::128].copy()             # one scale per 128 x 128 weight tile
             c, row = Case("fp8a8", A, AS, B, BS, M, N, K, 1, dev), "gemm_nt_q_fp8a8"
         wall, kern = time_case(c, row, steps, warmup, stream)
         fl = 2.0 * M * N * K

@@ -415,13 +415,14 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
                             const GemmPlan& Q) -> hipError_t {
         const dim3 grid((unsigned)(g.tiles * ukc)), block((unsigned)(64 * g.wv));
 #define R3D_PF_L(MODE_, WNF_, WMF_, WV_) PrefillLayout<WNF_, WMF_, 3, MODE_ == PF_F8 ? 2 : 1, WV_>
-#define R3D_PFW(MODE_, WNF_, WMF_, WV_)                                                    \
+#define R3D_PFW(MODE_, WNF_, WMF_, WV_) R3D_PFWS(MODE_, WNF_, WMF_, WV_, 0)
+#define R3D_PFWS(MODE_, WNF_, WMF_, WV_, SB_)                                              \
     static_assert(R3D_PF_L(MODE_, WNF_, WMF_, WV_)::LDS ==                                 \
                       3 * prefill_stage_bytes(WNF_, WMF_, MODE_ == PF_F8 ? 2 : 1, WV_),     \
                   "host and kernel ring sizes differ");                                    \
     if ((int)R3D_PF_L(MODE_, WNF_, WMF_, WV_)::LDS != g.lds || g.wv != WV_)                 \
         return hipErrorInvalidValue;                                                        \
-    hipLaunchKernelGGL((prefill_kernel<MODE_, WNF_, WMF_, WV_>), grid, block,               \
+    hipLaunchKernelGGL((prefill_kernel<MODE_, WNF_, WMF_, WV_, SB_>), grid, block,          \
                        (size_t)(R3D_PF_L(MODE_, WNF_, WMF_, WV_)::LDS),                     \
                        stream, A, AS, Q.B, (const uint8_t*)Q.BS, Q.Y, (int)Q.M, (int)Q.N,  \
                        g.steps, (int)g.grid_m, (int)g.tiles, Q.rblk, a_pitch, as_pitch,     \
@@ -433,6 +434,16 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
                 case 7: R3D_PF(PF_MX8, 7, 4); break;
                 case 6: R3D_PF(PF_MX8, 6, 4); break;
                 default: R3D_PF(PF_MX8, 4, 4); break;
+            }
+        } else if (mode == PF_F8 && Q.rblk == 128) {
+            /* the 128 x 128 block grid: one weight scale a tile and K group, folded into
+             * the token's scale before the flush */
+            if (g.wmf == 1) {
+                R3D_PFWS(PF_F8, 4, 1, 8, 1);
+            } else if (g.wv == 4) {
+                R3D_PFWS(PF_F8, 4, 8, 4, 1);
+            } else {
+                R3D_PFWS(PF_F8, 4, 2, 8, 1);
             }
         } else if (mode == PF_F8) {
             if (g.wmf == 1) {
@@ -456,6 +467,7 @@ static int launch_prefill(const GemmPlan& P, hipStream_t stream, int stage = 0,
         }
 #undef R3D_PF
 #undef R3D_PFW
+#undef R3D_PFWS
 #undef R3D_PF_L
         return hipGetLastError();
     };

@@ -57,7 +57,7 @@ __device__ __forceinline__ void r3d_mfma_mx_inplace(r3d_f32x4& acc, r3d_i32x4 a,
         : "v"(a), "v"(b), "v"(sa), "v"(sb));
 }
 
-template <int MODE, int WNF, int WMW, int WV = 8>
+template <int MODE, int WNF, int WMW, int WV = 8, int SBK = 0>
 __global__ __launch_bounds__(64 * WV) void prefill_kernel(
     const uint8_t* __restrict__ A, const void* __restrict__ ASv,
     const uint8_t* __restrict__ B, const uint8_t* __restrict__ BS,
@@ -66,6 +66,12 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
     int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch,
     int kc, int cst, float* __restrict__ part) {
     constexpr bool F8 = MODE == PF_F8;                   /* e4m3 weights, bf16 row scales */
+    /* e4m3 weights on the 128 x 128 block grid (SBK): the tile's 128 weight rows share one
+     * scale a K group, so the flush folds it into the token's scale first --
+     * acc += D * (sa * sb), one fused multiply-add an element (libref rounds (D * sa) * sb;
+     * the difference is one rounding of a product, inside the per-element bound) */
+    constexpr bool SB = F8 && SBK;
+    static_assert(!SB || 32 * WNF == 128, "one 128-row scale block a tile");
     constexpr int WH = F8 ? 2 : 1;                        /* 1 KB images per weight fragment */
     constexpr int WB = 64 * WH;                           /* weight bytes per row per step */
     using L = PrefillLayout<WNF, WMW, 3, WH, WV>;
@@ -237,6 +243,11 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
         sbP[set][ni][0] = __builtin_amdgcn_perm((uint32_t)v[1], (uint32_t)v[0], 0x05040100u);
         sbP[set][ni][1] = __builtin_amdgcn_perm((uint32_t)v[3], (uint32_t)v[2], 0x05040100u);
     };
+    /* SB: the tile's block scale of each weight set (every row's slot holds it; slot 0) */
+    float sbB[2] = {0.0f, 0.0f};
+    auto read_sb = [&](const uint8_t* st, int set) __attribute__((always_inline)) {
+        sbB[set] = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(st + L::S) << 16);
+    };
     r3d_i32x8 ar[4];
     int ax[4];
     float af[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -260,10 +271,13 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
                 const r3d_i32x4 hi =
                     *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + 1024 + rd);
                 wF[set][ni] = r3d_i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                if (SSF)
+                if (SB) {
+                    if (ni == 0) read_sb(st, set);
+                } else if (SSF) {
                     pack_sb(st + L::S + 4 * (16 * f + 4 * q), set, ni);
-                else
+                } else {
                     sbF[set][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::S + 4 * (16 * f + 4 * q));
+                }
             } else {
                 wS[set][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 1024 * f + rd);
                 xS[set][ni] = st[L::S + 4 * (16 * f + li) + q];
@@ -306,10 +320,17 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
 #pragma unroll
             for (int ni = 0; ni < WNF; ++ni) {
                 if (live) dq[dc][ni] = r3d_mfma_fp8_fp8(wF[set][ni], ar[slot]);
+                if (SB) {
+                    const float sf = sprev * sbB[ps];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float sb = __uint_as_float((uint32_t)sbF[ps][ni][i] << 16);
-                    acc[ni][pm][i] = acc[ni][pm][i] + (dq[dp][ni][i] * sprev) * sb;
+                    for (int i = 0; i < 4; ++i)
+                        acc[ni][pm][i] = __builtin_fmaf(dq[dp][ni][i], sf, acc[ni][pm][i]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float sb = __uint_as_float((uint32_t)sbF[ps][ni][i] << 16);
+                        acc[ni][pm][i] = acc[ni][pm][i] + (dq[dp][ni][i] * sprev) * sb;
+                    }
                 }
             }
             sprev = af[slot];
@@ -346,7 +367,11 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
             const r3d_i32x4 lo = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + rd);
             const r3d_i32x4 hi = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 2048 * f + 1024 + rd);
             wF[0][ni] = r3d_i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            pack_sb(st + L::S + 4 * (16 * f + 4 * q), sset, ni);
+            if (SB) {
+                if (ni == 0) read_sb(st, sset);
+            } else {
+                pack_sb(st + L::S + 4 * (16 * f + 4 * q), sset, ni);
+            }
         } else {
             wS[0][ni] = *reinterpret_cast<const r3d_i32x4*>(st + L::W + 1024 * f + rd);
             xS[0][ni] = st[L::S + 4 * (16 * f + li) + q];
@@ -358,9 +383,12 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
         const int nf = tt % WNF, mf = tt / WNF;
         const float sv = (!before && mf == mi) ? scur : sprev;
         const r3d_f32x4 d = dqr[tt % RR];
+        const float sf = SB ? sv * (before ? sbB[set ^ 1] : sbB[set]) : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (F8) {
+            if (SB) {
+                acc[nf][mf][i] = __builtin_fmaf(d[i], sf, acc[nf][mf][i]);
+            } else if (F8) {
                 const uint32_t pw = before ? (set ? sbP[0][nf][i >> 1] : sbP[1][nf][i >> 1])
                                            : (set ? sbP[1][nf][i >> 1] : sbP[0][nf][i >> 1]);
                 const float sb = __uint_as_float((i & 1) ? (pw & 0xFFFF0000u) : (pw << 16));
@@ -503,7 +531,10 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
             for (int i = 0; i < 4; ++i) {
                 const float d = (WMW & 1) ? ((ls ^ ((WMW - 1) & 1)) ? dq[1][ni][i] : dq[0][ni][i])
                                           : dq[(WMW - 1) & 1][ni][i];
-                if (F8) {
+                if (SB) {
+                    acc[ni][WMW - 1][i] = __builtin_fmaf(d, sprev * (ls ? sbB[1] : sbB[0]),
+                                                         acc[ni][WMW - 1][i]);
+                } else if (F8) {
                     const uint32_t sbb = (uint32_t)(ls ? sbF[1][ni][i] : sbF[0][ni][i]);
                     const float sb = __uint_as_float(sbb << 16);
                     acc[ni][WMW - 1][i] = acc[ni][WMW - 1][i] + (d * sprev) * sb;
