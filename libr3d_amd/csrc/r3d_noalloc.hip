@@ -74,6 +74,7 @@ extern "C" int r3d_rad_gemm_nt_q_mxfp4a16_noalloc(const RadArgs* a, RadStream s)
     long long K = 0;
     if (!rad_args_geti(a, "K", &K) || K <= 0) return RAD_E_SHAPE;
     const int64_t need = r3d::mxfp4a16_scratch_bytes(M, K);
+    if (need < 0) return RAD_E_SHAPE;                 /* M or K past any plan's bound */
     if (need > (int64_t)R3D_NOALLOC_SCRATCH_BYTES) {
         fprintf(stderr, "libr3d_gfx950: mxfp4a16_noalloc: M=%lld K=%lld needs %lld bytes of "
                         "scratch, the static buffer holds %lld (refused)\n",

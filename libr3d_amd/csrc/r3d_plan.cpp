@@ -149,7 +149,9 @@ int plan_mxfp4a8(const RadArgs* a, int64_t M, int64_t N, GemmPlan* P) {
 }
 
 int64_t mxfp4a16_scratch_bytes(int64_t M, int64_t K) {
+    /* past the planes' dimension bound no plan accepts the call: -1 (never enough) */
     if (M <= 0 || K <= 0) return 0;
+    if (M > kDimMax || K > kDimMax) return -1;
     return ((M * K + 255) / 256) * 256 + M * ((K + 31) / 32);
 }
 

@@ -21,6 +21,7 @@ VALS = [0, 1, 2, 3, 4, 7, 8, 15, 16, 17, 31, 32, 64, 127, 128, 129, 255, 256, 10
         -1, -128, 1 << 20, 1 << 31, 1 << 40, 1 << 62, -(1 << 62)]
 GEMM = ["r3d_rad_gemm_nt_q", "r3d_rad_gemm_nt_q_fp8", "r3d_rad_gemm_nt_q_mxfp4_decode",
         "r3d_rad_gemm_nt_q_fp8_decode", "r3d_rad_gemm_nt_q_mxfp4a16", "r3d_rad_gemm_nt_q_gated_fp8"]
+GEMM_ONLY = ["r3d_rad_gemm_nt_q_mxfp4a16_noalloc"]          # entries without a scratch hook
 BAND = {"quant": ("r3d_rad_quant_act_fp8", "quant_act_fp8_act"),
         "gated": ("r3d_rad_gated_quant_fp8", "gated_quant_fp8_act"),
         "rms": ("r3d_rad_rmsnorm_quant_fp8", "rmsnorm_quant_fp8"),
@@ -97,7 +98,7 @@ def test_plans_survive_mutated_operands(seed):
     call_entries = _no_gpu()
     buf = ctypes.create_string_buffer(512)
     gemm_rows = [r["name"] for r in R.rows() if "gemm_nt_q" in r["name"]]
-    ents = [_fn(n) for n in GEMM]
+    ents = [_fn(n) for n in GEMM + GEMM_ONLY]
     hooks = [_fn(n + "_scratch", hook=True) for n in GEMM]
     band = {k: _fn(v[0]) for k, v in BAND.items()}
     for _ in range(600):
