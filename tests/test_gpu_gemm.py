@@ -547,3 +547,28 @@ def test_decode_splitk_deterministic(gpu, splitk, dtype, M):
     rc, y2, guards = gu.run_row(row, dtype, A, AS, B, BS, M, N, K, gpu, tunables=tv)
     assert rc == R.RAD_OK and guards
     assert np.array_equal(y1, y2)
+
+
+@pytest.mark.parametrize("M,N,K,scratch", [(512, 16640, 1024, None), (300, 1000, 640, None),
+                                           (40, 1000, 2048, "hook"), (130, 384, 256, None)])
+def test_fp8_block_grid_matches_per_row_grid(gpu, M, N, K, scratch):
+    """The tile row on the 128 x 128 block grid folds the weight scale into the token's
+    (acc = fma(D, sa * sb, acc)).  With power-of-two a_scales and weight scales every
+    product in either order is exact, so it must equal, bit for bit, the per-row grid
+    holding the same scales replicated over each block's 128 rows (libref's
+    acc + (D * sa) * sb) -- distinct scales per block and K group, so a wrong block, group
+    or weight set shows; every tile kind: the four-wave tile with its 128 x 128 remainder,
+    the 128 x 128 tile alone, the split K over hook scratch, a partial last block."""
+    gu = _gu()
+    rng = np.random.default_rng(M + N + K)
+    A = synth.random_e4m3_codes((M, K), rng)
+    AS = np.exp2(rng.integers(-10, -4, size=(M, K // 128))).astype(np.float32)
+    B = synth.random_e4m3_codes((N, K), rng)
+    blocks = (N + 127) // 128
+    BSb = synth.bf16_bits(np.exp2(rng.integers(-12, -5, size=(blocks, K // 128))).astype(np.float32))
+    BSr = np.repeat(BSb, 128, axis=0)[:N].copy()
+    rc1, Y1, ok1 = gu.run_row(F8_TILE, "fp8a8", A, AS, B, BSb, M, N, K, gpu, scratch=scratch)
+    rc2, Y2, ok2 = gu.run_row(F8_TILE, "fp8a8", A, AS, B, BSr, M, N, K, gpu, scratch=scratch)
+    assert rc1 == R.RAD_OK and rc2 == R.RAD_OK and ok1 and ok2
+    assert not np.any(Y1 == gu.Y_SENTINEL)
+    assert np.array_equal(Y1, Y2), int((Y1 != Y2).sum())
