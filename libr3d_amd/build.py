@@ -6,8 +6,11 @@ hipcc compiles the HIP kernels for --offload-arch=gfx950 with packed-fp32 code
 generation switched off and matrix-core results written to ordinary VGPRs
 (-amdgpu-mfma-vgpr-form: the kernels scale and add every MFMA result with VALU
 instructions, which read only VGPRs; with results in AGPRs each element first needs a
-v_accvgpr_read, a third of the e4m3 prefill tile's VALU work).  The host C++ (row table,
-plans) goes into the same shared object.  The oracle (oracle/Makefile) is test infrastructure and is built beside it.
+v_accvgpr_read, a third of the e4m3 prefill tile's VALU work) and kernel-argument
+preloading (-amdgpu-kernarg-preload-count=16: the dispatch puts the leading 14 dwords of a
+kernel's arguments in SGPRs, so a wave's first loads do not wait on an argument fetch;
+firmware without the feature runs the compiler's fallback prologue that loads them).  The
+host C++ (row table, plans) goes into the same shared object.  The oracle (oracle/Makefile) is test infrastructure and is built beside it.
 """
 import hashlib
 import os
@@ -27,6 +30,7 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-function",
     "-I" + os.path.join(ROOT, "include"), "-I" + CSRC,
 ]

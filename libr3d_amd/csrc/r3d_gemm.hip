@@ -90,15 +90,17 @@ static int launch_quad(const GemmPlan& P, const QuadGeom& g, hipStream_t stream)
     const int sc16 = P.enc == ENC_MXFP4A8 && P.bs_pitch == P.K / 32 &&
                      ((uintptr_t)P.BS & 15) == 0;
     if ((g.wv != 4 && g.wv != 7 && g.wv != 8) || (g.qpw == 2 && g.wv != 4) ||
-        (g.wv == 7 && (g.chunks != 1 || P.xq)))
+        (g.wv == 7 && (g.chunks != 1 || P.xq)) || (g.chunks != 1 && g.chunks != 2 && g.chunks != 4) ||
+        P.M < 1 || P.M > 4 || !quad_fits(P))
         return RAD_E_UNSUPPORTED;
+    const int pk = quad_pack((int)P.M, g.chunks == 4 ? 2 : g.chunks == 2 ? 1 : 0, P.rblk == 128,
+                             sc16 != 0, P.as_pitch == P.K / 128);
 #define R3D_QUAD1(ENC_, MT_, Q_, D_, X_) R3D_QUADW(ENC_, MT_, Q_, D_, X_, 4)
 #define R3D_QUADW(ENC_, MT_, Q_, D_, X_, W_)                                                \
     hipLaunchKernelGGL((gemv_quad_kernel<ENC_, MT_, Q_, D_, X_, W_>), grid, block,          \
-                       (size_t)g.lds,                                                        \
-                       stream, P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K,       \
-                       g.chunks, P.rblk, g.gmax, g.xs_off, g.sc_off, g.sc_bytes, sc16,        \
-                       P.a_pitch, P.as_pitch, P.b_pitch, P.bs_pitch, P.y_pitch)
+                       (size_t)g.lds, stream, P.B, P.BS, P.A, P.AS, (int)P.N, (int)P.K,      \
+                       (int)P.b_pitch, (int)P.bs_pitch, (int)P.a_pitch, pk, (int)P.as_pitch, \
+                       P.Y, P.y_pitch)
 #define R3D_QUAD(ENC_, MT_, D_)                                                              \
     if (P.xq && g.wv == 8) R3D_QUADW(ENC_, MT_, 1, D_, 1, 8);                                \
     else if (P.xq) R3D_QUAD1(ENC_, MT_, 1, D_, 1);                                           \

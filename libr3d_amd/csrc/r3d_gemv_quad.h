@@ -101,25 +101,44 @@ __device__ __forceinline__ void r3d_quad_dma(const void* g, uint32_t lds) {
 }
 #pragma clang diagnostic pop
 
+/* The small launch parameters packed into one argument: M (1..4) in bits 0-2, log2 of the
+ * chunk count (0..2) in bits 3-4, fp8a8 weight scales on the 128 x 128 block grid in bit 5,
+ * mxfp4a8 scale rows contiguous and 16-byte aligned (1 KB staging loads) in bit 6, a_scale
+ * rows at a pitch of K / 128 floats in bit 7. */
+constexpr int quad_pack(int M, int log2_chunks, bool rblk128, bool sc16, bool as_dense) {
+    return M | (log2_chunks << 3) | ((int)rblk128 << 5) | ((int)sc16 << 6) | ((int)as_dense << 7);
+}
+
+/* The arguments every wave needs before its first load come first: the hardware preloads
+ * the leading 14 dwords of the argument block into registers at dispatch (the build asks
+ * for kernel-argument preloading), so the staging and the ring start without waiting on an
+ * argument fetch; as_pitch (M > 1 only), Y and its pitch are fetched as usual.  Pitches in
+ * bytes (b, a), bf16 / E8M0 elements (bs) or floats (as), all below 2^31 (quad_fits). */
 template <int ENC, int MT, int QPW, int D, int XQ = 0, int WV = 4>
 __global__ __launch_bounds__(64 * WV) void gemv_quad_kernel(
-    const uint8_t* A, const float* AS, const uint8_t* B, const void* BSv,
-    uint16_t* __restrict__ Y,
-    int M, int N, int K, int chunks, int rblk, int gmax, int xs_off, int sc_off, int sc_bytes,
-    int sc16,
-    int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch) {
+    const uint8_t* B, const void* BSv, const uint8_t* A, const float* AS,
+    int N, int K, int b_pitch, int bs_pitch, int a_pitch, int pk,
+    int as_pitch, uint16_t* __restrict__ Y, int64_t y_pitch) {
     constexpr int LPS = QPW * (ENC == ENC_MXFP4A8 ? 1 : 2);  /* weight loads per step */
     constexpr int RB = 4 * QPW;                               /* weight rows per wave */
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
+    const int M = pk & 7;
+    const int cl = (pk >> 3) & 3, chunks = 1 << cl;
+    const bool rblk128 = (pk >> 5) & 1;
+    const bool sc16 = (pk >> 6) & 1;
+    const bool as_dense = (pk >> 7) & 1;
+    const QuadLds ql = quad_lds(ENC, MT, QPW, WV, K, chunks);
+    const int xs_off = (int)ql.xs_off, sc_off = (int)ql.sc_off, sc_bytes = (int)ql.sc_bytes;
+
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int groups = K >> 7;
-    const int bpb = WV / chunks;                          /* row blocks per workgroup */
-    const int bi = wave / chunks, c = wave % chunks;
+    const int bpb = WV >> cl;                             /* row blocks per workgroup */
+    const int bi = wave >> cl, c = wave & (chunks - 1);
     const int64_t n0 = ((int64_t)blockIdx.x * bpb + bi) * RB;
-    const int g0 = (int)((int64_t)groups * c / chunks);
-    const int gc = (int)((int64_t)groups * (c + 1) / chunks) - g0;   /* >= 1: chunks <= groups */
+    const int g0 = (groups * c) >> cl;                    /* groups < 2^21: no overflow */
+    const int gc = ((groups * (c + 1)) >> cl) - g0;       /* >= 1: chunks <= groups */
     const int ns = (gc + 3) >> 2;                                     /* K steps of this wave */
     __builtin_assume(ns >= 1);
 
@@ -161,7 +180,7 @@ __global__ __launch_bounds__(64 * WV) void gemv_quad_kernel(
             int d = e / RB;
             if (d > gc - 1) d = gc - 1;
             const int64_t nr = n0 + (e % RB) < N ? n0 + (e % RB) : N - 1;
-            const int64_t sr = rblk == 1 ? nr : nr >> 7;
+            const int64_t sr = rblk128 ? nr >> 7 : nr;
             r3d_quad_dma<2>(BS16 + sr * bs_pitch + g0 + d, scl + 256 * h);
         }
     }
@@ -172,20 +191,32 @@ __global__ __launch_bounds__(64 * WV) void gemv_quad_kernel(
         const int nx = (MT * xp + 1023) >> 10;
         for (int i = wave; i < nx; i += WV) {
             const int b = 1024 * i + 16 * lane;
-            int t = b / xp, k = b - t * xp;
+            int t = 0;                                     /* b / xp, by compares */
+#pragma unroll
+            for (int j = 1; j <= MT; ++j) t += b >= j * xp;
+            int k = b - t * xp;
             if (t > MT - 1) { t = MT - 1; k = K - 16; }
             if (k > K - 16) k = K - 16;
-            const int tm = t < M ? t : M - 1;
+            const int tm = MT == 1 || t < M ? t : M - 1;
             r3d_quad_dma<16>(A + (int64_t)tm * a_pitch + k, lds0 + 1024 * i);
         }
         const int nxs = (MT * groups + 63) >> 6;
-        for (int h = wave; h < nxs; h += WV) {
-            const int e = lane + 64 * h;
-            int t = e / groups, g = e - t * groups;
-            if (t > MT - 1) { t = MT - 1; g = groups - 1; }
-            const int tm = t < M ? t : M - 1;
-            r3d_quad_dma<4>(AS + (int64_t)tm * as_pitch + g, lds0 + xs_off + 256 * h);
-        }
+        auto stage_as = [&](int64_t asp) {
+            for (int h = wave; h < nxs; h += WV) {
+                const int e = lane + 64 * h;
+                int t = 0;                                 /* e / groups, by compares */
+#pragma unroll
+                for (int j = 1; j <= MT; ++j) t += e >= j * groups;
+                int g = e - t * groups;
+                if (t > MT - 1) { t = MT - 1; g = groups - 1; }
+                const int tm = MT == 1 || t < M ? t : M - 1;
+                r3d_quad_dma<4>(AS + (int64_t)tm * asp + g, lds0 + xs_off + 256 * h);
+            }
+        };
+        /* one row, or rows at a pitch of groups floats: as_pitch (an argument past the
+         * preloaded ones, fetched on the other branch only) does not enter the address */
+        if (MT == 1 || as_dense) stage_as(groups);
+        else stage_as(as_pitch);
     }
 
     /* ---- 2. the weight stream, through a buffer resource over the wave's RB rows */
@@ -247,8 +278,11 @@ __global__ __launch_bounds__(64 * WV) void gemv_quad_kernel(
         for (int u = 0; u < XU; ++u) {
             const int c0 = 64 * (wave + WV * (batch * XU + u)) + lane;
             const int c = c0 < nchunk ? c0 : nchunk - 1;
-            const int t = c / cpr, k = 8 * (c - t * cpr);
-            const int tm = t < M ? t : M - 1;
+            int t = 0;                                     /* c / cpr, by compares */
+#pragma unroll
+            for (int j = 1; j < MT; ++j) t += c >= j * cpr;
+            const int k = 8 * (c - t * cpr);
+            const int tm = MT == 1 || t < M ? t : M - 1;
             xv[u] = *reinterpret_cast<const r3d_i32x4*>(A + (int64_t)tm * a_pitch + 2 * k);
         }
     };
@@ -268,7 +302,10 @@ __global__ __launch_bounds__(64 * WV) void gemv_quad_kernel(
 #pragma unroll
             for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
             if (c < nchunk) {                              /* whole 16-lane groups */
-                const int t = c / cpr, k = 8 * (c - t * cpr);
+                int t = 0;
+#pragma unroll
+                for (int j = 1; j < MT; ++j) t += c >= j * cpr;
+                const int k = 8 * (c - t * cpr);
                 const float sc = amax > 0.0f ? amax * (1.0f / 448.0f) : 1.0f;
                 const float inv = 1.0f / sc;
                 float cv[8];

@@ -336,7 +336,10 @@ void decode_geom(int64_t M, int64_t N, int64_t K, int64_t force_chunks, DecodeGe
     g->blocks = (g->tiles + g->tiles_per_block - 1) / g->tiles_per_block;
 }
 
-bool quad_fits(const GemmPlan& P) { return 8 * P.b_pitch < ((int64_t)1 << 31); }
+bool quad_fits(const GemmPlan& P) {
+    const int64_t lim = (int64_t)1 << 31;
+    return 8 * P.b_pitch < lim && P.a_pitch < lim && P.as_pitch < lim && P.bs_pitch < lim;
+}
 
 /* Quad geometry: split K until about env_quad_waves() waves are in flight (default 2048
  * at one activation row, 1280 at 2..4), keeping >= 16 groups per chunk.  A split doubles
@@ -373,20 +376,8 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
     int wv_env = env_quad_wv();
     if (wv_env == 7 && (c != 1 || xq || g->qpw != 1)) wv_env = 0;
     g->gmax = (g->groups + c - 1) / c;
-    const int64_t blob = ((int64_t)g->mt * (K + 16) + 1023) / 1024 * 1024;
-    const int64_t xs = ((int64_t)g->mt * g->groups * 4 + 255) / 256 * 256;
-    /* LDS of a workgroup of wv waves: the activation rows and a_scales (shared), then the
-     * weight scales -- mxfp4a8 stages the workgroup's rows over the whole K (1 KB loads),
-     * fp8a8 each wave's rows over its chunk; the fold reuses the blob's start */
-    auto lds_of = [&](int wv, int64_t* scb_out) {
-        const int64_t rbw = 4 * (int64_t)g->qpw * (wv / c);
-        const int64_t scb = enc == ENC_MXFP4A8 ? (rbw * 4 * g->groups + 1023) / 1024 * 1024
-                                               : (16 * g->qpw * (int64_t)g->gmax + 255) / 256 * 256;
-        int64_t lds = blob + xs + (enc == ENC_MXFP4A8 ? scb : (int64_t)wv * scb);
-        const int64_t fold = (int64_t)wv * g->qpw * 256;
-        if (scb_out) *scb_out = scb;
-        return lds < fold ? fold : lds;
-    };
+    /* LDS of a workgroup of wv waves (quad_lds, the layout the kernel computes too) */
+    auto lds_of = [&](int wv) { return quad_lds(enc, g->mt, g->qpw, wv, K, c).lds; };
     g->wv = g->qpw == 2 ? 4 : wv_env ? wv_env
           : (g->mt == 4 || (enc == ENC_FP8A8 && c == 1) || xq) ? 8 : 4;
     if (g->qpw == 1 && c == 1 && !xq && !wv_env) {
@@ -396,12 +387,12 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
          * against 1344 of 4, also 24) */
         const int w0 = g->wv;
         const int64_t b0 = (g->nblk + w0 - 1) / w0, b7 = (g->nblk + 6) / 7;
-        if (((b7 + 255) / 256) * 7 < ((b0 + 255) / 256) * w0 && lds_of(7, nullptr) <= kQuadMaxLds)
+        if (((b7 + 255) / 256) * 7 < ((b0 + 255) / 256) * w0 && lds_of(7) <= kQuadMaxLds)
             g->wv = 7;
     }
     /* the policy's seven or eight waves only where their LDS fits; four otherwise (a lever
      * that does not fit refuses, so the next kernel runs) */
-    if (!wv_env && g->wv != 4 && lds_of(g->wv, nullptr) > kQuadMaxLds) g->wv = 4;
+    if (!wv_env && g->wv != 4 && lds_of(g->wv) > kQuadMaxLds) g->wv = 4;
     g->bpb = g->wv / c;
     g->blocks = (g->nblk + g->bpb - 1) / g->bpb;
     {
@@ -417,13 +408,12 @@ bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, Q
         for (int d : kDepths)
             if (d <= want && d <= ns_min) { g->depth = d; break; }
     }
-    int64_t scb = 0;
-    const int64_t lds = lds_of(g->wv, &scb);
-    if (lds > kQuadMaxLds || g->blocks > 0x7FFFFFFF) return false;
-    g->xs_off = (int)blob;
-    g->sc_off = (int)(blob + xs);
-    g->sc_bytes = (int)scb;
-    g->lds = (int)lds;
+    const QuadLds ql = quad_lds(enc, g->mt, g->qpw, g->wv, K, c);
+    if (ql.lds > kQuadMaxLds || g->blocks > 0x7FFFFFFF) return false;
+    g->xs_off = (int)ql.xs_off;
+    g->sc_off = (int)ql.sc_off;
+    g->sc_bytes = (int)ql.sc_bytes;
+    g->lds = (int)ql.lds;
     return true;
 }
 

@@ -77,6 +77,31 @@ struct QuadGeom {
     int lds;                 /* dynamic LDS bytes per workgroup */
 };
 
+/* The quad GEMV's LDS layout, computed the same way by the kernel (from K and the chunk
+ * count) and by quad_geom: the activation rows [mt][K + 16] bytes at 0, rounded up to 1 KB;
+ * the a_scales [mt][groups] f32 at xs_off, rounded up to 256 B; the weight scales at sc_off
+ * -- mxfp4a8: the workgroup's rows over the whole K ([rows][groups dwords], rounded up to
+ * 1 KB: sc_bytes in all), fp8a8: sc_bytes per wave ([ceil(groups / chunks)][4 qpw rows]
+ * 4-byte slots, rounded up to 256 B); the fold after the K loop reuses the start
+ * (wv * qpw * 256 bytes).  chunks is a power of two (1, 2 or 4).  A constexpr function,
+ * so the kernel's copy is the same code. */
+struct QuadLds {
+    int64_t xs_off, sc_off, sc_bytes, lds;
+};
+constexpr QuadLds quad_lds(int enc, int mt, int qpw, int wv, int64_t K, int chunks) {
+    const int64_t groups = K >> 7;
+    const int64_t blob = ((mt * (K + 16) + 1023) >> 10) << 10;
+    const int64_t xs = ((mt * groups * 4 + 255) >> 8) << 8;
+    const int cl = __builtin_ctz((unsigned)chunks);
+    const int64_t gmax = (groups + chunks - 1) >> cl;
+    const int64_t scb = enc == ENC_MXFP4A8
+                            ? ((4 * qpw * (int64_t)(wv >> cl) * 4 * groups + 1023) >> 10) << 10
+                            : ((16 * qpw * gmax + 255) >> 8) << 8;
+    const int64_t lds = blob + xs + (enc == ENC_MXFP4A8 ? scb : wv * scb);
+    const int64_t fold = (int64_t)wv * qpw * 256;
+    return QuadLds{blob, blob + xs, scb, lds < fold ? fold : lds};
+}
+
 /* Launch geometry of the line GEMV (M <= 16): one wave per block of tw 16-row weight tiles
  * and K chunk, 4 waves per workgroup (4 / chunks blocks x chunks); a unit is one 128-byte
  * line of every row of the block (2 K groups at mxfp4a8, 1 at fp8a8). */
@@ -135,7 +160,7 @@ constexpr int kQuadMaxLds = 48 * 1024;
 bool quad_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, QuadGeom* g,
                int xq = 0);
 /* The quad kernel addresses a wave's (up to 8) weight rows through one buffer resource:
- * they must span less than 2^31 bytes. */
+ * they must span less than 2^31 bytes; it takes the operand pitches as 32-bit arguments. */
 bool quad_fits(const GemmPlan& P);
 /* Line GEMV geometry; false when the shape is outside what it serves (M outside 5..16, or a
  * wave's scale tables over the LDS budget), and the 16-row GEMV runs instead.  force_chunks:
