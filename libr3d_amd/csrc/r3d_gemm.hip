@@ -184,13 +184,17 @@ static hipError_t wide_launch(const GemmPlan& P, const WideGeom& w, int kc, floa
                               hipStream_t stream) {
     /* 32-bit lane offsets: a wave's 32 weight rows and the staged activation rows */
     const int64_t lim = (int64_t)1 << 31;
-    if (32 * P.b_pitch >= lim || w.tw != 2 || P.M > 64) return hipErrorInvalidValue;
+    if (32 * P.b_pitch >= lim || P.a_pitch >= lim || P.as_pitch >= lim || P.bs_pitch >= lim ||
+        w.tw != 2 || P.M < 1 || P.M > 64 || w.cg < 1 || w.cg > 0xFFFF || kc < 1 || kc > 0x7FFF ||
+        w.ntiles != (P.N + 255) / 256 || w.sclds != (16 * 2 * w.cg * 4 + 255) / 256 * 256)
+        return hipErrorInvalidValue;
+    const int pk = wide_pack((int)P.M, P.rblk == 128, P.a_pitch == P.K, P.as_pitch == P.K / 128);
+    const int cgkc = w.cg | (kc << 16);
     const dim3 grid((unsigned)(w.ntiles * kc)), block(512);
 #define R3D_WIDE(ENC_, D_, NTG_)                                                           \
     hipLaunchKernelGGL((gemv_wide_kernel<ENC_, 2, D_, NTG_>), grid, block, (size_t)w.lds,    \
-                       stream, P.A, P.AS, P.B, P.BS, part, (int)P.M, (int)P.N, (int)P.K, kc, \
-                       w.cg, (int)w.ntiles, P.rblk, w.sclds, P.a_pitch, P.as_pitch,         \
-                       P.b_pitch, P.bs_pitch)
+                       stream, P.A, P.AS, P.B, P.BS, (int)P.N, (int)P.K, (int)P.b_pitch,     \
+                       (int)P.bs_pitch, pk, cgkc, (int)P.a_pitch, (int)P.as_pitch, part)
 #define R3D_WIDE_N(ENC_, D_)                                                                \
     switch (w.ntg) {                                                                        \
         case 1: R3D_WIDE(ENC_, D_, 1); break;                                               \
@@ -211,12 +215,13 @@ static hipError_t wide_launch(const GemmPlan& P, const WideGeom& w, int kc, floa
 
 /* The in-order sum of kc f32 partial planes of M x N at part into bf16 Y. */
 static hipError_t splitk_reduce(const GemmPlan& P, int kc, const float* part, hipStream_t stream) {
-    const int64_t lanes = P.M * ((P.N + 3) / 4);
-    if (lanes <= 32768)
-        hipLaunchKernelGGL((splitk_reduce_kernel<64, 16>), dim3((unsigned)((lanes + 63) / 64)),
+    const int64_t cpr = (P.N + 3) / 4;                   /* column quads a row */
+    if (P.M < 1 || P.M > 65535 || cpr > 0x3FFFFFFF) return hipErrorInvalidValue;
+    if (P.M * cpr <= 32768)
+        hipLaunchKernelGGL((splitk_reduce_kernel<64, 16>), dim3((unsigned)((cpr + 63) / 64), (unsigned)P.M),
                            dim3(64), 0, stream, part, kc, (int)P.M, (int)P.N, P.Y, P.y_pitch);
     else
-        hipLaunchKernelGGL((splitk_reduce_kernel<256, 4>), dim3((unsigned)((lanes + 255) / 256)),
+        hipLaunchKernelGGL((splitk_reduce_kernel<256, 4>), dim3((unsigned)((cpr + 255) / 256), (unsigned)P.M),
                            dim3(256), 0, stream, part, kc, (int)P.M, (int)P.N, P.Y, P.y_pitch);
     return hipGetLastError();
 }

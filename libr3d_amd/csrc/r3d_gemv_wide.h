@@ -46,18 +46,36 @@ struct WideUnit {
     r3d_i32x4 w0[TW], w1[TW];
 };
 
+/* The small parameters packed into one argument: M (1..64) in bits 0-6, fp8a8 weight
+ * scales on the 128 x 128 block grid in bit 7, activation rows at a pitch of K bytes in
+ * bit 8, a_scale rows at a pitch of K / 128 floats in bit 9; and cg (< 2^16) | kc << 16 in
+ * another. */
+constexpr int wide_pack(int M, bool rblk128, bool a_dense, bool as_dense) {
+    return M | ((int)rblk128 << 7) | ((int)a_dense << 8) | ((int)as_dense << 9);
+}
+
+/* The arguments the prologue needs come first: the hardware preloads the leading 14 dwords
+ * of the argument block at dispatch (the build asks for kernel-argument preloading).  The
+ * activation pitches follow them and are fetched only when the rows are not dense; part is
+ * first used after the K walk.  Pitches in bytes (b, a), bf16 / E8M0 elements (bs) or
+ * floats (as), all below 2^31. */
 template <int ENC, int TW, int D, int NTG>
 __global__ __launch_bounds__(512) void gemv_wide_kernel(
     const uint8_t* A, const float* AS, const uint8_t* B, const void* BSv,
-    float* __restrict__ part,
-    int M, int N, int K, int kc, int cg, int ntiles, int rblk, int sclds,
-    int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch) {
+    int N, int K, int b_pitch, int bs_pitch, int pk, int cgkc,
+    int a_pitch, int as_pitch, float* __restrict__ part) {
     constexpr int ntg = NTG;                               /* 16-row activation groups */
     constexpr int G = ENC == ENC_MXFP4A8 ? 2 : 1;          /* K groups per 128-byte line */
     constexpr int WV = 8;                                  /* waves per workgroup */
     constexpr int RW = 16 * TW;                            /* weight rows per wave */
     constexpr int LPU = 2 * TW;                            /* loads per line of the ring */
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+    const int M = pk & 127;
+    const bool rblk128 = (pk >> 7) & 1, a_dense = (pk >> 8) & 1, as_dense = (pk >> 9) & 1;
+    const int cg = cgkc & 0xFFFF, kc = (int)((unsigned)cgkc >> 16);
+    const int ntiles = (N + WV * RW - 1) / (WV * RW);      /* WV * RW = 256: a shift */
+    const int sclds = ((16 * TW * cg * 4 + 255) >> 8) << 8;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -91,18 +109,28 @@ __global__ __launch_bounds__(512) void gemv_wide_kernel(
     {
         const int tm = (lane >> 3) & 7;                    /* row of this lane in an image */
         const int ch = (lane & 7) ^ tm;                    /* the chunk it fetches */
-        for (int i = wave; i < gc * rows8; i += WV) {
-            const int gi = i / rows8, ri = i - gi * rows8;
-            int m = 8 * ri + tm;
-            if (m > M - 1) m = M - 1;
-            r3d_quad_dma<16>(A + (int64_t)m * a_pitch + 128 * (int64_t)(g0 + gi) + 16 * ch,
-                             sbase + (uint32_t)(gi * gstride + ri * 1024));
-        }
-        for (int gi = wave; gi < gc; gi += WV) {
-            const int m = lane < M ? lane : M - 1;
-            r3d_quad_dma<4>(AS + (int64_t)m * as_pitch + g0 + gi,
-                            sbase + (uint32_t)(xs_off + 256 * gi));
-        }
+        /* dense rows take their pitch from K, so a_pitch / as_pitch (arguments past the
+         * preloaded ones) are fetched on the other branches only */
+        auto stage_x = [&](int64_t ap) {
+            for (int i = wave; i < gc * rows8; i += WV) {
+                const int gi = i / rows8, ri = i - gi * rows8;
+                int m = 8 * ri + tm;
+                if (m > M - 1) m = M - 1;
+                r3d_quad_dma<16>(A + (int64_t)m * ap + 128 * (int64_t)(g0 + gi) + 16 * ch,
+                                 sbase + (uint32_t)(gi * gstride + ri * 1024));
+            }
+        };
+        if (a_dense) stage_x(K);
+        else stage_x(a_pitch);
+        auto stage_as = [&](int64_t asp) {
+            for (int gi = wave; gi < gc; gi += WV) {
+                const int m = lane < M ? lane : M - 1;
+                r3d_quad_dma<4>(AS + (int64_t)m * asp + g0 + gi,
+                                sbase + (uint32_t)(xs_off + 256 * gi));
+            }
+        };
+        if (as_dense) stage_as(groups);
+        else stage_as(as_pitch);
     }
     const uint32_t wl = sbase + (uint32_t)(sc_off + wave * sclds);
     if (ENC == ENC_MXFP4A8) {
@@ -125,7 +153,7 @@ __global__ __launch_bounds__(512) void gemv_wide_kernel(
             const int r = e % RW;
             if (d > gc - 1) d = gc - 1;
             const int64_t nr = n0 + r < N ? n0 + r : N - 1;
-            const int64_t sr = rblk == 1 ? nr : nr >> 7;
+            const int64_t sr = rblk128 ? nr >> 7 : nr;
             r3d_quad_dma<2>(BS16 + sr * bs_pitch + g0 + d, wl + 256 * h);
         }
     }

@@ -625,10 +625,12 @@ template <int TH, int BATCH>
 __global__ __launch_bounds__(TH) void splitk_reduce_kernel(
     const float* __restrict__ part, int kc, int M, int N, uint16_t* __restrict__ Y,
     int64_t y_pitch) {
+    /* grid: (column quads / TH, M rows) -- the row is the workgroup's y index, so no lane
+     * divides by the row length before its first load */
     const int cpr = (N + 3) >> 2;
-    const int64_t e = (int64_t)blockIdx.x * TH + threadIdx.x;
-    if (e >= (int64_t)M * cpr) return;
-    const int m = (int)(e / cpr), n = 4 * (int)(e - (int64_t)m * cpr);
+    const int q = blockIdx.x * TH + threadIdx.x;
+    if (q >= cpr) return;
+    const int m = blockIdx.y, n = 4 * q;
     const int64_t plane = (int64_t)M * N;
     const float* p = part + (int64_t)m * N + n;
     r3d_f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
