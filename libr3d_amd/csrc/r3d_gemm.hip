@@ -142,11 +142,17 @@ static int launch_lines(const GemmPlan& P, const LinesGeom& g, hipStream_t strea
     if (forced_fail(passes > 1 ? "skinny" : "lines"))
         return launch_failed(passes > 1 ? "skinny line GEMV" : "line decode GEMV", hipSuccess);
     const dim3 grid((unsigned)g.blocks, (unsigned)passes), block(256);
+    const int64_t lim = (int64_t)1 << 31;
+    if (P.M < 1 || P.M > 127 || (g.chunks != 1 && g.chunks != 2 && g.chunks != 4) ||
+        P.a_pitch >= lim || P.as_pitch >= lim || P.b_pitch >= lim || P.bs_pitch >= lim ||
+        g.wlds != lines_wlds(P.enc, g.tw, P.K, g.chunks))
+        return RAD_E_UNSUPPORTED;
+    const int pk = lines_pack((int)P.M, g.chunks == 4 ? 2 : g.chunks == 2 ? 1 : 0, P.rblk == 128,
+                              P.as_pitch == P.K / 128);
 #define R3D_LINES(ENC_, MT_, TW_, D_)                                                        \
     hipLaunchKernelGGL((gemv_lines_kernel<ENC_, MT_, TW_, D_>), grid, block, (size_t)g.lds,    \
-                       stream, P.A, P.AS, P.B, P.BS, P.Y, (int)P.M, (int)P.N, (int)P.K,        \
-                       g.chunks, P.rblk, g.gmax, g.wlds, P.a_pitch, P.as_pitch, P.b_pitch,    \
-                       P.bs_pitch, P.y_pitch)
+                       stream, P.A, P.AS, P.B, P.BS, (int)P.N, (int)P.K, (int)P.b_pitch,     \
+                       (int)P.bs_pitch, (int)P.a_pitch, pk, (int)P.as_pitch, P.Y, P.y_pitch)
 #define R3D_LINES_T(ENC_, MT_, D_)                                                           \
     do {                                                                                     \
         if (g.tw == 4) R3D_LINES(ENC_, MT_, 4, (D_ > 2 ? 2 : D_));                           \

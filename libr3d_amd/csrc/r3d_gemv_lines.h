@@ -68,35 +68,50 @@ struct LinesUnit {
     r3d_i32x4 x1[MT == 16 ? G : 1];
 };
 
+/* The small parameters packed into one argument: M (1..64: the skinny band's passes see
+ * up to 16 each) in bits 0-6, log2 of the chunk count (0..2) in bits 7-8, fp8a8 weight
+ * scales on the 128 x 128 block grid in bit 9, a_scale rows at a pitch of K / 128 floats
+ * in bit 10. */
+constexpr int lines_pack(int M, int log2_chunks, bool rblk128, bool as_dense) {
+    return M | (log2_chunks << 7) | ((int)rblk128 << 9) | ((int)as_dense << 10);
+}
+
+/* The arguments the prologue needs come first (the hardware preloads the leading 14 dwords
+ * of the argument block at dispatch); as_pitch (rows not dense), Y and its pitch follow.
+ * Pitches in bytes (b, a), bf16 / E8M0 elements (bs) or floats (as), below 2^31. */
 template <int ENC, int MT, int TW, int D>
 __global__ __launch_bounds__(256) void gemv_lines_kernel(
     const uint8_t* A, const float* AS, const uint8_t* B, const void* BSv,
-    uint16_t* __restrict__ Y,
-    int M, int N, int K, int chunks, int rblk, int gmax, int wlds,
-    int64_t a_pitch, int64_t as_pitch, int64_t b_pitch, int64_t bs_pitch, int64_t y_pitch) {
+    int N, int K, int b_pitch, int bs_pitch, int a_pitch, int pk,
+    int as_pitch, uint16_t* __restrict__ Y, int64_t y_pitch) {
     constexpr int G = ENC == ENC_MXFP4A8 ? 2 : 1;          /* K groups per unit */
     constexpr int LPU = 2 * TW + G * (MT == 16 ? 2 : 1);   /* loads per unit */
     constexpr int RW = 16 * TW;                            /* weight rows per wave */
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    int M = pk & 127;
+    const int cl = (pk >> 7) & 3, chunks = 1 << cl;
+    const bool rblk128 = (pk >> 9) & 1, as_dense = (pk >> 10) & 1;
+    const int groups = K >> 7;
     /* grid.y > 1 (the skinny band): workgroup row y computes activation rows
-     * [16 y, 16 y + 16) of a taller A -- the same arithmetic as a 16-row call */
+     * [16 y, 16 y + 16) of a taller A -- the same arithmetic as a 16-row call (AS moves
+     * with it in the staging below) */
+    const int m0 = 16 * (int)blockIdx.y;
     {
-        const int m0 = 16 * (int)blockIdx.y;
-        A += m0 * a_pitch;
-        AS += m0 * as_pitch;
+        A += (int64_t)m0 * a_pitch;
         Y += m0 * y_pitch;
         M = M - m0 < 16 ? M - m0 : 16;
     }
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int groups = K >> 7;
     const int units = (groups + G - 1) / G;
-    const int tpb = 4 / chunks;                            /* row blocks per workgroup */
-    const int ti = wave / chunks, c = wave % chunks;
+    const int tpb = 4 >> cl;                               /* row blocks per workgroup */
+    const int ti = wave >> cl, c = wave & (chunks - 1);
     const int64_t n0 = ((int64_t)blockIdx.x * tpb + ti) * RW;
-    const int u0 = (int)((int64_t)units * c / chunks);
-    const int ns = (int)((int64_t)units * (c + 1) / chunks) - u0;   /* >= 1: chunks <= units */
+    const int u0 = (units * c) >> cl;                      /* units < 2^21: no overflow */
+    const int ns = ((units * (c + 1)) >> cl) - u0;         /* >= 1: chunks <= units */
+    const int gmax = G * ((units + chunks - 1) >> cl);
+    const int wlds = lines_wlds(ENC, TW, K, chunks);
     __builtin_assume(ns >= 1);
     const int g0 = G * u0;
     const int gc = (G * ns < groups - g0) ? G * ns : groups - g0;   /* real groups */
@@ -110,14 +125,20 @@ __global__ __launch_bounds__(256) void gemv_lines_kernel(
      * bytes of its slice, then the weight scales of its RW rows */
     const int xsb = (64 * gmax + 255) & ~255;
     const uint32_t wl = (uint32_t)(uintptr_t)smem + (uint32_t)(wave * wlds);
-    for (int h = 0; h < (xsb >> 8); ++h) {
-        const int e = lane + 64 * h;
-        int t = e / gmax, g = e - t * gmax;
-        if (t > 15) { t = 15; g = gmax - 1; }
-        if (g > gc - 1) g = gc - 1;
-        const int tm = t < M ? t : M - 1;
-        r3d_quad_dma<4>(AS + (int64_t)tm * as_pitch + g0 + g, wl + 256 * h);
-    }
+    /* dense a_scale rows take their pitch from K, so as_pitch (an argument past the
+     * preloaded ones) is fetched on the other branch only */
+    auto stage_as = [&](int64_t asp) {
+        for (int h = 0; h < (xsb >> 8); ++h) {
+            const int e = lane + 64 * h;
+            int t = e / gmax, g = e - t * gmax;
+            if (t > 15) { t = 15; g = gmax - 1; }
+            if (g > gc - 1) g = gc - 1;
+            const int tm = t < M ? t : M - 1;
+            r3d_quad_dma<4>(AS + (int64_t)(m0 + tm) * asp + g0 + g, wl + 256 * h);
+        }
+    };
+    if (as_dense) stage_as(groups);
+    else stage_as(as_pitch);
     const int nsc = (wlds - xsb) >> 8;
     if (ENC == ENC_MXFP4A8) {
         /* [RW rows][gmax] E8M0 dwords */
@@ -139,7 +160,7 @@ __global__ __launch_bounds__(256) void gemv_lines_kernel(
             const int r = e % RW;
             if (d > gc - 1) d = gc - 1;
             const int64_t nr = n0 + r < N ? n0 + r : N - 1;
-            const int64_t sr = rblk == 1 ? nr : nr >> 7;
+            const int64_t sr = rblk128 ? nr >> 7 : nr;
             r3d_quad_dma<2>(BS16 + sr * bs_pitch + g0 + d, wl + xsb + 256 * h);
         }
     }

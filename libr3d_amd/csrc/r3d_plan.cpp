@@ -442,10 +442,7 @@ bool lines_geom(int enc, int64_t M, int64_t N, int64_t K, int64_t force_chunks, 
     const int etw = env_lines_tw();
     g->tw = etw == 1 || etw == 2 || etw == 4 ? etw : 2;
     g->nblk = (g->tiles + g->tw - 1) / g->tw;
-    auto wlds_of = [&](int c) {
-        const int gm = G * ((g->units + c - 1) / c);
-        return (64 * gm + 255) / 256 * 256 + (64 * g->tw * gm + 255) / 256 * 256;
-    };
+    auto wlds_of = [&](int c) { return lines_wlds(enc, g->tw, K, c); };
     int c = 1;
     if (force_chunks > 0) {
         c = (int)force_chunks;

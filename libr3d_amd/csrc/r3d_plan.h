@@ -102,6 +102,16 @@ constexpr QuadLds quad_lds(int enc, int mt, int qpw, int wv, int64_t K, int chun
     return QuadLds{blob, blob + xs, scb, lds < fold ? fold : lds};
 }
 
+/* The line GEMV's per-wave LDS slice (a_scales [16][gmax] f32, then the weight scales of
+ * its 16 tw rows over gmax groups, each rounded up to 256 B) for `chunks` (1, 2 or 4) K
+ * chunks; the kernel computes it the same way. */
+constexpr int lines_wlds(int enc, int tw, int64_t K, int chunks) {
+    const int G = enc == ENC_MXFP4A8 ? 2 : 1;
+    const int units = (int)(((K >> 7) + G - 1) / G);
+    const int gm = G * ((units + chunks - 1) >> __builtin_ctz((unsigned)chunks));
+    return (((64 * gm + 255) >> 8) << 8) + (((64 * tw * gm + 255) >> 8) << 8);
+}
+
 /* Launch geometry of the line GEMV (M <= 16): one wave per block of tw 16-row weight tiles
  * and K chunk, 4 waves per workgroup (4 / chunks blocks x chunks); a unit is one 128-byte
  * line of every row of the block (2 K groups at mxfp4a8, 1 at fp8a8). */
