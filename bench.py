@@ -189,7 +189,11 @@ FLOOR_SIZES = {          # algorithmic bytes of the decode workloads the floors 
     "c2_gate_up_M1": lambda: mx_bytes(1, 21504, 5376),
     "c1": lambda: f8_bytes(1, 21504, 5376),
     "lm_head_M4": lambda: f8_bytes(4, 262144, 5376),
+    "c1_weight_plane": lambda: 21504 * 5376,
 }
+# a workload timed at one probe shape only: config 1's weight plane in the GEMV's own grid --
+# 768 workgroups of 7 waves, each wave streaming 4 rows x 5376 bytes = 21 KB
+FLOOR_ONLY_SHAPE = {"c1_weight_plane": [(21, 7)]}
 
 
 def bench_floors(dev, stream, min_s=0.03):
@@ -210,16 +214,17 @@ def bench_floors(dev, stream, min_s=0.03):
             b.view(torch.int32)[: nb // 4].fill_(0x01020304)
         rec = {"bytes": nb, "copies": len(bufs), "probe": {}}
         best = None
-        for kb in (16, 22, 32, 64, 128):
-            for wpg in (4, 8):
-                def go(i, kb=kb, wpg=wpg):
-                    rc = L.r3d_gfx950_stream_probe(ctypes_ptr(bufs[i % len(bufs)]), nb, wpg, kb,
-                                                   ctypes_ptr(sink), ctypes_ptr_stream(stream))
-                    assert rc == 0, rc
-                t, n = time_min(go, min_s)
-                rec["probe"]["%dKBx%d" % (kb, wpg)] = round(t * 1e6, 3)
-                if best is None or t < best[0]:
-                    best = (t, "%d KB a wave, %d waves a workgroup" % (kb, wpg))
+        shapes = FLOOR_ONLY_SHAPE.get(name) or [(kb, wpg) for kb in (16, 22, 32, 64, 128)
+                                                for wpg in (4, 8)]
+        for kb, wpg in shapes:
+            def go(i, kb=kb, wpg=wpg):
+                rc = L.r3d_gfx950_stream_probe(ctypes_ptr(bufs[i % len(bufs)]), nb, wpg, kb,
+                                               ctypes_ptr(sink), ctypes_ptr_stream(stream))
+                assert rc == 0, rc
+            t, n = time_min(go, min_s)
+            rec["probe"]["%dKBx%d" % (kb, wpg)] = round(t * 1e6, 3)
+            if best is None or t < best[0]:
+                best = (t, "%d KB a wave, %d waves a workgroup" % (kb, wpg))
         rec["probe_us"] = round(best[0] * 1e6, 3)
         rec["probe_best"] = best[1]
         rec["probe_GBps"] = round(nb / best[0] / 1e9, 1)
@@ -295,6 +300,28 @@ def cpu_baseline(seconds=10.0):
                       "when set) on %s" % (calls, el, nth, cpu or "host CPU")}
 
 
+def bench_overlap(dev, stream, iters=4096):
+    """How much VALU work one wave hides under its own MFMAs (r3d_gfx950_mfma_valu_probe):
+    shader-clock ticks per 16x16x128 e4m3 MFMA with nv independent f32 fused multiply-adds
+    issued between consecutive MFMAs, and with 4 / 8 that read the result of the MFMA issued
+    three earlier (the e4m3 prefill tile's flush).  Each case launched twice, the second
+    timed."""
+    import torch
+    import libr3d_amd as R
+    L = R.lib()
+    work = torch.zeros(256, dtype=torch.int32, device=dev)
+    cyc = torch.zeros(1, dtype=torch.int64, device=dev)
+    out = {}
+    for nv, lag3 in ((0, 0), (4, 0), (8, 0), (16, 0), (4, 1), (8, 1)):
+        for _ in range(2):
+            rc = L.r3d_gfx950_mfma_valu_probe(nv, lag3, iters, ctypes_ptr(work), ctypes_ptr(cyc),
+                                              ctypes_ptr_stream(stream))
+            assert rc == 0, rc
+        torch.cuda.synchronize()
+        out["nv%d%s" % (nv, "_lag3" if lag3 else "")] = round(int(cyc.item()) / (4 * iters), 2)
+    return {"ticks_per_mfma": out, "iters": iters}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -308,6 +335,8 @@ def main():
                     help="only measure the HBM stream ceilings and the launch floor, print JSON")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy (counter calibration for PMC runs)")
+    ap.add_argument("--overlap", action="store_true",
+                    help="only run the MFMA / VALU overlap probe (one wave), print JSON")
     ap.add_argument("--c3-only", action="store_true",
                     help="only time config 3 (mxfp4a16 prefill) and print its JSON (for profiling)")
     ap.add_argument("--case", default=None,
@@ -340,6 +369,9 @@ def main():
         return
     if args.floors:
         print(json.dumps(bench_floors(dev, stream)), flush=True)
+        return
+    if args.overlap:
+        print(json.dumps(bench_overlap(dev, stream)), flush=True)
         return
     if args.case:
         print(json.dumps(run_case(args.case, dev, stream, args.steps, args.warmup)), flush=True)

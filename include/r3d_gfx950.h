@@ -213,6 +213,18 @@ int r3d_gfx950_mxfp4a16_stage(const RadArgs* a, RadStream s, int stage);
 int r3d_gfx950_stream_probe(const void* src, int64_t bytes, int waves_per_wg, int64_t kb,
                             uint32_t* sink, RadStream s);
 
+/* Measurement diagnostic with no counterpart in the reference: one wave on `s` runs `iters`
+ * rounds of four 16 x 16 x 128 e4m3 MFMAs (four in-place accumulator chains) with `nv`
+ * independent f32 fused multiply-adds before each (nv 0, 4, 8 or 16; with lag3 != 0, 4 or 8
+ * multiply-adds that read the result of the MFMA issued three earlier), and writes the
+ * shader-clock ticks the loop took to the device int64 at `cycles`.  work: a device buffer
+ * of at least 1 KB (inputs read from its first 512 bytes, results written after them).
+ * Divided by 4 * iters it gives the cost of one MFMA plus its share of VALU work: how much
+ * VALU a wave hides under its own MFMAs.  RAD_OK, RAD_E_INVAL for a bad argument,
+ * RAD_E_DEVICE if the launch fails. */
+int r3d_gfx950_mfma_valu_probe(int nv, int lag3, int iters, void* work, int64_t* cycles,
+                               RadStream s);
+
 /* Build identity with no counterpart in the reference: the SHA-256 (hex) of the compile
  * flags and of the sources this library was compiled from -- the flags as one line, then
  * every file under libr3d_amd/csrc and include, in name order, each as "<relative

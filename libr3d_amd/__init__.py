@@ -195,6 +195,9 @@ def lib():
         L.r3d_gfx950_stream_probe.restype = ctypes.c_int
         L.r3d_gfx950_stream_probe.argtypes = [ctypes.c_void_p, _i64, ctypes.c_int, _i64,
                                               ctypes.c_void_p, ctypes.c_void_p]
+        L.r3d_gfx950_mfma_valu_probe.restype = ctypes.c_int
+        L.r3d_gfx950_mfma_valu_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         L.r3d_gfx950_logits_head_forget.restype = None
         L.r3d_gfx950_logits_head_forget.argtypes = [ctypes.c_void_p]
         _LIB = L

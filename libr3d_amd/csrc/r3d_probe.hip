@@ -1,6 +1,13 @@
 /* r3d_probe.hip -- measurement diagnostics with no counterpart in the reference: the
  * ceilings the decode GEMVs are held against (bench.py --floors).
  *
+ *   r3d_gfx950_mfma_valu_probe: one wave alone on the GPU issuing a loop of 16 x 16 x 128 e4m3
+ *   MFMAs (four independent accumulator chains) with `nv` independent f32 fused multiply-adds
+ *   between every two, timed in the shader clock with s_memtime around the loop -- how much
+ *   VALU work a wave hides under its own MFMAs (the flush of the e4m3 prefill tiles).
+ *   `lag3` makes the multiply-adds read the result of the MFMA issued three earlier, the
+ *   flush's own dependence.
+ *
  *   r3d_gfx950_stream_probe: a read-only stream over `bytes` of device memory, each wave
  *   reading its own contiguous run of `kb` KB with 1 KB loads (64 lanes x 16 bytes,
  *   non-temporal, the GEMVs' load instruction) kept 8 deep in flight, the bytes XOR-folded
@@ -47,6 +54,54 @@ __global__ __launch_bounds__(512) void stream_probe_kernel(const uint8_t* src, i
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+
+/* nv fused multiply-adds between consecutive MFMAs; the MFMAs accumulate in place over four
+ * chains, so none is loop-invariant and each waits only on the chain's MFMA four back. */
+template <int NV, bool LAG3>
+__global__ __launch_bounds__(64) void mfma_valu_probe_kernel(const int* in, float* out,
+                                                             long long* cycles, int iters) {
+    r3d_i32x8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = in[threadIdx.x + i];
+        b[i] = in[threadIdx.x + 8 + i];
+    }
+    r3d_f32x4 d[4];
+    float acc[16];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) d[m] = r3d_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = (float)in[i] * 0.5f;
+    const float s = out[0];
+    const long long t0 = __builtin_readcyclecounter();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            if (LAG3) {
+                const r3d_f32x4 r = d[(m + 1) & 3];            /* issued three MFMAs ago */
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    acc[(4 * m + j) & 15] = __builtin_fmaf(r[j & 3], s, acc[(4 * m + j) & 15]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    acc[(4 * m + j) & 15] =
+                        __builtin_fmaf(acc[(4 * m + j + 1) & 15], s, acc[(4 * m + j) & 15]);
+            }
+            d[m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                a, b, d[m], R3D_MFMA_FP8, R3D_MFMA_FP8, 0, R3D_E8M0_ONE, 0, R3D_E8M0_ONE);
+        }
+    }
+    const long long t1 = __builtin_readcyclecounter();
+    float z = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z += acc[i];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) z += d[m][0] + d[m][1] + d[m][2] + d[m][3];
+    out[1 + threadIdx.x] = z;
+    if (threadIdx.x == 0) cycles[0] = t1 - t0;
+}
+
 }  // namespace r3d
 
 extern "C" int r3d_gfx950_stream_probe(const void* src, int64_t bytes, int waves_per_wg,
@@ -59,5 +114,27 @@ extern "C" int r3d_gfx950_stream_probe(const void* src, int64_t bytes, int waves
     if (blocks > 0x7FFFFFFF || run > 0x7FFFFFFF) return RAD_E_SHAPE;
     hipLaunchKernelGGL(r3d::stream_probe_kernel, dim3((unsigned)blocks), dim3(64 * waves_per_wg),
                        0, (hipStream_t)s, (const uint8_t*)src, bytes, (int)run, sink);
+    return hipGetLastError() == hipSuccess ? RAD_OK : RAD_E_DEVICE;
+}
+
+extern "C" int r3d_gfx950_mfma_valu_probe(int nv, int lag3, int iters, void* work,
+                                          int64_t* cycles, RadStream s) {
+    if (!work || !cycles || iters < 1 || iters > (1 << 24)) return RAD_E_INVAL;
+    const int* in = reinterpret_cast<const int*>(work);
+    float* out = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(work) + 512);
+    long long* cyc = reinterpret_cast<long long*>(cycles);
+    const hipStream_t st = (hipStream_t)s;
+#define R3D_OVP(NV, L)                                                                        \
+    hipLaunchKernelGGL((r3d::mfma_valu_probe_kernel<NV, L>), dim3(1), dim3(64), 0, st, in, out, \
+                       cyc, iters)
+    if (lag3 && nv == 4) R3D_OVP(4, true);
+    else if (lag3 && nv == 8) R3D_OVP(8, true);
+    else if (lag3) return RAD_E_INVAL;
+    else if (nv == 0) R3D_OVP(0, false);
+    else if (nv == 4) R3D_OVP(4, false);
+    else if (nv == 8) R3D_OVP(8, false);
+    else if (nv == 16) R3D_OVP(16, false);
+    else return RAD_E_INVAL;
+#undef R3D_OVP
     return hipGetLastError() == hipSuccess ? RAD_OK : RAD_E_DEVICE;
 }
