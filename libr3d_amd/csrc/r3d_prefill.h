@@ -496,6 +496,24 @@ __global__ __launch_bounds__(64 * WV) void prefill_kernel(
     if (WMW > 1) read_a(smem, 1);
     int sl = 0;                                         /* ring slot of stage s */
     int s = 0;
+    /* e4m3 weights on the single-operand-set walk: six steps an iteration (the period of
+     * three ring slots and two weight sets), so every slot's LDS address is a constant and
+     * the reads take immediate offsets instead of per-read address arithmetic; the same
+     * steps in the same order as the two-step loop below, which takes the rest */
+    constexpr bool U6 = SS && F8;
+    if (U6) {
+        uint8_t* const r0 = smem;
+        uint8_t* const r1 = smem + L::STAGE;
+        uint8_t* const r2 = smem + 2 * L::STAGE;
+        for (; s + 6 <= steps; s += 6) {
+            step(s, 0, r0, r1, r2);
+            step(s + 1, 1, r1, r2, r0);
+            step(s + 2, 0, r2, r0, r1);
+            step(s + 3, 1, r0, r1, r2);
+            step(s + 4, 0, r1, r2, r0);
+            step(s + 5, 1, r2, r0, r1);
+        }
+    }
     for (; s + 2 <= steps; s += 2) {
         const int s1 = sl == 2 ? 0 : sl + 1, s2 = s1 == 2 ? 0 : s1 + 1;
         step(s, 0, smem + sl * L::STAGE, smem + s1 * L::STAGE, smem + s2 * L::STAGE);
